@@ -1,0 +1,321 @@
+/*
+ * inferc_hip.h — C-ABI of the MI355X (gfx950) backend for inferc's runtime
+ * hot path. Every entry point takes plain device pointers and sizes; no C++
+ * or torch types cross this boundary. All citations are path:line into the
+ * inferc repository, naming the reference function each entry point replaces.
+ *
+ * Conventions
+ *  - Every function returns an inferc_status; on failure a thread-local
+ *    message is available from inferc_hip_last_error(). No exception crosses
+ *    the ABI. (The reference throws std::runtime_error from its kernels, e.g.
+ *    src/kernels/attention.cc:35-39; a C++ caller rethrows on non-zero.)
+ *  - A context owns one device and one HIP stream. Kernel entry points are
+ *    asynchronous on that stream; h2d/d2h/sync synchronise it. A context is
+ *    single-threaded: one host thread at a time.
+ *  - Device pointers are caller-owned unless a function says otherwise.
+ *    Inputs are read-only; outputs must not alias inputs unless stated.
+ *  - Matrices are row-major with leading dimensions counted in elements.
+ */
+#ifndef INFERC_HIP_H_
+#define INFERC_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define INFERC_HIP_ABI_VERSION 1
+
+typedef enum {
+  INFERC_OK = 0,
+  INFERC_ERR_ARG = 1,         /* null pointer, bad enum, negative size      */
+  INFERC_ERR_SHAPE = 2,       /* inconsistent dimensions                    */
+  INFERC_ERR_HIP = 3,         /* HIP runtime error                          */
+  INFERC_ERR_OOM = 4,         /* device allocation failed                   */
+  INFERC_ERR_UNSUPPORTED = 5, /* op / dtype / configuration not supported   */
+  INFERC_ERR_STATE = 6        /* call out of order (e.g. missing input)     */
+} inferc_status;
+
+/* Epilogue activations. */
+typedef enum {
+  INFERC_ACT_NONE = 0,
+  INFERC_ACT_GELU_ERF = 1,  /* v*0.5*(1+erf(v*0.70710678)) */
+  INFERC_ACT_GELU_TANH = 2, /* 0.5*v*(1+tanh(0.79788456*(v+0.044715 v^3))) */
+  INFERC_ACT_RELU = 3
+} inferc_act;
+
+/* Kind of the C operand of a Gemm (the reference pre-fills the output with C,
+ * src/kernels/matmul.cc:174-193). */
+typedef enum {
+  INFERC_C_NONE = 0,
+  INFERC_C_ROW = 1,    /* C[N] broadcast over rows   */
+  INFERC_C_FULL = 2,   /* C[M,N] with leading dim ldc */
+  INFERC_C_SCALAR = 3  /* C[1]                        */
+} inferc_c_kind;
+
+/* Tensor element types (values of the reference's IR DType subset). */
+typedef enum {
+  INFERC_DT_F32 = 1,
+  INFERC_DT_U8 = 2,
+  INFERC_DT_I32 = 6,
+  INFERC_DT_I64 = 7,
+  INFERC_DT_BOOL = 9
+} inferc_dtype;
+
+typedef struct inferc_hip_ctx inferc_hip_ctx;
+
+/* ---------------- errors, context, memory ---------------- */
+
+const char* inferc_hip_last_error(void);
+int inferc_hip_abi_version(void);
+int inferc_hip_device_count(int* count);
+
+/* One device + one stream (replaces the process-wide state of
+ * src/util/parallel.cc:16-47 and the toggles of src/kernels/matmul.cc:56-61). */
+int inferc_hip_create(int device, inferc_hip_ctx** out);
+int inferc_hip_destroy(inferc_hip_ctx* ctx);
+/* Reserve at least `bytes` of context workspace (split-K partials, argmax
+ * partials, descriptor tables). Ops grow it on demand outside graph capture. */
+int inferc_hip_reserve_workspace(inferc_hip_ctx* ctx, size_t bytes);
+
+int inferc_hip_malloc(inferc_hip_ctx* ctx, size_t bytes, void** dptr);
+int inferc_hip_free(inferc_hip_ctx* ctx, void* dptr);
+int inferc_hip_h2d(inferc_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
+int inferc_hip_d2h(inferc_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
+int inferc_hip_d2d(inferc_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
+int inferc_hip_sync(inferc_hip_ctx* ctx);
+/* HIP-event timing on the context stream (the per-op wall clock of
+ * src/profiler/profiler.h:40-85, taken on the device). */
+int inferc_hip_timer_start(inferc_hip_ctx* ctx);
+int inferc_hip_timer_stop(inferc_hip_ctx* ctx, float* ms);
+
+/* ---------------- dense products ---------------- */
+
+/* ONNX Gemm: Y = act(alpha*op(A)*op(B) + beta*C (+ R)).
+ * Replaces rt::Gemm, src/kernels/matmul.cc:161-228 (incl. the M==1 sgemv
+ * route of :207-216), and — with c_kind/R/act — the MatMul->Add(b)->Add(res)
+ * and FusedMatMulAddGELU epilogues. op(A) is [M,K], op(B) is [K,N].
+ * R (nullable) is a residual [M,N] with leading dim ldr, added after C.
+ * Y may alias R (in-place residual update) but not A, B or C. */
+int inferc_hip_gemm_f32(inferc_hip_ctx* ctx, int trans_a, int trans_b,
+                        int64_t M, int64_t N, int64_t K, float alpha,
+                        const float* A, int64_t lda, const float* B,
+                        int64_t ldb, float beta, const float* C, int c_kind,
+                        int64_t ldc, const float* R, int64_t ldr, int act,
+                        float* Y, int64_t ldy);
+
+/* numpy MatMul over a flattened batch: Y[b] = A[b*stride_a] * B[b*stride_b],
+ * a stride of 0 broadcasts. Replaces rt::MatMul, src/kernels/matmul.cc:63-159. */
+int inferc_hip_matmul_f32(inferc_hip_ctx* ctx, int64_t batch, int64_t M,
+                          int64_t N, int64_t K, const float* A,
+                          int64_t stride_a, const float* B, int64_t stride_b,
+                          float* Y);
+
+/* Y[M,N] = GELU_erf(X[M,K]*W[K,N] + b[N]).
+ * Replaces rt::FusedMatMulAddGELU, src/kernels/fused_matmul_add_gelu.cc:13-80. */
+int inferc_hip_fused_matmul_add_gelu_f32(inferc_hip_ctx* ctx, int64_t M,
+                                         int64_t N, int64_t K, const float* X,
+                                         const float* W, const float* bias,
+                                         float* Y);
+
+/* Q,K,V[M,N] = X[M,K]*Wi[K,N] + bi[N], one launch for the three projections.
+ * Replaces rt::FusedQKVProjection, src/kernels/attention.cc:102-141. */
+int inferc_hip_fused_qkv_f32(inferc_hip_ctx* ctx, int64_t M, int64_t K,
+                             int64_t N, const float* X, const float* wq,
+                             const float* bq, const float* wk, const float* bk,
+                             const float* wv, const float* bv, float* q,
+                             float* k, float* v);
+
+/* ---------------- attention ---------------- */
+
+/* Multi-head attention over [B,S,H] (head h = columns [h*hd,(h+1)*hd)):
+ * O = softmax(mask(scale*Q_h K_h^T)) V_h with scale = 1/sqrtf(head_dim);
+ * masked scores take the value `fill`. `mask` (nullable, one byte per
+ * element, non-zero = masked) is read at
+ * b*ms[0] + h*ms[1] + i*ms[2] + j*ms[3]; `mask_strides` is a HOST array of 4.
+ * Replaces rt::FusedAttention, src/kernels/attention.cc:32-100
+ * (MaskStrides :17-29). */
+int inferc_hip_fused_attention_f32(inferc_hip_ctx* ctx, int64_t B, int64_t S,
+                                   int64_t H, int64_t head_dim, const float* q,
+                                   const float* k, const float* v,
+                                   const uint8_t* mask,
+                                   const int64_t* mask_strides, float fill,
+                                   float* out);
+
+/* ---------------- normalisation and pointwise ---------------- */
+
+/* y = LN(x (+ residual)) over the last `feat` elements of each row:
+ * mean, d = x-mean, var = mean(d^2), y = d*(1/sqrtf(var+eps))*gamma + beta.
+ * residual is nullable. Replaces rt::LayerNorm, src/kernels/activation.cc:103-150
+ * (dispatch of FusedLayerNorm at src/runtime/executor.cc:213-217). */
+int inferc_hip_layernorm_f32(inferc_hip_ctx* ctx, int64_t rows, int64_t feat,
+                             const float* x, const float* residual,
+                             const float* gamma, const float* beta, float eps,
+                             float* y);
+
+/* Pointwise activations; act is an inferc_act. Replaces rt::Gelu and
+ * rt::GeluTanh (src/kernels/activation.cc:15-50) and Relu
+ * (src/kernels/elementwise.cc). y may alias x. */
+int inferc_hip_activation_f32(inferc_hip_ctx* ctx, int64_t n, const float* x,
+                              int act, float* y);
+
+/* Softmax along an axis viewed as [outer, axis_dim, inner].
+ * Replaces rt::Softmax, src/kernels/activation.cc:52-101. */
+int inferc_hip_softmax_f32(inferc_hip_ctx* ctx, int64_t outer,
+                           int64_t axis_dim, int64_t inner, const float* x,
+                           float* y);
+
+/* y[i] = a[i] + b[i % b_n] (elementwise, row-bias or scalar broadcast).
+ * Replaces the hot-path forms of rt::Add, src/kernels/elementwise.cc:225. */
+int inferc_hip_add_f32(inferc_hip_ctx* ctx, int64_t n, const float* a,
+                       const float* b, int64_t b_n, float* y);
+
+/* out[k,:] = table[idx[k],:] for int64 device indices (negative wraps).
+ * Out-of-range indices write zeros and set *err_flag (device int32,
+ * nullable) to 1. Replaces rt::Gather axis 0, src/kernels/embedding.cc:9-72. */
+int inferc_hip_gather_f32(inferc_hip_ctx* ctx, int64_t rows, int64_t row_len,
+                          const float* table, const int64_t* idx,
+                          int64_t n_idx, float* out, int32_t* err_flag);
+
+/* Split / Concat of an [outer, axis, inner] view (QKV split, KV concat).
+ * parts / outs are HOST arrays of device pointers. Replace rt::Split and
+ * rt::Concat, src/kernels/movement.cc:391-431 and :142-189. */
+int inferc_hip_split_f32(inferc_hip_ctx* ctx, int64_t outer,
+                         int64_t axis_full, int64_t inner, int64_t n_parts,
+                         const int64_t* sizes, const float* x,
+                         float* const* outs);
+int inferc_hip_concat_f32(inferc_hip_ctx* ctx, int64_t outer, int64_t inner,
+                          int64_t n_parts, const int64_t* sizes,
+                          const float* const* parts, float* out);
+
+/* First index of the maximum of x[n] into *out_idx (device int64).
+ * Replaces the greedy argmax of src/cli/main.cpp:820-828,875-879. */
+int inferc_hip_argmax_f32(inferc_hip_ctx* ctx, int64_t n, const float* x,
+                          int64_t* out_idx);
+
+/* ---------------- batch-1 decode products ---------------- */
+
+/* y[N] = act(W[N,K] x (+ bias) (+ residual)); if ln_gamma is non-null the
+ * input is first normalised, x' = LN(x; ln_gamma, ln_beta, ln_eps), inside
+ * the kernel. W is the transB=1 layout (src/kernels/matmul.cc:207-216 routes
+ * exactly this form to cblas_sgemv); y may alias residual. */
+int inferc_hip_gemv_f32(inferc_hip_ctx* ctx, int64_t N, int64_t K,
+                        const float* W, const float* x, const float* ln_gamma,
+                        const float* ln_beta, float ln_eps, const float* bias,
+                        const float* residual, int act, float* y);
+
+/* int4 per-row-scale weights, reference layout: byte W[r*K/2 + k/2], low
+ * nibble = even k, q = nib - 8 (bench/amx/int4_gemv_amx.cc:258-271).
+ * unpack: out[r,k] = scales[r] * (float)q, bit-exact fp32 products. */
+int inferc_hip_int4_unpack(inferc_hip_ctx* ctx, int64_t N, int64_t K,
+                           const uint8_t* W, const float* scales, float* out);
+/* y[b,r] = sum_k (scales[r]*q[r,k]) * x[b,k] for b < batch (1..8).
+ * Replaces scalar_int4_gemv_perRow / amx_int4_gemv_b4_perRow,
+ * bench/amx/int4_gemv_amx.cc:258-356. K must be even. */
+int inferc_hip_int4_gemv(inferc_hip_ctx* ctx, int64_t N, int64_t K,
+                         const uint8_t* W, const float* scales,
+                         int64_t batch, const float* x, float* y);
+/* One launch over n_mats independent int4 GEMVs (all of a model's matrices).
+ * Ns, Ks and the pointer arrays are HOST arrays of length n_mats holding
+ * device pointers. x[i] is [batch, Ks[i]], y[i] is [batch, Ns[i]]. */
+int inferc_hip_int4_gemv_grouped(inferc_hip_ctx* ctx, int64_t n_mats,
+                                 const int64_t* Ns, const int64_t* Ks,
+                                 const uint8_t* const* W,
+                                 const float* const* scales, int64_t batch,
+                                 const float* const* x, float* const* y);
+
+/* Append one token's K/V (k_new/v_new [n_heads*head_dim]) at position *pos
+ * (device int64) of the caches [n_heads, max_t, head_dim], then attend:
+ * out = softmax((q.k_j)/sqrtf(head_dim), j <= pos) V. Replaces the
+ * with-past graph's Concat(past,new) -> MatMul -> Div -> Softmax -> MatMul
+ * (src/kernels/movement.cc:142-189 and the decode loop of
+ * src/cli/main.cpp:854-889). */
+int inferc_hip_kv_append_attend_f32(inferc_hip_ctx* ctx, int64_t n_heads,
+                                    int64_t head_dim, int64_t max_t,
+                                    const int64_t* pos, const float* q,
+                                    const float* k_new, const float* v_new,
+                                    float* k_cache, float* v_cache, float* out);
+
+/* ---------------- executor (rt::Executor) ---------------- */
+
+/* A host-side graph of (fused) nodes as the reference's passes leave it
+ * (src/ir/graph.h:45-97). Attributes are "name=value" pairs joined by ';'
+ * (ints, floats, comma-separated int lists). */
+typedef struct inferc_graph inferc_graph;
+int inferc_graph_create(inferc_graph** out);
+int inferc_graph_destroy(inferc_graph* g);
+int inferc_graph_add_initializer(inferc_graph* g, const char* name, int dtype,
+                                 int rank, const int64_t* shape,
+                                 const void* host_data);
+int inferc_graph_add_node(inferc_graph* g, const char* op_type,
+                          const char* name, int n_inputs,
+                          const char* const* inputs, int n_outputs,
+                          const char* const* outputs, const char* attrs);
+int inferc_graph_add_output(inferc_graph* g, const char* name);
+
+/* Executor: uploads every initializer once (src/runtime/executor.cc:89-96);
+ * run() walks the nodes in order and dispatches each op to a kernel
+ * (executor.cc:98-366). Unsupported ops fail with INFERC_ERR_UNSUPPORTED
+ * (executor.cc:340-343). After the first run for a given input shape the
+ * launch sequence is captured in a HIP graph and replayed. */
+typedef struct inferc_executor inferc_executor;
+int inferc_executor_create(inferc_hip_ctx* ctx, const inferc_graph* g,
+                           inferc_executor** out);
+int inferc_executor_destroy(inferc_executor* ex);
+/* Bind an input from host memory (copied to the device) or a device pointer
+ * (borrowed until the next set_input of that name). */
+int inferc_executor_set_input(inferc_executor* ex, const char* name, int dtype,
+                              int rank, const int64_t* shape,
+                              const void* host_data);
+int inferc_executor_set_input_device(inferc_executor* ex, const char* name,
+                                     int dtype, int rank, const int64_t* shape,
+                                     const void* dev_data);
+/* Enqueue one forward pass on the context stream. */
+int inferc_executor_run(inferc_executor* ex);
+/* Shape and dtype of a graph output after run(); shape has room for 8 dims. */
+int inferc_executor_output_info(inferc_executor* ex, const char* name,
+                                int* dtype, int* rank, int64_t* shape);
+/* Copy an output to host memory (synchronises the stream). */
+int inferc_executor_get_output(inferc_executor* ex, const char* name,
+                               void* host_dst, size_t capacity_bytes);
+/* 0 = eager dispatch every run, 1 = capture/replay HIP graphs (default). */
+int inferc_executor_set_graph_mode(inferc_executor* ex, int enabled);
+
+/* ---------------- GPT-2 greedy decode (inferc decode) ---------------- */
+
+typedef struct {
+  int64_t layers, hidden, heads, ffn, vocab, max_pos;
+  float eps;
+} inferc_gpt2_config;
+
+/* Weights are host pointers in this order (fp32, [K,N] = ONNX Gemm layout):
+ *   0 wte [V,H]  1 wpe [P,H]
+ *   per layer l, base 2+12l: +0 ln1_g +1 ln1_b +2 attn_w [H,3H] +3 attn_b
+ *     +4 proj_w [H,H] +5 proj_b +6 ln2_g +7 ln2_b +8 fc_w [H,F] +9 fc_b
+ *     +10 fcproj_w [F,H] +11 fcproj_b
+ *   tail, base 2+12L: +0 lnf_g +1 lnf_b
+ * Uploaded once; the LM head is the tied wte. max_t bounds prompt+generated. */
+typedef struct inferc_gpt2 inferc_gpt2;
+int inferc_gpt2_create(inferc_hip_ctx* ctx, const inferc_gpt2_config* cfg,
+                       const float* const* host_weights, int64_t max_t,
+                       inferc_gpt2** out);
+int inferc_gpt2_destroy(inferc_gpt2* m);
+/* The decode loop of src/cli/main.cpp:786-896: prefill over the prompt,
+ * argmax, then max_tokens-1 cached steps (one replayed HIP graph each).
+ * tokens_out[max_tokens] (host). step_ms (host, nullable) receives the
+ * device time of each post-prefill step; last_logits (host, nullable, [V])
+ * the final step's logits. */
+int inferc_gpt2_generate(inferc_gpt2* m, const int64_t* prompt,
+                         int64_t n_prompt, int64_t max_tokens,
+                         int64_t* tokens_out, float* step_ms,
+                         float* last_logits);
+/* Full-sequence forward logits [n, V] (host) for every position. */
+int inferc_gpt2_forward(inferc_gpt2* m, const int64_t* ids, int64_t n,
+                        float* logits);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* INFERC_HIP_H_ */

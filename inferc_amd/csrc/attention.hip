@@ -1,0 +1,321 @@
+// Fused multi-head attention (prefill / encoder) on CDNA4 matrix cores.
+//
+// Reference: rt::FusedAttention, src/kernels/attention.cc:32-100. Per
+// (batch, head): scores = (1/sqrt(d)) * Q_h K_h^T, masked entries set to
+// `fill`, softmax with max subtraction, context = P V_h, written in place into
+// the [B,S,H] output at column offset h*d.
+//
+// Design (head_dim 64): a wave owns 32 queries and walks the keys in tiles of
+// 32 that the block stages through LDS (double-buffered). Scores are computed
+// transposed, S^T = K Q^T, with v_mfma_f32_32x32x2_f32: in that layout every
+// lane holds 16 scores of ONE query (column lane%32), so
+//   - the online-softmax max/sum need one cross-half shuffle per tile,
+//   - the rescale of the running output is a per-lane scalar, and
+//   - the probabilities are already in the B-operand layout of the next MFMA,
+//     O^T += V^T P^T, once the key index of the V operand is permuted to match
+//     (the summation index of an MFMA is a dummy index).
+// Softmax is online (running max and sum, output rescaled per tile); the
+// reference's two-pass softmax is reproduced to fp32 rounding. Key tiles past
+// the last unmasked key of a query-independent mask, and tiles above the
+// causal diagonal, are skipped; that is exact because exp(fill - max) is 0 in
+// fp32 once one unmasked key has been seen.
+#include "common.h"
+
+namespace ih {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kD = 64;     // head_dim of the MFMA kernel
+constexpr int kKT = 32;    // keys per tile
+constexpr int kKS = kD + 1;  // LDS row stride of K (odd: conflict-free column reads)
+constexpr int kVS = kD + 4;  // LDS row stride of V (float4-aligned rows)
+
+struct AttnP {
+  int64_t B, S, nH;
+  const float* q;
+  const float* k;
+  const float* v;
+  int64_t ldq, ldk, ldv, ldo;
+  const uint8_t* mask;
+  int64_t ms0, ms1, ms2, ms3;
+  float fill, scale;
+  int causal;
+  float* out;
+};
+
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
+  constexpr int NT = 64 * WAVES;
+  __shared__ __attribute__((aligned(16))) float Ks[2][kKT * kKS];
+  __shared__ __attribute__((aligned(16))) float Vs[2][kKT * kVS];
+  __shared__ int s_last_valid;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const int64_t qb0 = int64_t(blockIdx.x) * (32 * WAVES);
+  const int64_t q0 = qb0 + 32 * wave;
+  const int64_t qi = q0 + l32;  // this lane's query
+  const int64_t S = p.S;
+
+  const float* qbase = p.q + b * S * p.ldq + h * kD;
+  const float* kbase = p.k + b * S * p.ldk + h * kD;
+  const float* vbase = p.v + b * S * p.ldv + h * kD;
+  const uint8_t* mbase = p.mask ? p.mask + b * p.ms0 + h * p.ms1 : nullptr;
+
+  // Key range of this block.
+  int64_t key_end = S;
+  if (p.causal) {
+    const int64_t qlast = qb0 + 32 * WAVES;
+    key_end = qlast < S ? qlast : S;
+  } else if (mbase && p.ms2 == 0) {
+    // Query-independent mask: stop after the last unmasked key. If every key
+    // is masked, keep all of them (softmax over `fill` values, as the
+    // reference computes it).
+    if (tid == 0) s_last_valid = -1;
+    __syncthreads();
+    int last = -1;
+    for (int64_t j = tid; j < S; j += NT)
+      if (!mbase[j * p.ms3]) last = int(j);
+    if (last >= 0) atomicMax(&s_last_valid, last);
+    __syncthreads();
+    if (s_last_valid >= 0) key_end = s_last_valid + 1;
+  }
+  const int64_t ntiles = (key_end + kKT - 1) / kKT;
+
+  // Q^T operand: step s covers dims 2s, 2s+1; lane supplies Q[qi][2s+half].
+  float qf[kD / 2];
+#pragma unroll
+  for (int s = 0; s < kD / 2; ++s) qf[s] = (qi < S) ? qbase[qi * p.ldq + 2 * s + half] : 0.0f;
+
+  floatx16 oacc[2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) oacc[d][v] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  // Cooperative K/V tile staging: 32 keys x 64 dims = 512 float4 per tensor.
+  constexpr int NV = (kKT * kD / 4 + NT - 1) / NT;
+  float4 kr[NV], vr[NV];
+  auto load_tile = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int idx = tid + NT * i;
+      const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
+      kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      vr[i] = kr[i];
+      if (idx < kKT * kD / 4 && k0 + key < S) {
+        const float* kp = kbase + (k0 + key) * p.ldk + dq;
+        const float* vp = vbase + (k0 + key) * p.ldv + dq;
+        kr[i] = make_float4(kp[0], kp[1], kp[2], kp[3]);
+        vr[i] = make_float4(vp[0], vp[1], vp[2], vp[3]);
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int idx = tid + NT * i;
+      if (idx < kKT * kD / 4) {
+        const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
+        float* ks = &Ks[buf][key * kKS + dq];
+        ks[0] = kr[i].x; ks[1] = kr[i].y; ks[2] = kr[i].z; ks[3] = kr[i].w;
+        *reinterpret_cast<float4*>(&Vs[buf][key * kVS + dq]) = vr[i];
+      }
+    }
+  };
+
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int64_t t = 0; t < ntiles; ++t) {
+    const int cur = int(t & 1);
+    const int64_t k0 = t * kKT;
+    if (t + 1 < ntiles) load_tile(k0 + kKT);
+
+    // A wave whose 32 queries all lie above this tile's keys skips it
+    // (causal), as does a wave past the end of the sequence.
+    const bool skip = (q0 >= S) || (p.causal && k0 > q0 + 31);
+    if (!skip) {
+      const float* ks = Ks[cur];
+      const float* vs = Vs[cur];
+      floatx16 sacc;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < kD / 2; ++s) {
+        const float a = ks[l32 * kKS + 2 * s + half];
+        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, qf[s], sacc, 0, 0, 0);
+      }
+      // sacc[v]: key k0 + 8*(v/4) + 4*half + v%4, query qi.
+      float sv[16];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t j = k0 + 8 * (v >> 2) + 4 * half + (v & 3);
+        float s = p.scale * sacc[v];
+        if (j >= S) {
+          s = -INFINITY;  // key does not exist
+        } else if (p.causal) {
+          if (j > qi) s = p.fill;
+        } else if (mbase && qi < S) {
+          if (mbase[qi * p.ms2 + j * p.ms3]) s = p.fill;
+        }
+        sv[v] = s;
+        tmax = fmaxf(tmax, s);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      const float m_new = fmaxf(m_run, tmax);
+      const float corr = __expf(m_run - m_new);
+      float lsum = 0.0f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        sv[v] = __expf(sv[v] - m_new);
+        lsum += sv[v];
+      }
+      lsum += __shfl_xor(lsum, 32, 64);
+      l_run = l_run * corr + lsum;
+      m_run = m_new;
+#pragma unroll
+      for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) oacc[d][v] *= corr;
+      // O^T[dim][query] += V^T[dim][key] P^T[key][query]; step s pairs key
+      // 8*(s/4) + 4*kidx + s%4 with the MFMA summation index kidx.
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const int key = 8 * (s >> 2) + 4 * half + (s & 3);
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const float a = vs[key * kVS + d * 32 + l32];
+          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, sv[s], oacc[d], 0, 0, 0);
+        }
+      }
+    }
+    if (t + 1 < ntiles) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  if (qi >= S) return;
+  const float inv = 1.0f / l_run;
+  float* orow = p.out + (b * S + qi) * p.ldo + h * kD;
+  // oacc[d][v]: dim d*32 + 8*(v/4) + 4*half + v%4 of query qi.
+  const bool vec = (p.ldo % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0);
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float* dst = orow + d * 32 + 8 * g + 4 * half;
+      const float4 o = make_float4(oacc[d][4 * g] * inv, oacc[d][4 * g + 1] * inv,
+                                   oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv);
+      if (vec) {
+        *reinterpret_cast<float4*>(dst) = o;
+      } else {
+        dst[0] = o.x; dst[1] = o.y; dst[2] = o.z; dst[3] = o.w;
+      }
+    }
+}
+
+// Any head_dim up to 256: one thread per (b, h, query) with an online softmax
+// over the keys. Used for shapes the MFMA kernel does not cover.
+constexpr int kMaxGenericD = 256;
+
+__global__ __launch_bounds__(128) void attn_fwd_generic(AttnP p, int64_t D) {
+  const int64_t total = p.B * p.nH * p.S;
+  const int64_t t = int64_t(blockIdx.x) * 128 + threadIdx.x;
+  if (t >= total) return;
+  const int64_t i = t % p.S, h = (t / p.S) % p.nH, b = t / (p.S * p.nH);
+  const float* qr = p.q + (b * p.S + i) * p.ldq + h * D;
+  const uint8_t* mb = p.mask ? p.mask + b * p.ms0 + h * p.ms1 + i * p.ms2 : nullptr;
+  float o[kMaxGenericD];
+  for (int64_t d = 0; d < D; ++d) o[d] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+  for (int64_t j = 0; j < p.S; ++j) {
+    const float* kr = p.k + (b * p.S + j) * p.ldk + h * D;
+    float acc = 0.0f;
+    for (int64_t d = 0; d < D; ++d) acc += qr[d] * kr[d];
+    float s = p.scale * acc;
+    if (p.causal ? (j > i) : (mb && mb[j * p.ms3])) s = p.fill;
+    const float m_new = fmaxf(m, s);
+    const float corr = expf(m - m_new);
+    const float e = expf(s - m_new);
+    l = l * corr + e;
+    const float* vr = p.v + (b * p.S + j) * p.ldv + h * D;
+    for (int64_t d = 0; d < D; ++d) o[d] = o[d] * corr + e * vr[d];
+    m = m_new;
+  }
+  float* orow = p.out + (b * p.S + i) * p.ldo + h * D;
+  const float inv = 1.0f / l;
+  for (int64_t d = 0; d < D; ++d) orow[d] = o[d] * inv;
+}
+
+}  // namespace
+
+void attention(inferc_hip_ctx* ctx, const AttnArgs& a) {
+  IH_REQUIRE(a.B >= 0 && a.S >= 0 && a.H > 0 && a.head_dim > 0, INFERC_ERR_SHAPE,
+             "attention: bad shape");
+  IH_REQUIRE(a.H % a.head_dim == 0, INFERC_ERR_SHAPE,
+             "FusedAttention: H not divisible by head_dim");
+  if (a.B == 0 || a.S == 0) return;
+  IH_REQUIRE(a.q && a.k && a.v && a.out, INFERC_ERR_ARG, "attention: null pointer");
+  IH_REQUIRE(a.ldq >= a.H && a.ldk >= a.H && a.ldv >= a.H && a.ldo >= a.H, INFERC_ERR_SHAPE,
+             "attention: row stride smaller than H");
+  AttnP p{};
+  p.B = a.B; p.S = a.S; p.nH = a.H / a.head_dim;
+  p.q = a.q; p.k = a.k; p.v = a.v;
+  p.ldq = a.ldq; p.ldk = a.ldk; p.ldv = a.ldv; p.ldo = a.ldo;
+  p.mask = a.mask;
+  p.ms0 = a.ms[0]; p.ms1 = a.ms[1]; p.ms2 = a.ms[2]; p.ms3 = a.ms[3];
+  p.fill = a.fill;
+  p.scale = 1.0f / sqrtf(float(a.head_dim));
+  p.causal = a.causal;
+  p.out = a.out;
+  if (a.head_dim == kD) {
+    IH_REQUIRE(a.B < 65536 && p.nH < 65536, INFERC_ERR_SHAPE, "attention: grid too large");
+    const int64_t blocks4 = ceil_div(a.S, 128) * p.nH * a.B;
+    if (blocks4 >= ctx->num_cus) {
+      dim3 grid(unsigned(ceil_div(a.S, 128)), unsigned(p.nH), unsigned(a.B));
+      hipLaunchKernelGGL(attn_fwd_d64<4>, grid, dim3(256), 0, ctx->stream, p);
+    } else {
+      dim3 grid(unsigned(ceil_div(a.S, 32)), unsigned(p.nH), unsigned(a.B));
+      hipLaunchKernelGGL(attn_fwd_d64<1>, grid, dim3(64), 0, ctx->stream, p);
+    }
+    check_launch("attn_fwd_d64");
+    return;
+  }
+  IH_REQUIRE(a.head_dim <= kMaxGenericD, INFERC_ERR_UNSUPPORTED,
+             "attention: head_dim > 256 is not supported");
+  const int64_t total = a.B * p.nH * a.S;
+  hipLaunchKernelGGL(attn_fwd_generic, dim3(unsigned(ceil_div(total, 128))), dim3(128), 0,
+                     ctx->stream, p, a.head_dim);
+  check_launch("attn_fwd_generic");
+}
+
+}  // namespace ih
+
+extern "C" int inferc_hip_fused_attention_f32(inferc_hip_ctx* ctx, int64_t B, int64_t S,
+                                              int64_t H, int64_t head_dim, const float* q,
+                                              const float* k, const float* v,
+                                              const uint8_t* mask, const int64_t* mask_strides,
+                                              float fill, float* out) {
+  return ih::guard([&] {
+    ih::check_ctx(ctx)->make_current();
+    ih::AttnArgs a;
+    a.B = B; a.S = S; a.H = H; a.head_dim = head_dim;
+    a.q = q; a.k = k; a.v = v;
+    a.ldq = a.ldk = a.ldv = a.ldo = H;
+    a.mask = mask;
+    if (mask) {
+      IH_REQUIRE(mask_strides != nullptr, INFERC_ERR_ARG, "attention: mask without strides");
+      for (int i = 0; i < 4; ++i) a.ms[i] = mask_strides[i];
+    }
+    a.fill = fill;
+    a.out = out;
+    ih::attention(ctx, a);
+  });
+}

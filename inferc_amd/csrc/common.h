@@ -1,0 +1,206 @@
+// Shared internals of the gfx950 backend: error plumbing, the context, and
+// small device helpers. Not part of the C-ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/inferc_hip.h"
+
+namespace ih {
+
+// Internal error carried to the ABI edge, where it becomes a status code plus
+// the thread-local message.
+struct Error {
+  int code;
+  std::string msg;
+};
+
+void set_last_error(const std::string& msg);
+
+[[noreturn]] inline void fail(int code, const std::string& msg) {
+  throw Error{code, msg};
+}
+
+#define IH_HIP(expr)                                                        \
+  do {                                                                      \
+    hipError_t ih_e_ = (expr);                                              \
+    if (ih_e_ != hipSuccess)                                                \
+      ::ih::fail(ih_e_ == hipErrorOutOfMemory ? INFERC_ERR_OOM              \
+                                              : INFERC_ERR_HIP,             \
+                 std::string(#expr) + ": " + hipGetErrorString(ih_e_));     \
+  } while (0)
+
+#define IH_REQUIRE(cond, code, msg)          \
+  do {                                       \
+    if (!(cond)) ::ih::fail((code), (msg));  \
+  } while (0)
+
+// Runs `f`, converting every failure into a status code (no exception crosses
+// the C-ABI).
+template <class F>
+int guard(F&& f) {
+  try {
+    f();
+    return INFERC_OK;
+  } catch (const Error& e) {
+    set_last_error(e.msg);
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    set_last_error("host allocation failed");
+    return INFERC_ERR_OOM;
+  } catch (const std::exception& e) {
+    set_last_error(e.what());
+    return INFERC_ERR_HIP;
+  } catch (...) {
+    set_last_error("unknown error");
+    return INFERC_ERR_HIP;
+  }
+}
+
+// Throws if the last launch failed (bad configuration, missing code object).
+inline void check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) fail(INFERC_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace ih
+
+// One device, one stream, one growable workspace.
+struct inferc_hip_ctx {
+  int device = 0;
+  int num_cus = 256;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
+  // Bumped whenever the workspace is reallocated: a captured HIP graph that
+  // baked in the old address must be re-captured.
+  uint64_t ws_generation = 0;
+  bool capturing = false;  // set while a HIP graph is being recorded
+
+  // Returns a workspace of at least `bytes`; grows it outside capture only.
+  void* ws(size_t bytes);
+  void make_current() const;
+};
+
+namespace ih {
+
+inferc_hip_ctx* check_ctx(inferc_hip_ctx* ctx);
+
+// ---------------- device helpers ----------------
+
+__device__ __forceinline__ float gelu_erf_f(float v) {
+  // src/kernels/fused_matmul_add_gelu.cc:56,73-75: multiply by 1/sqrt(2).
+  return v * 0.5f * (1.0f + erff(v * 0.70710678118654752440f));
+}
+
+__device__ __forceinline__ float gelu_tanh_f(float v) {
+  // src/kernels/activation.cc:42-47.
+  const float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+  return 0.5f * v * (1.0f + tanhf(inner));
+}
+
+__device__ __forceinline__ float apply_act(float v, int act) {
+  switch (act) {
+    case INFERC_ACT_GELU_ERF: return gelu_erf_f(v);
+    case INFERC_ACT_GELU_TANH: return gelu_tanh_f(v);
+    case INFERC_ACT_RELU: return v > 0.0f ? v : 0.0f;
+    default: return v;
+  }
+}
+
+// Wave64 butterfly reductions (all lanes receive the result).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+}  // namespace ih
+
+// Internal launchers shared between translation units (all enqueue on
+// ctx->stream and throw ih::Error on bad arguments).
+namespace ih {
+
+struct GemmArgs {
+  int trans_a = 0, trans_b = 0;
+  int64_t M = 0, N = 0, K = 0;
+  float alpha = 1.0f, beta = 0.0f;
+  const float* A = nullptr;
+  int64_t lda = 0;
+  const float* B = nullptr;
+  int64_t ldb = 0;
+  const float* C = nullptr;
+  int c_kind = INFERC_C_NONE;
+  int64_t ldc = 0;
+  const float* R = nullptr;
+  int64_t ldr = 0;
+  int act = INFERC_ACT_NONE;
+  float* Y = nullptr;
+  int64_t ldy = 0;
+  // batching: blockIdx.z selects slice b; strides in elements (0 broadcasts)
+  int64_t batch = 1, stride_a = 0, stride_b = 0, stride_y = 0, stride_r = 0;
+};
+
+void gemm(inferc_hip_ctx* ctx, const GemmArgs& a);
+
+// Three projections that share X in one launch: Y_i = X*W_i + b_i.
+void gemm_qkv(inferc_hip_ctx* ctx, int64_t M, int64_t K, int64_t N, const float* X,
+              const float* const w[3], const float* const b[3], float* const y[3],
+              int64_t ldy);
+
+struct AttnArgs {
+  int64_t B = 0, S = 0, H = 0, head_dim = 0;
+  const float* q = nullptr;
+  const float* k = nullptr;
+  const float* v = nullptr;
+  int64_t ldq = 0, ldk = 0, ldv = 0, ldo = 0;  // row strides (elements)
+  const uint8_t* mask = nullptr;
+  int64_t ms[4] = {0, 0, 0, 0};
+  float fill = -3.0e38f;
+  int causal = 0;  // mask j > i with `fill` (GPT-2 prefill)
+  float* out = nullptr;
+};
+
+void attention(inferc_hip_ctx* ctx, const AttnArgs& a);
+
+void layernorm(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
+               const float* residual, const float* gamma, const float* beta, float eps,
+               float* y);
+void activation(inferc_hip_ctx* ctx, int64_t n, const float* x, int act, float* y);
+void add_bcast(inferc_hip_ctx* ctx, int64_t n, const float* a, const float* b, int64_t b_n,
+               float* y);
+void gather_rows(inferc_hip_ctx* ctx, int64_t rows, int64_t row_len, const float* table,
+                 const int64_t* idx, int64_t n_idx, float* out, int32_t* err_flag);
+// `partial` (nullable) is caller-owned scratch of kArgmaxScratchBytes; when
+// null the context workspace is used.
+constexpr size_t kArgmaxScratchBytes = 256 * 16;
+void argmax(inferc_hip_ctx* ctx, int64_t n, const float* x, int64_t* out_idx,
+            void* partial = nullptr);
+void copy2d(inferc_hip_ctx* ctx, float* dst, int64_t dpitch, const float* src, int64_t spitch,
+            int64_t width, int64_t height);
+void equal_i64(inferc_hip_ctx* ctx, int64_t n, const int64_t* a, const int64_t* b, int64_t b_n,
+               uint8_t* out);
+void kv_append_attend(inferc_hip_ctx* ctx, int64_t nH, int64_t D, int64_t T,
+                      const int64_t* pos, const float* q, const float* k_new,
+                      const float* v_new, float* kc, float* vc, float* out);
+
+void gemv(inferc_hip_ctx* ctx, int64_t N, int64_t K, const float* W, const float* x,
+          const float* ln_g, const float* ln_b, float ln_eps, const float* bias,
+          const float* residual, int act, float* y);
+
+}  // namespace ih

@@ -1,0 +1,550 @@
+// GPT-2 greedy decode on one GPU: device-resident weights, a preallocated
+// device KV cache, and a decode step that is captured once as a HIP graph and
+// replayed per token. The step's kernels read the position and the current
+// token from a small device state block that the step itself advances, so the
+// host only launches the graph.
+//
+// Reference: `inferc decode` (src/cli/main.cpp:700-936) running the GPT-2
+// with-past graph through rt::Executor. Per layer the graph computes
+//   LN -> Gemm(c_attn) -> Split -> Concat(past, new) -> QK^T -> Div(8) ->
+//   Where(causal) -> Softmax -> PV -> Gemm(c_proj) -> Add(residual) -> LN ->
+//   Gemm(c_fc) -> GeluTanh -> Gemm(c_proj) -> Add(residual)
+// then final LN and logits = h * wte^T (folded transpose,
+// src/ir/passes/constant_fold.cc:12-54), and the host takes the first argmax
+// (main.cpp:875-879). Here each Gemm at M=1 is one HBM-streaming GEMV with the
+// preceding LayerNorm fused into its prologue and bias / residual / GELU in
+// its epilogue; Concat+attention is one kernel over the device cache.
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace ih {
+namespace {
+
+constexpr int kBlock = 256;
+
+struct KvP {
+  int64_t nH, D, T;
+  const int64_t* pos;
+  const float* q;
+  const float* k_new;
+  const float* v_new;
+  float* kc;  // [nH, T, D]
+  float* vc;
+  float* out;  // [nH*D]
+};
+
+// One block per head. Appends the token's K/V at *pos, then computes
+// softmax((q.k_j)/sqrt(D)) over j <= pos and the weighted sum of V rows.
+__global__ __launch_bounds__(kBlock) void kv_append_attend_kernel(KvP p) {
+  extern __shared__ float sc[];  // [T] scores / probabilities
+  __shared__ float qs[256];
+  __shared__ float red[kBlock / 64];
+  __shared__ float opart[kBlock];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t h = blockIdx.x, D = p.D, T = p.T;
+  const int64_t pos = *p.pos;
+  if (pos < 0 || pos >= T) return;  // host guarantees the range
+  const int64_t t = pos + 1;
+  float* kc = p.kc + h * T * D;
+  float* vc = p.vc + h * T * D;
+  const float* kn = p.k_new + h * D;
+  const float* vn = p.v_new + h * D;
+  for (int64_t d = tid; d < D; d += kBlock) {
+    kc[pos * D + d] = kn[d];
+    vc[pos * D + d] = vn[d];
+    qs[d] = p.q[h * D + d];
+  }
+  __syncthreads();
+  // Scores: D/4 lanes per key, each lane a float4 slice of the row.
+  const int lpk = int(D / 4), kpw = 64 / lpk;
+  const float rs = sqrtf(float(D));
+  for (int64_t base = int64_t(wave) * kpw; base < t; base += int64_t(kBlock / 64) * kpw) {
+    const int64_t j = base + lane / lpk;
+    const int dl = (lane % lpk) * 4;
+    float dot = 0.0f;
+    if (j < t && lane < kpw * lpk) {
+      // The new row is read from the input vector, not back from the cache.
+      const float* kr = (j == pos) ? kn : kc + j * D;
+      const float4 kv = *reinterpret_cast<const float4*>(kr + dl);
+      dot = qs[dl] * kv.x + qs[dl + 1] * kv.y + qs[dl + 2] * kv.z + qs[dl + 3] * kv.w;
+    }
+    for (int o = lpk / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
+    if (j < t && (lane % lpk) == 0 && lane < kpw * lpk) sc[j] = dot / rs;
+  }
+  __syncthreads();
+  float m = -INFINITY;
+  for (int64_t j = tid; j < t; j += kBlock) m = fmaxf(m, sc[j]);
+  m = wave_max(m);
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  m = red[0];
+  for (int w = 1; w < kBlock / 64; ++w) m = fmaxf(m, red[w]);
+  __syncthreads();
+  float s = 0.0f;
+  for (int64_t j = tid; j < t; j += kBlock) {
+    const float e = expf(sc[j] - m);
+    sc[j] = e;
+    s += e;
+  }
+  s = wave_sum(s);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  s = 0.0f;
+  for (int w = 0; w < kBlock / 64; ++w) s += red[w];
+  const float inv = 1.0f / s;
+  // out[d] = sum_j p_j v[j][d]: thread (d, g) sums keys j = g (mod groups).
+  const int groups = int(kBlock / D);
+  const int d = tid % int(D), g = tid / int(D);
+  float acc = 0.0f;
+  if (g < groups) {
+    for (int64_t j = g; j < t; j += groups) {
+      const float* vr = (j == pos) ? vn : vc + j * D;
+      acc += (sc[j] * inv) * vr[d];
+    }
+  }
+  opart[tid] = acc;
+  __syncthreads();
+  if (tid < D) {
+    float o = 0.0f;
+    for (int gg = 0; gg < groups; ++gg) o += opart[gg * D + tid];
+    p.out[h * D + tid] = o;
+  }
+}
+
+// h[c] = wte[tok][c] + wpe[pos][c] with (pos, tok) = (state[0], state[1]).
+__global__ __launch_bounds__(kBlock) void embed_step_kernel(const float* __restrict__ wte,
+                                                            const float* __restrict__ wpe,
+                                                            const int64_t* __restrict__ state,
+                                                            int64_t H, float* __restrict__ h) {
+  const int64_t pos = state[0], tok = state[1];
+  for (int64_t c = int64_t(blockIdx.x) * kBlock + threadIdx.x; c < H;
+       c += int64_t(gridDim.x) * kBlock)
+    h[c] = wte[tok * H + c] + wpe[pos * H + c];
+}
+
+// Prefill embedding: rows i < n, ids validated on the host.
+__global__ __launch_bounds__(kBlock) void embed_rows_kernel(const float* __restrict__ wte,
+                                                            const float* __restrict__ wpe,
+                                                            const int64_t* __restrict__ ids,
+                                                            int64_t n, int64_t H,
+                                                            float* __restrict__ h) {
+  for (int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x; e < n * H;
+       e += int64_t(gridDim.x) * kBlock) {
+    const int64_t i = e / H, c = e % H;
+    h[e] = wte[ids[i] * H + c] + wpe[i * H + c];
+  }
+}
+
+// Scatter the K and V columns of qkv rows [n, 3H] into the caches at
+// positions pos0 .. pos0+n-1 ([nH, T, D] per tensor).
+__global__ __launch_bounds__(kBlock) void kv_scatter_kernel(const float* __restrict__ qkv,
+                                                            int64_t n, int64_t pos0, int64_t nH,
+                                                            int64_t D, int64_t T,
+                                                            float* __restrict__ kc,
+                                                            float* __restrict__ vc) {
+  const int64_t H = nH * D;
+  for (int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x; e < n * H;
+       e += int64_t(gridDim.x) * kBlock) {
+    const int64_t i = e / H, c = e % H, hh = c / D, d = c % D;
+    kc[(hh * T + pos0 + i) * D + d] = qkv[i * 3 * H + H + c];
+    vc[(hh * T + pos0 + i) * D + d] = qkv[i * 3 * H + 2 * H + c];
+  }
+}
+
+// After the argmax of a step whose input sat at state[0]: record the token at
+// sequence position state[0]+1 and advance the state.
+__global__ void advance_state_kernel(int64_t* __restrict__ state, int64_t* __restrict__ tokens) {
+  if (threadIdx.x == 0) {
+    const int64_t pos = state[0], tok = state[2];
+    tokens[pos + 1] = tok;
+    state[1] = tok;
+    state[0] = pos + 1;
+  }
+}
+
+}  // namespace
+
+void kv_append_attend(inferc_hip_ctx* ctx, int64_t nH, int64_t D, int64_t T,
+                      const int64_t* pos, const float* q, const float* k_new,
+                      const float* v_new, float* kc, float* vc, float* out) {
+  IH_REQUIRE(nH > 0 && D > 0 && T > 0, INFERC_ERR_SHAPE, "kv_append_attend: bad shape");
+  IH_REQUIRE(D % 4 == 0 && D <= 256 && 64 % (D / 4) == 0, INFERC_ERR_UNSUPPORTED,
+             "kv_append_attend: head_dim must be a multiple of 4 dividing 256");
+  IH_REQUIRE(T <= 16384, INFERC_ERR_UNSUPPORTED, "kv_append_attend: max_t > 16384");
+  IH_REQUIRE(pos && q && k_new && v_new && kc && vc && out, INFERC_ERR_ARG,
+             "kv_append_attend: null pointer");
+  IH_REQUIRE(aligned16(q) && aligned16(k_new) && aligned16(kc) && aligned16(vc),
+             INFERC_ERR_ARG, "kv_append_attend: pointers must be 16-byte aligned");
+  KvP p{nH, D, T, pos, q, k_new, v_new, kc, vc, out};
+  hipLaunchKernelGGL(kv_append_attend_kernel, dim3(unsigned(nH)), dim3(kBlock),
+                     size_t(T) * sizeof(float), ctx->stream, p);
+  check_launch("kv_append_attend");
+}
+
+}  // namespace ih
+
+// ---------------------------------------------------------------- GPT-2 model
+
+struct inferc_gpt2 {
+  inferc_hip_ctx* ctx = nullptr;
+  inferc_gpt2_config cfg{};
+  int64_t max_t = 0;
+  std::vector<void*> allocs;
+  float* wte = nullptr;  // [V, H]: tied LM head, already the [N, K] GEMV layout
+  float* wpe = nullptr;
+  struct Layer {
+    float *ln1_g, *ln1_b, *attn_w, *attn_b, *proj_w, *proj_b;
+    float *ln2_g, *ln2_b, *fc_w, *fc_b, *fcproj_w, *fcproj_b;  // *_w are [N, K]
+  };
+  std::vector<Layer> layers;
+  float *lnf_g = nullptr, *lnf_b = nullptr;
+  float *kc = nullptr, *vc = nullptr;  // [L, nH, max_t, D]
+  float *h = nullptr, *qkv = nullptr, *att = nullptr, *f = nullptr, *logits = nullptr;
+  int64_t* state = nullptr;   // [0] pos of the next input token, [1] that token, [2] argmax
+  int64_t* tokens = nullptr;  // [max_t + 1]
+  void* argmax_ws = nullptr;  // model-owned, so the captured step never uses ctx->ws
+  int64_t* ids = nullptr;     // [max_t]
+  float *ph = nullptr, *pa = nullptr, *pqkv = nullptr, *patt = nullptr, *pf = nullptr;
+  hipGraphExec_t step_exec = nullptr;
+  hipGraph_t step_graph = nullptr;
+  std::vector<hipEvent_t> events;
+
+  template <class T>
+  T* alloc(size_t n) {
+    void* p = nullptr;
+    IH_HIP(hipMalloc(&p, n * sizeof(T)));
+    allocs.push_back(p);
+    return static_cast<T*>(p);
+  }
+  void release() {
+    if (step_exec) (void)hipGraphExecDestroy(step_exec);
+    if (step_graph) (void)hipGraphDestroy(step_graph);
+    for (auto e : events) (void)hipEventDestroy(e);
+    for (void* p : allocs) (void)hipFree(p);
+    allocs.clear();
+    events.clear();
+    step_exec = nullptr;
+    step_graph = nullptr;
+  }
+
+  float* upload(const float* src, size_t n) {
+    float* d = alloc<float>(n);
+    IH_HIP(hipMemcpy(d, src, n * sizeof(float), hipMemcpyHostToDevice));
+    return d;
+  }
+  // ONNX Gemm weights are [K, N]; the GEMV streams rows of [N, K].
+  float* upload_transposed(const float* src, int64_t K, int64_t N) {
+    std::vector<float> t(size_t(K) * size_t(N));
+    for (int64_t k = 0; k < K; ++k)
+      for (int64_t n = 0; n < N; ++n) t[size_t(n) * K + k] = src[size_t(k) * N + n];
+    return upload(t.data(), t.size());
+  }
+
+  int64_t H() const { return cfg.hidden; }
+  int64_t D() const { return cfg.hidden / cfg.heads; }
+  float* kc_l(int64_t l) const { return kc + l * cfg.heads * max_t * D(); }
+  float* vc_l(int64_t l) const { return vc + l * cfg.heads * max_t * D(); }
+
+  // One decode step for the token in state[1] at position state[0].
+  void enqueue_step() {
+    hipStream_t s = ctx->stream;
+    const int64_t Hh = H(), F = cfg.ffn, V = cfg.vocab;
+    hipLaunchKernelGGL(ih::embed_step_kernel, dim3(unsigned(ih::ceil_div(Hh, ih::kBlock))),
+                       dim3(ih::kBlock), 0, s, wte, wpe, state, Hh, h);
+    ih::check_launch("embed_step");
+    for (int64_t l = 0; l < cfg.layers; ++l) {
+      const Layer& L = layers[size_t(l)];
+      ih::gemv(ctx, 3 * Hh, Hh, L.attn_w, h, L.ln1_g, L.ln1_b, cfg.eps, L.attn_b, nullptr,
+               INFERC_ACT_NONE, qkv);
+      ih::kv_append_attend(ctx, cfg.heads, D(), max_t, state, qkv, qkv + Hh, qkv + 2 * Hh,
+                           kc_l(l), vc_l(l), att);
+      ih::gemv(ctx, Hh, Hh, L.proj_w, att, nullptr, nullptr, 0.0f, L.proj_b, h, INFERC_ACT_NONE,
+               h);
+      ih::gemv(ctx, F, Hh, L.fc_w, h, L.ln2_g, L.ln2_b, cfg.eps, L.fc_b, nullptr,
+               INFERC_ACT_GELU_TANH, f);
+      ih::gemv(ctx, Hh, F, L.fcproj_w, f, nullptr, nullptr, 0.0f, L.fcproj_b, h, INFERC_ACT_NONE,
+               h);
+    }
+    ih::gemv(ctx, V, Hh, wte, h, lnf_g, lnf_b, cfg.eps, nullptr, nullptr, INFERC_ACT_NONE,
+             logits);
+    finish_token();
+  }
+
+  // argmax of `logits` -> tokens[state[0]+1], state advanced by one position.
+  void finish_token() {
+    ih::argmax(ctx, cfg.vocab, logits, state + 2, argmax_ws);
+    hipLaunchKernelGGL(ih::advance_state_kernel, dim3(1), dim3(64), 0, ctx->stream, state,
+                       tokens);
+    ih::check_launch("advance_state");
+  }
+
+  // Prefill over n prompt tokens (ids already on the device): fills the
+  // cache at positions [0, n) and leaves the final-LN-free hidden rows in ph.
+  void enqueue_prefill_blocks(int64_t n) {
+    hipStream_t s = ctx->stream;
+    const int64_t Hh = H(), F = cfg.ffn;
+    {
+      int64_t blocks = ih::ceil_div(n * Hh, ih::kBlock);
+      hipLaunchKernelGGL(ih::embed_rows_kernel, dim3(unsigned(blocks < 8192 ? blocks : 8192)),
+                         dim3(ih::kBlock), 0, s, wte, wpe, ids, n, Hh, ph);
+      ih::check_launch("embed_rows");
+    }
+    for (int64_t l = 0; l < cfg.layers; ++l) {
+      const Layer& L = layers[size_t(l)];
+      ih::layernorm(ctx, n, Hh, ph, nullptr, L.ln1_g, L.ln1_b, cfg.eps, pa);
+      ih::GemmArgs g;
+      g.trans_b = 1; g.M = n; g.N = 3 * Hh; g.K = Hh;
+      g.A = pa; g.lda = Hh; g.B = L.attn_w; g.ldb = Hh;
+      g.beta = 1.0f; g.C = L.attn_b; g.c_kind = INFERC_C_ROW;
+      g.Y = pqkv; g.ldy = 3 * Hh;
+      ih::gemm(ctx, g);
+      int64_t blocks = ih::ceil_div(n * Hh, ih::kBlock);
+      hipLaunchKernelGGL(ih::kv_scatter_kernel, dim3(unsigned(blocks < 8192 ? blocks : 8192)),
+                         dim3(ih::kBlock), 0, s, pqkv, n, int64_t(0), cfg.heads, D(), max_t,
+                         kc_l(l), vc_l(l));
+      ih::check_launch("kv_scatter");
+      ih::AttnArgs a;
+      a.B = 1; a.S = n; a.H = Hh; a.head_dim = D();
+      a.q = pqkv; a.k = pqkv + Hh; a.v = pqkv + 2 * Hh;
+      a.ldq = a.ldk = a.ldv = 3 * Hh; a.ldo = Hh;
+      a.causal = 1;
+      a.fill = -3.4028234663852886e38f;  // torch.finfo(float32).min of the export
+      a.out = patt;
+      ih::attention(ctx, a);
+      ih::GemmArgs g2;
+      g2.trans_b = 1; g2.M = n; g2.N = Hh; g2.K = Hh;
+      g2.A = patt; g2.lda = Hh; g2.B = L.proj_w; g2.ldb = Hh;
+      g2.beta = 1.0f; g2.C = L.proj_b; g2.c_kind = INFERC_C_ROW;
+      g2.R = ph; g2.ldr = Hh; g2.Y = ph; g2.ldy = Hh;
+      ih::gemm(ctx, g2);
+      ih::layernorm(ctx, n, Hh, ph, nullptr, L.ln2_g, L.ln2_b, cfg.eps, pa);
+      ih::GemmArgs g3;
+      g3.trans_b = 1; g3.M = n; g3.N = F; g3.K = Hh;
+      g3.A = pa; g3.lda = Hh; g3.B = L.fc_w; g3.ldb = Hh;
+      g3.beta = 1.0f; g3.C = L.fc_b; g3.c_kind = INFERC_C_ROW;
+      g3.act = INFERC_ACT_GELU_TANH; g3.Y = pf; g3.ldy = F;
+      ih::gemm(ctx, g3);
+      ih::GemmArgs g4;
+      g4.trans_b = 1; g4.M = n; g4.N = Hh; g4.K = F;
+      g4.A = pf; g4.lda = F; g4.B = L.fcproj_w; g4.ldb = F;
+      g4.beta = 1.0f; g4.C = L.fcproj_b; g4.c_kind = INFERC_C_ROW;
+      g4.R = ph; g4.ldr = Hh; g4.Y = ph; g4.ldy = Hh;
+      ih::gemm(ctx, g4);
+    }
+  }
+
+  void capture_step() {
+    if (step_exec) return;
+    IH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    try {
+      enqueue_step();
+    } catch (...) {
+      ctx->capturing = false;
+      hipGraph_t g = nullptr;
+      (void)hipStreamEndCapture(ctx->stream, &g);
+      if (g) (void)hipGraphDestroy(g);
+      throw;
+    }
+    ctx->capturing = false;
+    IH_HIP(hipStreamEndCapture(ctx->stream, &step_graph));
+    IH_HIP(hipGraphInstantiate(&step_exec, step_graph, nullptr, nullptr, 0));
+  }
+};
+
+namespace {
+
+void check_model(inferc_gpt2* m) {
+  IH_REQUIRE(m != nullptr && m->ctx != nullptr, INFERC_ERR_ARG, "null GPT-2 model");
+  m->ctx->make_current();
+}
+
+void upload_ids(inferc_gpt2* m, const int64_t* ids, int64_t n) {
+  IH_REQUIRE(ids != nullptr, INFERC_ERR_ARG, "null token ids");
+  for (int64_t i = 0; i < n; ++i)
+    IH_REQUIRE(ids[i] >= 0 && ids[i] < m->cfg.vocab, INFERC_ERR_ARG,
+               "token id " + std::to_string(ids[i]) + " out of range");
+  IH_HIP(hipMemcpyAsync(m->ids, ids, size_t(n) * sizeof(int64_t), hipMemcpyHostToDevice,
+                        m->ctx->stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int inferc_hip_kv_append_attend_f32(inferc_hip_ctx* ctx, int64_t n_heads, int64_t head_dim,
+                                    int64_t max_t, const int64_t* pos, const float* q,
+                                    const float* k_new, const float* v_new, float* k_cache,
+                                    float* v_cache, float* out) {
+  return ih::guard([&] {
+    ih::check_ctx(ctx)->make_current();
+    ih::kv_append_attend(ctx, n_heads, head_dim, max_t, pos, q, k_new, v_new, k_cache, v_cache,
+                         out);
+  });
+}
+
+int inferc_gpt2_create(inferc_hip_ctx* ctx, const inferc_gpt2_config* cfg,
+                       const float* const* w, int64_t max_t, inferc_gpt2** out) {
+  return ih::guard([&] {
+    ih::check_ctx(ctx)->make_current();
+    IH_REQUIRE(cfg && w && out, INFERC_ERR_ARG, "gpt2_create: null argument");
+    *out = nullptr;
+    IH_REQUIRE(cfg->layers > 0 && cfg->hidden > 0 && cfg->heads > 0 && cfg->ffn > 0 &&
+                   cfg->vocab > 0 && cfg->max_pos > 0,
+               INFERC_ERR_SHAPE, "gpt2_create: bad config");
+    IH_REQUIRE(cfg->hidden % cfg->heads == 0, INFERC_ERR_SHAPE,
+               "gpt2_create: hidden not divisible by heads");
+    IH_REQUIRE(max_t > 0 && max_t <= cfg->max_pos, INFERC_ERR_SHAPE,
+               "gpt2_create: max_t must be in [1, max_pos]");
+    const int64_t H = cfg->hidden, F = cfg->ffn, V = cfg->vocab, L = cfg->layers;
+    for (int64_t i = 0; i < 2 + 12 * L + 2; ++i)
+      IH_REQUIRE(w[i] != nullptr, INFERC_ERR_ARG, "gpt2_create: null weight pointer");
+    auto* m = new inferc_gpt2();
+    m->ctx = ctx;
+    m->cfg = *cfg;
+    m->max_t = max_t;
+    try {
+      m->wte = m->upload(w[0], size_t(V * H));
+      m->wpe = m->upload(w[1], size_t(cfg->max_pos * H));
+      for (int64_t l = 0; l < L; ++l) {
+        const float* const* lw = w + 2 + 12 * l;
+        inferc_gpt2::Layer Ly{};
+        Ly.ln1_g = m->upload(lw[0], size_t(H));
+        Ly.ln1_b = m->upload(lw[1], size_t(H));
+        Ly.attn_w = m->upload_transposed(lw[2], H, 3 * H);
+        Ly.attn_b = m->upload(lw[3], size_t(3 * H));
+        Ly.proj_w = m->upload_transposed(lw[4], H, H);
+        Ly.proj_b = m->upload(lw[5], size_t(H));
+        Ly.ln2_g = m->upload(lw[6], size_t(H));
+        Ly.ln2_b = m->upload(lw[7], size_t(H));
+        Ly.fc_w = m->upload_transposed(lw[8], H, F);
+        Ly.fc_b = m->upload(lw[9], size_t(F));
+        Ly.fcproj_w = m->upload_transposed(lw[10], F, H);
+        Ly.fcproj_b = m->upload(lw[11], size_t(H));
+        m->layers.push_back(Ly);
+      }
+      m->lnf_g = m->upload(w[2 + 12 * L], size_t(H));
+      m->lnf_b = m->upload(w[2 + 12 * L + 1], size_t(H));
+      const size_t cache = size_t(L * cfg->heads * max_t * (H / cfg->heads));
+      m->kc = m->alloc<float>(cache);
+      m->vc = m->alloc<float>(cache);
+      m->h = m->alloc<float>(size_t(H));
+      m->qkv = m->alloc<float>(size_t(3 * H));
+      m->att = m->alloc<float>(size_t(H));
+      m->f = m->alloc<float>(size_t(F));
+      m->logits = m->alloc<float>(size_t(V));
+      m->state = m->alloc<int64_t>(4);
+      m->tokens = m->alloc<int64_t>(size_t(max_t + 1));
+      m->argmax_ws = m->alloc<uint8_t>(ih::kArgmaxScratchBytes);
+      m->ids = m->alloc<int64_t>(size_t(max_t));
+      m->ph = m->alloc<float>(size_t(max_t * H));
+      m->pa = m->alloc<float>(size_t(max_t * H));
+      m->pqkv = m->alloc<float>(size_t(max_t * 3 * H));
+      m->patt = m->alloc<float>(size_t(max_t * H));
+      m->pf = m->alloc<float>(size_t(max_t * F));
+      IH_HIP(hipMemset(m->kc, 0, cache * sizeof(float)));
+      IH_HIP(hipMemset(m->vc, 0, cache * sizeof(float)));
+    } catch (...) {
+      m->release();
+      delete m;
+      throw;
+    }
+    *out = m;
+  });
+}
+
+int inferc_gpt2_destroy(inferc_gpt2* m) {
+  return ih::guard([&] {
+    if (!m) return;
+    if (m->ctx) {
+      m->ctx->make_current();
+      (void)hipStreamSynchronize(m->ctx->stream);
+    }
+    m->release();
+    delete m;
+  });
+}
+
+int inferc_gpt2_generate(inferc_gpt2* m, const int64_t* prompt, int64_t n_prompt,
+                         int64_t max_tokens, int64_t* tokens_out, float* step_ms,
+                         float* last_logits) {
+  return ih::guard([&] {
+    check_model(m);
+    IH_REQUIRE(n_prompt > 0, INFERC_ERR_ARG, "inferc decode: empty prompt");
+    IH_REQUIRE(max_tokens > 0, INFERC_ERR_ARG, "inferc decode: max_tokens must be > 0");
+    IH_REQUIRE(tokens_out != nullptr, INFERC_ERR_ARG, "null tokens_out");
+    IH_REQUIRE(n_prompt + max_tokens - 1 <= m->max_t, INFERC_ERR_SHAPE,
+               "prompt + generated tokens exceed the KV cache (max_t)");
+    inferc_hip_ctx* ctx = m->ctx;
+    hipStream_t s = ctx->stream;
+    const int64_t H = m->H(), V = m->cfg.vocab;
+    // state = {pos = n_prompt - 1}: the prefill's last row plays the role of
+    // a step input, so finish_token() records the first generated token at
+    // position n_prompt and leaves the state at the first decode step.
+    const int64_t init[4] = {n_prompt - 1, 0, 0, 0};
+    IH_HIP(hipMemcpyAsync(m->state, init, sizeof(init), hipMemcpyHostToDevice, s));
+    upload_ids(m, prompt, n_prompt);
+    m->enqueue_prefill_blocks(n_prompt);
+    // First token: final LN + LM head on the last prompt row (main.cpp:820-828).
+    ih::gemv(ctx, V, H, m->wte, m->ph + (n_prompt - 1) * H, m->lnf_g, m->lnf_b, m->cfg.eps,
+             nullptr, nullptr, INFERC_ACT_NONE, m->logits);
+    m->finish_token();
+    m->capture_step();
+    const int64_t steps = max_tokens - 1;
+    if (step_ms && steps > 0) {
+      while (int64_t(m->events.size()) < steps + 1) {
+        hipEvent_t e;
+        IH_HIP(hipEventCreate(&e));
+        m->events.push_back(e);
+      }
+      IH_HIP(hipEventRecord(m->events[0], s));
+    }
+    for (int64_t i = 0; i < steps; ++i) {
+      IH_HIP(hipGraphLaunch(m->step_exec, s));
+      if (step_ms) IH_HIP(hipEventRecord(m->events[size_t(i + 1)], s));
+    }
+    IH_HIP(hipStreamSynchronize(s));
+    IH_HIP(hipMemcpy(tokens_out, m->tokens + n_prompt, size_t(max_tokens) * sizeof(int64_t),
+                     hipMemcpyDeviceToHost));
+    if (step_ms)
+      for (int64_t i = 0; i < steps; ++i)
+        IH_HIP(hipEventElapsedTime(&step_ms[i], m->events[size_t(i)], m->events[size_t(i + 1)]));
+    if (last_logits)
+      IH_HIP(hipMemcpy(last_logits, m->logits, size_t(V) * sizeof(float),
+                       hipMemcpyDeviceToHost));
+  });
+}
+
+int inferc_gpt2_forward(inferc_gpt2* m, const int64_t* ids, int64_t n, float* logits) {
+  return ih::guard([&] {
+    check_model(m);
+    IH_REQUIRE(n > 0 && n <= m->max_t, INFERC_ERR_SHAPE, "gpt2_forward: n out of range");
+    IH_REQUIRE(logits != nullptr, INFERC_ERR_ARG, "null logits");
+    inferc_hip_ctx* ctx = m->ctx;
+    const int64_t H = m->H(), V = m->cfg.vocab;
+    upload_ids(m, ids, n);
+    m->enqueue_prefill_blocks(n);
+    ih::layernorm(ctx, n, H, m->ph, nullptr, m->lnf_g, m->lnf_b, m->cfg.eps, m->pa);
+    float* dl = nullptr;
+    IH_HIP(hipMalloc(&dl, size_t(n * V) * sizeof(float)));
+    try {
+      ih::GemmArgs g;
+      g.trans_b = 1; g.M = n; g.N = V; g.K = H;
+      g.A = m->pa; g.lda = H; g.B = m->wte; g.ldb = H;
+      g.Y = dl; g.ldy = V;
+      ih::gemm(ctx, g);
+      IH_HIP(hipStreamSynchronize(ctx->stream));
+      IH_HIP(hipMemcpy(logits, dl, size_t(n * V) * sizeof(float), hipMemcpyDeviceToHost));
+    } catch (...) {
+      (void)hipStreamSynchronize(ctx->stream);
+      (void)hipFree(dl);
+      throw;
+    }
+    IH_HIP(hipFree(dl));
+  });
+}
+
+}  // extern "C"

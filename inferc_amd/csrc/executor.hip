@@ -1,0 +1,1089 @@
+// Graph executor: the device counterpart of rt::Executor
+// (src/runtime/executor.h:24-41, executor.cc:89-366).
+//
+//  - The constructor uploads every initializer to the device once
+//    (executor.cc:89-96) and keeps a host copy for shape plumbing.
+//  - run() walks the nodes in order and dispatches each op_type to a kernel
+//    (executor.cc:123-352); multi-output ops (Split, FusedQKV) bind every
+//    output. Unsupported ops fail with INFERC_ERR_UNSUPPORTED
+//    (executor.cc:340-343); missing tensors with INFERC_ERR_STATE (:104-110).
+//  - Integer shape plumbing (Shape, Gather/Range/Slice/Unsqueeze/Concat on
+//    int64 data known on the host) is evaluated on the host; its results are
+//    uploaded only if a device kernel consumes them.
+//  - Peephole fusion at construction: MatMul -> Add(bias) -> Add(residual)
+//    with single-use intermediates becomes one GEMM with a bias+residual
+//    epilogue, and Gemm -> Relu one GEMM with a ReLU epilogue. The arithmetic
+//    is the unfused sequence's, (acc + b) + r, in the same order.
+//  - Activation buffers live in a per-executor arena keyed by tensor name, so
+//    repeated runs with the same input shapes touch no allocator; the second
+//    such run is captured into a HIP graph that later runs replay.
+#include <cstring>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "common.h"
+
+struct inferc_graph {
+  struct Init {
+    std::string name;
+    int dtype;
+    std::vector<int64_t> shape;
+    std::vector<uint8_t> data;
+  };
+  struct Node {
+    std::string op, name;
+    std::vector<std::string> in, out;
+    std::map<std::string, std::string> attrs;
+  };
+  std::vector<Init> inits;
+  std::vector<Node> nodes;
+  std::vector<std::string> outputs;
+};
+
+namespace ih {
+namespace {
+
+size_t dtype_size(int dt) {
+  switch (dt) {
+    case INFERC_DT_F32: return 4;
+    case INFERC_DT_U8: return 1;
+    case INFERC_DT_BOOL: return 1;
+    case INFERC_DT_I32: return 4;
+    case INFERC_DT_I64: return 8;
+    default: fail(INFERC_ERR_UNSUPPORTED, "unsupported dtype code " + std::to_string(dt));
+  }
+}
+
+int64_t numel_of(const std::vector<int64_t>& s) {
+  int64_t n = 1;
+  for (int64_t d : s) n *= d;
+  return n;
+}
+
+std::string shape_str(const std::vector<int64_t>& s) {
+  std::ostringstream o;
+  o << "[";
+  for (size_t i = 0; i < s.size(); ++i) o << (i ? "," : "") << s[i];
+  o << "]";
+  return o.str();
+}
+
+// A tensor during a run: device data and/or a host copy (initializers and
+// host-evaluated shape math).
+struct Value {
+  int dtype = 0;
+  std::vector<int64_t> shape;
+  void* dev = nullptr;
+  std::shared_ptr<std::vector<uint8_t>> host;  // set when known on the host
+  int64_t numel() const { return numel_of(shape); }
+  size_t bytes() const { return size_t(numel()) * dtype_size(dtype); }
+  const float* f32() const { return static_cast<const float*>(dev); }
+  template <class T>
+  T host_at(int64_t i) const {
+    return reinterpret_cast<const T*>(host->data())[i];
+  }
+};
+
+int64_t attr_int(const inferc_graph::Node& n, const char* key, int64_t def) {
+  auto it = n.attrs.find(key);
+  if (it == n.attrs.end()) return def;
+  return std::stoll(it->second);
+}
+
+float attr_float(const inferc_graph::Node& n, const char* key, float def) {
+  auto it = n.attrs.find(key);
+  if (it == n.attrs.end()) return def;
+  return std::stof(it->second);
+}
+
+std::vector<int64_t> attr_ints(const inferc_graph::Node& n, const char* key) {
+  std::vector<int64_t> v;
+  auto it = n.attrs.find(key);
+  if (it == n.attrs.end() || it->second.empty()) return v;
+  std::stringstream ss(it->second);
+  std::string tok;
+  while (std::getline(ss, tok, ',')) v.push_back(std::stoll(tok));
+  return v;
+}
+
+// Mask strides of `in_shape` right-aligned against [B,nH,S,S], 0 on
+// broadcast axes (src/kernels/attention.cc:17-29).
+void mask_strides(const std::vector<int64_t>& in_shape, int64_t s[4]) {
+  s[0] = s[1] = s[2] = s[3] = 0;
+  int64_t st = 1;
+  const int r = int(in_shape.size());
+  for (int i = r - 1; i >= 0; --i) {
+    const int od = 4 - (r - i);
+    if (od >= 0) s[od] = (in_shape[size_t(i)] == 1) ? 0 : st;
+    st *= in_shape[size_t(i)];
+  }
+}
+
+}  // namespace
+}  // namespace ih
+
+struct inferc_executor {
+  inferc_hip_ctx* ctx = nullptr;
+  std::vector<inferc_graph::Node> nodes;
+  std::vector<std::string> outputs;
+  std::unordered_map<std::string, ih::Value> inits;
+  std::vector<void*> init_allocs;
+  struct Input {
+    ih::Value v;
+    bool from_host = false;
+    std::vector<uint8_t> staged;  // host bytes awaiting upload
+  };
+  std::unordered_map<std::string, Input> inputs;
+  std::unordered_map<std::string, ih::Value> vals;  // the "tape" of the last run
+  struct Buf {
+    void* p = nullptr;
+    size_t bytes = 0;
+  };
+  std::unordered_map<std::string, Buf> arena;
+  std::unordered_map<std::string, int> fused_act;  // Gemm name -> folded activation
+  bool graph_mode = true;
+  std::string last_sig;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::string graph_sig;
+  uint64_t graph_ws_gen = 0;
+
+  ~inferc_executor() {
+    drop_graph();
+    for (auto& kv : arena) (void)hipFree(kv.second.p);
+    for (auto& kv : inputs)
+      if (kv.second.from_host && kv.second.v.dev) (void)hipFree(kv.second.v.dev);
+    for (void* p : init_allocs) (void)hipFree(p);
+  }
+
+  void drop_graph() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    exec = nullptr;
+    graph = nullptr;
+    graph_sig.clear();
+  }
+
+  // Device buffer for tensor `name` of at least `bytes`, reused across runs.
+  void* buf(const std::string& name, size_t bytes) {
+    Buf& b = arena[name];
+    if (b.p && b.bytes >= bytes) return b.p;
+    IH_REQUIRE(!ctx->capturing, INFERC_ERR_STATE, "executor: allocation during graph capture");
+    if (b.p) {
+      IH_HIP(hipStreamSynchronize(ctx->stream));
+      IH_HIP(hipFree(b.p));
+      b.p = nullptr;
+    }
+    IH_HIP(hipMalloc(&b.p, bytes > 0 ? bytes : 4));
+    b.bytes = bytes;
+    return b.p;
+  }
+
+  const ih::Value& get(const std::string& name) const {
+    auto it = vals.find(name);
+    if (it == vals.end()) ih::fail(INFERC_ERR_STATE, "Executor: missing tensor '" + name + "'");
+    return it->second;
+  }
+
+  // Device pointer of a value. Host-only values (shape math consumed by a
+  // kernel) are uploaded into the arena once and reused while their bytes
+  // stay the same, so a captured run needs no copy.
+  struct Upload {
+    std::vector<uint8_t> bytes;
+    void* p = nullptr;
+  };
+  std::unordered_map<std::string, Upload> uploads;
+  void* dev_of(const std::string& name) {
+    ih::Value& v = vals.at(name);
+    if (v.dev) return v.dev;
+    IH_REQUIRE(v.host != nullptr, INFERC_ERR_STATE, "tensor '" + name + "' has no data");
+    Upload& up = uploads[name];
+    if (up.p && up.bytes == *v.host) {
+      v.dev = up.p;
+      return up.p;
+    }
+    IH_REQUIRE(!ctx->capturing, INFERC_ERR_STATE, "host constant changed inside capture");
+    up.bytes = *v.host;
+    up.p = buf("__h2d__" + name, v.bytes());
+    IH_HIP(hipMemcpyAsync(up.p, up.bytes.data(), up.bytes.size(), hipMemcpyHostToDevice,
+                          ctx->stream));
+    v.dev = up.p;
+    return up.p;
+  }
+
+  ih::Value& make_dev(const std::string& name, int dtype, std::vector<int64_t> shape) {
+    ih::Value v;
+    v.dtype = dtype;
+    v.shape = std::move(shape);
+    v.dev = buf(name, v.bytes());
+    vals[name] = v;
+    return vals[name];
+  }
+
+  ih::Value& make_host(const std::string& name, int dtype, std::vector<int64_t> shape,
+                       const void* data) {
+    ih::Value v;
+    v.dtype = dtype;
+    v.shape = std::move(shape);
+    v.host = std::make_shared<std::vector<uint8_t>>(v.bytes());
+    if (v.bytes()) std::memcpy(v.host->data(), data, v.bytes());
+    vals[name] = v;
+    return vals[name];
+  }
+
+  void alias(const std::string& out, const ih::Value& in, std::vector<int64_t> shape) {
+    ih::Value v = in;
+    IH_REQUIRE(ih::numel_of(shape) == in.numel(), INFERC_ERR_SHAPE,
+               "reshape: element count changes " + ih::shape_str(in.shape) + " -> " +
+                   ih::shape_str(shape));
+    v.shape = std::move(shape);
+    vals[out] = v;
+  }
+
+  void peephole();
+  void exec_node(const inferc_graph::Node& n);
+  void walk();
+  std::string signature() const;
+  void run();
+};
+
+namespace ih {
+namespace {
+
+using Node = inferc_graph::Node;
+
+std::vector<int64_t> host_i64(const Value& v, const std::string& what) {
+  IH_REQUIRE(v.host != nullptr, INFERC_ERR_UNSUPPORTED,
+             what + ": needs host-known int64 data (constant shape plumbing)");
+  IH_REQUIRE(v.dtype == INFERC_DT_I64 || v.dtype == INFERC_DT_I32, INFERC_ERR_ARG,
+             what + ": expected an integer tensor");
+  std::vector<int64_t> r(size_t(v.numel()));
+  for (int64_t i = 0; i < v.numel(); ++i)
+    r[size_t(i)] = v.dtype == INFERC_DT_I64 ? v.host_at<int64_t>(i) : v.host_at<int32_t>(i);
+  return r;
+}
+
+// Right-aligned numpy broadcast test: b broadcasts into a as a repeated
+// suffix (every leading dim of b is 1 or absent).
+bool suffix_broadcast(const std::vector<int64_t>& a, const std::vector<int64_t>& b) {
+  size_t lead = 0;
+  while (lead < b.size() && b[lead] == 1) ++lead;
+  const size_t r = b.size() - lead;
+  if (r > a.size()) return false;
+  for (size_t i = 0; i < r; ++i)
+    if (b[lead + i] != a[a.size() - r + i]) return false;
+  return true;
+}
+
+std::vector<int64_t> broadcast_shape(const std::vector<int64_t>& a, const std::vector<int64_t>& b) {
+  const size_t r = a.size() > b.size() ? a.size() : b.size();
+  std::vector<int64_t> out(r);
+  for (size_t i = 0; i < r; ++i) {
+    const int64_t da = i < a.size() ? a[a.size() - 1 - i] : 1;
+    const int64_t db = i < b.size() ? b[b.size() - 1 - i] : 1;
+    IH_REQUIRE(da == db || da == 1 || db == 1, INFERC_ERR_SHAPE, "incompatible broadcast");
+    out[r - 1 - i] = da == 1 ? db : da;
+  }
+  return out;
+}
+
+}  // namespace
+}  // namespace ih
+
+void inferc_executor::peephole() {
+  // consumer counts (graph outputs count as consumers)
+  std::unordered_map<std::string, int> uses;
+  for (const auto& n : nodes)
+    for (const auto& i : n.in) ++uses[i];
+  for (const auto& o : outputs) ++uses[o];
+  auto producer = [&](const std::string& t) -> int {
+    for (size_t i = 0; i < nodes.size(); ++i)
+      for (const auto& o : nodes[i].out)
+        if (o == t) return int(i);
+    return -1;
+  };
+  std::vector<bool> dead(nodes.size(), false);
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    inferc_graph::Node& n = nodes[i];
+    if (dead[i]) continue;
+    // MatMul(x, W) -> Add(., b) [-> Add(., r)]  ==>  FusedGemmEpilogue
+    if (n.op == "MatMul" && n.in.size() == 2 && inits.count(n.in[1]) &&
+        inits.at(n.in[1]).shape.size() == 2 && uses[n.out[0]] == 1) {
+      const std::string mm_out = n.out[0];
+      int a1 = -1;
+      for (size_t j = i + 1; j < nodes.size(); ++j)
+        if (!dead[j] && nodes[j].op == "Add" &&
+            (nodes[j].in[0] == mm_out || nodes[j].in[1] == mm_out)) {
+          a1 = int(j);
+          break;
+        }
+      if (a1 < 0) continue;
+      inferc_graph::Node& add1 = nodes[size_t(a1)];
+      const std::string bias = add1.in[0] == mm_out ? add1.in[1] : add1.in[0];
+      auto bit = inits.find(bias);
+      if (bit == inits.end() || bit->second.shape.size() != 1 ||
+          bit->second.shape[0] != inits.at(n.in[1]).shape[1])
+        continue;
+      inferc_graph::Node fused;
+      fused.op = "FusedGemmEpilogue";
+      fused.name = n.name + "+bias";
+      fused.in = {n.in[0], n.in[1], bias};
+      fused.out = add1.out;
+      // optional residual add consuming the biased output once
+      if (uses[add1.out[0]] == 1) {
+        const std::string t = add1.out[0];
+        for (size_t j = size_t(a1) + 1; j < nodes.size(); ++j) {
+          if (dead[j] || nodes[j].op != "Add") continue;
+          if (nodes[j].in[0] != t && nodes[j].in[1] != t) continue;
+          const std::string res = nodes[j].in[0] == t ? nodes[j].in[1] : nodes[j].in[0];
+          if (inits.count(res)) break;  // a second bias is not a residual
+          // the residual must be produced before the MatMul runs
+          const int pr = producer(res);
+          if (pr >= int(i)) break;
+          fused.in.push_back(res);
+          fused.out = nodes[j].out;
+          fused.name += "+residual";
+          dead[j] = true;
+          break;
+        }
+      }
+      dead[size_t(a1)] = true;
+      n = fused;
+      continue;
+    }
+    // Gemm -> Relu  ==>  Gemm with a ReLU epilogue
+    if (n.op == "Gemm" && uses[n.out[0]] == 1) {
+      for (size_t j = i + 1; j < nodes.size(); ++j) {
+        if (dead[j] || nodes[j].op != "Relu" || nodes[j].in[0] != n.out[0]) continue;
+        n.out = nodes[j].out;
+        n.attrs["__act"] = std::to_string(INFERC_ACT_RELU);
+        dead[j] = true;
+        break;
+      }
+    }
+  }
+  std::vector<inferc_graph::Node> kept;
+  for (size_t i = 0; i < nodes.size(); ++i)
+    if (!dead[i]) kept.push_back(std::move(nodes[i]));
+  nodes = std::move(kept);
+}
+
+void inferc_executor::exec_node(const inferc_graph::Node& n) {
+  using namespace ih;
+  const std::string& op = n.op;
+  auto in = [&](size_t i) -> const Value& {
+    IH_REQUIRE(i < n.in.size(), INFERC_ERR_ARG, op + ": missing input " + std::to_string(i));
+    return get(n.in[i]);
+  };
+  auto require_f32 = [&](const Value& v, const char* what) {
+    IH_REQUIRE(v.dtype == INFERC_DT_F32, INFERC_ERR_UNSUPPORTED,
+               op + ": " + what + " must be float32");
+  };
+  IH_REQUIRE(!n.out.empty(), INFERC_ERR_ARG, op + ": node has no outputs");
+
+  if (op == "FusedQKV") {
+    const Value& x = in(0);
+    require_f32(x, "X");
+    const int64_t K = x.shape.back(), M = x.numel() / K;
+    const Value& wq = in(1);
+    IH_REQUIRE(wq.shape.size() == 2 && wq.shape[0] == K, INFERC_ERR_SHAPE, "FusedQKV: W shape");
+    const int64_t N = wq.shape[1];
+    std::vector<int64_t> os = x.shape;
+    os.back() = N;
+    const float* w[3];
+    const float* b[3];
+    float* y[3];
+    for (int i = 0; i < 3; ++i) {
+      const Value& wi = in(size_t(1 + 2 * i));
+      const Value& bi = in(size_t(2 + 2 * i));
+      IH_REQUIRE(wi.shape == wq.shape && bi.numel() == N, INFERC_ERR_SHAPE,
+                 "FusedQKV: projections must share shapes");
+      w[i] = static_cast<const float*>(dev_of(n.in[size_t(1 + 2 * i)]));
+      b[i] = static_cast<const float*>(dev_of(n.in[size_t(2 + 2 * i)]));
+      IH_REQUIRE(i < int(n.out.size()), INFERC_ERR_ARG, "FusedQKV: needs three outputs");
+      y[i] = static_cast<float*>(make_dev(n.out[size_t(i)], INFERC_DT_F32, os).dev);
+    }
+    gemm_qkv(ctx, M, K, N, static_cast<const float*>(dev_of(n.in[0])), w, b, y, N);
+    return;
+  }
+  if (op == "FusedAttention") {
+    const Value& q = in(0);
+    require_f32(q, "Q");
+    IH_REQUIRE(q.shape.size() == 3, INFERC_ERR_SHAPE, "FusedAttention: expect [B,S,H]");
+    IH_REQUIRE(in(1).shape == q.shape && in(2).shape == q.shape, INFERC_ERR_SHAPE,
+               "FusedAttention: Q/K/V shapes differ");
+    AttnArgs a;
+    a.B = q.shape[0]; a.S = q.shape[1]; a.H = q.shape[2];
+    a.head_dim = attr_int(n, "head_dim", 64);
+    a.fill = attr_float(n, "fill", -3.0e38f);
+    a.q = static_cast<const float*>(dev_of(n.in[0]));
+    a.k = static_cast<const float*>(dev_of(n.in[1]));
+    a.v = static_cast<const float*>(dev_of(n.in[2]));
+    a.ldq = a.ldk = a.ldv = a.ldo = a.H;
+    if (n.in.size() >= 4 && !n.in[3].empty()) {
+      const Value& m = in(3);
+      IH_REQUIRE(m.dtype == INFERC_DT_BOOL || m.dtype == INFERC_DT_U8, INFERC_ERR_UNSUPPORTED,
+                 "FusedAttention: mask must be bool");
+      IH_REQUIRE(m.shape.size() <= 4, INFERC_ERR_SHAPE, "FusedAttention: mask rank > 4");
+      a.mask = static_cast<const uint8_t*>(dev_of(n.in[3]));
+      mask_strides(m.shape, a.ms);
+    }
+    a.out = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, q.shape).dev);
+    attention(ctx, a);
+    return;
+  }
+  if (op == "FusedMatMulAddGELU" || op == "FusedGemmEpilogue" || op == "MatMul") {
+    const Value& x = in(0);
+    const Value& w = in(1);
+    require_f32(x, "A");
+    require_f32(w, "B");
+    if (op == "MatMul" && (w.shape.size() != 2 || x.shape.size() < 2)) {
+      // numpy-batched MatMul with broadcast batch dims (matmul.cc:63-159)
+      IH_REQUIRE(x.shape.size() >= 2 && w.shape.size() >= 2, INFERC_ERR_UNSUPPORTED,
+                 "MatMul: 1-D operands are not supported");
+      const int64_t M = x.shape[x.shape.size() - 2], K = x.shape.back();
+      const int64_t N = w.shape.back();
+      IH_REQUIRE(w.shape[w.shape.size() - 2] == K, INFERC_ERR_SHAPE,
+                 "MatMul: inner dim mismatch (K!=K)");
+      std::vector<int64_t> ab(x.shape.begin(), x.shape.end() - 2);
+      std::vector<int64_t> bb(w.shape.begin(), w.shape.end() - 2);
+      std::vector<int64_t> ob = broadcast_shape(ab, bb);
+      const int64_t batch = numel_of(ob);
+      const int64_t na = numel_of(ab), nb = numel_of(bb);
+      IH_REQUIRE((na == batch || na == 1) && (nb == batch || nb == 1), INFERC_ERR_UNSUPPORTED,
+                 "MatMul: partial batch broadcast is not supported");
+      std::vector<int64_t> os = ob;
+      os.push_back(M);
+      os.push_back(N);
+      GemmArgs g;
+      g.M = M; g.N = N; g.K = K;
+      g.A = static_cast<const float*>(dev_of(n.in[0])); g.lda = K;
+      g.B = static_cast<const float*>(dev_of(n.in[1])); g.ldb = N;
+      g.batch = batch;
+      g.stride_a = na == 1 ? 0 : M * K;
+      g.stride_b = nb == 1 ? 0 : K * N;
+      g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
+      g.ldy = N; g.stride_y = M * N;
+      gemm(ctx, g);
+      return;
+    }
+    IH_REQUIRE(w.shape.size() == 2, INFERC_ERR_SHAPE, op + ": W must be 2D [K,N]");
+    const int64_t K = w.shape[0], N = w.shape[1];
+    IH_REQUIRE(!x.shape.empty() && x.shape.back() == K, INFERC_ERR_SHAPE,
+               op + ": K mismatch between X and W");
+    const int64_t M = x.numel() / K;
+    std::vector<int64_t> os = x.shape;
+    os.back() = N;
+    GemmArgs g;
+    g.M = M; g.N = N; g.K = K;
+    g.A = static_cast<const float*>(dev_of(n.in[0])); g.lda = K;
+    g.B = static_cast<const float*>(dev_of(n.in[1])); g.ldb = N;
+    g.ldy = N;
+    if (op != "MatMul") {
+      IH_REQUIRE(in(2).numel() == N, INFERC_ERR_SHAPE, op + ": bias size must equal N");
+      g.beta = 1.0f;
+      g.C = static_cast<const float*>(dev_of(n.in[2]));
+      g.c_kind = INFERC_C_ROW;
+    }
+    if (op == "FusedMatMulAddGELU") g.act = INFERC_ACT_GELU_ERF;
+    if (op == "FusedGemmEpilogue" && n.in.size() >= 4) {
+      const Value& r = in(3);
+      IH_REQUIRE(r.numel() == M * N, INFERC_ERR_UNSUPPORTED,
+                 "fused residual must match the product's shape");
+      g.R = static_cast<const float*>(dev_of(n.in[3]));
+      g.ldr = N;
+    }
+    g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
+    gemm(ctx, g);
+    return;
+  }
+  if (op == "Gemm") {
+    const Value& a = in(0);
+    const Value& b = in(1);
+    require_f32(a, "A");
+    require_f32(b, "B");
+    IH_REQUIRE(a.shape.size() == 2 && b.shape.size() == 2, INFERC_ERR_SHAPE,
+               "Gemm: 2D inputs only");
+    GemmArgs g;
+    g.trans_a = int(attr_int(n, "transA", 0));
+    g.trans_b = int(attr_int(n, "transB", 0));
+    g.alpha = attr_float(n, "alpha", 1.0f);
+    g.beta = attr_float(n, "beta", 1.0f);
+    g.M = g.trans_a ? a.shape[1] : a.shape[0];
+    g.K = g.trans_a ? a.shape[0] : a.shape[1];
+    const int64_t Kb = g.trans_b ? b.shape[1] : b.shape[0];
+    g.N = g.trans_b ? b.shape[0] : b.shape[1];
+    IH_REQUIRE(g.K == Kb, INFERC_ERR_SHAPE, "Gemm: K mismatch");
+    g.A = static_cast<const float*>(dev_of(n.in[0]));
+    g.lda = a.shape[1];
+    g.B = static_cast<const float*>(dev_of(n.in[1]));
+    g.ldb = b.shape[1];
+    if (n.in.size() >= 3 && !n.in[2].empty() && g.beta != 0.0f) {
+      const Value& c = in(2);
+      if (c.numel() == g.M * g.N) {
+        g.c_kind = INFERC_C_FULL;
+        g.ldc = g.N;
+      } else if (c.shape.size() == 1 && c.shape[0] == g.N) {
+        g.c_kind = INFERC_C_ROW;
+      } else if (c.numel() == 1) {
+        g.c_kind = INFERC_C_SCALAR;
+      } else {
+        fail(INFERC_ERR_SHAPE, "Gemm: unsupported C shape for broadcast");
+      }
+      g.C = static_cast<const float*>(dev_of(n.in[2]));
+    }
+    g.act = int(attr_int(n, "__act", INFERC_ACT_NONE));
+    g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, {g.M, g.N}).dev);
+    g.ldy = g.N;
+    gemm(ctx, g);
+    return;
+  }
+  if (op == "FusedLayerNorm") {
+    const Value& x = in(0);
+    require_f32(x, "X");
+    const int64_t feat = x.shape.back();
+    IH_REQUIRE(in(1).numel() == feat && in(2).numel() == feat, INFERC_ERR_SHAPE,
+               "LayerNorm: scale/bias size mismatch with feature dim");
+    const float eps = attr_float(n, "epsilon", 1e-5f);
+    float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, x.shape).dev);
+    layernorm(ctx, x.numel() / feat, feat, static_cast<const float*>(dev_of(n.in[0])), nullptr,
+              static_cast<const float*>(dev_of(n.in[1])),
+              static_cast<const float*>(dev_of(n.in[2])), eps, y);
+    return;
+  }
+  if (op == "Gelu" || op == "GeluTanh" || op == "Relu") {
+    const Value& x = in(0);
+    require_f32(x, "X");
+    const int act = op == "Gelu" ? INFERC_ACT_GELU_ERF
+                    : op == "GeluTanh" ? INFERC_ACT_GELU_TANH
+                                       : INFERC_ACT_RELU;
+    float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, x.shape).dev);
+    activation(ctx, x.numel(), static_cast<const float*>(dev_of(n.in[0])), act, y);
+    return;
+  }
+  if (op == "Softmax") {
+    const Value& x = in(0);
+    require_f32(x, "X");
+    int64_t axis = attr_int(n, "axis", -1);
+    const int64_t r = int64_t(x.shape.size());
+    if (axis < 0) axis += r;
+    IH_REQUIRE(axis >= 0 && axis < r, INFERC_ERR_ARG, "Softmax: axis out of range");
+    int64_t outer = 1, inner = 1;
+    for (int64_t i = 0; i < axis; ++i) outer *= x.shape[size_t(i)];
+    for (int64_t i = axis + 1; i < r; ++i) inner *= x.shape[size_t(i)];
+    float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, x.shape).dev);
+    IH_REQUIRE(inferc_hip_softmax_f32(ctx, outer, x.shape[size_t(axis)], inner,
+                                      static_cast<const float*>(dev_of(n.in[0])), y) == 0,
+               INFERC_ERR_HIP, inferc_hip_last_error());
+    return;
+  }
+  if (op == "Add") {
+    const Value& a0 = in(0);
+    const Value& b0 = in(1);
+    if (a0.host && b0.host && a0.dtype == INFERC_DT_I64 && b0.dtype == INFERC_DT_I64 &&
+        b0.numel() == 1) {
+      std::vector<int64_t> r = host_i64(a0, "Add");
+      const int64_t s = b0.host_at<int64_t>(0);
+      for (auto& e : r) e += s;
+      make_host(n.out[0], INFERC_DT_I64, a0.shape, r.data());
+      return;
+    }
+    require_f32(a0, "A");
+    require_f32(b0, "B");
+    // the larger operand carries the output shape; the other broadcasts as a suffix
+    const bool swap = b0.numel() > a0.numel();
+    const std::string& an = swap ? n.in[1] : n.in[0];
+    const std::string& bn = swap ? n.in[0] : n.in[1];
+    const Value& a = get(an);
+    const Value& b = get(bn);
+    IH_REQUIRE(b.numel() == a.numel() || suffix_broadcast(a.shape, b.shape), INFERC_ERR_UNSUPPORTED,
+               "Add: only suffix broadcasts are supported, got " + shape_str(a.shape) + " + " +
+                   shape_str(b.shape));
+    std::vector<int64_t> os = a.shape;
+    if (b.numel() == a.numel() && b.shape.size() > a.shape.size()) os = b.shape;
+    const float* ap = static_cast<const float*>(dev_of(an));
+    const float* bp = static_cast<const float*>(dev_of(bn));
+    float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
+    // y = a + b elementwise is commutative in IEEE arithmetic, so swapping the
+    // operands for the broadcast does not change any result bit.
+    add_bcast(ctx, a.numel(), ap, bp, b.numel(), y);
+    return;
+  }
+  if (op == "Equal") {
+    const Value& a = in(0);
+    const Value& b = in(1);
+    IH_REQUIRE(a.dtype == INFERC_DT_I64 && b.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED,
+               "Equal: int64 operands only");
+    IH_REQUIRE(b.numel() == a.numel() || b.numel() == 1 || suffix_broadcast(a.shape, b.shape),
+               INFERC_ERR_UNSUPPORTED, "Equal: unsupported broadcast");
+    uint8_t* y = static_cast<uint8_t*>(make_dev(n.out[0], INFERC_DT_BOOL, a.shape).dev);
+    equal_i64(ctx, a.numel(), static_cast<const int64_t*>(dev_of(n.in[0])),
+              static_cast<const int64_t*>(dev_of(n.in[1])), b.numel(), y);
+    return;
+  }
+  if (op == "Gather") {
+    const Value& data = in(0);
+    const Value& idx = in(1);
+    int64_t axis = attr_int(n, "axis", 0);
+    const int64_t r = int64_t(data.shape.size());
+    if (axis < 0) axis += r;
+    IH_REQUIRE(axis >= 0 && axis < r, INFERC_ERR_ARG, "Gather: axis out of range");
+    std::vector<int64_t> os(data.shape.begin(), data.shape.begin() + axis);
+    for (int64_t d : idx.shape) os.push_back(d);
+    for (int64_t i = axis + 1; i < r; ++i) os.push_back(data.shape[size_t(i)]);
+    if (data.host && (data.dtype == INFERC_DT_I64 || data.dtype == INFERC_DT_I32)) {
+      // host shape plumbing (e.g. Gather(Shape(x), 1))
+      IH_REQUIRE(axis == 0 && r == 1, INFERC_ERR_UNSUPPORTED, "Gather: host data must be 1-D");
+      std::vector<int64_t> d = host_i64(data, "Gather"), ix = host_i64(idx, "Gather");
+      std::vector<int64_t> res;
+      for (int64_t i : ix) {
+        if (i < 0) i += int64_t(d.size());
+        IH_REQUIRE(i >= 0 && i < int64_t(d.size()), INFERC_ERR_ARG, "Gather: index out of range");
+        res.push_back(d[size_t(i)]);
+      }
+      make_host(n.out[0], INFERC_DT_I64, os, res.data());
+      return;
+    }
+    require_f32(data, "data");
+    int64_t outer = 1, inner = 1;
+    for (int64_t i = 0; i < axis; ++i) outer *= data.shape[size_t(i)];
+    for (int64_t i = axis + 1; i < r; ++i) inner *= data.shape[size_t(i)];
+    const int64_t ad = data.shape[size_t(axis)];
+    float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
+    const float* dp = static_cast<const float*>(dev_of(n.in[0]));
+    if (axis == 0 && !idx.host) {
+      IH_REQUIRE(idx.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED,
+                 "Gather: device indices must be int64");
+      gather_rows(ctx, ad, inner, dp, static_cast<const int64_t*>(dev_of(n.in[1])), idx.numel(), y,
+                  nullptr);
+      return;
+    }
+    // host-known indices: one strided copy per index
+    const std::vector<int64_t> ix = host_i64(idx, "Gather");
+    const int64_t ni = int64_t(ix.size());
+    for (int64_t k = 0; k < ni; ++k) {
+      int64_t i = ix[size_t(k)];
+      if (i < 0) i += ad;
+      IH_REQUIRE(i >= 0 && i < ad, INFERC_ERR_ARG, "Gather: index out of range");
+      copy2d(ctx, y + k * inner, ni * inner, dp + i * inner, ad * inner, inner, outer);
+    }
+    return;
+  }
+  if (op == "Shape") {
+    const Value& x = in(0);
+    std::vector<int64_t> s = x.shape;
+    make_host(n.out[0], INFERC_DT_I64, {int64_t(s.size())}, s.data());
+    return;
+  }
+  if (op == "Range") {
+    const int64_t s = host_i64(in(0), "Range")[0], l = host_i64(in(1), "Range")[0],
+                  d = host_i64(in(2), "Range")[0];
+    IH_REQUIRE(d != 0, INFERC_ERR_ARG, "Range: delta must be non-zero");
+    std::vector<int64_t> r;
+    for (int64_t v = s; d > 0 ? v < l : v > l; v += d) r.push_back(v);
+    make_host(n.out[0], INFERC_DT_I64, {int64_t(r.size())}, r.data());
+    return;
+  }
+  if (op == "Unsqueeze" || op == "Squeeze" || op == "Reshape" || op == "Identity" ||
+      op == "Flatten") {
+    const Value& x = in(0);
+    std::vector<int64_t> s = x.shape;
+    if (op == "Unsqueeze" || op == "Squeeze") {
+      std::vector<int64_t> axes =
+          n.in.size() >= 2 ? host_i64(in(1), op) : attr_ints(n, "axes");
+      if (op == "Unsqueeze") {
+        const int64_t out_r = int64_t(s.size() + axes.size());
+        for (auto& a : axes) if (a < 0) a += out_r;
+        std::vector<int64_t> os;
+        size_t k = 0;
+        for (int64_t i = 0; i < out_r; ++i) {
+          bool ins = false;
+          for (int64_t a : axes) ins = ins || a == i;
+          if (ins) os.push_back(1);
+          else os.push_back(s[k++]);
+        }
+        s = os;
+      } else {
+        const int64_t r = int64_t(s.size());
+        for (auto& a : axes) if (a < 0) a += r;
+        std::vector<int64_t> os;
+        for (int64_t i = 0; i < r; ++i) {
+          bool drop = axes.empty() ? s[size_t(i)] == 1 : false;
+          for (int64_t a : axes) drop = drop || a == i;
+          if (!drop) os.push_back(s[size_t(i)]);
+        }
+        s = os;
+      }
+    } else if (op == "Reshape") {
+      std::vector<int64_t> t = host_i64(in(1), "Reshape");
+      int64_t known = 1, neg = -1;
+      for (size_t i = 0; i < t.size(); ++i) {
+        if (t[i] == 0) t[i] = s[i];
+        if (t[i] == -1) neg = int64_t(i);
+        else known *= t[i];
+      }
+      if (neg >= 0) t[size_t(neg)] = known ? x.numel() / known : 0;
+      s = t;
+    } else if (op == "Flatten") {
+      int64_t axis = attr_int(n, "axis", 1);
+      if (axis < 0) axis += int64_t(s.size());
+      int64_t a = 1;
+      for (int64_t i = 0; i < axis; ++i) a *= s[size_t(i)];
+      s = {a, x.numel() / (a ? a : 1)};
+    }
+    alias(n.out[0], x, s);
+    return;
+  }
+  if (op == "Split") {
+    const Value& x = in(0);
+    require_f32(x, "X");
+    int64_t axis = attr_int(n, "axis", 0);
+    const int64_t r = int64_t(x.shape.size());
+    if (axis < 0) axis += r;
+    IH_REQUIRE(axis >= 0 && axis < r, INFERC_ERR_ARG, "Split: axis out of range");
+    std::vector<int64_t> sizes =
+        n.in.size() >= 2 && !n.in[1].empty() ? host_i64(in(1), "Split") : attr_ints(n, "split");
+    if (sizes.empty()) {
+      const int64_t total = x.shape[size_t(axis)], k = int64_t(n.out.size());
+      IH_REQUIRE(k > 0 && total % k == 0, INFERC_ERR_SHAPE, "Split: cannot infer split sizes");
+      sizes.assign(size_t(k), total / k);
+    }
+    int64_t outer = 1, inner = 1;
+    for (int64_t i = 0; i < axis; ++i) outer *= x.shape[size_t(i)];
+    for (int64_t i = axis + 1; i < r; ++i) inner *= x.shape[size_t(i)];
+    std::vector<float*> outs;
+    for (size_t i = 0; i < sizes.size() && i < n.out.size(); ++i) {
+      std::vector<int64_t> s = x.shape;
+      s[size_t(axis)] = sizes[i];
+      outs.push_back(static_cast<float*>(make_dev(n.out[i], INFERC_DT_F32, s).dev));
+    }
+    IH_REQUIRE(outs.size() == sizes.size(), INFERC_ERR_ARG, "Split: fewer outputs than parts");
+    IH_REQUIRE(inferc_hip_split_f32(ctx, outer, x.shape[size_t(axis)], inner,
+                                    int64_t(sizes.size()), sizes.data(),
+                                    static_cast<const float*>(dev_of(n.in[0])), outs.data()) == 0,
+               INFERC_ERR_SHAPE, inferc_hip_last_error());
+    return;
+  }
+  if (op == "Concat") {
+    int64_t axis = attr_int(n, "axis", 0);
+    const Value& x0 = in(0);
+    const int64_t r = int64_t(x0.shape.size());
+    if (axis < 0) axis += r;
+    IH_REQUIRE(axis >= 0 && axis < r, INFERC_ERR_ARG, "Concat: axis out of range");
+    std::vector<int64_t> os = x0.shape;
+    os[size_t(axis)] = 0;
+    std::vector<int64_t> sizes;
+    for (size_t i = 0; i < n.in.size(); ++i) {
+      const Value& p = in(i);
+      IH_REQUIRE(p.shape.size() == x0.shape.size() && p.dtype == x0.dtype, INFERC_ERR_SHAPE,
+                 "Concat: rank/dtype mismatch");
+      for (int64_t d = 0; d < r; ++d)
+        IH_REQUIRE(d == axis || p.shape[size_t(d)] == x0.shape[size_t(d)], INFERC_ERR_SHAPE,
+                   "Concat: dim mismatch outside axis");
+      sizes.push_back(p.shape[size_t(axis)]);
+      os[size_t(axis)] += p.shape[size_t(axis)];
+    }
+    if (x0.dtype == INFERC_DT_I64) {
+      bool all_host = true;
+      for (size_t i = 0; i < n.in.size(); ++i) all_host = all_host && in(i).host != nullptr;
+      IH_REQUIRE(all_host && r == 1, INFERC_ERR_UNSUPPORTED, "Concat: int64 only as shape math");
+      std::vector<int64_t> res;
+      for (size_t i = 0; i < n.in.size(); ++i) {
+        auto v = host_i64(in(i), "Concat");
+        res.insert(res.end(), v.begin(), v.end());
+      }
+      make_host(n.out[0], INFERC_DT_I64, os, res.data());
+      return;
+    }
+    require_f32(x0, "inputs");
+    int64_t outer = 1, inner = 1;
+    for (int64_t i = 0; i < axis; ++i) outer *= os[size_t(i)];
+    for (int64_t i = axis + 1; i < r; ++i) inner *= os[size_t(i)];
+    std::vector<const float*> parts;
+    for (size_t i = 0; i < n.in.size(); ++i) parts.push_back(static_cast<const float*>(dev_of(n.in[i])));
+    float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
+    IH_REQUIRE(inferc_hip_concat_f32(ctx, outer, inner, int64_t(parts.size()), sizes.data(),
+                                     parts.data(), y) == 0,
+               INFERC_ERR_SHAPE, inferc_hip_last_error());
+    return;
+  }
+  fail(INFERC_ERR_UNSUPPORTED, "Executor: unsupported op '" + op + "' (node: " + n.name + ")");
+}
+
+void inferc_executor::walk() {
+  vals = inits;
+  for (auto& kv : inputs) vals[kv.first] = kv.second.v;
+  for (const auto& n : nodes) exec_node(n);
+  for (const auto& o : outputs) get(o);  // every graph output must exist
+}
+
+std::string inferc_executor::signature() const {
+  std::ostringstream o;
+  std::map<std::string, const Input*> sorted;
+  for (const auto& kv : inputs) sorted[kv.first] = &kv.second;
+  for (const auto& kv : sorted)
+    o << kv.first << ":" << kv.second->v.dtype << ih::shape_str(kv.second->v.shape) << "@"
+      << kv.second->v.dev << ";";
+  return o.str();
+}
+
+void inferc_executor::run() {
+  ctx->make_current();
+  // stage host inputs into their device buffers (outside any graph)
+  for (auto& kv : inputs) {
+    Input& in = kv.second;
+    if (!in.from_host) continue;
+    const size_t bytes = in.v.bytes();
+    IH_HIP(hipMemcpyAsync(in.v.dev, in.staged.data(), bytes, hipMemcpyHostToDevice, ctx->stream));
+  }
+  const std::string sig = signature();
+  if (graph_mode && exec && graph_sig == sig && graph_ws_gen == ctx->ws_generation) {
+    IH_HIP(hipGraphLaunch(exec, ctx->stream));
+    return;
+  }
+  if (!graph_mode || sig != last_sig) {
+    // first run for this input signature: eager (allocates the arena)
+    drop_graph();
+    walk();
+    last_sig = sig;
+    return;
+  }
+  // second run with the same signature: record it, then replay
+  drop_graph();
+  const uint64_t gen = ctx->ws_generation;
+  IH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+  ctx->capturing = true;
+  try {
+    walk();
+  } catch (...) {
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(ctx->stream, &g);
+    if (g) (void)hipGraphDestroy(g);
+    throw;
+  }
+  ctx->capturing = false;
+  IH_HIP(hipStreamEndCapture(ctx->stream, &graph));
+  IH_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+  graph_sig = sig;
+  graph_ws_gen = gen;
+  IH_HIP(hipGraphLaunch(exec, ctx->stream));
+}
+
+namespace {
+
+inferc_graph* check_graph(inferc_graph* g) {
+  IH_REQUIRE(g != nullptr, INFERC_ERR_ARG, "null graph");
+  return g;
+}
+
+inferc_executor* check_ex(inferc_executor* ex) {
+  IH_REQUIRE(ex != nullptr && ex->ctx != nullptr, INFERC_ERR_ARG, "null executor");
+  ex->ctx->make_current();
+  return ex;
+}
+
+std::vector<int64_t> read_shape(int rank, const int64_t* shape) {
+  IH_REQUIRE(rank >= 0 && rank <= 8, INFERC_ERR_SHAPE, "rank must be in [0, 8]");
+  IH_REQUIRE(rank == 0 || shape != nullptr, INFERC_ERR_ARG, "null shape");
+  std::vector<int64_t> s(shape, shape + rank);
+  for (int64_t d : s) IH_REQUIRE(d >= 0, INFERC_ERR_SHAPE, "negative dimension");
+  return s;
+}
+
+}  // namespace
+
+extern "C" {
+
+int inferc_graph_create(inferc_graph** out) {
+  return ih::guard([&] {
+    IH_REQUIRE(out != nullptr, INFERC_ERR_ARG, "null output pointer");
+    *out = new inferc_graph();
+  });
+}
+
+int inferc_graph_destroy(inferc_graph* g) {
+  return ih::guard([&] { delete g; });
+}
+
+int inferc_graph_add_initializer(inferc_graph* g, const char* name, int dtype, int rank,
+                                 const int64_t* shape, const void* host_data) {
+  return ih::guard([&] {
+    check_graph(g);
+    IH_REQUIRE(name != nullptr && *name, INFERC_ERR_ARG, "initializer needs a name");
+    inferc_graph::Init in;
+    in.name = name;
+    in.dtype = dtype;
+    in.shape = read_shape(rank, shape);
+    const size_t bytes = size_t(ih::numel_of(in.shape)) * ih::dtype_size(dtype);
+    IH_REQUIRE(bytes == 0 || host_data != nullptr, INFERC_ERR_ARG, "null initializer data");
+    in.data.assign(static_cast<const uint8_t*>(host_data),
+                   static_cast<const uint8_t*>(host_data) + bytes);
+    g->inits.push_back(std::move(in));
+  });
+}
+
+int inferc_graph_add_node(inferc_graph* g, const char* op_type, const char* name, int n_inputs,
+                          const char* const* inputs, int n_outputs, const char* const* outputs,
+                          const char* attrs) {
+  return ih::guard([&] {
+    check_graph(g);
+    IH_REQUIRE(op_type != nullptr && n_inputs >= 0 && n_outputs >= 0, INFERC_ERR_ARG,
+               "bad node arguments");
+    inferc_graph::Node n;
+    n.op = op_type;
+    n.name = name ? name : "";
+    for (int i = 0; i < n_inputs; ++i) n.in.push_back(inputs[i] ? inputs[i] : "");
+    for (int i = 0; i < n_outputs; ++i) n.out.push_back(outputs[i] ? outputs[i] : "");
+    if (attrs) {
+      std::stringstream ss(attrs);
+      std::string kv;
+      while (std::getline(ss, kv, ';')) {
+        if (kv.empty()) continue;
+        const size_t eq = kv.find('=');
+        IH_REQUIRE(eq != std::string::npos, INFERC_ERR_ARG, "attribute without '=': " + kv);
+        n.attrs[kv.substr(0, eq)] = kv.substr(eq + 1);
+      }
+    }
+    g->nodes.push_back(std::move(n));
+  });
+}
+
+int inferc_graph_add_output(inferc_graph* g, const char* name) {
+  return ih::guard([&] {
+    check_graph(g);
+    IH_REQUIRE(name != nullptr, INFERC_ERR_ARG, "null output name");
+    g->outputs.push_back(name);
+  });
+}
+
+int inferc_executor_create(inferc_hip_ctx* ctx, const inferc_graph* g, inferc_executor** out) {
+  return ih::guard([&] {
+    ih::check_ctx(ctx)->make_current();
+    IH_REQUIRE(g != nullptr && out != nullptr, INFERC_ERR_ARG, "null argument");
+    *out = nullptr;
+    auto ex = std::make_unique<inferc_executor>();
+    ex->ctx = ctx;
+    ex->nodes = g->nodes;
+    ex->outputs = g->outputs;
+    for (const auto& in : g->inits) {
+      ih::Value v;
+      v.dtype = in.dtype;
+      v.shape = in.shape;
+      v.host = std::make_shared<std::vector<uint8_t>>(in.data);
+      if (!in.data.empty()) {
+        IH_HIP(hipMalloc(&v.dev, in.data.size()));
+        ex->init_allocs.push_back(v.dev);
+        IH_HIP(hipMemcpy(v.dev, in.data.data(), in.data.size(), hipMemcpyHostToDevice));
+      }
+      ex->inits[in.name] = v;
+    }
+    ex->peephole();
+    *out = ex.release();
+  });
+}
+
+int inferc_executor_destroy(inferc_executor* ex) {
+  return ih::guard([&] {
+    if (!ex) return;
+    if (ex->ctx) {
+      ex->ctx->make_current();
+      (void)hipStreamSynchronize(ex->ctx->stream);
+    }
+    delete ex;
+  });
+}
+
+int inferc_executor_set_input(inferc_executor* ex, const char* name, int dtype, int rank,
+                              const int64_t* shape, const void* host_data) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(name != nullptr, INFERC_ERR_ARG, "null input name");
+    inferc_executor::Input& in = ex->inputs[name];
+    std::vector<int64_t> s = read_shape(rank, shape);
+    const size_t bytes = size_t(ih::numel_of(s)) * ih::dtype_size(dtype);
+    IH_REQUIRE(bytes == 0 || host_data != nullptr, INFERC_ERR_ARG, "null input data");
+    if (!in.from_host || in.v.bytes() != bytes) {
+      if (in.from_host && in.v.dev) {
+        IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+        IH_HIP(hipFree(in.v.dev));
+      }
+      in.v.dev = nullptr;
+      IH_HIP(hipMalloc(&in.v.dev, bytes > 0 ? bytes : 8));
+    }
+    in.from_host = true;
+    in.v.dtype = dtype;
+    in.v.shape = s;
+    in.v.host.reset();
+    in.staged.assign(static_cast<const uint8_t*>(host_data),
+                     static_cast<const uint8_t*>(host_data) + bytes);
+  });
+}
+
+int inferc_executor_set_input_device(inferc_executor* ex, const char* name, int dtype, int rank,
+                                     const int64_t* shape, const void* dev_data) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(name != nullptr, INFERC_ERR_ARG, "null input name");
+    inferc_executor::Input& in = ex->inputs[name];
+    if (in.from_host && in.v.dev) {
+      IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+      IH_HIP(hipFree(in.v.dev));
+    }
+    in.from_host = false;
+    in.staged.clear();
+    in.v.dtype = dtype;
+    in.v.shape = read_shape(rank, shape);
+    (void)ih::dtype_size(dtype);
+    IH_REQUIRE(in.v.numel() == 0 || dev_data != nullptr, INFERC_ERR_ARG, "null device input");
+    in.v.dev = const_cast<void*>(dev_data);
+    in.v.host.reset();
+  });
+}
+
+int inferc_executor_run(inferc_executor* ex) {
+  return ih::guard([&] { check_ex(ex)->run(); });
+}
+
+int inferc_executor_output_info(inferc_executor* ex, const char* name, int* dtype, int* rank,
+                                int64_t* shape) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(name && dtype && rank && shape, INFERC_ERR_ARG, "null argument");
+    const ih::Value& v = ex->get(name);
+    IH_REQUIRE(v.shape.size() <= 8, INFERC_ERR_SHAPE, "output rank > 8");
+    *dtype = v.dtype;
+    *rank = int(v.shape.size());
+    for (size_t i = 0; i < v.shape.size(); ++i) shape[i] = v.shape[i];
+  });
+}
+
+int inferc_executor_get_output(inferc_executor* ex, const char* name, void* host_dst,
+                               size_t capacity_bytes) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(name && host_dst, INFERC_ERR_ARG, "null argument");
+    const ih::Value& v = ex->get(name);
+    IH_REQUIRE(capacity_bytes >= v.bytes(), INFERC_ERR_ARG, "output buffer too small");
+    IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+    if (v.dev) {
+      IH_HIP(hipMemcpy(host_dst, v.dev, v.bytes(), hipMemcpyDeviceToHost));
+    } else if (v.host) {
+      std::memcpy(host_dst, v.host->data(), v.bytes());
+    }
+  });
+}
+
+int inferc_executor_set_graph_mode(inferc_executor* ex, int enabled) {
+  return ih::guard([&] {
+    check_ex(ex);
+    ex->graph_mode = enabled != 0;
+    if (!ex->graph_mode) ex->drop_graph();
+  });
+}
+
+}  // extern "C"

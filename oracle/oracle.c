@@ -1,0 +1,578 @@
+/*
+ * CPU oracle — kernels and model restatements (TEST INFRASTRUCTURE ONLY).
+ *
+ * Each function names the reference code it restates (paths relative to the
+ * inferc repository) and the check that pins it (tests/test_oracle.py).
+ * Compiled with -ffp-contract=off so products such as the int4 dequant
+ * scale*(nib-8) round exactly once, as the reference writes them.
+ */
+#include "oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+int orc_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+void orc_set_num_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
+/* numpy MatMul over a flattened batch (src/kernels/matmul.cc:63-159): one
+ * sgemm per batch slice; a stride of 0 broadcasts that operand.
+ * Pinned: kernels_test.cc:65-92 (Basic2D, BatchedBroadcast). */
+void orc_matmul(int64_t batch, int64_t M, int64_t N, int64_t K,
+                const float* A, int64_t stride_a, const float* B,
+                int64_t stride_b, float* Y) {
+  for (int64_t b = 0; b < batch; ++b)
+    orc_sgemm(0, 0, M, N, K, 1.0f, A + b * stride_a, K, B + b * stride_b, N,
+              0.0f, Y + b * M * N, N);
+}
+
+/* ONNX Gemm (src/kernels/matmul.cc:161-228): the output is pre-filled with C
+ * (full copy, row broadcast [N] or scalar), then alpha*op(A)op(B) + beta*out.
+ * Pinned: kernels_test.cc:94-104 (BiasAdded), :111-159 (GEMV paths, alpha/beta). */
+void orc_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+              float alpha, const float* A, const float* B, float beta,
+              const float* C, int c_kind, float* Y) {
+  for (int64_t i = 0; i < M * N; ++i) Y[i] = 0.0f;
+  if (C != NULL && beta != 0.0f) {
+    for (int64_t i = 0; i < M; ++i)
+      for (int64_t j = 0; j < N; ++j) {
+        float c = 0.0f;
+        if (c_kind == ORC_C_FULL) c = C[i * N + j];
+        else if (c_kind == ORC_C_ROW) c = C[j];
+        else if (c_kind == ORC_C_SCALAR) c = C[0];
+        Y[i * N + j] = c;
+      }
+  }
+  orc_sgemm(trans_a, trans_b, M, N, K, alpha, A, trans_a ? M : K, B,
+            trans_b ? K : N, beta, Y, N);
+}
+
+static float gelu_erf(float v) {
+  /* src/kernels/fused_matmul_add_gelu.cc:56,73-75 and activation.cc:24-27 */
+  const float kInvSqrt2 = 0.70710678118654752440f;
+  return v * 0.5f * (1.0f + erff(v * kInvSqrt2));
+}
+
+static float gelu_tanh(float v) {
+  /* src/kernels/activation.cc:42-47 */
+  const float kSqrt2OverPi = 0.7978845608028654f;
+  const float kCoef = 0.044715f;
+  const float inner = kSqrt2OverPi * (v + kCoef * v * v * v);
+  return 0.5f * v * (1.0f + tanhf(inner));
+}
+
+/* src/kernels/fused_matmul_add_gelu.cc:13-80: sgemm, then v = acc + b[c],
+ * y = GELU_erf(v). Pinned: GEMM fixtures + Gelu known values
+ * (kernels_test.cc:304-311) + a float64 composition check. */
+void orc_fused_matmul_add_gelu(int64_t M, int64_t N, int64_t K, const float* X,
+                               const float* W, const float* b, float* Y) {
+  orc_sgemm(0, 0, M, N, K, 1.0f, X, K, W, N, 0.0f, Y, N);
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < M; ++r)
+    for (int64_t c = 0; c < N; ++c) Y[r * N + c] = gelu_erf(Y[r * N + c] + b[c]);
+}
+
+/* src/kernels/attention.cc:102-141: three independent X*Wi, then += bi. */
+void orc_fused_qkv(int64_t M, int64_t K, int64_t N, const float* X,
+                   const float* wq, const float* bq, const float* wk,
+                   const float* bk, const float* wv, const float* bv,
+                   float* q, float* k, float* v) {
+  const float* ws[3] = {wq, wk, wv};
+  const float* bs[3] = {bq, bk, bv};
+  float* os[3] = {q, k, v};
+  for (int i = 0; i < 3; ++i) {
+    orc_sgemm(0, 0, M, N, K, 1.0f, X, K, ws[i], N, 0.0f, os[i], N);
+    for (int64_t r = 0; r < M; ++r)
+      for (int64_t c = 0; c < N; ++c) os[i][r * N + c] += bs[i][c];
+  }
+}
+
+/* src/kernels/attention.cc:32-100: per (b,h) scores = scale*Q_h K_h^T
+ * (scale = 1/sqrtf(head_dim) as the sgemm alpha), masked entries set to
+ * `fill`, two-pass softmax (max, exp(x-max), sequential sum, *1/sum), then
+ * P V_h written at column offset h*head_dim.
+ * Pinned: kernels_test.cc:222-252 (single-head values, masked key -> V[0]),
+ * float64 brute force on small shapes, rows of P sum to 1. */
+void orc_fused_attention(int64_t B, int64_t S, int64_t H, int64_t head_dim,
+                         const float* Q, const float* K, const float* V,
+                         const uint8_t* M, const int64_t* ms, float fill,
+                         float* O) {
+  const int64_t nH = H / head_dim;
+  const float scale = 1.0f / sqrtf((float)head_dim);
+#pragma omp parallel for schedule(static)
+  for (int64_t bh = 0; bh < B * nH; ++bh) {
+    const int64_t b = bh / nH, h = bh % nH;
+    float* scores = (float*)malloc(sizeof(float) * (size_t)(S * S));
+    const float* Qh = Q + b * S * H + h * head_dim;
+    const float* Kh = K + b * S * H + h * head_dim;
+    const float* Vh = V + b * S * H + h * head_dim;
+    float* Oh = O + b * S * H + h * head_dim;
+    for (int64_t i = 0; i < S; ++i)
+      for (int64_t j = 0; j < S; ++j) {
+        float acc = 0.0f;
+        for (int64_t d = 0; d < head_dim; ++d) acc += Qh[i * H + d] * Kh[j * H + d];
+        scores[i * S + j] = scale * acc;
+      }
+    for (int64_t i = 0; i < S; ++i) {
+      float* row = scores + i * S;
+      if (M != NULL) {
+        for (int64_t j = 0; j < S; ++j)
+          if (M[b * ms[0] + h * ms[1] + i * ms[2] + j * ms[3]]) row[j] = fill;
+      }
+      float m = row[0];
+      for (int64_t j = 1; j < S; ++j) m = row[j] > m ? row[j] : m;
+      const float neg_m = -m;
+      for (int64_t j = 0; j < S; ++j) row[j] += neg_m;
+      for (int64_t j = 0; j < S; ++j) row[j] = expf(row[j]);
+      float sum = 0.0f;
+      for (int64_t j = 0; j < S; ++j) sum += row[j];
+      const float inv = 1.0f / sum;
+      for (int64_t j = 0; j < S; ++j) row[j] *= inv;
+    }
+    for (int64_t i = 0; i < S; ++i)
+      for (int64_t d = 0; d < head_dim; ++d) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < S; ++j) acc += scores[i * S + j] * Vh[j * H + d];
+        Oh[i * H + d] = acc;
+      }
+    free(scores);
+  }
+}
+
+/* src/kernels/activation.cc:103-150 (vDSP meanv / vsadd / measqv / vsmul /
+ * vma): mean = sum/n; d = x-mean; var = sum(d^2)/n; inv = 1/sqrtf(var+eps);
+ * y = (d*inv)*gamma + beta. Pinned: kernels_test.cc:343-362 (mean 0, var 1)
+ * and a float64 closed form. */
+void orc_layernorm(int64_t rows, int64_t feat, const float* x,
+                   const float* gamma, const float* beta, float eps, float* y) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* p = x + r * feat;
+    float* q = y + r * feat;
+    float sum = 0.0f;
+    for (int64_t i = 0; i < feat; ++i) sum += p[i];
+    const float mean = sum / (float)feat;
+    float sq = 0.0f;
+    for (int64_t i = 0; i < feat; ++i) {
+      const float d = p[i] - mean;
+      q[i] = d;
+      sq += d * d;
+    }
+    const float var = sq / (float)feat;
+    const float inv = 1.0f / sqrtf(var + eps);
+    for (int64_t i = 0; i < feat; ++i) q[i] = (q[i] * inv) * gamma[i] + beta[i];
+  }
+}
+
+/* src/kernels/activation.cc:15-29. Pinned: kernels_test.cc:304-311. */
+void orc_gelu(int64_t n, const float* x, float* y) {
+  for (int64_t i = 0; i < n; ++i) y[i] = gelu_erf(x[i]);
+}
+
+/* src/kernels/activation.cc:31-50. Pinned: kernels_test.cc:255-265 and
+ * float64 evaluation of the same closed form. */
+void orc_gelu_tanh(int64_t n, const float* x, float* y) {
+  for (int64_t i = 0; i < n; ++i) y[i] = gelu_tanh(x[i]);
+}
+
+/* src/kernels/elementwise.cc (Relu, unary). */
+void orc_relu(int64_t n, const float* x, float* y) {
+  for (int64_t i = 0; i < n; ++i) y[i] = x[i] > 0.0f ? x[i] : 0.0f;
+}
+
+/* src/kernels/activation.cc:52-101: per (outer, inner) row along the axis:
+ * max, e = expf(x-max) summed sequentially, then *= 1/sum.
+ * Pinned: kernels_test.cc:313-341 (stability at 1000+, axis=1 rows sum to 1). */
+void orc_softmax(int64_t outer, int64_t axis_dim, int64_t inner,
+                 const float* p, float* q) {
+  for (int64_t o = 0; o < outer; ++o)
+    for (int64_t in = 0; in < inner; ++in) {
+      const float* rp = p + o * axis_dim * inner + in;
+      float* rq = q + o * axis_dim * inner + in;
+      float m = -INFINITY;
+      for (int64_t k = 0; k < axis_dim; ++k)
+        if (rp[k * inner] > m) m = rp[k * inner];
+      float sum = 0.0f;
+      for (int64_t k = 0; k < axis_dim; ++k) {
+        const float e = expf(rp[k * inner] - m);
+        rq[k * inner] = e;
+        sum += e;
+      }
+      const float inv = 1.0f / sum;
+      for (int64_t k = 0; k < axis_dim; ++k) rq[k * inner] *= inv;
+    }
+}
+
+/* src/kernels/elementwise.cc:69-189,225 (broadcast Add), restricted to the
+ * trailing-repeat broadcasts the hot path uses. Pinned: kernels_test.cc
+ * Elementwise.* known answers. */
+void orc_add_bcast(int64_t n, const float* a, const float* b, int64_t b_n,
+                   float* y) {
+  for (int64_t i = 0; i < n; ++i) y[i] = a[i] + b[i % b_n];
+}
+
+/* src/kernels/embedding.cc:9-72 (axis 0, negative indices wrap, out of range
+ * is an error). Pinned: kernels_test.cc:377-400 (exact). */
+int orc_gather_rows(int64_t rows, int64_t row_len, const float* table,
+                    const int64_t* idx, int64_t n_idx, float* out) {
+  for (int64_t k = 0; k < n_idx; ++k) {
+    int64_t i = idx[k];
+    if (i < 0) i += rows;
+    if (i < 0 || i >= rows) return -1;
+    memcpy(out + k * row_len, table + i * row_len, sizeof(float) * (size_t)row_len);
+  }
+  return 0;
+}
+
+/* src/kernels/movement.cc:391-431 (Split). Pinned: kernels_test.cc:458-505. */
+void orc_split(int64_t outer, int64_t axis_full, int64_t inner,
+               int64_t n_parts, const int64_t* sizes, const float* x,
+               float* const* outs) {
+  int64_t off = 0;
+  for (int64_t p = 0; p < n_parts; ++p) {
+    const int64_t sz = sizes[p];
+    for (int64_t o = 0; o < outer; ++o)
+      memcpy(outs[p] + o * sz * inner, x + (o * axis_full + off) * inner,
+             sizeof(float) * (size_t)(sz * inner));
+    off += sz;
+  }
+}
+
+/* src/kernels/movement.cc:142-189 (Concat). Pinned: kernels_test.cc:428-436. */
+void orc_concat(int64_t outer, int64_t inner, int64_t n_parts,
+                const int64_t* sizes, const float* const* parts, float* out) {
+  int64_t total = 0;
+  for (int64_t p = 0; p < n_parts; ++p) total += sizes[p];
+  for (int64_t o = 0; o < outer; ++o) {
+    int64_t pos = 0;
+    for (int64_t p = 0; p < n_parts; ++p) {
+      memcpy(out + (o * total + pos) * inner, parts[p] + o * sizes[p] * inner,
+             sizeof(float) * (size_t)(sizes[p] * inner));
+      pos += sizes[p];
+    }
+  }
+}
+
+/* src/cli/main.cpp:820-828,875-879: best = x[0]; strict '>' keeps the first
+ * maximal index. Pinned: tie cases in tests/test_oracle.py. */
+int64_t orc_argmax(int64_t n, const float* x) {
+  int64_t best_i = 0;
+  float best = x[0];
+  for (int64_t v = 1; v < n; ++v)
+    if (x[v] > best) { best = x[v]; best_i = v; }
+  return best_i;
+}
+
+/* bench/amx/int4_gemv_amx.cc:258-271 (scalar_int4_gemv_perRow): byte
+ * W[r*K/2 + k/2], nib = (k&1) ? byte>>4 : byte&0xf, acc (double) +=
+ * double(s_r*float(nib-8)) * double(x_k); y = float(acc).
+ * Pinned: the reference's closed-form fixture (int4_gemv_amx.cc:482-546)
+ * recomputed independently in float64 numpy, committed under tests/golden. */
+void orc_int4_gemv_per_row(const uint8_t* W, const float* scales,
+                           const float* x, float* y, int64_t N, int64_t K) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < N; ++r) {
+    double acc = 0;
+    const float s = scales[r];
+    for (int64_t k = 0; k < K; ++k) {
+      const uint8_t byte = W[r * (K / 2) + k / 2];
+      const int nibble = (k & 1) ? (byte >> 4) : (byte & 0xf);
+      acc += (double)(s * (float)(nibble - 8)) * (double)x[k];
+    }
+    y[r] = (float)acc;
+  }
+}
+
+void orc_int4_gemv_per_row_batched(const uint8_t* W, const float* scales,
+                                   const float* x, float* y, int64_t N,
+                                   int64_t K, int64_t B) {
+  for (int64_t b = 0; b < B; ++b)
+    orc_int4_gemv_per_row(W, scales, x + b * K, y + b * N, N, K);
+}
+
+/* bench/amx/int4_gemv_amx.cc:243-256 (scalar_int4_gemv, one scale). */
+void orc_int4_gemv_per_tensor(const uint8_t* W, float scale, const float* x,
+                              float* y, int64_t N, int64_t K) {
+  for (int64_t r = 0; r < N; ++r) {
+    double acc = 0;
+    for (int64_t k = 0; k < K; ++k) {
+      const uint8_t byte = W[r * (K / 2) + k / 2];
+      const int nibble = (k & 1) ? (byte >> 4) : (byte & 0xf);
+      acc += (double)(scale * (float)(nibble - 8)) * (double)x[k];
+    }
+    y[r] = (float)acc;
+  }
+}
+
+/* The dequantised weight the reference multiplies by x (int4_gemv_amx.cc:267
+ * and the pre-scaled tables of :285-288): s_r * float(nib - 8), one IEEE RNE
+ * product. Pinned exactly: nibble rule + numpy float32 product. */
+void orc_int4_unpack(const uint8_t* W, const float* scales, int64_t N,
+                     int64_t K, float* out) {
+  for (int64_t r = 0; r < N; ++r)
+    for (int64_t k = 0; k < K; ++k) {
+      const uint8_t byte = W[r * (K / 2) + k / 2];
+      const int nibble = (k & 1) ? (byte >> 4) : (byte & 0xf);
+      out[r * K + k] = scales[r] * (float)(nibble - 8);
+    }
+}
+
+/* ------------------------------------------------------------------------
+ * Model restatements.
+ *
+ * Encoder: the post-`optimize` fused DistilBERT graph the reference executes
+ * (src/cli/main.cpp:270-276 pass order; per layer FusedQKV -> FusedAttention
+ * -> MatMul -> Add(b) -> Add(residual) -> FusedLayerNorm ->
+ * FusedMatMulAddGELU -> MatMul -> Add(b) -> Add(residual) -> FusedLayerNorm,
+ * dispatch at src/runtime/executor.cc:151-225). Classifier head: CLS row ->
+ * Gemm + Relu -> Gemm.
+ *
+ * Weight pointer order (w[]):
+ *   0 word_emb [V,H]  1 pos_emb [P,H]  2 emb_ln_g [H]  3 emb_ln_b [H]
+ *   per layer l, base 4+16l:
+ *     +0 wq [H,H] +1 bq +2 wk +3 bk +4 wv +5 bv +6 wo [H,H] +7 bo
+ *     +8 ln1_g +9 ln1_b +10 w1 [H,F] +11 b1 [F] +12 w2 [F,H] +13 b2
+ *     +14 ln2_g +15 ln2_b
+ *   tail, base 4+16L: +0 pre_w [H,H] +1 pre_b +2 cls_w [C,H] +3 cls_b [C]
+ *   (the head's weights are [out,in]: torch Linear exports as Gemm transB=1)
+ * ------------------------------------------------------------------------ */
+int orc_encoder_forward(const orc_encoder_cfg* cfg, const float* const* w,
+                        int64_t B, int64_t S, const int64_t* ids,
+                        const int64_t* attn_mask, float* logits) {
+  const int64_t H = cfg->hidden, F = cfg->ffn, L = cfg->layers;
+  const int64_t M = B * S, C = cfg->n_classes;
+  const int64_t hd = H / cfg->heads;
+  float* h = (float*)malloc(sizeof(float) * (size_t)(M * H));
+  float* t = (float*)malloc(sizeof(float) * (size_t)(M * H));
+  float* q = (float*)malloc(sizeof(float) * (size_t)(M * H));
+  float* k = (float*)malloc(sizeof(float) * (size_t)(M * H));
+  float* v = (float*)malloc(sizeof(float) * (size_t)(M * H));
+  float* ctx = (float*)malloc(sizeof(float) * (size_t)(M * H));
+  float* f = (float*)malloc(sizeof(float) * (size_t)(M * F));
+  uint8_t* mask = (uint8_t*)malloc((size_t)M);
+  int rc = 0;
+  /* embeddings: Gather(word) + Gather(pos), LayerNorm */
+  for (int64_t b = 0; b < B && rc == 0; ++b)
+    for (int64_t s = 0; s < S; ++s) {
+      const int64_t id = ids[b * S + s];
+      if (id < 0 || id >= cfg->vocab || s >= cfg->max_pos) { rc = -1; break; }
+      for (int64_t c = 0; c < H; ++c)
+        t[(b * S + s) * H + c] = w[0][id * H + c] + w[1][s * H + c];
+    }
+  if (rc == 0) {
+    orc_layernorm(M, H, t, w[2], w[3], cfg->eps, h);
+    /* mask cond = Equal(attention_mask, 0), broadcast [B,1,1,S] */
+    for (int64_t i = 0; i < M; ++i) mask[i] = attn_mask[i] == 0;
+    const int64_t ms[4] = {S, 0, 0, 1};
+    for (int64_t l = 0; l < L; ++l) {
+      const float* const* lw = w + 4 + 16 * l;
+      orc_fused_qkv(M, H, H, h, lw[0], lw[1], lw[2], lw[3], lw[4], lw[5], q, k, v);
+      orc_fused_attention(B, S, H, hd, q, k, v, mask, ms, -FLT_MAX, ctx);
+      orc_sgemm(0, 0, M, H, H, 1.0f, ctx, H, lw[6], H, 0.0f, t, H);
+      for (int64_t r = 0; r < M; ++r)
+        for (int64_t c = 0; c < H; ++c)
+          t[r * H + c] = (t[r * H + c] + lw[7][c]) + h[r * H + c];
+      orc_layernorm(M, H, t, lw[8], lw[9], cfg->eps, h);
+      orc_fused_matmul_add_gelu(M, F, H, h, lw[10], lw[11], f);
+      orc_sgemm(0, 0, M, H, F, 1.0f, f, F, lw[12], H, 0.0f, t, H);
+      for (int64_t r = 0; r < M; ++r)
+        for (int64_t c = 0; c < H; ++c)
+          t[r * H + c] = (t[r * H + c] + lw[13][c]) + h[r * H + c];
+      orc_layernorm(M, H, t, lw[14], lw[15], cfg->eps, h);
+    }
+    /* CLS token rows -> pre_classifier Gemm + Relu -> classifier Gemm */
+    const float* const* tw = w + 4 + 16 * L;
+    float* cls = (float*)malloc(sizeof(float) * (size_t)(B * H));
+    float* pre = (float*)malloc(sizeof(float) * (size_t)(B * H));
+    for (int64_t b = 0; b < B; ++b) memcpy(cls + b * H, h + b * S * H, sizeof(float) * (size_t)H);
+    orc_gemm(0, 1, B, H, H, 1.0f, cls, tw[0], 1.0f, tw[1], ORC_C_ROW, pre);
+    orc_relu(B * H, pre, pre);
+    orc_gemm(0, 1, B, C, H, 1.0f, pre, tw[2], 1.0f, tw[3], ORC_C_ROW, logits);
+    free(cls);
+    free(pre);
+  }
+  free(h); free(t); free(q); free(k); free(v); free(ctx); free(f); free(mask);
+  return rc;
+}
+
+/* ------------------------------------------------------------------------
+ * GPT-2 (HF GPT-2 as exported to ONNX, run by `inferc decode`,
+ * src/cli/main.cpp:700-936; op sequence per layer from the with-past graph:
+ * LN -> Gemm(c_attn) -> Split -> QK^T MatMul -> Div(sqrt(64)) -> Where(causal)
+ * -> Softmax -> PV MatMul -> Gemm(c_proj) -> Add(residual) -> LN ->
+ * Gemm(c_fc) -> GeluTanh -> Gemm(c_proj) -> Add(residual); final LN; logits =
+ * h * wte^T (the folded transpose of constant_fold.cc:12-54)).
+ * Gemm's bias is added after the product: y = acc + b (matmul.cc:174-226).
+ *
+ * Weight pointer order (w[]):
+ *   0 wte [V,H]  1 wpe [P,H]
+ *   per layer l, base 2+12l:
+ *     +0 ln1_g +1 ln1_b +2 attn_w [H,3H] +3 attn_b [3H] +4 proj_w [H,H]
+ *     +5 proj_b +6 ln2_g +7 ln2_b +8 fc_w [H,F] +9 fc_b [F]
+ *     +10 fcproj_w [F,H] +11 fcproj_b [H]
+ *   tail, base 2+12L: +0 lnf_g +1 lnf_b
+ * KV cache per layer: [nH, Tmax, hd] for K and V (present.* in the graph).
+ * ------------------------------------------------------------------------ */
+typedef struct {
+  const orc_gpt2_cfg* cfg;
+  const float* const* w;
+  int64_t tmax;
+  float* kc; /* [L, nH, tmax, hd] */
+  float* vc;
+} gpt2_state;
+
+/* Run `n` new tokens at positions [pos0, pos0+n) through the stack, append
+ * their K/V to the cache, and write the final-LN hidden rows to hout [n,H]. */
+static int gpt2_block_run(gpt2_state* st, const int64_t* ids, int64_t n,
+                          int64_t pos0, float* hout) {
+  const orc_gpt2_cfg* cfg = st->cfg;
+  const float* const* w = st->w;
+  const int64_t H = cfg->hidden, F = cfg->ffn, L = cfg->layers, nH = cfg->heads;
+  const int64_t hd = H / nH, T = st->tmax;
+  float* h = (float*)malloc(sizeof(float) * (size_t)(n * H));
+  float* a = (float*)malloc(sizeof(float) * (size_t)(n * H));
+  float* qkv = (float*)malloc(sizeof(float) * (size_t)(n * 3 * H));
+  float* att = (float*)malloc(sizeof(float) * (size_t)(n * H));
+  float* o = (float*)malloc(sizeof(float) * (size_t)(n * H));
+  float* f = (float*)malloc(sizeof(float) * (size_t)(n * F));
+  float* sc = (float*)malloc(sizeof(float) * (size_t)(pos0 + n));
+  int rc = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t id = ids[i], p = pos0 + i;
+    if (id < 0 || id >= cfg->vocab || p >= cfg->max_pos || p >= T) { rc = -1; break; }
+    for (int64_t c = 0; c < H; ++c) h[i * H + c] = w[0][id * H + c] + w[1][p * H + c];
+  }
+  for (int64_t l = 0; l < L && rc == 0; ++l) {
+    const float* const* lw = w + 2 + 12 * l;
+    float* kc = st->kc + l * nH * T * hd;
+    float* vc = st->vc + l * nH * T * hd;
+    orc_layernorm(n, H, h, lw[0], lw[1], cfg->eps, a);
+    orc_sgemm(0, 0, n, 3 * H, H, 1.0f, a, H, lw[2], 3 * H, 0.0f, qkv, 3 * H);
+    for (int64_t i = 0; i < n; ++i)
+      for (int64_t c = 0; c < 3 * H; ++c) qkv[i * 3 * H + c] += lw[3][c];
+    /* Split -> present = Concat(past, new) */
+    for (int64_t i = 0; i < n; ++i)
+      for (int64_t hh = 0; hh < nH; ++hh)
+        for (int64_t d = 0; d < hd; ++d) {
+          kc[(hh * T + pos0 + i) * hd + d] = qkv[i * 3 * H + H + hh * hd + d];
+          vc[(hh * T + pos0 + i) * hd + d] = qkv[i * 3 * H + 2 * H + hh * hd + d];
+        }
+    for (int64_t i = 0; i < n; ++i) {
+      const int64_t t = pos0 + i + 1; /* causal: keys 0..pos0+i */
+      for (int64_t hh = 0; hh < nH; ++hh) {
+        const float* qv = qkv + i * 3 * H + hh * hd;
+        for (int64_t j = 0; j < t; ++j) {
+          float acc = 0.0f;
+          for (int64_t d = 0; d < hd; ++d) acc += qv[d] * kc[(hh * T + j) * hd + d];
+          sc[j] = acc / sqrtf((float)hd);
+        }
+        float m = -INFINITY;
+        for (int64_t j = 0; j < t; ++j) if (sc[j] > m) m = sc[j];
+        float sum = 0.0f;
+        for (int64_t j = 0; j < t; ++j) { sc[j] = expf(sc[j] - m); sum += sc[j]; }
+        const float inv = 1.0f / sum;
+        for (int64_t j = 0; j < t; ++j) sc[j] *= inv;
+        for (int64_t d = 0; d < hd; ++d) {
+          float acc = 0.0f;
+          for (int64_t j = 0; j < t; ++j) acc += sc[j] * vc[(hh * T + j) * hd + d];
+          att[i * H + hh * hd + d] = acc;
+        }
+      }
+    }
+    orc_sgemm(0, 0, n, H, H, 1.0f, att, H, lw[4], H, 0.0f, o, H);
+    for (int64_t i = 0; i < n * H; ++i) h[i] = h[i] + (o[i] + lw[5][i % H]);
+    orc_layernorm(n, H, h, lw[6], lw[7], cfg->eps, a);
+    orc_sgemm(0, 0, n, F, H, 1.0f, a, H, lw[8], F, 0.0f, f, F);
+    for (int64_t i = 0; i < n * F; ++i) f[i] = gelu_tanh(f[i] + lw[9][i % F]);
+    orc_sgemm(0, 0, n, H, F, 1.0f, f, F, lw[10], H, 0.0f, o, H);
+    for (int64_t i = 0; i < n * H; ++i) h[i] = h[i] + (o[i] + lw[11][i % H]);
+  }
+  if (rc == 0) {
+    const float* const* tw = w + 2 + 12 * L;
+    orc_layernorm(n, H, h, tw[0], tw[1], cfg->eps, hout);
+  }
+  free(h); free(a); free(qkv); free(att); free(o); free(f); free(sc);
+  return rc;
+}
+
+/* logits[n,V] = hrows[n,H] * wte^T: the LM head reads wte rows directly, which
+ * is the same product as the reference's MatMul against the folded wte^T. */
+static void gpt2_lm_head(const orc_gpt2_cfg* cfg, const float* wte,
+                         const float* hrows, int64_t n, float* logits) {
+  orc_sgemm(0, 1, n, cfg->vocab, cfg->hidden, 1.0f, hrows, cfg->hidden, wte,
+            cfg->hidden, 0.0f, logits, cfg->vocab);
+}
+
+int orc_gpt2_forward(const orc_gpt2_cfg* cfg, const float* const* w,
+                     const int64_t* ids, int64_t n, float* logits) {
+  gpt2_state st;
+  st.cfg = cfg; st.w = w; st.tmax = n;
+  const int64_t nH = cfg->heads, hd = cfg->hidden / cfg->heads;
+  st.kc = (float*)malloc(sizeof(float) * (size_t)(cfg->layers * nH * n * hd));
+  st.vc = (float*)malloc(sizeof(float) * (size_t)(cfg->layers * nH * n * hd));
+  float* hrows = (float*)malloc(sizeof(float) * (size_t)(n * cfg->hidden));
+  int rc = gpt2_block_run(&st, ids, n, 0, hrows);
+  if (rc == 0) gpt2_lm_head(cfg, w[0], hrows, n, logits);
+  free(st.kc); free(st.vc); free(hrows);
+  return rc;
+}
+
+static float top2_margin(int64_t n, const float* x, int64_t best) {
+  float second = -INFINITY;
+  for (int64_t v = 0; v < n; ++v)
+    if (v != best && x[v] > second) second = x[v];
+  return x[best] - second;
+}
+
+int orc_gpt2_generate(const orc_gpt2_cfg* cfg, const float* const* w,
+                      const int64_t* prompt, int64_t n_prompt,
+                      int64_t max_tokens, int64_t* tokens_out,
+                      float* last_logits, float* margins) {
+  if (n_prompt <= 0 || max_tokens <= 0) return -1;
+  gpt2_state st;
+  st.cfg = cfg; st.w = w; st.tmax = n_prompt + max_tokens;
+  const int64_t nH = cfg->heads, hd = cfg->hidden / cfg->heads, V = cfg->vocab;
+  st.kc = (float*)calloc((size_t)(cfg->layers * nH * st.tmax * hd), sizeof(float));
+  st.vc = (float*)calloc((size_t)(cfg->layers * nH * st.tmax * hd), sizeof(float));
+  float* hrows = (float*)malloc(sizeof(float) * (size_t)(n_prompt * cfg->hidden));
+  float* logits = (float*)malloc(sizeof(float) * (size_t)V);
+  /* prefill; only the last position's logits are read (main.cpp:820-828) */
+  int rc = gpt2_block_run(&st, prompt, n_prompt, 0, hrows);
+  if (rc == 0) {
+    gpt2_lm_head(cfg, w[0], hrows + (n_prompt - 1) * cfg->hidden, 1, logits);
+    int64_t next = orc_argmax(V, logits);
+    tokens_out[0] = next;
+    if (margins) margins[0] = top2_margin(V, logits, next);
+    int64_t pos = n_prompt;
+    for (int64_t step = 1; step < max_tokens && rc == 0; ++step) {
+      rc = gpt2_block_run(&st, &next, 1, pos, hrows);
+      if (rc != 0) break;
+      gpt2_lm_head(cfg, w[0], hrows, 1, logits);
+      next = orc_argmax(V, logits);
+      tokens_out[step] = next;
+      if (margins) margins[step] = top2_margin(V, logits, next);
+      pos += 1;
+    }
+    if (rc == 0 && last_logits) memcpy(last_logits, logits, sizeof(float) * (size_t)V);
+  }
+  free(st.kc); free(st.vc); free(hrows); free(logits);
+  return rc;
+}

@@ -1,0 +1,112 @@
+"""End-to-end GPU parity: the executor running the fused DistilBERT graph and
+the GPT-2 greedy decoder against the CPU oracle on identical seeded inputs
+(BASELINE configs 1 and 4). Logits within 1e-4 max-abs-diff; greedy token
+sequences bit-exact."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from inferc_amd import graphs, rt
+
+pytestmark = pytest.mark.gpu
+
+
+def _encoder(ctx, cfg, seed):
+    w = graphs.encoder_weights(cfg, seed)
+    ex = rt.Executor(ctx, graphs.encoder_graph(cfg, w))
+    return w, ex
+
+
+def test_encoder_small_ragged_and_graph_replay(ctx):
+    cfg = graphs.small_encoder_cfg()
+    w, ex = _encoder(ctx, cfg, 21)
+    ids, mask = graphs.encoder_inputs(cfg, 3, 40, ragged=True)
+    ref = O.encoder_forward(cfg, w, ids, mask)
+    outs = [ex.run({"input_ids": ids, "attention_mask": mask}, ["logits"])["logits"]
+            for _ in range(4)]  # eager, capture, replay, replay
+    assert outs[0].shape == (3, 2)
+    np.testing.assert_allclose(outs[0], ref, atol=1e-4)
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+    ex.set_graph_mode(False)
+    np.testing.assert_array_equal(
+        ex.run({"input_ids": ids, "attention_mask": mask}, ["logits"])["logits"], outs[0])
+    # a new input shape re-plans
+    ids2, mask2 = graphs.encoder_inputs(cfg, 2, 17, seed=8)
+    np.testing.assert_allclose(
+        ex.run({"input_ids": ids2, "attention_mask": mask2}, ["logits"])["logits"],
+        O.encoder_forward(cfg, w, ids2, mask2), atol=1e-4)
+
+
+def test_encoder_unsupported_op_raises(ctx):
+    g = rt.Graph()
+    g.add_node("NonZero", ["x"], ["y"])
+    g.add_output("y")
+    ex = rt.Executor(ctx, g)
+    ex.set_input("x", np.ones(3, np.float32))
+    with pytest.raises(RuntimeError, match="unsupported op 'NonZero'"):
+        ex.run_async()
+
+
+@pytest.mark.parametrize("B,ragged", [(1, False), (32, False), (32, True)])
+def test_distilbert_encoder_config1(ctx, B, ragged):
+    """6 layers, H 768, 12x64, FFN 3072, S=128."""
+    cfg = graphs.DISTILBERT
+    w, ex = _encoder(ctx, cfg, 1)
+    ids, mask = graphs.encoder_inputs(cfg, B, 128, ragged=ragged)
+    got = ex.run({"input_ids": ids, "attention_mask": mask}, ["logits"])["logits"]
+    ref = O.encoder_forward(cfg, w, ids, mask)
+    assert got.shape == (B, 2)
+    assert np.max(np.abs(got - ref)) <= 1e-4, np.max(np.abs(got - ref))
+    again = ex.run({"input_ids": ids, "attention_mask": mask}, ["logits"])["logits"]
+    np.testing.assert_array_equal(again, got)
+
+
+def test_gpt2_small_generate_and_forward(ctx):
+    cfg = graphs.small_gpt2_cfg()
+    w = graphs.gpt2_weights(cfg, 22)
+    prompt = graphs.gpt2_prompt(cfg, 9)
+    dec = rt.Gpt2Decoder(ctx, cfg, w, max_t=64)
+    toks, steps, logits = dec.generate(prompt, 20, want_step_ms=True, want_logits=True)
+    ref_toks, ref_logits, margins = O.gpt2_generate(cfg, w, prompt, 20)
+    np.testing.assert_array_equal(toks, ref_toks)
+    np.testing.assert_allclose(logits, ref_logits, atol=1e-4)
+    assert steps.shape == (19,) and np.all(steps > 0)
+    np.testing.assert_allclose(dec.forward(prompt), O.gpt2_forward(cfg, w, prompt), atol=1e-4)
+    # a second generate on the same model reuses the captured step
+    toks2, _, _ = dec.generate(prompt, 20)
+    np.testing.assert_array_equal(toks2, toks)
+    with pytest.raises(RuntimeError, match="exceed the KV cache"):
+        dec.generate(prompt, 60)
+    with pytest.raises(RuntimeError, match="out of range"):
+        dec.generate(np.array([cfg["vocab"]], np.int64), 2)
+
+
+@pytest.fixture(scope="module")
+def gpt2_full():
+    cfg = graphs.GPT2_SMALL
+    return cfg, graphs.gpt2_weights(cfg, 2)
+
+
+def test_gpt2_forward_logits_config4(ctx, gpt2_full):
+    cfg, w = gpt2_full
+    prompt = graphs.gpt2_prompt(cfg, 32)
+    dec = rt.Gpt2Decoder(ctx, cfg, w, max_t=160)
+    got = dec.forward(prompt)
+    ref = O.gpt2_forward(cfg, w, prompt)
+    assert np.max(np.abs(got - ref)) <= 1e-4, np.max(np.abs(got - ref))
+
+
+def test_gpt2_greedy_decode_config4_bit_exact(ctx, gpt2_full):
+    """prompt 32, 128 generated tokens, sequence bit-exact."""
+    cfg, w = gpt2_full
+    prompt = graphs.gpt2_prompt(cfg, 32)
+    dec = rt.Gpt2Decoder(ctx, cfg, w, max_t=160)
+    toks, steps, logits = dec.generate(prompt, 128, want_step_ms=True, want_logits=True)
+    ref_toks, ref_logits, margins = O.gpt2_generate(cfg, w, prompt, 128)
+    print(f"min top-2 margin {margins.min():.3e}; max |dlogit| "
+          f"{np.max(np.abs(logits - ref_logits)):.3e}; ms/token {steps.mean():.4f}")
+    np.testing.assert_array_equal(toks, ref_toks)
+    assert np.max(np.abs(logits - ref_logits)) <= 1e-4
