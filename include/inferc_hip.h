@@ -264,6 +264,13 @@ typedef struct inferc_executor inferc_executor;
 int inferc_executor_create(inferc_hip_ctx* ctx, const inferc_graph* g,
                            inferc_executor** out);
 int inferc_executor_destroy(inferc_executor* ex);
+/* Device-free executor for planning: run() performs the node walk with shape
+ * inference, host shape plumbing and peephole fusion but launches nothing
+ * (the role of InferShapes, src/ir/shape_inference.cc:577-633, for the fused
+ * graph); output_info() then reports every output's shape. */
+int inferc_executor_create_dry(const inferc_graph* g, inferc_executor** out);
+/* Number of nodes after peephole fusion. */
+int inferc_executor_node_count(inferc_executor* ex, int* count);
 /* Bind an input from host memory (copied to the device) or a device pointer
  * (borrowed until the next set_input of that name). */
 int inferc_executor_set_input(inferc_executor* ex, const char* name, int dtype,

@@ -146,6 +146,9 @@ struct inferc_executor {
   std::unordered_map<std::string, Buf> arena;
   std::unordered_map<std::string, int> fused_act;  // Gemm name -> folded activation
   bool graph_mode = true;
+  // Dry run: shape inference and peephole only, no device (host-logic tests).
+  bool dry = false;
+  uintptr_t dry_next = 0x10000;
   std::string last_sig;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -153,6 +156,7 @@ struct inferc_executor {
   uint64_t graph_ws_gen = 0;
 
   ~inferc_executor() {
+    if (dry) return;
     drop_graph();
     for (auto& kv : arena) (void)hipFree(kv.second.p);
     for (auto& kv : inputs)
@@ -169,9 +173,20 @@ struct inferc_executor {
   }
 
   // Device buffer for tensor `name` of at least `bytes`, reused across runs.
+  void* fake_ptr(size_t bytes) {
+    void* p = reinterpret_cast<void*>(dry_next);
+    dry_next += (bytes + 255) / 256 * 256 + 256;
+    return p;
+  }
+
   void* buf(const std::string& name, size_t bytes) {
     Buf& b = arena[name];
     if (b.p && b.bytes >= bytes) return b.p;
+    if (dry) {
+      b.p = fake_ptr(bytes);
+      b.bytes = bytes;
+      return b.p;
+    }
     IH_REQUIRE(!ctx->capturing, INFERC_ERR_STATE, "executor: allocation during graph capture");
     if (b.p) {
       IH_HIP(hipStreamSynchronize(ctx->stream));
@@ -206,9 +221,13 @@ struct inferc_executor {
       v.dev = up.p;
       return up.p;
     }
-    IH_REQUIRE(!ctx->capturing, INFERC_ERR_STATE, "host constant changed inside capture");
+    IH_REQUIRE(dry || !ctx->capturing, INFERC_ERR_STATE, "host constant changed inside capture");
     up.bytes = *v.host;
     up.p = buf("__h2d__" + name, v.bytes());
+    if (dry) {
+      v.dev = up.p;
+      return up.p;
+    }
     IH_HIP(hipMemcpyAsync(up.p, up.bytes.data(), up.bytes.size(), hipMemcpyHostToDevice,
                           ctx->stream));
     v.dev = up.p;
@@ -375,21 +394,21 @@ void inferc_executor::peephole() {
 void inferc_executor::exec_node(const inferc_graph::Node& n) {
   using namespace ih;
   const std::string& op = n.op;
-  auto in = [&](size_t i) -> const Value& {
+  auto in = [&](size_t i) -> Value {
     IH_REQUIRE(i < n.in.size(), INFERC_ERR_ARG, op + ": missing input " + std::to_string(i));
     return get(n.in[i]);
   };
-  auto require_f32 = [&](const Value& v, const char* what) {
+  auto require_f32 = [&](const Value v, const char* what) {
     IH_REQUIRE(v.dtype == INFERC_DT_F32, INFERC_ERR_UNSUPPORTED,
                op + ": " + what + " must be float32");
   };
   IH_REQUIRE(!n.out.empty(), INFERC_ERR_ARG, op + ": node has no outputs");
 
   if (op == "FusedQKV") {
-    const Value& x = in(0);
+    const Value x = in(0);
     require_f32(x, "X");
     const int64_t K = x.shape.back(), M = x.numel() / K;
-    const Value& wq = in(1);
+    const Value wq = in(1);
     IH_REQUIRE(wq.shape.size() == 2 && wq.shape[0] == K, INFERC_ERR_SHAPE, "FusedQKV: W shape");
     const int64_t N = wq.shape[1];
     std::vector<int64_t> os = x.shape;
@@ -398,8 +417,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     const float* b[3];
     float* y[3];
     for (int i = 0; i < 3; ++i) {
-      const Value& wi = in(size_t(1 + 2 * i));
-      const Value& bi = in(size_t(2 + 2 * i));
+      const Value wi = in(size_t(1 + 2 * i));
+      const Value bi = in(size_t(2 + 2 * i));
       IH_REQUIRE(wi.shape == wq.shape && bi.numel() == N, INFERC_ERR_SHAPE,
                  "FusedQKV: projections must share shapes");
       w[i] = static_cast<const float*>(dev_of(n.in[size_t(1 + 2 * i)]));
@@ -407,11 +426,13 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       IH_REQUIRE(i < int(n.out.size()), INFERC_ERR_ARG, "FusedQKV: needs three outputs");
       y[i] = static_cast<float*>(make_dev(n.out[size_t(i)], INFERC_DT_F32, os).dev);
     }
-    gemm_qkv(ctx, M, K, N, static_cast<const float*>(dev_of(n.in[0])), w, b, y, N);
+    if (!dry) {
+      gemm_qkv(ctx, M, K, N, static_cast<const float*>(dev_of(n.in[0])), w, b, y, N);
+    }
     return;
   }
   if (op == "FusedAttention") {
-    const Value& q = in(0);
+    const Value q = in(0);
     require_f32(q, "Q");
     IH_REQUIRE(q.shape.size() == 3, INFERC_ERR_SHAPE, "FusedAttention: expect [B,S,H]");
     IH_REQUIRE(in(1).shape == q.shape && in(2).shape == q.shape, INFERC_ERR_SHAPE,
@@ -425,7 +446,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     a.v = static_cast<const float*>(dev_of(n.in[2]));
     a.ldq = a.ldk = a.ldv = a.ldo = a.H;
     if (n.in.size() >= 4 && !n.in[3].empty()) {
-      const Value& m = in(3);
+      const Value m = in(3);
       IH_REQUIRE(m.dtype == INFERC_DT_BOOL || m.dtype == INFERC_DT_U8, INFERC_ERR_UNSUPPORTED,
                  "FusedAttention: mask must be bool");
       IH_REQUIRE(m.shape.size() <= 4, INFERC_ERR_SHAPE, "FusedAttention: mask rank > 4");
@@ -433,12 +454,14 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       mask_strides(m.shape, a.ms);
     }
     a.out = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, q.shape).dev);
-    attention(ctx, a);
+    if (!dry) {
+      attention(ctx, a);
+    }
     return;
   }
   if (op == "FusedMatMulAddGELU" || op == "FusedGemmEpilogue" || op == "MatMul") {
-    const Value& x = in(0);
-    const Value& w = in(1);
+    const Value x = in(0);
+    const Value w = in(1);
     require_f32(x, "A");
     require_f32(w, "B");
     if (op == "MatMul" && (w.shape.size() != 2 || x.shape.size() < 2)) {
@@ -468,7 +491,9 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       g.stride_b = nb == 1 ? 0 : K * N;
       g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
       g.ldy = N; g.stride_y = M * N;
-      gemm(ctx, g);
+      if (!dry) {
+        gemm(ctx, g);
+      }
       return;
     }
     IH_REQUIRE(w.shape.size() == 2, INFERC_ERR_SHAPE, op + ": W must be 2D [K,N]");
@@ -491,23 +516,25 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     }
     if (op == "FusedMatMulAddGELU") g.act = INFERC_ACT_GELU_ERF;
     if (op == "FusedGemmEpilogue" && n.in.size() >= 4) {
-      const Value& r = in(3);
+      const Value r = in(3);
       IH_REQUIRE(r.numel() == M * N, INFERC_ERR_UNSUPPORTED,
                  "fused residual must match the product's shape");
       g.R = static_cast<const float*>(dev_of(n.in[3]));
       g.ldr = N;
     }
     g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
-    gemm(ctx, g);
+    if (!dry) {
+      gemm(ctx, g);
+    }
     return;
   }
   if (op == "Gemm") {
-    const Value& a = in(0);
-    const Value& b = in(1);
+    const Value a = in(0);
+    const Value b = in(1);
     require_f32(a, "A");
     require_f32(b, "B");
     IH_REQUIRE(a.shape.size() == 2 && b.shape.size() == 2, INFERC_ERR_SHAPE,
-               "Gemm: 2D inputs only");
+               "Gemm: 2D inputs only, got " + shape_str(a.shape) + " and " + shape_str(b.shape));
     GemmArgs g;
     g.trans_a = int(attr_int(n, "transA", 0));
     g.trans_b = int(attr_int(n, "transB", 0));
@@ -523,7 +550,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     g.B = static_cast<const float*>(dev_of(n.in[1]));
     g.ldb = b.shape[1];
     if (n.in.size() >= 3 && !n.in[2].empty() && g.beta != 0.0f) {
-      const Value& c = in(2);
+      const Value c = in(2);
       if (c.numel() == g.M * g.N) {
         g.c_kind = INFERC_C_FULL;
         g.ldc = g.N;
@@ -539,34 +566,40 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     g.act = int(attr_int(n, "__act", INFERC_ACT_NONE));
     g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, {g.M, g.N}).dev);
     g.ldy = g.N;
-    gemm(ctx, g);
+    if (!dry) {
+      gemm(ctx, g);
+    }
     return;
   }
   if (op == "FusedLayerNorm") {
-    const Value& x = in(0);
+    const Value x = in(0);
     require_f32(x, "X");
     const int64_t feat = x.shape.back();
     IH_REQUIRE(in(1).numel() == feat && in(2).numel() == feat, INFERC_ERR_SHAPE,
                "LayerNorm: scale/bias size mismatch with feature dim");
     const float eps = attr_float(n, "epsilon", 1e-5f);
     float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, x.shape).dev);
-    layernorm(ctx, x.numel() / feat, feat, static_cast<const float*>(dev_of(n.in[0])), nullptr,
-              static_cast<const float*>(dev_of(n.in[1])),
-              static_cast<const float*>(dev_of(n.in[2])), eps, y);
+    if (!dry) {
+      layernorm(ctx, x.numel() / feat, feat, static_cast<const float*>(dev_of(n.in[0])), nullptr,
+                static_cast<const float*>(dev_of(n.in[1])),
+                static_cast<const float*>(dev_of(n.in[2])), eps, y);
+    }
     return;
   }
   if (op == "Gelu" || op == "GeluTanh" || op == "Relu") {
-    const Value& x = in(0);
+    const Value x = in(0);
     require_f32(x, "X");
     const int act = op == "Gelu" ? INFERC_ACT_GELU_ERF
                     : op == "GeluTanh" ? INFERC_ACT_GELU_TANH
                                        : INFERC_ACT_RELU;
     float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, x.shape).dev);
-    activation(ctx, x.numel(), static_cast<const float*>(dev_of(n.in[0])), act, y);
+    if (!dry) {
+      activation(ctx, x.numel(), static_cast<const float*>(dev_of(n.in[0])), act, y);
+    }
     return;
   }
   if (op == "Softmax") {
-    const Value& x = in(0);
+    const Value x = in(0);
     require_f32(x, "X");
     int64_t axis = attr_int(n, "axis", -1);
     const int64_t r = int64_t(x.shape.size());
@@ -576,14 +609,16 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     for (int64_t i = 0; i < axis; ++i) outer *= x.shape[size_t(i)];
     for (int64_t i = axis + 1; i < r; ++i) inner *= x.shape[size_t(i)];
     float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, x.shape).dev);
-    IH_REQUIRE(inferc_hip_softmax_f32(ctx, outer, x.shape[size_t(axis)], inner,
-                                      static_cast<const float*>(dev_of(n.in[0])), y) == 0,
-               INFERC_ERR_HIP, inferc_hip_last_error());
+    if (!dry) {
+      IH_REQUIRE(inferc_hip_softmax_f32(ctx, outer, x.shape[size_t(axis)], inner,
+                                        static_cast<const float*>(dev_of(n.in[0])), y) == 0,
+                 INFERC_ERR_HIP, inferc_hip_last_error());
+    }
     return;
   }
   if (op == "Add") {
-    const Value& a0 = in(0);
-    const Value& b0 = in(1);
+    const Value a0 = in(0);
+    const Value b0 = in(1);
     if (a0.host && b0.host && a0.dtype == INFERC_DT_I64 && b0.dtype == INFERC_DT_I64 &&
         b0.numel() == 1) {
       std::vector<int64_t> r = host_i64(a0, "Add");
@@ -598,8 +633,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     const bool swap = b0.numel() > a0.numel();
     const std::string& an = swap ? n.in[1] : n.in[0];
     const std::string& bn = swap ? n.in[0] : n.in[1];
-    const Value& a = get(an);
-    const Value& b = get(bn);
+    const Value a = get(an);
+    const Value b = get(bn);
     IH_REQUIRE(b.numel() == a.numel() || suffix_broadcast(a.shape, b.shape), INFERC_ERR_UNSUPPORTED,
                "Add: only suffix broadcasts are supported, got " + shape_str(a.shape) + " + " +
                    shape_str(b.shape));
@@ -610,24 +645,28 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
     // y = a + b elementwise is commutative in IEEE arithmetic, so swapping the
     // operands for the broadcast does not change any result bit.
-    add_bcast(ctx, a.numel(), ap, bp, b.numel(), y);
+    if (!dry) {
+      add_bcast(ctx, a.numel(), ap, bp, b.numel(), y);
+    }
     return;
   }
   if (op == "Equal") {
-    const Value& a = in(0);
-    const Value& b = in(1);
+    const Value a = in(0);
+    const Value b = in(1);
     IH_REQUIRE(a.dtype == INFERC_DT_I64 && b.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED,
                "Equal: int64 operands only");
     IH_REQUIRE(b.numel() == a.numel() || b.numel() == 1 || suffix_broadcast(a.shape, b.shape),
                INFERC_ERR_UNSUPPORTED, "Equal: unsupported broadcast");
     uint8_t* y = static_cast<uint8_t*>(make_dev(n.out[0], INFERC_DT_BOOL, a.shape).dev);
-    equal_i64(ctx, a.numel(), static_cast<const int64_t*>(dev_of(n.in[0])),
-              static_cast<const int64_t*>(dev_of(n.in[1])), b.numel(), y);
+    if (!dry) {
+      equal_i64(ctx, a.numel(), static_cast<const int64_t*>(dev_of(n.in[0])),
+                static_cast<const int64_t*>(dev_of(n.in[1])), b.numel(), y);
+    }
     return;
   }
   if (op == "Gather") {
-    const Value& data = in(0);
-    const Value& idx = in(1);
+    const Value data = in(0);
+    const Value idx = in(1);
     int64_t axis = attr_int(n, "axis", 0);
     const int64_t r = int64_t(data.shape.size());
     if (axis < 0) axis += r;
@@ -658,8 +697,10 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     if (axis == 0 && !idx.host) {
       IH_REQUIRE(idx.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED,
                  "Gather: device indices must be int64");
-      gather_rows(ctx, ad, inner, dp, static_cast<const int64_t*>(dev_of(n.in[1])), idx.numel(), y,
-                  nullptr);
+      if (!dry) {
+        gather_rows(ctx, ad, inner, dp, static_cast<const int64_t*>(dev_of(n.in[1])), idx.numel(), y,
+                    nullptr);
+      }
       return;
     }
     // host-known indices: one strided copy per index
@@ -669,12 +710,14 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       int64_t i = ix[size_t(k)];
       if (i < 0) i += ad;
       IH_REQUIRE(i >= 0 && i < ad, INFERC_ERR_ARG, "Gather: index out of range");
-      copy2d(ctx, y + k * inner, ni * inner, dp + i * inner, ad * inner, inner, outer);
+      if (!dry) {
+        copy2d(ctx, y + k * inner, ni * inner, dp + i * inner, ad * inner, inner, outer);
+      }
     }
     return;
   }
   if (op == "Shape") {
-    const Value& x = in(0);
+    const Value x = in(0);
     std::vector<int64_t> s = x.shape;
     make_host(n.out[0], INFERC_DT_I64, {int64_t(s.size())}, s.data());
     return;
@@ -690,7 +733,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
   }
   if (op == "Unsqueeze" || op == "Squeeze" || op == "Reshape" || op == "Identity" ||
       op == "Flatten") {
-    const Value& x = in(0);
+    const Value x = in(0);
     std::vector<int64_t> s = x.shape;
     if (op == "Unsqueeze" || op == "Squeeze") {
       std::vector<int64_t> axes =
@@ -739,7 +782,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "Split") {
-    const Value& x = in(0);
+    const Value x = in(0);
     require_f32(x, "X");
     int64_t axis = attr_int(n, "axis", 0);
     const int64_t r = int64_t(x.shape.size());
@@ -762,15 +805,17 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       outs.push_back(static_cast<float*>(make_dev(n.out[i], INFERC_DT_F32, s).dev));
     }
     IH_REQUIRE(outs.size() == sizes.size(), INFERC_ERR_ARG, "Split: fewer outputs than parts");
-    IH_REQUIRE(inferc_hip_split_f32(ctx, outer, x.shape[size_t(axis)], inner,
-                                    int64_t(sizes.size()), sizes.data(),
-                                    static_cast<const float*>(dev_of(n.in[0])), outs.data()) == 0,
-               INFERC_ERR_SHAPE, inferc_hip_last_error());
+    if (!dry) {
+      IH_REQUIRE(inferc_hip_split_f32(ctx, outer, x.shape[size_t(axis)], inner,
+                                      int64_t(sizes.size()), sizes.data(),
+                                      static_cast<const float*>(dev_of(n.in[0])), outs.data()) == 0,
+                 INFERC_ERR_SHAPE, inferc_hip_last_error());
+    }
     return;
   }
   if (op == "Concat") {
     int64_t axis = attr_int(n, "axis", 0);
-    const Value& x0 = in(0);
+    const Value x0 = in(0);
     const int64_t r = int64_t(x0.shape.size());
     if (axis < 0) axis += r;
     IH_REQUIRE(axis >= 0 && axis < r, INFERC_ERR_ARG, "Concat: axis out of range");
@@ -778,7 +823,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     os[size_t(axis)] = 0;
     std::vector<int64_t> sizes;
     for (size_t i = 0; i < n.in.size(); ++i) {
-      const Value& p = in(i);
+      const Value p = in(i);
       IH_REQUIRE(p.shape.size() == x0.shape.size() && p.dtype == x0.dtype, INFERC_ERR_SHAPE,
                  "Concat: rank/dtype mismatch");
       for (int64_t d = 0; d < r; ++d)
@@ -806,9 +851,11 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     std::vector<const float*> parts;
     for (size_t i = 0; i < n.in.size(); ++i) parts.push_back(static_cast<const float*>(dev_of(n.in[i])));
     float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
-    IH_REQUIRE(inferc_hip_concat_f32(ctx, outer, inner, int64_t(parts.size()), sizes.data(),
-                                     parts.data(), y) == 0,
-               INFERC_ERR_SHAPE, inferc_hip_last_error());
+    if (!dry) {
+      IH_REQUIRE(inferc_hip_concat_f32(ctx, outer, inner, int64_t(parts.size()), sizes.data(),
+                                       parts.data(), y) == 0,
+                 INFERC_ERR_SHAPE, inferc_hip_last_error());
+    }
     return;
   }
   fail(INFERC_ERR_UNSUPPORTED, "Executor: unsupported op '" + op + "' (node: " + n.name + ")");
@@ -817,7 +864,14 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
 void inferc_executor::walk() {
   vals = inits;
   for (auto& kv : inputs) vals[kv.first] = kv.second.v;
-  for (const auto& n : nodes) exec_node(n);
+  for (const auto& n : nodes) {
+    try {
+      exec_node(n);
+    } catch (ih::Error& e) {
+      e.msg += " [node '" + n.name + "', op " + n.op + "]";
+      throw;
+    }
+  }
   for (const auto& o : outputs) get(o);  // every graph output must exist
 }
 
@@ -832,6 +886,10 @@ std::string inferc_executor::signature() const {
 }
 
 void inferc_executor::run() {
+  if (dry) {
+    walk();
+    return;
+  }
   ctx->make_current();
   // stage host inputs into their device buffers (outside any graph)
   for (auto& kv : inputs) {
@@ -882,8 +940,8 @@ inferc_graph* check_graph(inferc_graph* g) {
 }
 
 inferc_executor* check_ex(inferc_executor* ex) {
-  IH_REQUIRE(ex != nullptr && ex->ctx != nullptr, INFERC_ERR_ARG, "null executor");
-  ex->ctx->make_current();
+  IH_REQUIRE(ex != nullptr && (ex->dry || ex->ctx != nullptr), INFERC_ERR_ARG, "null executor");
+  if (!ex->dry) ex->ctx->make_current();
   return ex;
 }
 
@@ -987,10 +1045,39 @@ int inferc_executor_create(inferc_hip_ctx* ctx, const inferc_graph* g, inferc_ex
   });
 }
 
+int inferc_executor_create_dry(const inferc_graph* g, inferc_executor** out) {
+  return ih::guard([&] {
+    IH_REQUIRE(g != nullptr && out != nullptr, INFERC_ERR_ARG, "null argument");
+    *out = nullptr;
+    auto ex = std::make_unique<inferc_executor>();
+    ex->dry = true;
+    ex->graph_mode = false;
+    ex->nodes = g->nodes;
+    ex->outputs = g->outputs;
+    for (const auto& in : g->inits) {
+      ih::Value v;
+      v.dtype = in.dtype;
+      v.shape = in.shape;
+      v.host = std::make_shared<std::vector<uint8_t>>(in.data);
+      v.dev = ex->fake_ptr(in.data.size());
+      ex->inits[in.name] = v;
+    }
+    ex->peephole();
+    *out = ex.release();
+  });
+}
+
+int inferc_executor_node_count(inferc_executor* ex, int* count) {
+  return ih::guard([&] {
+    IH_REQUIRE(ex != nullptr && count != nullptr, INFERC_ERR_ARG, "null argument");
+    *count = int(ex->nodes.size());
+  });
+}
+
 int inferc_executor_destroy(inferc_executor* ex) {
   return ih::guard([&] {
     if (!ex) return;
-    if (ex->ctx) {
+    if (ex->ctx && !ex->dry) {
       ex->ctx->make_current();
       (void)hipStreamSynchronize(ex->ctx->stream);
     }
@@ -1007,7 +1094,9 @@ int inferc_executor_set_input(inferc_executor* ex, const char* name, int dtype, 
     std::vector<int64_t> s = read_shape(rank, shape);
     const size_t bytes = size_t(ih::numel_of(s)) * ih::dtype_size(dtype);
     IH_REQUIRE(bytes == 0 || host_data != nullptr, INFERC_ERR_ARG, "null input data");
-    if (!in.from_host || in.v.bytes() != bytes) {
+    if (ex->dry) {
+      in.v.dev = ex->fake_ptr(bytes);
+    } else if (!in.from_host || in.v.bytes() != bytes) {
       if (in.from_host && in.v.dev) {
         IH_HIP(hipStreamSynchronize(ex->ctx->stream));
         IH_HIP(hipFree(in.v.dev));
@@ -1030,7 +1119,7 @@ int inferc_executor_set_input_device(inferc_executor* ex, const char* name, int 
     check_ex(ex);
     IH_REQUIRE(name != nullptr, INFERC_ERR_ARG, "null input name");
     inferc_executor::Input& in = ex->inputs[name];
-    if (in.from_host && in.v.dev) {
+    if (in.from_host && in.v.dev && !ex->dry) {
       IH_HIP(hipStreamSynchronize(ex->ctx->stream));
       IH_HIP(hipFree(in.v.dev));
     }
@@ -1067,6 +1156,7 @@ int inferc_executor_get_output(inferc_executor* ex, const char* name, void* host
   return ih::guard([&] {
     check_ex(ex);
     IH_REQUIRE(name && host_dst, INFERC_ERR_ARG, "null argument");
+    IH_REQUIRE(!ex->dry, INFERC_ERR_STATE, "a dry-run executor has no output data");
     const ih::Value& v = ex->get(name);
     IH_REQUIRE(capacity_bytes >= v.bytes(), INFERC_ERR_ARG, "output buffer too small");
     IH_HIP(hipStreamSynchronize(ex->ctx->stream));

@@ -89,6 +89,8 @@ _SIGS = {
     "inferc_graph_add_output": [vp, C.c_char_p],
     "inferc_executor_create": [vp, vp, P(vp)],
     "inferc_executor_destroy": [vp],
+    "inferc_executor_create_dry": [vp, P(vp)],
+    "inferc_executor_node_count": [vp, P(i32)],
     "inferc_executor_set_input": [vp, C.c_char_p, i32, i32, P(i64), vp],
     "inferc_executor_set_input_device": [vp, C.c_char_p, i32, i32, P(i64), vp],
     "inferc_executor_run": [vp],

@@ -29,6 +29,12 @@ _NP2DT = {
 _DT2NP = {v: k for k, v in _NP2DT.items()}
 
 
+def _c_order(arr, dtype=None) -> np.ndarray:
+    """C-contiguous view/copy that keeps 0-d arrays 0-d (np.ascontiguousarray
+    would promote a scalar to shape (1,))."""
+    return np.asarray(arr, dtype=dtype, order="C")
+
+
 def _i64_array(vals: Sequence[int]):
     arr = (C.c_int64 * max(1, len(vals)))(*vals)
     return arr
@@ -121,7 +127,7 @@ class Tensor:
 
     @staticmethod
     def from_numpy(ctx: Context, arr) -> "Tensor":
-        a = np.ascontiguousarray(arr)
+        a = _c_order(arr)
         t = Tensor(ctx, a.shape, a.dtype)
         if a.nbytes:
             check(ctx._lib.inferc_hip_h2d(ctx.handle, t.ptr, a.ctypes.data, a.nbytes))
@@ -522,7 +528,7 @@ class Graph:
         self.op_types: list[str] = []
 
     def add_initializer(self, name: str, arr: np.ndarray) -> None:
-        a = np.ascontiguousarray(arr)
+        a = _c_order(arr)
         dt = _NP2DT[a.dtype]
         shape = _i64_array(list(a.shape))
         check(self._lib.inferc_graph_add_initializer(self.handle, name.encode(), dt, a.ndim, shape,
@@ -560,20 +566,50 @@ class Graph:
             pass
 
 
-class Executor:
-    """rt::Executor (src/runtime/executor.h:24-41) on the device."""
+class _NoDevice:
+    """Stands in for a Context in a dry-run executor (no device calls)."""
 
-    def __init__(self, ctx: Context, graph: Graph):
+    def __init__(self):
+        self._lib = L.load_library()
+        self.handle = None
+
+
+class Executor:
+    """rt::Executor (src/runtime/executor.h:24-41) on the device.
+
+    ``Executor.dry(graph)`` builds a device-free executor whose run() only
+    plans: shape inference, host shape plumbing and peephole fusion."""
+
+    def __init__(self, ctx: Context, graph: Graph, _dry: bool = False):
         self.ctx = ctx
         h = C.c_void_p()
-        check(ctx._lib.inferc_executor_create(ctx.handle, graph.handle, C.byref(h)))
+        if _dry:
+            check(ctx._lib.inferc_executor_create_dry(graph.handle, C.byref(h)))
+        else:
+            check(ctx._lib.inferc_executor_create(ctx.handle, graph.handle, C.byref(h)))
         self.handle = h.value
+
+    @classmethod
+    def dry(cls, graph: Graph) -> "Executor":
+        return cls(_NoDevice(), graph, _dry=True)
+
+    def node_count(self) -> int:
+        n = C.c_int()
+        check(self.ctx._lib.inferc_executor_node_count(self.handle, C.byref(n)))
+        return n.value
+
+    def output_shape(self, name: str) -> tuple[tuple[int, ...], np.dtype]:
+        dt, rank = C.c_int(), C.c_int()
+        shape = (C.c_int64 * 8)()
+        check(self.ctx._lib.inferc_executor_output_info(self.handle, name.encode(), C.byref(dt),
+                                                        C.byref(rank), shape))
+        return tuple(shape[i] for i in range(rank.value)), _DT2NP[dt.value]
 
     def set_graph_mode(self, enabled: bool) -> None:
         check(self.ctx._lib.inferc_executor_set_graph_mode(self.handle, int(enabled)))
 
     def set_input(self, name: str, arr: np.ndarray) -> None:
-        a = np.ascontiguousarray(arr)
+        a = _c_order(arr)
         check(self.ctx._lib.inferc_executor_set_input(
             self.handle, name.encode(), _NP2DT[a.dtype], a.ndim, _i64_array(list(a.shape)),
             a.ctypes.data if a.nbytes else None))
@@ -630,7 +666,7 @@ class Gpt2Decoder:
     def __init__(self, ctx: Context, cfg: dict, weights: Sequence[np.ndarray], max_t: int):
         self.ctx = ctx
         self.cfg = cfg
-        self._w = [np.ascontiguousarray(w, dtype=np.float32) for w in weights]
+        self._w = [_c_order(w, np.float32) for w in weights]
         ptrs = (C.c_void_p * len(self._w))(*[w.ctypes.data for w in self._w])
         c = Gpt2Config(cfg["layers"], cfg["hidden"], cfg["heads"], cfg["ffn"], cfg["vocab"],
                        cfg["max_pos"], cfg["eps"])
@@ -641,7 +677,7 @@ class Gpt2Decoder:
 
     def generate(self, prompt: np.ndarray, max_tokens: int, want_step_ms: bool = False,
                  want_logits: bool = False):
-        p = np.ascontiguousarray(prompt, dtype=np.int64)
+        p = _c_order(prompt, np.int64)
         toks = np.empty(max_tokens, np.int64)
         steps = np.empty(max(1, max_tokens - 1), np.float32) if want_step_ms else None
         logits = np.empty(self.cfg["vocab"], np.float32) if want_logits else None
@@ -654,7 +690,7 @@ class Gpt2Decoder:
         return toks, (steps[:max_tokens - 1] if steps is not None else None), logits
 
     def forward(self, ids: np.ndarray) -> np.ndarray:
-        i = np.ascontiguousarray(ids, dtype=np.int64)
+        i = _c_order(ids, np.int64)
         out = np.empty((i.size, self.cfg["vocab"]), np.float32)
         check(self.ctx._lib.inferc_gpt2_forward(self.handle, i.ctypes.data_as(C.POINTER(C.c_int64)),
                                                 i.size,
