@@ -1,0 +1,387 @@
+#!/usr/bin/env python3
+"""Benchmark of inferc's runtime hot path on one MI355X (gfx950).
+
+Primary metric: "encoder fwd ms (b1,s128) + GPT-2 decode
+ms/token; % MFMA/HBM roofline". `value` is the DistilBERT-shape encoder
+forward latency at batch 1, seq 128 (config 1), one step = one forward of the
+fused graph through the executor, inputs already resident in HBM, replayed as
+a HIP graph, timed with HIP events on the context stream. The same JSON line
+carries the GPT-2 greedy-decode ms/token (config 4), the other configs
+(encoder b=32, FFN+LN, QKV+MHA, int4 GEMV) under "extra", the roofline of the
+dominant kernel of the primary workload, and the CPU oracle timed on this
+host's cores as the CPU baseline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "encoder fwd ms (b1,s128) + GPT-2 decode ms/token; % MFMA/HBM roofline"
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBPS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_executor(ctx, ex, steps: int, warmup: int) -> float:
+    """ms per executor run (graph replay after the first two runs)."""
+    for _ in range(max(warmup, 2)):
+        ex.run_async()
+    ctx.sync()
+    ctx.timer_start()
+    for _ in range(steps):
+        ex.run_async()
+    return ctx.timer_stop() / steps
+
+
+def time_replays(ctx, cap, launches_per_replay: int, total_launches: int) -> float:
+    """ms per launch of a captured sequence, replayed back to back so the
+    GPU, not host submission, sets the pace."""
+    cap.replay()
+    ctx.sync()
+    replays = max(2, total_launches // launches_per_replay)
+    ctx.timer_start()
+    for _ in range(replays):
+        cap.replay()
+    ms = ctx.timer_stop() / (replays * launches_per_replay)
+    cap.close()
+    return ms
+
+
+def encoder_flops(cfg: dict, B: int, S: int) -> float:
+    H, F, L = cfg["hidden"], cfg["ffn"], cfg["layers"]
+    M = B * S
+    per_layer = 2 * M * H * 3 * H + 2 * M * H * H + 4 * M * H * F + 4 * B * S * S * H
+    return float(L * per_layer)
+
+
+def device_inputs(ctx, ex, arrays: dict):
+    from inferc_amd import rt
+
+    keep = []
+    for name, arr in arrays.items():
+        t = rt.Tensor.from_numpy(ctx, arr)
+        ex.set_input_device(name, t)
+        keep.append(t)
+    return keep
+
+
+def bench_encoder(ctx, B: int, steps: int, warmup: int, weights=None):
+    from inferc_amd import graphs, rt
+
+    cfg = graphs.DISTILBERT
+    w = weights if weights is not None else graphs.encoder_weights(cfg, 1)
+    ex = rt.Executor(ctx, graphs.encoder_graph(cfg, w))
+    ids, mask = graphs.encoder_inputs(cfg, B, 128)
+    keep = device_inputs(ctx, ex, {"input_ids": ids, "attention_mask": mask})
+    ms = time_executor(ctx, ex, steps, warmup)
+    out = ex.output("logits")
+    del keep
+    ex.close()
+    return ms, out, w
+
+
+def ffn_ln_graph(M: int, seed: int = 3):
+    """Config 2: LN_{1e-12}(GELU(X W1 + b1) W2 + b2), X [M,768]."""
+    from inferc_amd import graphs, rt
+
+    g = rt.Graph()
+    n = graphs.normal
+    g.add_initializer("w1", n(seed, "w1", (768, 3072)))
+    g.add_initializer("b1", n(seed, "b1", (3072,)))
+    g.add_initializer("w2", n(seed, "w2", (3072, 768)))
+    g.add_initializer("b2", n(seed, "b2", (768,)))
+    g.add_initializer("g", np.ones(768, np.float32))
+    g.add_initializer("b", np.zeros(768, np.float32))
+    g.add_node("FusedMatMulAddGELU", ["x", "w1", "b1"], ["f"])
+    g.add_node("MatMul", ["f", "w2"], ["y_mm"])
+    g.add_node("Add", ["y_mm", "b2"], ["y"])
+    g.add_node("FusedLayerNorm", ["y", "g", "b"], ["out"], epsilon=1e-12)
+    g.add_output("out")
+    x = graphs.normal(seed, f"x{M}", (M, 768), std=1.0)
+    return g, x
+
+
+def qkv_mha_graph(S: int, seed: int = 4):
+    """Config 3: FusedQKV + FusedAttention, B=32, valid length U[16,S]."""
+    from inferc_amd import graphs, rt
+
+    B = 32
+    g = rt.Graph()
+    for i, nm in enumerate(("wq", "wk", "wv")):
+        g.add_initializer(nm, graphs.normal(seed, nm, (768, 768)))
+        g.add_initializer("b" + nm[1], graphs.normal(seed, "b" + nm[1], (768,)))
+    g.add_node("FusedQKV", ["x", "wq", "bq", "wk", "bk", "wv", "bv"], ["q", "k", "v"])
+    g.add_node("FusedAttention", ["q", "k", "v", "mask"], ["ctx"], head_dim=64,
+               fill=graphs.FILL_MIN)
+    g.add_output("ctx")
+    x = graphs.normal(seed, f"x{S}", (B, S, 768), std=1.0)
+    lens = graphs.rng_for(seed, f"lens{S}").integers(16, S + 1, size=B)
+    mask = (np.arange(S)[None, :] >= lens[:, None]).reshape(B, 1, 1, S)
+    return g, x, mask.astype(np.bool_), lens
+
+
+def bench_graph(ctx, g, inputs: dict, steps: int, warmup: int) -> float:
+    from inferc_amd import rt
+
+    ex = rt.Executor(ctx, g)
+    keep = device_inputs(ctx, ex, inputs)
+    ms = time_executor(ctx, ex, steps, warmup)
+    del keep
+    ex.close()
+    return ms
+
+
+def bench_decode(ctx, max_tokens: int = 128, prompt_len: int = 32):
+    from inferc_amd import graphs, rt
+
+    cfg = graphs.GPT2_SMALL
+    w = graphs.gpt2_weights(cfg, 2)
+    dec = rt.Gpt2Decoder(ctx, cfg, w, max_t=prompt_len + max_tokens)
+    prompt = graphs.gpt2_prompt(cfg, prompt_len)
+    # One generate call: the step graph is captured before its first timed
+    # step, and every post-prefill step is timed (main.cpp:863-872).
+    toks, steps, _ = dec.generate(prompt, max_tokens, want_step_ms=True)
+    dec.close()
+    return float(np.mean(steps)), float(np.median(steps)), float(np.min(steps)), toks, w, prompt
+
+
+def gpt2_bytes_per_token(cfg: dict, mean_ctx: float) -> float:
+    H, F, V, L = cfg["hidden"], cfg["ffn"], cfg["vocab"], cfg["layers"]
+    weights = L * (3 * H * H + H * H + 2 * H * F) + V * H
+    small = L * (3 * H + H + F + H + 4 * H) + 2 * H + H * 2  # biases, LN, wpe row
+    kv = L * 2 * H * mean_ctx
+    return 4.0 * (weights + small + kv)
+
+
+def bench_int4(ctx, batch: int, copies: int = 5, reps: int = 200):
+    """Config 5: all 49 GPT-2-small matrices in one grouped launch; `copies`
+    weight sets (>= 316 MB, beyond the 256 MB Infinity Cache) are rotated so
+    every launch streams its weights from HBM."""
+    from inferc_amd import graphs, rt
+
+    shapes = graphs.int4_matrices()
+    sets = []
+    for c in range(copies):
+        mats = []
+        for i, (N, K) in enumerate(shapes):
+            W, s = graphs.int4_weights(N, K, 100 + c, f"b{i}")
+            x = graphs.normal(200 + c, f"x{i}_{batch}", (batch, K), std=1.0)
+            mats.append((rt.Tensor.from_numpy(ctx, W), rt.Tensor.from_numpy(ctx, s),
+                         rt.Tensor.from_numpy(ctx, x), rt.Tensor.empty(ctx, (batch, N)), K))
+        sets.append(mats)
+    for mats in sets:
+        rt.int4_gemv_grouped(ctx, mats, batch)  # uploads + caches each table
+    per_graph = 4 * copies
+    cap = ctx.capture(lambda: [rt.int4_gemv_grouped(ctx, sets[r % copies], batch)
+                               for r in range(per_graph)])
+    ms = time_replays(ctx, cap, per_graph, reps)
+    n_w = sum(N * K for N, K in shapes)
+    n_rows = sum(N for N, _ in shapes)
+    int4_bytes = n_w // 2
+    compulsory = int4_bytes + 4 * n_rows + 4 * batch * sum(K for _, K in shapes) + \
+        4 * batch * n_rows
+    return {"ms": ms, "int4_bytes": int4_bytes, "compulsory_bytes": compulsory,
+            "gbps_compulsory": compulsory / (ms * 1e-3) / 1e9,
+            "gbps_int4_only": int4_bytes / (ms * 1e-3) / 1e9,
+            "hbm_frac": compulsory / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+            "copies_rotated": copies}
+
+
+def roofline_ffn_up_gemm(ctx, reps: int = 200):
+    """Dominant kernel of the primary workload: the FFN-up GEMM with the fused
+    bias + erf-GELU epilogue at the b=1, s=128 shape (M=128, N=3072, K=768),
+    launched through the C-ABI exactly as the executor launches it, timed
+    with HIP events over `reps` back-to-back launches."""
+    from inferc_amd import graphs, rt
+
+    M, N, K = 128, 3072, 768
+    x = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rx", (M, K), 1.0))
+    w = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rw", (K, N)))
+    b = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rb", (N,)))
+    y = rt.Tensor.empty(ctx, (M, N))
+    lib = ctx._lib
+
+    def launch():
+        rc = lib.inferc_hip_fused_matmul_add_gelu_f32(ctx.handle, M, N, K, x.ptr, w.ptr, b.ptr,
+                                                       y.ptr)
+        if rc:
+            from inferc_amd.lib import check
+            check(rc)
+
+    launch()
+    per_graph = 20
+    cap = ctx.capture(lambda: [launch() for _ in range(per_graph)])
+    ms = time_replays(ctx, cap, per_graph, reps)
+    flops = 2.0 * M * N * K
+    achieved = flops / (ms * 1e-3) / 1e12
+    traffic = None
+    tf = ROOT / "profiles" / "traffic.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get("gemm_ffn_up_b1")
+    return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+            "traffic": traffic, "kernel": "gemm_f32_mfma (FusedMatMulAddGELU)",
+            "shape": [M, N, K], "algorithmic_flops_per_launch": flops,
+            "avg_launch_us": round(ms * 1e3, 3)}
+
+
+def cpu_baseline_encoder(weights, budget_s: float = 12.0):
+    import oracle as O
+    from inferc_amd import graphs
+
+    cfg = graphs.DISTILBERT
+    ids, mask = graphs.encoder_inputs(cfg, 1, 128)
+    O.encoder_forward(cfg, weights, ids, mask)  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.encoder_forward(cfg, weights, ids, mask)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 200:
+            break
+    return el / n * 1e3, n, O.num_threads()
+
+
+def cpu_baseline_decode(weights, prompt, tokens: int = 6):
+    import oracle as O
+    from inferc_amd import graphs
+
+    cfg = graphs.GPT2_SMALL
+    t0 = time.perf_counter()
+    O.gpt2_generate(cfg, weights, prompt[:8], 1)
+    prefill = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    O.gpt2_generate(cfg, weights, prompt[:8], tokens + 1)
+    total = time.perf_counter() - t0
+    return (total - prefill) / tokens * 1e3
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="primary workload and roofline only")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "multi-GPU runs are out of scope", file=sys.stderr)
+        return 2
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: launched with WORLD_SIZE > 1; one GPU only", file=sys.stderr)
+        return 2
+
+    from inferc_amd import graphs, rt
+
+    ctx = rt.Context(0)
+    extra = {}
+    log("encoder b1 s128")
+    ms_b1, _, enc_w = bench_encoder(ctx, 1, args.steps, args.warmup)
+    fl_b1 = encoder_flops(graphs.DISTILBERT, 1, 128)
+    extra["encoder_b1_s128"] = {"ms": round(ms_b1, 4), "gflop": round(fl_b1 / 1e9, 3),
+                                "mfma_frac_fp32": round(fl_b1 / (ms_b1 * 1e-3) / 1e12 /
+                                                        PEAK_FP32_TFLOPS, 4)}
+    log(f"  {ms_b1:.4f} ms/forward")
+    log("roofline kernel")
+    roof = roofline_ffn_up_gemm(ctx)
+    log(f"  {roof['avg_launch_us']} us, {roof['achieved']} TFLOP/s")
+
+    dec = None
+    if not args.quick:
+        log("encoder b32 s128")
+        ms_b32, _, _ = bench_encoder(ctx, 32, max(5, args.steps // 5), 2, enc_w)
+        fl_b32 = encoder_flops(graphs.DISTILBERT, 32, 128)
+        extra["encoder_b32_s128"] = {"ms": round(ms_b32, 4), "gflop": round(fl_b32 / 1e9, 2),
+                                     "tflops": round(fl_b32 / (ms_b32 * 1e-3) / 1e12, 2),
+                                     "mfma_frac_fp32": round(fl_b32 / (ms_b32 * 1e-3) / 1e12 /
+                                                             PEAK_FP32_TFLOPS, 4)}
+        log(f"  {ms_b32:.4f} ms/forward")
+        for M in (128, 1024, 4096):
+            g, x = ffn_ln_graph(M)
+            ms = bench_graph(ctx, g, {"x": x}, max(10, args.steps // 2), 3)
+            fl = 4.0 * M * 768 * 3072
+            extra[f"ffn_ln_m{M}"] = {"ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+                                     "mfma_frac_fp32": round(fl / (ms * 1e-3) / 1e12 /
+                                                             PEAK_FP32_TFLOPS, 4)}
+            log(f"  ffn+ln M={M}: {ms:.4f} ms")
+        for S in (128, 512):
+            g, x, mask, _ = qkv_mha_graph(S)
+            ms = bench_graph(ctx, g, {"x": x, "mask": mask}, max(10, args.steps // 2), 3)
+            fl = 2.0 * 32 * S * 768 * 2304 + 4.0 * 32 * 12 * S * S * 64
+            extra[f"qkv_mha_b32_s{S}"] = {"ms": round(ms, 4),
+                                          "tflops_dense": round(fl / (ms * 1e-3) / 1e12, 2),
+                                          "mfma_frac_fp32": round(fl / (ms * 1e-3) / 1e12 /
+                                                                  PEAK_FP32_TFLOPS, 4)}
+            log(f"  qkv+mha S={S}: {ms:.4f} ms")
+        log("gpt2 decode")
+        d_mean, d_p50, d_min, toks, gw, prompt = bench_decode(ctx)
+        bpt = gpt2_bytes_per_token(graphs.GPT2_SMALL, 32 + 64)
+        dec = {"ms_per_token": round(d_mean, 4), "p50": round(d_p50, 4),
+               "min": round(d_min, 4), "tokens_per_s": round(1e3 / d_mean, 1),
+               "prompt": 32, "generated": 128, "timed_steps": 127,
+               "bytes_per_token": int(bpt),
+               "hbm_gbps": round(bpt / (d_mean * 1e-3) / 1e9, 1),
+               "hbm_frac": round(bpt / (d_mean * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+        log(f"  {d_mean:.4f} ms/token")
+        for B in (1, 8):
+            log(f"int4 grouped GEMV B={B}")
+            r = bench_int4(ctx, B)
+            extra[f"int4_gemv_b{B}"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                        for k, v in r.items()}
+            log(f"  {r['ms'] * 1e3:.2f} us, {r['gbps_compulsory']:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle) encoder b1 s128")
+        cms, n, thr = cpu_baseline_encoder(enc_w)
+        cpu = {"value": round(cms, 3), "unit": "ms", "cores": thr, "kind": "port",
+               "sample": f"{n} encoder forwards at b1 s128 (C oracle, OpenMP {thr} threads)"}
+        if dec is not None:
+            cdec = cpu_baseline_decode(gw, prompt)
+            cpu["gpt2_decode_ms_per_token"] = round(cdec, 3)
+            cpu["sample"] += "; GPT-2 decode 6 tokens after an 8-token prompt"
+        log(f"  {cms:.2f} ms/forward on {thr} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": round(ms_b1, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_b1, 4),
+        "higher_is_better": False,
+        "scaling": "strong",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded random-init weights of the DistilBERT / GPT-2-small shapes)",
+        "config": {"workload": "distilbert_encoder_fwd_b1_s128", "batch": 1, "seq_len": 128,
+                   "layers": 6, "hidden": 768, "heads": 12, "ffn": 3072},
+        "gpt2_decode": dec,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

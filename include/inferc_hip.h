@@ -91,6 +91,19 @@ int inferc_hip_sync(inferc_hip_ctx* ctx);
 int inferc_hip_timer_start(inferc_hip_ctx* ctx);
 int inferc_hip_timer_stop(inferc_hip_ctx* ctx, float* ms);
 
+/* Record the kernels of any sequence of entry points on the context stream
+ * into a HIP graph, then replay it with one launch (the reference re-walks
+ * its graph per call; a replay issues the whole sequence at once). Entry
+ * points that would allocate or upload during capture fail with
+ * INFERC_ERR_STATE, so run the sequence once before capturing it. A replay
+ * fails with INFERC_ERR_STATE if the context workspace was reallocated after
+ * the capture. */
+typedef struct inferc_hip_capture inferc_hip_capture;
+int inferc_hip_capture_begin(inferc_hip_ctx* ctx);
+int inferc_hip_capture_end(inferc_hip_ctx* ctx, inferc_hip_capture** out);
+int inferc_hip_capture_replay(inferc_hip_capture* cap);
+int inferc_hip_capture_destroy(inferc_hip_capture* cap);
+
 /* ---------------- dense products ---------------- */
 
 /* ONNX Gemm: Y = act(alpha*op(A)*op(B) + beta*C (+ R)).

@@ -186,6 +186,9 @@ void add_bcast(inferc_hip_ctx* ctx, int64_t n, const float* a, const float* b, i
                float* y);
 void gather_rows(inferc_hip_ctx* ctx, int64_t rows, int64_t row_len, const float* table,
                  const int64_t* idx, int64_t n_idx, float* out, int32_t* err_flag);
+void gather_axis(inferc_hip_ctx* ctx, int64_t outer, int64_t rows, int64_t row_len,
+                 const float* table, const int64_t* idx, int64_t n_idx, float* out,
+                 int32_t* err_flag);
 // `partial` (nullable) is caller-owned scratch of kArgmaxScratchBytes; when
 // null the context workspace is used.
 constexpr size_t kArgmaxScratchBytes = 256 * 16;
@@ -202,5 +205,35 @@ void kv_append_attend(inferc_hip_ctx* ctx, int64_t nH, int64_t D, int64_t T,
 void gemv(inferc_hip_ctx* ctx, int64_t N, int64_t K, const float* W, const float* x,
           const float* ln_g, const float* ln_b, float ln_eps, const float* bias,
           const float* residual, int act, float* y);
+
+// ---- batch-1 decode building blocks ----
+
+// (value, index) partial of an argmax.
+struct ValIdxPart {
+  float v;
+  int64_t i;
+};
+constexpr int kDecChunk = 32;  // keys per chunk of the decode attention
+
+// y = act(W x' + bias + residual) with W [N, K], where x' is x or LN(x).
+// When amax is non-null each block also writes the (max, first index) of
+// its outputs.
+// Returns the number of blocks launched (the size amax needs).
+struct Gemv2Args {
+  int64_t N = 0, K = 0;
+  const float* W = nullptr;
+  const float* x = nullptr;
+  const float* ln_g = nullptr;
+  const float* ln_b = nullptr;
+  float ln_eps = 0.0f;
+  const float* bias = nullptr;
+  const float* res = nullptr;
+  int act = INFERC_ACT_NONE;
+  float* y = nullptr;
+  ValIdxPart* amax = nullptr;
+};
+bool gemv2_supported(int64_t K);
+int64_t gemv2_blocks(inferc_hip_ctx* ctx, int64_t N, int64_t K, bool argmax);
+void gemv2(inferc_hip_ctx* ctx, const Gemv2Args& a);
 
 }  // namespace ih

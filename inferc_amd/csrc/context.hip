@@ -159,6 +159,68 @@ int inferc_hip_sync(inferc_hip_ctx* ctx) {
   });
 }
 
+}  // extern "C"
+
+struct inferc_hip_capture {
+  inferc_hip_ctx* ctx = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  uint64_t ws_generation = 0;
+};
+
+extern "C" {
+
+int inferc_hip_capture_begin(inferc_hip_ctx* ctx) {
+  return ih::guard([&] {
+    ih::check_ctx(ctx)->make_current();
+    IH_REQUIRE(!ctx->capturing, INFERC_ERR_STATE, "a capture is already in progress");
+    IH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+  });
+}
+
+int inferc_hip_capture_end(inferc_hip_ctx* ctx, inferc_hip_capture** out) {
+  return ih::guard([&] {
+    ih::check_ctx(ctx)->make_current();
+    IH_REQUIRE(out != nullptr, INFERC_ERR_ARG, "null output pointer");
+    *out = nullptr;
+    IH_REQUIRE(ctx->capturing, INFERC_ERR_STATE, "no capture in progress");
+    ctx->capturing = false;
+    auto* c = new inferc_hip_capture();
+    c->ctx = ctx;
+    c->ws_generation = ctx->ws_generation;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &c->graph);
+    if (e == hipSuccess) e = hipGraphInstantiate(&c->exec, c->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+      if (c->graph) (void)hipGraphDestroy(c->graph);
+      delete c;
+      ih::fail(INFERC_ERR_HIP, std::string("capture: ") + hipGetErrorString(e));
+    }
+    *out = c;
+  });
+}
+
+int inferc_hip_capture_replay(inferc_hip_capture* cap) {
+  return ih::guard([&] {
+    IH_REQUIRE(cap != nullptr && cap->exec != nullptr, INFERC_ERR_ARG, "null capture");
+    cap->ctx->make_current();
+    IH_REQUIRE(cap->ws_generation == cap->ctx->ws_generation, INFERC_ERR_STATE,
+               "the context workspace was reallocated after this capture; capture again");
+    IH_HIP(hipGraphLaunch(cap->exec, cap->ctx->stream));
+  });
+}
+
+int inferc_hip_capture_destroy(inferc_hip_capture* cap) {
+  return ih::guard([&] {
+    if (!cap) return;
+    cap->ctx->make_current();
+    (void)hipStreamSynchronize(cap->ctx->stream);
+    if (cap->exec) (void)hipGraphExecDestroy(cap->exec);
+    if (cap->graph) (void)hipGraphDestroy(cap->graph);
+    delete cap;
+  });
+}
+
 int inferc_hip_timer_start(inferc_hip_ctx* ctx) {
   return ih::guard([&] {
     ih::check_ctx(ctx)->make_current();

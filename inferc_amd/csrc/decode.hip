@@ -114,6 +114,168 @@ __global__ __launch_bounds__(kBlock) void kv_append_attend_kernel(KvP p) {
   }
 }
 
+// Decode attention for head_dim 64, one block (4 waves) per head. The block
+// appends the token's K/V at *pos, then wave w walks key chunks w, w+4, ...
+// of 32 keys. For a chunk every K and V load is issued before any is used
+// (indices past the last key are clamped to it and weighted by 0), so a
+// chunk costs one memory round trip. Per chunk: s_j = (q . k_j) / sqrt(64)
+// (the with-past graph's MatMul -> Div), m = max s_j, e_j = exp(s_j - m),
+// l = sum e_j, O = sum e_j v_j; chunks are merged online within a wave and
+// the four waves through LDS in wave order; out = O / L.
+struct AttnDecP {
+  int64_t T;
+  const int64_t* pos;
+  const float* q;
+  const float* k_new;
+  const float* v_new;
+  float* kc;
+  float* vc;
+  float* out;
+};
+
+constexpr int kDecWaves = 4;
+
+__global__ __launch_bounds__(64 * kDecWaves) void attn_decode_d64(AttnDecP p) {
+  constexpr int D = 64;
+  __shared__ float sm[kDecWaves], sl[kDecWaves];
+  __shared__ float so[kDecWaves][D];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t h = blockIdx.x;
+  const int64_t pos = *p.pos;
+  if (pos < 0 || pos >= p.T) return;  // uniform: the host keeps pos < T
+  const int64_t t = pos + 1;
+  float* kc = p.kc + h * p.T * D;
+  float* vc = p.vc + h * p.T * D;
+  const float* kn = p.k_new + h * D;
+  const float* vn = p.v_new + h * D;
+  if (wave == 0) {
+    // Rows of position pos are read from kn/vn below, never from the cache,
+    // so this append needs no barrier.
+    kc[pos * D + lane] = kn[lane];
+    vc[pos * D + lane] = vn[lane];
+  }
+  const int dh = (lane & 1) * 32;
+  float4 qv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) qv[i] = *reinterpret_cast<const float4*>(p.q + h * D + dh + 4 * i);
+  const float rs = sqrtf(float(D));
+  float M = -INFINITY, L = 0.0f, O = 0.0f;
+  for (int64_t j0 = int64_t(wave) * kDecChunk; j0 < t; j0 += kDecWaves * kDecChunk) {
+    const int64_t jl = j0 + (lane >> 1);
+    const int64_t jc = jl < t ? jl : t - 1;
+    const float* kr = (jc == pos) ? kn : kc + jc * D;
+    float4 kv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kv[i] = *reinterpret_cast<const float4*>(kr + dh + 4 * i);
+    float vv[kDecChunk];
+#pragma unroll
+    for (int k = 0; k < kDecChunk; ++k) {
+      const int64_t jv = (j0 + k < t) ? j0 + k : t - 1;
+      vv[k] = ((jv == pos) ? vn : vc + jv * D)[lane];
+    }
+    float dot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      dot += qv[i].x * kv[i].x + qv[i].y * kv[i].y + qv[i].z * kv[i].z + qv[i].w * kv[i].w;
+    dot += __shfl_xor(dot, 1, 64);
+    const float s = (jl < t) ? dot / rs : -INFINITY;
+    const float m = wave_max(s);
+    const float e = (jl < t) ? expf(s - m) : 0.0f;
+    const float l = wave_sum((lane & 1) ? 0.0f : e);
+    float o = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kDecChunk; ++k) o += __shfl(e, 2 * k, 64) * vv[k];
+    const float Mn = fmaxf(M, m);
+    const float a = expf(M - Mn), b = expf(m - Mn);
+    L = L * a + l * b;
+    O = O * a + o * b;
+    M = Mn;
+  }
+  if (lane == 0) {
+    sm[wave] = M;
+    sl[wave] = L;
+  }
+  so[wave][lane] = O;
+  __syncthreads();
+  if (wave == 0) {
+    float Mx = sm[0];
+    for (int w = 1; w < kDecWaves; ++w) Mx = fmaxf(Mx, sm[w]);
+    float Lt = 0.0f, Ot = 0.0f;
+    for (int w = 0; w < kDecWaves; ++w) {
+      const float c = expf(sm[w] - Mx);
+      Lt += c * sl[w];
+      Ot += c * so[w][lane];
+    }
+    p.out[h * D + lane] = Ot / Lt;
+  }
+}
+
+// The decode step's tail, one block of 1024 threads: merges the LM-head
+// blocks' (max logit, first index) partials (the strict '>' rule of
+// main.cpp:875-879), records tokens[pos+1], advances state = {pos+1, tok,
+// tok}, and writes the next step's input h = wte[tok] + wpe[pos+1]. Each
+// thread loads all of its partials before merging them (one memory round
+// trip instead of one per partial).
+constexpr int kFinishThreads = 1024;
+constexpr int kFinishPerThread = 8;  // up to 8192 partials
+
+__global__ __launch_bounds__(kFinishThreads) void decode_finish_kernel(
+    const ValIdxPart* __restrict__ parts, int n, int64_t* __restrict__ state,
+    int64_t* __restrict__ tokens, const float* __restrict__ wte, const float* __restrict__ wpe,
+    float* __restrict__ h, int64_t H, int64_t max_pos) {
+  __shared__ float sv[kFinishThreads / 64];
+  __shared__ int64_t si[kFinishThreads / 64];
+  __shared__ int64_t s_tok, s_pos;
+  ValIdxPart q[kFinishPerThread];
+#pragma unroll
+  for (int k = 0; k < kFinishPerThread; ++k) {
+    const int e = threadIdx.x + k * kFinishThreads;
+    q[k] = e < n ? parts[e] : ValIdxPart{-INFINITY, INT64_MAX};
+  }
+  float v = -INFINITY;
+  int64_t i = INT64_MAX;
+#pragma unroll
+  for (int k = 0; k < kFinishPerThread; ++k)
+    if (q[k].v > v || (q[k].v == v && q[k].i < i)) {
+      v = q[k].v;
+      i = q[k].i;
+    }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float w = __shfl_xor(v, o, 64);
+    const int64_t j = __shfl_xor(i, o, 64);
+    if (w > v || (w == v && j < i)) {
+      v = w;
+      i = j;
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = v;
+    si[wave] = i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kFinishThreads / 64; ++w)
+      if (sv[w] > v || (sv[w] == v && si[w] < i)) {
+        v = sv[w];
+        i = si[w];
+      }
+    const int64_t tok = (i == INT64_MAX) ? 0 : i;
+    const int64_t pos = state[0];
+    tokens[pos + 1] = tok;
+    state[2] = tok;
+    state[1] = tok;
+    state[0] = pos + 1;
+    s_tok = tok;
+    s_pos = pos + 1;
+  }
+  __syncthreads();
+  if (s_pos < max_pos)
+    for (int64_t c = threadIdx.x; c < H; c += kFinishThreads)
+      h[c] = wte[s_tok * H + c] + wpe[s_pos * H + c];
+}
+
 // h[c] = wte[tok][c] + wpe[pos][c] with (pos, tok) = (state[0], state[1]).
 __global__ __launch_bounds__(kBlock) void embed_step_kernel(const float* __restrict__ wte,
                                                             const float* __restrict__ wpe,
@@ -178,6 +340,13 @@ void kv_append_attend(inferc_hip_ctx* ctx, int64_t nH, int64_t D, int64_t T,
              "kv_append_attend: null pointer");
   IH_REQUIRE(aligned16(q) && aligned16(k_new) && aligned16(kc) && aligned16(vc),
              INFERC_ERR_ARG, "kv_append_attend: pointers must be 16-byte aligned");
+  if (D == 64) {
+    AttnDecP ap{T, pos, q, k_new, v_new, kc, vc, out};
+    hipLaunchKernelGGL(attn_decode_d64, dim3(unsigned(nH)), dim3(64 * kDecWaves), 0, ctx->stream,
+                       ap);
+    check_launch("attn_decode");
+    return;
+  }
   KvP p{nH, D, T, pos, q, k_new, v_new, kc, vc, out};
   hipLaunchKernelGGL(kv_append_attend_kernel, dim3(unsigned(nH)), dim3(kBlock),
                      size_t(T) * sizeof(float), ctx->stream, p);
@@ -206,6 +375,8 @@ struct inferc_gpt2 {
   int64_t* state = nullptr;   // [0] pos of the next input token, [1] that token, [2] argmax
   int64_t* tokens = nullptr;  // [max_t + 1]
   void* argmax_ws = nullptr;  // model-owned, so the captured step never uses ctx->ws
+  ih::ValIdxPart* amax = nullptr;  // LM-head block partials of the argmax
+  int64_t amax_n = 0;
   int64_t* ids = nullptr;     // [max_t]
   float *ph = nullptr, *pa = nullptr, *pqkv = nullptr, *patt = nullptr, *pf = nullptr;
   hipGraphExec_t step_exec = nullptr;
@@ -248,34 +419,67 @@ struct inferc_gpt2 {
   float* kc_l(int64_t l) const { return kc + l * cfg.heads * max_t * D(); }
   float* vc_l(int64_t l) const { return vc + l * cfg.heads * max_t * D(); }
 
-  // One decode step for the token in state[1] at position state[0].
+  // GPT-2-small dimensions take the short-chain kernels (register-resident
+  // x, split-KV attention, argmax fused into the LM head); other shapes use
+  // the general GEMV / attention kernels.
+  bool fast() const {
+    return D() == 64 && H() == 768 && ih::gemv2_supported(cfg.ffn);
+  }
+
+  // One decode step for the token in state[1] at position state[0]. On the
+  // fast path the step's input embedding h was written by the previous
+  // step's LM-head tail (or the prefill's), so the step starts with layer 0.
   void enqueue_step() {
     hipStream_t s = ctx->stream;
-    const int64_t Hh = H(), F = cfg.ffn, V = cfg.vocab;
-    hipLaunchKernelGGL(ih::embed_step_kernel, dim3(unsigned(ih::ceil_div(Hh, ih::kBlock))),
-                       dim3(ih::kBlock), 0, s, wte, wpe, state, Hh, h);
-    ih::check_launch("embed_step");
+    const int64_t Hh = H(), F = cfg.ffn;
+    if (!fast()) {
+      hipLaunchKernelGGL(ih::embed_step_kernel, dim3(unsigned(ih::ceil_div(Hh, ih::kBlock))),
+                         dim3(ih::kBlock), 0, s, wte, wpe, state, Hh, h);
+      ih::check_launch("embed_step");
+    }
     for (int64_t l = 0; l < cfg.layers; ++l) {
       const Layer& L = layers[size_t(l)];
       ih::gemv(ctx, 3 * Hh, Hh, L.attn_w, h, L.ln1_g, L.ln1_b, cfg.eps, L.attn_b, nullptr,
                INFERC_ACT_NONE, qkv);
-      ih::kv_append_attend(ctx, cfg.heads, D(), max_t, state, qkv, qkv + Hh, qkv + 2 * Hh,
-                           kc_l(l), vc_l(l), att);
-      ih::gemv(ctx, Hh, Hh, L.proj_w, att, nullptr, nullptr, 0.0f, L.proj_b, h, INFERC_ACT_NONE,
-               h);
+      if (fast()) {
+        ih::AttnDecP ap{max_t, state, qkv, qkv + Hh, qkv + 2 * Hh, kc_l(l), vc_l(l), att};
+        hipLaunchKernelGGL(ih::attn_decode_d64, dim3(unsigned(cfg.heads)),
+                           dim3(64 * ih::kDecWaves), 0, s, ap);
+        ih::check_launch("attn_decode");
+        ih::gemv(ctx, Hh, Hh, L.proj_w, att, nullptr, nullptr, 0.0f, L.proj_b, h,
+                 INFERC_ACT_NONE, h);
+      } else {
+        ih::kv_append_attend(ctx, cfg.heads, D(), max_t, state, qkv, qkv + Hh, qkv + 2 * Hh,
+                             kc_l(l), vc_l(l), att);
+        ih::gemv(ctx, Hh, Hh, L.proj_w, att, nullptr, nullptr, 0.0f, L.proj_b, h,
+                 INFERC_ACT_NONE, h);
+      }
       ih::gemv(ctx, F, Hh, L.fc_w, h, L.ln2_g, L.ln2_b, cfg.eps, L.fc_b, nullptr,
                INFERC_ACT_GELU_TANH, f);
       ih::gemv(ctx, Hh, F, L.fcproj_w, f, nullptr, nullptr, 0.0f, L.fcproj_b, h, INFERC_ACT_NONE,
                h);
     }
-    ih::gemv(ctx, V, Hh, wte, h, lnf_g, lnf_b, cfg.eps, nullptr, nullptr, INFERC_ACT_NONE,
-             logits);
-    finish_token();
+    lm_head_finish(h);
   }
 
-  // argmax of `logits` -> tokens[state[0]+1], state advanced by one position.
-  void finish_token() {
-    ih::argmax(ctx, cfg.vocab, logits, state + 2, argmax_ws);
+  // Final LN + LM head on one hidden row, then the greedy token:
+  // tokens[state[0]+1] = argmax (first max), state advanced by one position.
+  void lm_head_finish(const float* hrow) {
+    const int64_t Hh = H(), V = cfg.vocab;
+    if (fast()) {
+      ih::Gemv2Args a;
+      a.N = V; a.K = Hh; a.W = wte; a.x = hrow; a.ln_g = lnf_g; a.ln_b = lnf_b;
+      a.ln_eps = cfg.eps; a.y = logits; a.amax = amax;
+      ih::gemv2(ctx, a);
+      hipLaunchKernelGGL(ih::decode_finish_kernel, dim3(1), dim3(ih::kFinishThreads), 0,
+                         ctx->stream, amax, int(amax_n), state, tokens, wte, wpe, h, Hh,
+                         cfg.max_pos);
+      ih::check_launch("decode_finish");
+      return;
+    }
+    ih::gemv(ctx, V, Hh, wte, hrow, lnf_g, lnf_b, cfg.eps, nullptr, nullptr, INFERC_ACT_NONE,
+             logits);
+    ih::argmax(ctx, V, logits, state + 2, argmax_ws);
     hipLaunchKernelGGL(ih::advance_state_kernel, dim3(1), dim3(64), 0, ctx->stream, state,
                        tokens);
     ih::check_launch("advance_state");
@@ -439,6 +643,10 @@ int inferc_gpt2_create(inferc_hip_ctx* ctx, const inferc_gpt2_config* cfg,
       m->state = m->alloc<int64_t>(4);
       m->tokens = m->alloc<int64_t>(size_t(max_t + 1));
       m->argmax_ws = m->alloc<uint8_t>(ih::kArgmaxScratchBytes);
+      m->amax_n = ih::gemv2_blocks(ctx, V, H, true);
+      m->amax = m->alloc<ih::ValIdxPart>(size_t(m->amax_n));
+      IH_REQUIRE(m->amax_n <= ih::kFinishThreads * ih::kFinishPerThread, INFERC_ERR_UNSUPPORTED,
+                 "gpt2_create: vocabulary too large for the argmax tail");
       m->ids = m->alloc<int64_t>(size_t(max_t));
       m->ph = m->alloc<float>(size_t(max_t * H));
       m->pa = m->alloc<float>(size_t(max_t * H));
@@ -447,6 +655,7 @@ int inferc_gpt2_create(inferc_hip_ctx* ctx, const inferc_gpt2_config* cfg,
       m->pf = m->alloc<float>(size_t(max_t * F));
       IH_HIP(hipMemset(m->kc, 0, cache * sizeof(float)));
       IH_HIP(hipMemset(m->vc, 0, cache * sizeof(float)));
+      IH_HIP(hipDeviceSynchronize());
     } catch (...) {
       m->release();
       delete m;
@@ -489,9 +698,7 @@ int inferc_gpt2_generate(inferc_gpt2* m, const int64_t* prompt, int64_t n_prompt
     upload_ids(m, prompt, n_prompt);
     m->enqueue_prefill_blocks(n_prompt);
     // First token: final LN + LM head on the last prompt row (main.cpp:820-828).
-    ih::gemv(ctx, V, H, m->wte, m->ph + (n_prompt - 1) * H, m->lnf_g, m->lnf_b, m->cfg.eps,
-             nullptr, nullptr, INFERC_ACT_NONE, m->logits);
-    m->finish_token();
+    m->lm_head_finish(m->ph + (n_prompt - 1) * H);
     m->capture_step();
     const int64_t steps = max_tokens - 1;
     if (step_ms && steps > 0) {

@@ -694,25 +694,19 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     const int64_t ad = data.shape[size_t(axis)];
     float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
     const float* dp = static_cast<const float*>(dev_of(n.in[0]));
-    if (axis == 0 && !idx.host) {
+    // one device gather for any axis; host-known indices are validated here
+    // and uploaded once (device indices are checked by the kernel's flag)
+    if (idx.host) {
+      for (int64_t i : host_i64(idx, "Gather"))
+        IH_REQUIRE(i >= -ad && i < ad, INFERC_ERR_ARG, "Gather: index out of range");
+    } else {
       IH_REQUIRE(idx.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED,
                  "Gather: device indices must be int64");
-      if (!dry) {
-        gather_rows(ctx, ad, inner, dp, static_cast<const int64_t*>(dev_of(n.in[1])), idx.numel(), y,
-                    nullptr);
-      }
-      return;
     }
-    // host-known indices: one strided copy per index
-    const std::vector<int64_t> ix = host_i64(idx, "Gather");
-    const int64_t ni = int64_t(ix.size());
-    for (int64_t k = 0; k < ni; ++k) {
-      int64_t i = ix[size_t(k)];
-      if (i < 0) i += ad;
-      IH_REQUIRE(i >= 0 && i < ad, INFERC_ERR_ARG, "Gather: index out of range");
-      if (!dry) {
-        copy2d(ctx, y + k * inner, ni * inner, dp + i * inner, ad * inner, inner, outer);
-      }
+    IH_REQUIRE(idx.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED, "Gather: int64 indices only");
+    const int64_t* ip = static_cast<const int64_t*>(dev_of(n.in[1]));
+    if (!dry) {
+      gather_axis(ctx, outer, ad, inner, dp, ip, idx.numel(), y, nullptr);
     }
     return;
   }

@@ -113,6 +113,124 @@ __global__ __launch_bounds__(kBlock) void gemv_f32_kernel(GemvP p) {
   }
 }
 
+// ------------------------------------------------- fp32 GEMV, short-chain form
+//
+// For K = 256*KV a wave owns R consecutive rows. Lane l's part of every row
+// is the KV float4 at k = 4l + 256j, and it needs x at exactly those k, so x
+// lives in registers, not LDS. The kernel's latency chain is one global load
+// round trip: the weight loads are issued first (they depend on nothing), x
+// is fetched (from L2) and, for XSRC_LN, normalised with wave-wide shuffles
+// while they are in flight. There is no LDS and no block barrier.
+//
+// ARGMAX: each block also leaves (max logit, first index) of its rows for the
+// decode step's final kernel.
+enum { XSRC_PLAIN = 0, XSRC_LN = 1 };
+
+struct Gemv2P {
+  int64_t N;
+  const float* W;
+  const float* x;
+  const float* ln_g;
+  const float* ln_b;
+  float ln_eps;
+  const float* bias;
+  const float* res;
+  int act;
+  float* y;
+  // ARGMAX
+  ValIdxPart* amax;      // [gridDim.x]
+};
+
+template <int KV, int XSRC>
+__device__ __forceinline__ void gemv2_x(const Gemv2P& p, int lane, float4 (&xv)[KV]) {
+  constexpr int K = 256 * KV;
+#pragma unroll
+  for (int j = 0; j < KV; ++j) xv[j] = *reinterpret_cast<const float4*>(p.x + 4 * lane + 256 * j);
+  if (XSRC == XSRC_LN) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KV; ++j) s += (xv[j].x + xv[j].y) + (xv[j].z + xv[j].w);
+    const float mean = wave_sum(s) / float(K);
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KV; ++j) {
+      xv[j].x -= mean; xv[j].y -= mean; xv[j].z -= mean; xv[j].w -= mean;
+      q += (xv[j].x * xv[j].x + xv[j].y * xv[j].y) + (xv[j].z * xv[j].z + xv[j].w * xv[j].w);
+    }
+    const float var = wave_sum(q) / float(K);
+    const float inv = 1.0f / sqrtf(var + p.ln_eps);
+#pragma unroll
+    for (int j = 0; j < KV; ++j) {
+      const float4 g = *reinterpret_cast<const float4*>(p.ln_g + 4 * lane + 256 * j);
+      const float4 b = *reinterpret_cast<const float4*>(p.ln_b + 4 * lane + 256 * j);
+      xv[j].x = (xv[j].x * inv) * g.x + b.x;
+      xv[j].y = (xv[j].y * inv) * g.y + b.y;
+      xv[j].z = (xv[j].z * inv) * g.z + b.z;
+      xv[j].w = (xv[j].w * inv) * g.w + b.w;
+    }
+  }
+}
+
+template <int R, int KV, int XSRC, bool ARGMAX>
+__global__ __launch_bounds__(kBlock) void gemv2_kernel(Gemv2P p) {
+  constexpr int K = 256 * KV;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r0 = (int64_t(blockIdx.x) * kWaves + wave) * R;
+  float4 w[R][KV];
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int j = 0; j < KV; ++j)
+      w[i][j] = (r0 + i < p.N)
+                    ? *reinterpret_cast<const float4*>(p.W + (r0 + i) * K + 4 * lane + 256 * j)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 xv[KV];
+  gemv2_x<KV, XSRC>(p, lane, xv);
+  float acc[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KV; ++j)
+      a += w[i][j].x * xv[j].x + w[i][j].y * xv[j].y + w[i][j].z * xv[j].z + w[i][j].w * xv[j].w;
+    acc[i] = wave_sum(a);
+  }
+  float bv = -INFINITY;
+  int64_t bi = INT64_MAX;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int64_t r = r0 + i;
+    if (r < p.N) {
+      float v = acc[i];
+      if (p.bias) v = v + p.bias[r];
+      if (p.res) v = v + p.res[r];
+      v = apply_act(v, p.act);
+      if (lane == i) p.y[r] = v;
+      if (ARGMAX && v > bv) {  // rows ascend: strict '>' keeps the first max
+        bv = v;
+        bi = r;
+      }
+    }
+  }
+  if (ARGMAX) {
+    __shared__ float sv[kWaves];
+    __shared__ int64_t si[kWaves];
+    if (lane == 0) {
+      sv[wave] = bv;
+      si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w2 = 1; w2 < kWaves; ++w2)
+        if (sv[w2] > bv || (sv[w2] == bv && si[w2] < bi)) {
+          bv = sv[w2];
+          bi = si[w2];
+        }
+      p.amax[blockIdx.x] = ValIdxPart{bv, bi};
+    }
+  }
+}
+
 // ---------------------------------------------------------------- int4 GEMV
 
 // One matrix of a (grouped) int4 GEMV launch.
@@ -256,6 +374,60 @@ __global__ __launch_bounds__(kBlock) void int4_unpack_kernel(const uint8_t* __re
 
 }  // namespace
 
+bool gemv2_supported(int64_t K) { return K == 768 || K == 3072; }
+
+namespace {
+
+// Rows per wave: enough waves to keep ~8 per CU streaming, within the
+// register budget (the K=3072 form holds 12 float4 of x per lane).
+int gemv2_rows(inferc_hip_ctx* ctx, int64_t N, int64_t K) {
+  if (K == 3072) return 1;
+  const int64_t cus = ctx->num_cus;
+  return N >= 32 * cus ? 4 : N >= 16 * cus ? 2 : 1;
+}
+
+template <int R, int KV>
+void gemv2_launch_r(const Gemv2P& p, unsigned blocks, int xsrc, bool argmax, hipStream_t s) {
+  const dim3 g(blocks), b(kBlock);
+  if (argmax) {
+    if (xsrc == XSRC_LN) hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_LN, true>), g, b, 0, s, p);
+    else hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_PLAIN, true>), g, b, 0, s, p);
+    return;
+  }
+  if (xsrc == XSRC_LN) hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_LN, false>), g, b, 0, s, p);
+  else hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_PLAIN, false>), g, b, 0, s, p);
+}
+
+}  // namespace
+
+int64_t gemv2_blocks(inferc_hip_ctx* ctx, int64_t N, int64_t K, bool /*argmax*/) {
+  return ceil_div(ceil_div(N, gemv2_rows(ctx, N, K)), kWaves);
+}
+
+void gemv2(inferc_hip_ctx* ctx, const Gemv2Args& a) {
+  IH_REQUIRE(gemv2_supported(a.K), INFERC_ERR_UNSUPPORTED, "gemv2: K must be 768 or 3072");
+  IH_REQUIRE(a.N > 0 && a.W && a.y, INFERC_ERR_ARG, "gemv2: bad arguments");
+  const int xsrc = a.ln_g ? XSRC_LN : XSRC_PLAIN;
+  IH_REQUIRE(a.x, INFERC_ERR_ARG, "gemv2: null x");
+  Gemv2P p{};
+  p.N = a.N; p.W = a.W; p.x = a.x; p.ln_g = a.ln_g; p.ln_b = a.ln_b; p.ln_eps = a.ln_eps;
+  p.bias = a.bias; p.res = a.res; p.act = a.act; p.y = a.y;
+  p.amax = a.amax;
+  const int R = gemv2_rows(ctx, a.N, a.K);
+  const int64_t blocks = ceil_div(ceil_div(a.N, R), kWaves);
+  IH_REQUIRE(blocks < (int64_t(1) << 31), INFERC_ERR_SHAPE, "gemv2: too many rows");
+  const unsigned nb = unsigned(blocks);
+  const bool am = a.amax != nullptr;
+  if (a.K == 768) {
+    if (R == 4) gemv2_launch_r<4, 3>(p, nb, xsrc, am, ctx->stream);
+    else if (R == 2) gemv2_launch_r<2, 3>(p, nb, xsrc, am, ctx->stream);
+    else gemv2_launch_r<1, 3>(p, nb, xsrc, am, ctx->stream);
+  } else {
+    gemv2_launch_r<1, 12>(p, nb, xsrc, am, ctx->stream);
+  }
+  check_launch("gemv2");
+}
+
 void gemv(inferc_hip_ctx* ctx, int64_t N, int64_t K, const float* W, const float* x,
           const float* ln_g, const float* ln_b, float ln_eps, const float* bias,
           const float* residual, int act, float* y) {
@@ -269,6 +441,14 @@ void gemv(inferc_hip_ctx* ctx, int64_t N, int64_t K, const float* W, const float
   IH_REQUIRE(!ln_g || K > 0, INFERC_ERR_SHAPE, "gemv: LayerNorm over an empty vector");
   IH_REQUIRE(K * sizeof(float) <= 64 * 1024, INFERC_ERR_UNSUPPORTED,
              "gemv: K > 16384 does not fit the on-chip activation buffer");
+  if (gemv2_supported(K) && aligned16(W) && aligned16(x) && (!ln_g || (aligned16(ln_g) &&
+                                                                      aligned16(ln_b)))) {
+    Gemv2Args a;
+    a.N = N; a.K = K; a.W = W; a.x = x; a.ln_g = ln_g; a.ln_b = ln_b; a.ln_eps = ln_eps;
+    a.bias = bias; a.res = residual; a.act = act; a.y = y;
+    gemv2(ctx, a);
+    return;
+  }
   GemvP p{N, K, W, x, ln_g, ln_b, ln_eps, bias, residual, act, y};
   const bool vec = aligned16(W) && K % 4 == 0;
   const size_t lds = size_t(K > 0 ? K : 1) * sizeof(float);

@@ -114,22 +114,26 @@ __global__ __launch_bounds__(kBlock) void add_kernel(int64_t n, const float* __r
     y[i] = a[i] + b[b_n == n ? i : i % b_n];
 }
 
-__global__ __launch_bounds__(kBlock) void gather_kernel(int64_t rows, int64_t row_len,
+// out[o, k, c] = table[o, idx[k], c] over the [outer, rows, row_len] view
+// (Gather along any axis); negative indices wrap, out-of-range ones write 0
+// and raise the error flag.
+__global__ __launch_bounds__(kBlock) void gather_kernel(int64_t outer, int64_t rows,
+                                                        int64_t row_len,
                                                         const float* __restrict__ table,
                                                         const int64_t* __restrict__ idx,
                                                         int64_t n_idx, float* __restrict__ out,
                                                         int32_t* err) {
-  const int64_t total = n_idx * row_len;
+  const int64_t total = outer * n_idx * row_len;
   for (int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x; e < total;
        e += int64_t(gridDim.x) * kBlock) {
-    const int64_t k = e / row_len, c = e % row_len;
+    const int64_t c = e % row_len, k = (e / row_len) % n_idx, o = e / (row_len * n_idx);
     int64_t i = idx[k];
     if (i < 0) i += rows;
     if (i < 0 || i >= rows) {
       out[e] = 0.0f;
       if (err) *err = 1;
     } else {
-      out[e] = table[i * row_len + c];
+      out[e] = table[(o * rows + i) * row_len + c];
     }
   }
 }
@@ -258,14 +262,21 @@ void add_bcast(inferc_hip_ctx* ctx, int64_t n, const float* a, const float* b, i
   check_launch("add");
 }
 
+void gather_axis(inferc_hip_ctx* ctx, int64_t outer, int64_t rows, int64_t row_len,
+                 const float* table, const int64_t* idx, int64_t n_idx, float* out,
+                 int32_t* err_flag) {
+  IH_REQUIRE(outer >= 0 && rows > 0 && row_len >= 0 && n_idx >= 0, INFERC_ERR_SHAPE,
+             "gather: bad shape");
+  if (outer == 0 || n_idx == 0 || row_len == 0) return;
+  IH_REQUIRE(table && idx && out, INFERC_ERR_ARG, "gather: null pointer");
+  hipLaunchKernelGGL(gather_kernel, dim3(grid_for(outer * n_idx * row_len)), dim3(kBlock), 0,
+                     ctx->stream, outer, rows, row_len, table, idx, n_idx, out, err_flag);
+  check_launch("gather");
+}
+
 void gather_rows(inferc_hip_ctx* ctx, int64_t rows, int64_t row_len, const float* table,
                  const int64_t* idx, int64_t n_idx, float* out, int32_t* err_flag) {
-  IH_REQUIRE(rows > 0 && row_len >= 0 && n_idx >= 0, INFERC_ERR_SHAPE, "gather: bad shape");
-  if (n_idx == 0 || row_len == 0) return;
-  IH_REQUIRE(table && idx && out, INFERC_ERR_ARG, "gather: null pointer");
-  hipLaunchKernelGGL(gather_kernel, dim3(grid_for(n_idx * row_len)), dim3(kBlock), 0, ctx->stream,
-                     rows, row_len, table, idx, n_idx, out, err_flag);
-  check_launch("gather");
+  gather_axis(ctx, 1, rows, row_len, table, idx, n_idx, out, err_flag);
 }
 
 void argmax(inferc_hip_ctx* ctx, int64_t n, const float* x, int64_t* out_idx, void* partial) {

@@ -62,6 +62,10 @@ _SIGS = {
     "inferc_hip_sync": [vp],
     "inferc_hip_timer_start": [vp],
     "inferc_hip_timer_stop": [vp, P(f32)],
+    "inferc_hip_capture_begin": [vp],
+    "inferc_hip_capture_end": [vp, P(vp)],
+    "inferc_hip_capture_replay": [vp],
+    "inferc_hip_capture_destroy": [vp],
     "inferc_hip_gemm_f32": [vp, i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i32,
                             i64, vp, i64, i32, vp, i64],
     "inferc_hip_matmul_f32": [vp, i64, i64, i64, i64, vp, i64, vp, i64, vp],

@@ -89,6 +89,40 @@ class Context:
         check(self._lib.inferc_hip_timer_stop(self.handle, C.byref(ms)))
         return float(ms.value)
 
+    def capture(self, fn) -> "Capture":
+        """Records the kernels `fn()` enqueues into a replayable HIP graph.
+        Run `fn` once beforehand so nothing allocates during capture."""
+        check(self._lib.inferc_hip_capture_begin(self.handle))
+        h = C.c_void_p()
+        try:
+            fn()
+        finally:
+            rc = self._lib.inferc_hip_capture_end(self.handle, C.byref(h))
+        check(rc)
+        return Capture(self, h.value)
+
+
+class Capture:
+    """A recorded sequence of entry points (inferc_hip_capture)."""
+
+    def __init__(self, ctx: Context, handle: int):
+        self.ctx = ctx
+        self.handle = handle
+
+    def replay(self) -> None:
+        check(self.ctx._lib.inferc_hip_capture_replay(self.handle))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.ctx._lib.inferc_hip_capture_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
 
 class Tensor:
     """Device tensor: dtype + shape over a device allocation (rt::Tensor,
