@@ -44,6 +44,97 @@ struct AttnP {
   float* out;
 };
 
+// Orders a wave's LDS writes before its later LDS reads by other lanes of
+// the same wave (no cross-wave synchronisation).
+__device__ __forceinline__ void wave_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One 32-key tile for a wave's 32 queries: S^T = K Q^T on the matrix cores,
+// scale, mask, online-softmax update, then O^T += V^T P^T.
+__device__ __forceinline__ void attn_tile(const AttnP& p, const float* __restrict__ ks,
+                                          const float* __restrict__ vs, int64_t k0, int64_t qi,
+                                          const uint8_t* mbase, const float (&qf)[kD / 2],
+                                          floatx16 (&oacc)[2], float& m_run, float& l_run,
+                                          int half, int l32) {
+  const int64_t S = p.S;
+  floatx16 sacc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kD / 2; ++s) {
+    const float a = ks[l32 * kKS + 2 * s + half];
+    sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, qf[s], sacc, 0, 0, 0);
+  }
+  // sacc[v]: key k0 + 8*(v/4) + 4*half + v%4, query qi.
+  float sv[16];
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int64_t j = k0 + 8 * (v >> 2) + 4 * half + (v & 3);
+    float s = p.scale * sacc[v];
+    if (j >= S) {
+      s = -INFINITY;  // key does not exist
+    } else if (p.causal) {
+      if (j > qi) s = p.fill;
+    } else if (mbase && qi < S) {
+      if (mbase[qi * p.ms2 + j * p.ms3]) s = p.fill;
+    }
+    sv[v] = s;
+    tmax = fmaxf(tmax, s);
+  }
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  const float m_new = fmaxf(m_run, tmax);
+  const float corr = __expf(m_run - m_new);
+  float lsum = 0.0f;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    sv[v] = __expf(sv[v] - m_new);
+    lsum += sv[v];
+  }
+  lsum += __shfl_xor(lsum, 32, 64);
+  l_run = l_run * corr + lsum;
+  m_run = m_new;
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) oacc[d][v] *= corr;
+  // O^T[dim][query] += V^T[dim][key] P^T[key][query]; step s pairs key
+  // 8*(s/4) + 4*kidx + s%4 with the MFMA summation index kidx.
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const int key = 8 * (s >> 2) + 4 * half + (s & 3);
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const float a = vs[key * kVS + d * 32 + l32];
+      oacc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, sv[s], oacc[d], 0, 0, 0);
+    }
+  }
+}
+
+// Writes query qi's 64 outputs: oacc[d][v] holds dim d*32 + 8*(v/4) +
+// 4*half + v%4, scaled by inv = 1/l.
+__device__ __forceinline__ void attn_store(const AttnP& p, int64_t b, int64_t h, int64_t qi,
+                                           const floatx16 (&oacc)[2], float inv, int half) {
+  float* orow = p.out + (b * p.S + qi) * p.ldo + h * kD;
+  const bool vec = (p.ldo % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0);
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float* dst = orow + d * 32 + 8 * g + 4 * half;
+      const float4 o = make_float4(oacc[d][4 * g] * inv, oacc[d][4 * g + 1] * inv,
+                                   oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv);
+      if (vec) {
+        *reinterpret_cast<float4*>(dst) = o;
+      } else {
+        dst[0] = o.x; dst[1] = o.y; dst[2] = o.z; dst[3] = o.w;
+      }
+    }
+}
+
 template <int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
   constexpr int NT = 64 * WAVES;
@@ -141,84 +232,128 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
     // A wave whose 32 queries all lie above this tile's keys skips it
     // (causal), as does a wave past the end of the sequence.
     const bool skip = (q0 >= S) || (p.causal && k0 > q0 + 31);
-    if (!skip) {
-      const float* ks = Ks[cur];
-      const float* vs = Vs[cur];
-      floatx16 sacc;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
-#pragma unroll
-      for (int s = 0; s < kD / 2; ++s) {
-        const float a = ks[l32 * kKS + 2 * s + half];
-        sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, qf[s], sacc, 0, 0, 0);
-      }
-      // sacc[v]: key k0 + 8*(v/4) + 4*half + v%4, query qi.
-      float sv[16];
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t j = k0 + 8 * (v >> 2) + 4 * half + (v & 3);
-        float s = p.scale * sacc[v];
-        if (j >= S) {
-          s = -INFINITY;  // key does not exist
-        } else if (p.causal) {
-          if (j > qi) s = p.fill;
-        } else if (mbase && qi < S) {
-          if (mbase[qi * p.ms2 + j * p.ms3]) s = p.fill;
-        }
-        sv[v] = s;
-        tmax = fmaxf(tmax, s);
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m_run, tmax);
-      const float corr = __expf(m_run - m_new);
-      float lsum = 0.0f;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        sv[v] = __expf(sv[v] - m_new);
-        lsum += sv[v];
-      }
-      lsum += __shfl_xor(lsum, 32, 64);
-      l_run = l_run * corr + lsum;
-      m_run = m_new;
-#pragma unroll
-      for (int d = 0; d < 2; ++d)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) oacc[d][v] *= corr;
-      // O^T[dim][query] += V^T[dim][key] P^T[key][query]; step s pairs key
-      // 8*(s/4) + 4*kidx + s%4 with the MFMA summation index kidx.
-#pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        const int key = 8 * (s >> 2) + 4 * half + (s & 3);
-#pragma unroll
-        for (int d = 0; d < 2; ++d) {
-          const float a = vs[key * kVS + d * 32 + l32];
-          oacc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, sv[s], oacc[d], 0, 0, 0);
-        }
-      }
-    }
+    if (!skip) attn_tile(p, Ks[cur], Vs[cur], k0, qi, mbase, qf, oacc, m_run, l_run, half, l32);
     if (t + 1 < ntiles) store_tile(cur ^ 1);
     __syncthreads();
   }
+  if (qi < S) attn_store(p, b, h, qi, oacc, 1.0f / l_run, half);
+}
 
-  if (qi >= S) return;
-  const float inv = 1.0f / l_run;
-  float* orow = p.out + (b * S + qi) * p.ldo + h * kD;
-  // oacc[d][v]: dim d*32 + 8*(v/4) + 4*half + v%4 of query qi.
-  const bool vec = (p.ldo % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0);
+// Small grids (b=1): the KW waves of a block share the same 32 queries and
+// split the key tiles (wave w takes tiles w, w+KW, ...), each staging its
+// tiles in its own LDS slice, so a block finishes after ceil(tiles/KW) tile
+// steps instead of all of them. The KW partial states (m, l, O) are merged
+// through LDS: M = max_w m_w, O = sum_w exp(m_w - M) O_w, l likewise.
+template <int KW>
+__global__ __launch_bounds__(64 * KW) void attn_fwd_d64_ks(AttnP p) {
+  constexpr int NT = 64 * KW;
+  __shared__ __attribute__((aligned(16))) float Ks[KW][kKT * kKS];
+  __shared__ __attribute__((aligned(16))) float Vs[KW][kKT * kVS];
+  __shared__ int s_last_valid;
+  __shared__ float sm[KW][32], sl[KW][32];
+  static_assert(KW * 32 * kD <= KW * kKT * kKS, "O merge buffer must fit in Ks");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const int64_t q0 = int64_t(blockIdx.x) * 32;
+  const int64_t qi = q0 + l32;
+  const int64_t S = p.S;
+  const float* qbase = p.q + b * S * p.ldq + h * kD;
+  const float* kbase = p.k + b * S * p.ldk + h * kD;
+  const float* vbase = p.v + b * S * p.ldv + h * kD;
+  const uint8_t* mbase = p.mask ? p.mask + b * p.ms0 + h * p.ms1 : nullptr;
+
+  int64_t key_end = S;
+  if (p.causal) {
+    key_end = (q0 + 32) < S ? q0 + 32 : S;
+  } else if (mbase && p.ms2 == 0) {
+    if (tid == 0) s_last_valid = -1;
+    __syncthreads();
+    int last = -1;
+    for (int64_t j = tid; j < S; j += NT)
+      if (!mbase[j * p.ms3]) last = int(j);
+    if (last >= 0) atomicMax(&s_last_valid, last);
+    __syncthreads();
+    if (s_last_valid >= 0) key_end = s_last_valid + 1;
+  }
+  const int64_t ntiles = (key_end + kKT - 1) / kKT;
+
+  float qf[kD / 2];
+#pragma unroll
+  for (int s = 0; s < kD / 2; ++s) qf[s] = (qi < S) ? qbase[qi * p.ldq + 2 * s + half] : 0.0f;
+  floatx16 oacc[2];
 #pragma unroll
   for (int d = 0; d < 2; ++d)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      float* dst = orow + d * 32 + 8 * g + 4 * half;
-      const float4 o = make_float4(oacc[d][4 * g] * inv, oacc[d][4 * g + 1] * inv,
-                                   oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv);
-      if (vec) {
-        *reinterpret_cast<float4*>(dst) = o;
-      } else {
-        dst[0] = o.x; dst[1] = o.y; dst[2] = o.z; dst[3] = o.w;
+    for (int v = 0; v < 16; ++v) oacc[d][v] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  float* ks = Ks[wave];
+  float* vs = Vs[wave];
+  for (int64_t t = wave; t < ntiles; t += KW) {
+    const int64_t k0 = t * kKT;
+    // wave-private staging of 32 keys x 64 dims of K and V (8 float4 per lane)
+    float4 kr[8], vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int idx = lane + 64 * i;
+      const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
+      kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      vr[i] = kr[i];
+      if (k0 + key < S) {
+        const float* kp = kbase + (k0 + key) * p.ldk + dq;
+        const float* vp = vbase + (k0 + key) * p.ldv + dq;
+        kr[i] = make_float4(kp[0], kp[1], kp[2], kp[3]);
+        vr[i] = make_float4(vp[0], vp[1], vp[2], vp[3]);
       }
     }
+    wave_lds_barrier();  // the previous tile's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int idx = lane + 64 * i;
+      const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
+      float* kd = ks + key * kKS + dq;
+      kd[0] = kr[i].x; kd[1] = kr[i].y; kd[2] = kr[i].z; kd[3] = kr[i].w;
+      *reinterpret_cast<float4*>(vs + key * kVS + dq) = vr[i];
+    }
+    wave_lds_barrier();  // this tile is visible to every lane of the wave
+    if (!(q0 >= S || (p.causal && k0 > q0 + 31)))
+      attn_tile(p, ks, vs, k0, qi, mbase, qf, oacc, m_run, l_run, half, l32);
+  }
+
+  __syncthreads();  // every wave is done with its K/V slice: reuse Ks for O
+  float* obuf = &Ks[0][0];  // [KW][32 queries][64 dims]
+  if (half == 0) {
+    sm[wave][l32] = m_run;
+    sl[wave][l32] = l_run;
+  }
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      obuf[(wave * 32 + l32) * kD + d * 32 + 8 * (v >> 2) + 4 * half + (v & 3)] = oacc[d][v];
+  __syncthreads();
+  if (wave != 0 || qi >= S) return;
+  float M = sm[0][l32];
+  for (int w = 1; w < KW; ++w) M = fmaxf(M, sm[w][l32]);
+  float L = 0.0f, cw[KW];
+#pragma unroll
+  for (int w = 0; w < KW; ++w) {
+    cw[w] = __expf(sm[w][l32] - M);
+    L += cw[w] * sl[w][l32];
+  }
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      float o = 0.0f;
+#pragma unroll
+      for (int w = 0; w < KW; ++w)
+        o += cw[w] * obuf[(w * 32 + l32) * kD + d * 32 + 8 * (v >> 2) + 4 * half + (v & 3)];
+      oacc[d][v] = o;
+    }
+  attn_store(p, b, h, qi, oacc, 1.0f / L, half);
 }
 
 // Any head_dim up to 256: one thread per (b, h, query) with an online softmax
@@ -282,8 +417,9 @@ void attention(inferc_hip_ctx* ctx, const AttnArgs& a) {
       dim3 grid(unsigned(ceil_div(a.S, 128)), unsigned(p.nH), unsigned(a.B));
       hipLaunchKernelGGL(attn_fwd_d64<4>, grid, dim3(256), 0, ctx->stream, p);
     } else {
+      // few blocks: four waves per 32 queries, splitting the key tiles
       dim3 grid(unsigned(ceil_div(a.S, 32)), unsigned(p.nH), unsigned(a.B));
-      hipLaunchKernelGGL(attn_fwd_d64<1>, grid, dim3(64), 0, ctx->stream, p);
+      hipLaunchKernelGGL(attn_fwd_d64_ks<4>, grid, dim3(256), 0, ctx->stream, p);
     }
     check_launch("attn_fwd_d64");
     return;
