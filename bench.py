@@ -240,6 +240,33 @@ def roofline_ffn_up_gemm(ctx, reps: int = 200):
             "avg_launch_us": round(ms * 1e3, 3)}
 
 
+def roofline_only(ctx, launches: int = 50) -> dict:
+    """For counter runs (rocprofv3 --pmc): `launches` eager launches of the
+    roofline kernel, then one 64 MiB device-to-device copy whose FETCH_SIZE /
+    WRITE_SIZE calibrate the counters (the copy moves exactly 64 MiB each way)."""
+    from inferc_amd import graphs, rt
+
+    M, N, K = 128, 3072, 768
+    x = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rx", (M, K), 1.0))
+    w = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rw", (K, N)))
+    b = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rb", (N,)))
+    y = rt.Tensor.empty(ctx, (M, N))
+    for _ in range(launches):
+        rc = ctx._lib.inferc_hip_fused_matmul_add_gelu_f32(ctx.handle, M, N, K, x.ptr, w.ptr,
+                                                            b.ptr, y.ptr)
+        if rc:
+            from inferc_amd.lib import check
+            check(rc)
+    nbytes = 64 << 20
+    src, dst = rt.Tensor.empty(ctx, (nbytes // 4,)), rt.Tensor.empty(ctx, (nbytes // 4,))
+    ctx.sync()
+    from inferc_amd.lib import check
+    check(ctx._lib.inferc_hip_d2d(ctx.handle, dst.ptr, src.ptr, nbytes))
+    ctx.sync()
+    return {"roofline_kernel_launches": launches, "copy_bytes": nbytes,
+            "algorithmic_bytes_per_launch": 4 * (M * K + K * N + N + M * N)}
+
+
 def cpu_baseline_encoder(weights, budget_s: float = 12.0):
     import oracle as O
     from inferc_amd import graphs
@@ -278,6 +305,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="primary workload and roofline only")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="roofline kernel + calibration copy only (for rocprofv3 --pmc runs)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -290,6 +319,10 @@ def main(argv=None) -> int:
     from inferc_amd import graphs, rt
 
     ctx = rt.Context(0)
+    if args.roofline_only:
+        print(json.dumps(roofline_only(ctx)), flush=True)
+        ctx.close()
+        return 0
     extra = {}
     log("encoder b1 s128")
     ms_b1, _, enc_w = bench_encoder(ctx, 1, args.steps, args.warmup)

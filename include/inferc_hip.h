@@ -55,7 +55,8 @@ typedef enum {
   INFERC_C_SCALAR = 3  /* C[1]                        */
 } inferc_c_kind;
 
-/* Tensor element types (values of the reference's IR DType subset). */
+/* Tensor element types, as ONNX TensorProto.DataType codes (the reference
+ * maps its IR DType to these with DTypeToOnnx, src/ir/graph.h:27-28). */
 typedef enum {
   INFERC_DT_F32 = 1,
   INFERC_DT_U8 = 2,

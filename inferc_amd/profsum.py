@@ -6,6 +6,13 @@ average durations. Reads either the CSV trace (``--output-format csv``:
 ``*_kernel_trace.csv``) or the SQLite database rocprofv3 writes by default.
 
 Usage: python -m inferc_amd.profsum <trace.csv | results.db> [--top N]
+       python -m inferc_amd.profsum --traffic FETCH.csv WRITE.csv --copy-bytes B
+
+The ``--traffic`` form reads two ``rocprofv3 --pmc FETCH_SIZE`` /
+``--pmc WRITE_SIZE`` counter CSVs of the same program, takes the largest
+``__amd_rocclr_copyBuffer`` dispatch (a device copy of ``B`` bytes) as the
+calibration (counter KiB that a copy of known size reads), and prints every
+other kernel's mean per-dispatch HBM bytes scaled by that factor.
 """
 from __future__ import annotations
 
@@ -51,11 +58,54 @@ def summarize(rows, top: int = 25) -> str:
     return "\n".join(lines)
 
 
+def _counter_means(path: str):
+    per = defaultdict(list)
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            per[(r["Kernel_Name"], int(r["Grid_Size"]))].append(float(r["Counter_Value"]))
+    return per
+
+
+def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> dict:
+    """Per-(kernel, grid) mean fetch/write KiB and calibrated HBM bytes."""
+    out = {}
+    scales = {}
+    for tag, path in (("fetch", fetch_csv), ("write", write_csv)):
+        per = _counter_means(path)
+        copies = [max(v) for (n, _), v in per.items() if "copyBuffer" in n]
+        if not copies:
+            raise SystemExit(f"{path}: no copy dispatch to calibrate against")
+        scales[tag] = copy_bytes / 1024.0 / max(copies)
+        for (name, grid), v in per.items():
+            if "copyBuffer" in name:
+                continue
+            e = out.setdefault((name, grid), {"dispatches": len(v)})
+            e[f"{tag}_kib"] = sum(v) / len(v)
+    for e in out.values():
+        e["bytes"] = 1024.0 * (e.get("fetch_kib", 0.0) * scales["fetch"] +
+                               e.get("write_kib", 0.0) * scales["write"])
+    return {"fetch_scale": scales["fetch"], "write_scale": scales["write"], "kernels": out}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
-    ap.add_argument("trace")
+    ap.add_argument("trace", nargs="?")
     ap.add_argument("--top", type=int, default=25)
+    ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    ap.add_argument("--copy-bytes", type=int, default=64 << 20)
     a = ap.parse_args(argv)
+    if a.traffic:
+        t = traffic(a.traffic[0], a.traffic[1], a.copy_bytes)
+        print(f"calibration: FETCH_SIZE x{t['fetch_scale']:.4f}, "
+              f"WRITE_SIZE x{t['write_scale']:.4f} (copy of {a.copy_bytes} bytes)")
+        print(f"{'dispatches':>10} {'fetch_KiB':>11} {'write_KiB':>11} {'HBM_bytes':>13}  "
+              f"{'grid':>8}  kernel")
+        for (name, grid), e in sorted(t["kernels"].items(), key=lambda kv: -kv[1]["bytes"]):
+            print(f"{e['dispatches']:10d} {e.get('fetch_kib', 0):11.1f} "
+                  f"{e.get('write_kib', 0):11.1f} {e['bytes']:13.0f}  {grid:>8}  {_short(name)}")
+        return 0
+    if not a.trace:
+        ap.error("a trace file is required")
     print(summarize(load(a.trace), a.top))
     return 0
 
