@@ -14,10 +14,15 @@
 // panels staged through LDS, double-buffered: the global loads of panel t+1
 // are in flight while panel t feeds the matrix cores. Both operands sit in
 // LDS k-major ([BK][outer]) so every MFMA operand read is 32 consecutive
-// floats per half-wave. Shapes that leave most of the 256 CUs idle (b=1,
-// M=128) split K over blocks; partial sums land in the context workspace and
-// a second kernel reduces them in fixed order (deterministic) and applies the
-// epilogue.
+// floats per half-wave.
+//
+// Shapes with too few 128x128 tiles to fill the 256 CUs go to one of two
+// other paths. Small M with float4-aligned row-major A (the b=1 encoder, GPT-2
+// prefill) goes to gemm_f32_ksplit: K is split between the waves of a block,
+// and the partial tiles are summed through LDS in the same launch. Other
+// shapes run the 64x64 kernel with K split over blocks; partial sums land in
+// the context workspace, and a second kernel reduces them in fixed order
+// (deterministic) and applies the epilogue.
 #include "common.h"
 
 namespace ih {
@@ -250,6 +255,237 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(GemmParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Small-M product (M up to a few hundred rows: the b=1 encoder, GPT-2
+// prefill). One block per WM x WN output tile; its W waves split K between
+// them, each wave running v_mfma_f32_16x16x4f32 on operands loaded straight
+// from global memory into registers (no LDS staging: every operand element is
+// used by exactly one wave of the block). The W partial tiles are summed
+// through LDS in wave order (deterministic) and the epilogue is applied once.
+// This replaces the split-K launch + reduce launch pair for these shapes.
+//
+// Operand layout (lane l, r = l%16, g = l/16). One k-group is 16 consecutive
+// k; MFMA step e (0..3) of the group gives lane-group g the k index 4g+e:
+//   A (row-major [M,K]):  float4 A[m0+16i+r][k0+4g .. k0+4g+3]
+//   B (TB=0, [K,N]):      row k0+4g+e, CB consecutive columns starting at
+//                         n0+CB*r (float4/float2); column block j of the
+//                         MFMA takes column n0 + CB*r + j
+//   B (TB=1, [N,K]):      float4 B[n0+16j+r][k0+4g .. k0+4g+3]
+// Accumulator register v of lane l holds row 4*(l/16)+v, column l%16 of its
+// 16x16 block.
+// ---------------------------------------------------------------------------
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+
+template <int WM, int WN, bool TB>
+struct KsFrag {
+  static constexpr int RA = WM / 16, CB = WN / 16;
+  float4 a[RA];
+  float b[4][CB];  // b[e][j]: B operand of MFMA step e, column block j
+  bool kin;        // this lane group's 4 k lie inside the wave's K range
+
+  // Loads are unconditional, from addresses clamped into the operands. A row
+  // of A past M only feeds output rows that are never stored, and a column
+  // of B past N only output columns that are never stored, so those need no
+  // masking. k past the wave's range is masked in mma(), where the value is
+  // consumed: nothing touches a load result before the MFMA that needs it,
+  // so the compiler keeps every ring slot in flight.
+  __device__ __forceinline__ void load(const float* __restrict__ A, int64_t lda,
+                                       const float* __restrict__ B, int64_t ldb, int64_t M,
+                                       int64_t N, int64_t K, int64_t m0, int64_t n0, int64_t k0,
+                                       int64_t ke, int r, int g) {
+    const int64_t kq = k0 + 4 * g;  // first k of this lane group (a multiple of 4)
+    kin = kq < ke;
+    const int64_t kc = kq < K - 4 ? kq : K - 4;  // K % 4 == 0 and K >= 4
+#pragma unroll
+    for (int i = 0; i < RA; ++i) {
+      const int64_t row = m0 + 16 * i + r;
+      const int64_t rc = row < M ? row : M - 1;
+      a[i] = *reinterpret_cast<const float4*>(A + rc * lda + kc);
+    }
+    if constexpr (TB) {
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        const int64_t n = n0 + 16 * j + r;
+        const int64_t nc = n < N ? n : N - 1;
+        const float4 t = *reinterpret_cast<const float4*>(B + nc * ldb + kc);
+        b[0][j] = t.x; b[1][j] = t.y; b[2][j] = t.z; b[3][j] = t.w;
+      }
+    } else {
+      // N % 4 == 0, so a CB-wide vector at a multiple of CB is all in or all
+      // out, and N - CB is a valid start.
+      const int64_t n = n0 + CB * r;
+      const int64_t nc = n < N ? n : N - CB;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float* src = B + (kc + e) * ldb + nc;
+        if constexpr (CB == 4) {
+          const float4 t = *reinterpret_cast<const float4*>(src);
+          b[e][0] = t.x; b[e][1] = t.y; b[e][2] = t.z; b[e][3] = t.w;
+        } else if constexpr (CB == 2) {
+          const float2 t = *reinterpret_cast<const float2*>(src);
+          b[e][0] = t.x; b[e][1] = t.y;
+        } else {
+          b[e][0] = *src;
+        }
+      }
+    }
+  }
+
+  // Both operands of a masked k are zeroed, so a non-finite value at the
+  // clamped address cannot leak into the sum.
+  __device__ __forceinline__ void mma(floatx4 (&acc)[RA][CB]) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float av[RA], bv[CB];
+#pragma unroll
+      for (int i = 0; i < RA; ++i) {
+        const float x = e == 0 ? a[i].x : e == 1 ? a[i].y : e == 2 ? a[i].z : a[i].w;
+        av[i] = kin ? x : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < CB; ++j) bv[j] = kin ? b[e][j] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < RA; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+  }
+};
+
+// P is the register ring depth: k-groups in flight per wave.
+template <int WM, int WN, int W, int P, bool TB>
+__global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t tiles_m,
+                                                          int64_t tiles_n) {
+  constexpr int RA = WM / 16, CB = WN / 16;
+  static_assert(W * WM * WN * 4 <= 65536, "partial tiles must fit the LDS of one block");
+  __shared__ __attribute__((aligned(16))) float red[W * WM * WN];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+
+  // XCD-aware tile order: consecutive blocks go to different XCDs (round
+  // robin over 8), so block b works on tile (b%8)*per + b/8. Each XCD then
+  // holds a contiguous run of tiles, n-major, and the m-tiles that share a
+  // B column panel read it through the same L2.
+  const int64_t T = tiles_m * tiles_n, per = T / 8;
+  const int64_t bid = blockIdx.x;
+  const int64_t t = bid < 8 * per ? (bid % 8) * per + bid / 8 : bid;
+  const int64_t m0 = (t % tiles_m) * WM, n0 = (t / tiles_m) * WN;
+
+  const int slice = blockIdx.y;
+  const float* A = p.A + slice * p.sa;
+  const float* B = p.use_table ? p.Bt[slice] : p.B + slice * p.sb;
+
+  // Wave w owns K range [kb, ke); it runs `rings` rounds of P 16-deep
+  // k-groups (the host sizes k_per_split so that rounds are mostly full;
+  // groups past ke load zeros).
+  const int64_t kb = int64_t(wave) * p.k_per_split;
+  const int64_t ke = kb + p.k_per_split < p.K ? kb + p.k_per_split : p.K;
+  const int64_t rings = (p.k_per_split + 16 * P - 1) / (16 * P);
+
+  floatx4 acc[RA][CB];
+#pragma unroll
+  for (int i = 0; i < RA; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  KsFrag<WM, WN, TB> f[P];
+  if (kb < ke) {
+#pragma unroll
+    for (int q = 0; q < P; ++q)
+      f[q].load(A, p.lda, B, p.ldb, p.M, p.N, p.K, m0, n0, kb + 16 * q, ke, r, g);
+    for (int64_t ring = 1; ring < rings; ++ring) {
+      const int64_t k_next = kb + 16 * P * ring;
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        // Slot by slot: the scheduler may not merge slots, so each MFMA
+        // group waits only for its own loads and the refill of slot q goes
+        // out as soon as slot q has been consumed.
+        __builtin_amdgcn_sched_barrier(0);
+        f[q].mma(acc);
+        f[q].load(A, p.lda, B, p.ldb, p.M, p.N, p.K, m0, n0, k_next + 16 * q, ke, r, g);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      __builtin_amdgcn_sched_barrier(0);
+      f[q].mma(acc);
+    }
+  }
+
+  // Partial tiles to LDS in [row][col] order of the block's output tile.
+  float* mine = red + wave * (WM * WN);
+#pragma unroll
+  for (int i = 0; i < RA; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      const int col = TB ? 16 * j + r : CB * r + j;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) mine[(16 * i + 4 * g + v) * WN + col] = acc[i][j][v];
+    }
+  __syncthreads();
+
+  const float* C = p.use_table ? p.Ct[slice] : p.C;
+  const float* R = p.R ? p.R + slice * p.sr : nullptr;
+  float* Y = p.use_table ? p.Yt[slice] : p.Y + slice * p.sy;
+  for (int e = tid; e < WM * WN; e += 64 * W) {
+    float s = red[e];
+#pragma unroll
+    for (int w = 1; w < W; ++w) s += red[w * (WM * WN) + e];
+    const int64_t row = m0 + e / WN, col = n0 + e % WN;
+    if (row < p.M && col < p.N) Y[row * p.ldy + col] = epilogue(p, C, R, s, row, col);
+  }
+}
+
+struct KsCfg { int wm, wn, w, p; };
+
+// K per wave: whole rings of P k-groups, split as evenly as that allows.
+inline int64_t ks_k_per_wave(int64_t K, int w, int depth) {
+  return ceil_div(ceil_div(K, w), 16 * depth) * 16 * depth;
+}
+
+template <int WM, int WN, int W, int P>
+void launch_ksplit(GemmParams p, int64_t slices, bool tb, hipStream_t s) {
+  p.splits = 1;
+  p.partial = nullptr;
+  p.k_per_split = ks_k_per_wave(p.K, W, P);
+  const int64_t tm = ceil_div(p.M, WM), tn = ceil_div(p.N, WN);
+  const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(slices));
+  if (tb)
+    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, true>), grid, dim3(64 * W), 0, s, p, tm, tn);
+  else
+    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, false>), grid, dim3(64 * W), 0, s, p, tm, tn);
+}
+
+// Two shapes cover the small-M products (measured on MI355X at M=32..256,
+// N=768..3072, K=768..3072): 32x64 tiles with 8 waves when that alone gives
+// at least half as many blocks as CUs (the b=1 FFN-up and QKV), else 16x32
+// tiles with 16 waves (out-proj, FFN-down, prefill), trading operand reuse
+// for blocks to spread over the CUs. Ring depth 3 in both: deeper rings
+// measured no faster.
+KsCfg pick_ksplit(int64_t M, int64_t N, int64_t slices, int64_t cus) {
+  const int64_t big_blocks = ceil_div(M, 32) * ceil_div(N, 64) * slices;
+  if (2 * big_blocks >= cus) return KsCfg{32, 64, 8, 3};
+  return KsCfg{16, 32, 16, 3};
+}
+
+bool ksplit_supported(const GemmParams& p, int64_t slices, bool ta, bool vec, int64_t cus,
+                      int64_t big_tiles) {
+  // Operands need float4 rows (vec), A row-major; the shape must be one the
+  // LDS-tiled kernel would have split over K (too few 128x128 tiles).
+  return !ta && vec && big_tiles < cus && p.M <= 512 && p.K > 0 && slices < 65536;
+}
+
+void run_ksplit(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool tb) {
+  const KsCfg c = pick_ksplit(p.M, p.N, slices, ctx->num_cus);
+  if (c.wm == 32) launch_ksplit<32, 64, 8, 3>(p, slices, tb, ctx->stream);
+  else launch_ksplit<16, 32, 16, 3>(p, slices, tb, ctx->stream);
+  check_launch("gemm_f32_ksplit");
+}
+
 template <int BM, int BN, int BK, bool TA, bool TB, bool VEC>
 void launch_cfg(const GemmParams& p, int64_t slices, hipStream_t s) {
   dim3 grid(unsigned(ceil_div(p.N, BN)), unsigned(ceil_div(p.M, BM)),
@@ -280,6 +516,7 @@ void run(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool ta, bool tb, bo
   const int64_t cus = ctx->num_cus;
   const Cfg big{128, 128, 16}, small{64, 64, 32};
   auto tiles = [&](const Cfg& c) { return ceil_div(p.M, c.bm) * ceil_div(p.N, c.bn) * slices; };
+  if (ksplit_supported(p, slices, ta, vec, cus, tiles(big))) return run_ksplit(ctx, p, slices, tb);
   Cfg c = tiles(big) >= cus ? big : small;
   int64_t splits = 1;
   if (c.bm == small.bm) {
