@@ -356,6 +356,164 @@ __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_ks(AttnP p) {
   attn_store(p, b, h, qi, oacc, 1.0f / L, half);
 }
 
+// Small grids with 16-byte aligned rows (the b=1 encoder, GPT-2 prefill): 16
+// queries per block on v_mfma_f32_16x16x4f32, so twice as many blocks as the
+// 32-query kernels and half the matrix-core chain per wave. The KW waves
+// split the 32-key tiles (wave w takes tiles w, w+KW, ...) and load their
+// operands straight into registers, mask bytes included; nothing waits on a
+// block-wide scan. Lane l (r = l%16, g = l/16):
+//   S^T = K Q^T:  step s pairs MFMA k-index g with head dim 16g + s, so the
+//                 lane's Q row (query q0+r) and K rows (keys k0+16kb+r) are
+//                 four float4 loads of dims [16g, 16g+16) each;
+//                 score register v of key block kb: key k0+16kb+4g+v, query r.
+//   O^T += V^T P^T: step (kb, v) pairs k-index g with key k0+16kb+4g+v, which
+//                 is exactly the probability the lane already holds; the V^T
+//                 operand is V[that key][16db + r].
+// The KW partial states (m, l, O) are merged through LDS, wave w merging dim
+// block w for all 16 queries.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int KW>
+__global__ __launch_bounds__(64 * KW) void attn_fwd_d64_q16(AttnP p) {
+  __shared__ __attribute__((aligned(16))) float obuf[KW][16][kD + 4];
+  __shared__ float sm[KW][16], sl[KW][16];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t b = blockIdx.z, h = blockIdx.y, S = p.S;
+  const int64_t q0 = int64_t(blockIdx.x) * 16;
+  const int64_t qi = q0 + r;
+  const int64_t qc = qi < S ? qi : S - 1;
+  const float* qbase = p.q + b * S * p.ldq + h * kD;
+  const float* kbase = p.k + b * S * p.ldk + h * kD;
+  const float* vbase = p.v + b * S * p.ldv + h * kD;
+  const uint8_t* mbase = p.mask ? p.mask + b * p.ms0 + h * p.ms1 : nullptr;
+
+  float4 qv[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    qv[c] = *reinterpret_cast<const float4*>(qbase + qc * p.ldq + 16 * g + 4 * c);
+
+  floatx4 oacc[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) oacc[d] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  const int64_t ntiles = (S + kKT - 1) / kKT;
+  for (int64_t t = wave; t < ntiles; t += KW) {
+    const int64_t k0 = t * kKT;
+    if (p.causal && k0 > q0 + 15) break;  // later tiles are masked for every query here
+    // Operands of this tile, all loads issued before any use.
+    float4 kv[2][4];
+    float vv[2][4][4];  // [kb][v][db]
+    uint8_t mk[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int64_t kr = k0 + 16 * kb + r;
+      const float* kp = kbase + (kr < S ? kr : S - 1) * p.ldk + 16 * g;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) kv[kb][c] = *reinterpret_cast<const float4*>(kp + 4 * c);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t key = k0 + 16 * kb + 4 * g + v;
+        const int64_t kc = key < S ? key : S - 1;
+        const float* vp = vbase + kc * p.ldv + r;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) vv[kb][v][db] = vp[16 * db];
+        mk[kb][v] = (mbase && !p.causal && qi < S) ? mbase[qi * p.ms2 + kc * p.ms3] : uint8_t(0);
+      }
+    }
+    floatx4 sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sacc[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 16; ++s) {
+        const float4 kq = kv[kb][s >> 2], qq = qv[s >> 2];
+        const int e = s & 3;
+        const float a = e == 0 ? kq.x : e == 1 ? kq.y : e == 2 ? kq.z : kq.w;
+        const float bq = e == 0 ? qq.x : e == 1 ? qq.y : e == 2 ? qq.z : qq.w;
+        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bq, sacc[kb], 0, 0, 0);
+      }
+    }
+    float sv[2][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t j = k0 + 16 * kb + 4 * g + v;
+        float s = p.scale * sacc[kb][v];
+        if (j >= S) s = -INFINITY;  // key does not exist
+        else if (p.causal ? (j > qi) : (mk[kb][v] != 0)) s = p.fill;
+        sv[kb][v] = s;
+        tmax = fmaxf(tmax, s);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    // A fill of -inf can leave a tile with no finite score; keep the state.
+    const bool none = m_new == -INFINITY;
+    const float corr = none ? 1.0f : __expf(m_run - m_new);
+    float lsum = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        sv[kb][v] = none ? 0.0f : __expf(sv[kb][v] - m_new);
+        lsum += sv[kb][v];
+      }
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    l_run = l_run * corr + lsum;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) oacc[db] *= corr;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[kb][v][db], sv[kb][v], oacc[db], 0,
+                                                          0, 0);
+  }
+
+  // oacc[db] register v: dim 16db + 4g + v of query r.
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) obuf[wave][r][16 * db + 4 * g + v] = oacc[db][v];
+  if (g == 0) {
+    sm[wave][r] = m_run;
+    sl[wave][r] = l_run;
+  }
+  __syncthreads();
+  if (qi >= S) return;
+  float M = sm[0][r];
+#pragma unroll
+  for (int w = 1; w < KW; ++w) M = fmaxf(M, sm[w][r]);
+  float cw[KW], L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < KW; ++w) {
+    cw[w] = __expf(sm[w][r] - M);  // 0 for a wave that saw no tile (m = -inf)
+    L += cw[w] * sl[w][r];
+  }
+  const float inv = 1.0f / L;
+  float* orow = p.out + (b * S + qi) * p.ldo + h * kD;
+  for (int db = wave; db < 4; db += KW) {
+    float o[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int w = 0; w < KW; ++w) acc += cw[w] * obuf[w][r][16 * db + 4 * g + v];
+      o[v] = acc * inv;
+    }
+    *reinterpret_cast<float4*>(orow + 16 * db + 4 * g) = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // Any head_dim up to 256: one thread per (b, h, query) with an online softmax
 // over the keys. Used for shapes the MFMA kernel does not cover.
 constexpr int kMaxGenericD = 256;
@@ -413,7 +571,13 @@ void attention(inferc_hip_ctx* ctx, const AttnArgs& a) {
   if (a.head_dim == kD) {
     IH_REQUIRE(a.B < 65536 && p.nH < 65536, INFERC_ERR_SHAPE, "attention: grid too large");
     const int64_t blocks4 = ceil_div(a.S, 128) * p.nH * a.B;
-    if (blocks4 >= ctx->num_cus) {
+    const bool vec = a.ldq % 4 == 0 && a.ldk % 4 == 0 && a.ldv % 4 == 0 && a.ldo % 4 == 0 &&
+                     aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.out);
+    if (blocks4 < ctx->num_cus && vec) {
+      // few blocks: 16 queries per block, four waves splitting the key tiles
+      dim3 grid(unsigned(ceil_div(a.S, 16)), unsigned(p.nH), unsigned(a.B));
+      hipLaunchKernelGGL(attn_fwd_d64_q16<4>, grid, dim3(256), 0, ctx->stream, p);
+    } else if (blocks4 >= ctx->num_cus) {
       dim3 grid(unsigned(ceil_div(a.S, 128)), unsigned(p.nH), unsigned(a.B));
       hipLaunchKernelGGL(attn_fwd_d64<4>, grid, dim3(256), 0, ctx->stream, p);
     } else {
