@@ -571,6 +571,20 @@ void gemm(inferc_hip_ctx* ctx, const GemmArgs& a) {
                  a.batch < 4096,
              INFERC_ERR_SHAPE, "gemm: problem too large for one launch grid");
 
+  // One row times a [N,K] row-major B^T is the batch-1 GEMV, which the
+  // reference also sends to sgemv (src/kernels/matmul.cc:207-216). The GEMV
+  // applies bias, residual and act in the GEMM's order.
+  if (a.M == 1 && a.batch == 1 && !a.trans_a && a.trans_b && a.alpha == 1.0f && a.ldb == a.K &&
+      a.K > 0 && a.K <= 16384 &&
+      (a.c_kind == INFERC_C_NONE || a.beta == 0.0f ||
+       ((a.c_kind == INFERC_C_ROW || a.c_kind == INFERC_C_FULL) && a.beta == 1.0f))) {
+    // with one row, a full C is a row of N values like a bias
+    const bool has_c = (a.c_kind == INFERC_C_ROW || a.c_kind == INFERC_C_FULL) && a.beta != 0.0f;
+    const float* bias = has_c ? a.C : nullptr;
+    gemv(ctx, a.N, a.K, a.B, a.A, nullptr, nullptr, 0.0f, bias, a.R, a.act, a.Y);
+    return;
+  }
+
   GemmParams p{};
   p.M = a.M; p.N = a.N; p.K = a.K;
   p.A = a.A; p.lda = a.lda; p.sa = a.stride_a;

@@ -33,15 +33,20 @@ __global__ __launch_bounds__(kBlock) void layernorm_kernel(int64_t rows, int64_t
   float* yr = y + row * feat;
   const float inv_n = 1.0f / float(feat);
   if (feat <= 64 * VPL) {
-    float v[VPL];
-    float s = 0.0f;
+    // gamma and beta are loaded with x, so the row costs one memory round
+    // trip before the reductions instead of a second one after them.
+    float v[VPL], gv[VPL], bv[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int64_t c = lane + 64 * i;
-      v[i] = 0.0f;
-      if (c < feat) v[i] = rr ? xr[c] + rr[c] : xr[c];
-      s += v[i];
+      const bool in = c < feat;
+      v[i] = in ? (rr ? xr[c] + rr[c] : xr[c]) : 0.0f;
+      gv[i] = in ? g[c] : 0.0f;
+      bv[i] = in ? b[c] : 0.0f;
     }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) s += v[i];
     const float mean = wave_sum(s) * inv_n;
     float q = 0.0f;
 #pragma unroll
@@ -56,7 +61,7 @@ __global__ __launch_bounds__(kBlock) void layernorm_kernel(int64_t rows, int64_t
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int64_t c = lane + 64 * i;
-      if (c < feat) yr[c] = (v[i] * inv) * g[c] + b[c];
+      if (c < feat) yr[c] = (v[i] * inv) * gv[i] + bv[i];
     }
     return;
   }

@@ -121,6 +121,20 @@ def test_gemm_epilogues(ctx, act):
     close(got, ref)
 
 
+@pytest.mark.parametrize("N,K", [(2, 768), (768, 768), (50, 3072), (33, 100)])
+def test_gemm_single_row_transb_epilogues(ctx, N, K):
+    """M=1 with B^T takes the GEMV route (matmul.cc:207-216); bias, residual and
+    activation must match the GEMM epilogue."""
+    A, B = rnd((1, K), 90 + N), rnd((N, K), 91 + K, 0.05)
+    bias, res = rnd(N, 92), rnd((1, N), 93)
+    for act in (L.ACT_NONE, L.ACT_RELU, L.ACT_GELU_TANH):
+        got = rt.Gemm(T(ctx, A), T(ctx, B), T(ctx, bias), 1.0, 1.0, trans_b=True,
+                      residual=T(ctx, res), act=act).numpy()
+        v = (A.astype(np.float64) @ B.T.astype(np.float64) + bias) + res
+        ref = {L.ACT_NONE: v, L.ACT_RELU: np.maximum(v, 0), L.ACT_GELU_TANH: ref64.gelu_tanh(v)}[act]
+        close(got, ref)
+
+
 def test_gemm_c_kinds_alpha_beta(ctx):
     A, B = rnd((37, 29), 5), rnd((29, 41), 6)
     for C in (rnd(41, 7), rnd((37, 41), 8), np.array([1.5], np.float32)):
