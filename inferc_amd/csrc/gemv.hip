@@ -9,6 +9,8 @@
 // Both kernels are HBM-streaming: every weight byte is read exactly once per
 // call with 16-byte loads, the activation vector stays on chip, and the
 // row reductions are done in a fixed order (run-to-run deterministic).
+#include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <vector>
 
@@ -233,6 +235,41 @@ __global__ __launch_bounds__(kBlock) void gemv2_kernel(Gemv2P p) {
 
 // ---------------------------------------------------------------- int4 GEMV
 
+// Pointers read from a descriptor table are generic to the compiler, which
+// then emits flat accesses that wait on both memory counters and serialise.
+// They all point into device global memory, so access them as such.
+// (The integer round trip makes the cast stick; a direct pointer cast is
+// folded back to a generic access. Native vector types, not HIP's vector
+// classes, can be read through an address-space-qualified pointer.)
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 gload_u4(const uint4* p) {
+  const u32x4_t v = *reinterpret_cast<const __attribute__((address_space(1))) u32x4_t*>(
+      reinterpret_cast<uintptr_t>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 gload_f4(const float4* p) {
+  const f32x4_t v = *reinterpret_cast<const __attribute__((address_space(1))) f32x4_t*>(
+      reinterpret_cast<uintptr_t>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t gload_u32(const uint32_t* p) {
+  return *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(
+      reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ int64_t gload_i64(const int64_t* p) {
+  return *reinterpret_cast<const __attribute__((address_space(1))) int64_t*>(
+      reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ float gload_f(const float* p) {
+  return *reinterpret_cast<const __attribute__((address_space(1))) float*>(
+      reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ void gstore_f(float* p, float v) {
+  *reinterpret_cast<__attribute__((address_space(1))) float*>(reinterpret_cast<uintptr_t>(p)) = v;
+}
+
 // One matrix of a (grouped) int4 GEMV launch.
 struct Int4Mat {
   const uint8_t* W;  // [N, K/2], byte k/2 of row r: low nibble k even, high k odd
@@ -285,7 +322,7 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_kernel(const Int4Mat* __rest
   for (int j = 0; j < kRowsPerThread; ++j) {
     const int64_t r = rbase + g + int64_t(groups) * j;
     w[j] = make_uint4(0u, 0u, 0u, 0u);
-    if (active && r < m.N) w[j] = *reinterpret_cast<const uint4*>(m.W + r * rb + c * 16);
+    if (active && r < m.N) w[j] = gload_u4(reinterpret_cast<const uint4*>(m.W + r * rb + c * 16));
   }
   for (int b = 0; b < batch; ++b) {
     float acc[kRowsPerThread];
@@ -297,7 +334,7 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_kernel(const Int4Mat* __rest
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         // 8 consecutive k values: word q of the chunk holds k = 8q .. 8q+7.
-        const float4 xa = xp[2 * q], xb = xp[2 * q + 1];
+        const float4 xa = gload_f4(xp + 2 * q), xb = gload_f4(xp + 2 * q + 1);
         xsum += (xa.x + xa.y) + (xa.z + xa.w) + (xb.x + xb.y) + (xb.z + xb.w);
 #pragma unroll
         for (int j = 0; j < kRowsPerThread; ++j) {
@@ -334,8 +371,361 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_kernel(const Int4Mat* __rest
     const float* pp = part + (b * kRowsPerThread * groups + jg) * cpr;
     float s = 0.0f;
     for (int q = 0; q < cpr; ++q) s += pp[q];
-    m.y[b * m.N + r] = m.s[r] * s;
+    gstore_f(m.y + b * m.N + r, gload_f(m.s + r) * s);
   }
+}
+
+// Batch-1 int4 GEMV on the vector ALUs (the streaming form of the fp32
+// GEMV). Rows are contiguous in memory and L lanes share a row (L a power of
+// two, L * DW dwords = K/8): lane s owns dwords [DW*s, DW*s + DW) of every
+// row it visits, i.e. 8*DW consecutive weights, so one load instruction
+// covers 64/L whole consecutive rows and the lane's 8*DW x values are loaded
+// once per wave and reused for all of its rows. A wave-task is kI4Passes
+// passes of 64/L rows, all loads issued before any use. Row sums reduce over
+// the L lanes with a fixed butterfly (deterministic); the -8 offset is
+// folded: sum (nib-8) x = sum nib*x - 8*sum x. One launch serves two DW
+// values (the wave's matrix picks one, wave-uniformly), so matrices of two
+// row lengths overlap instead of running back to back; the descriptors live
+// in a device table.
+constexpr int kI4Passes = 4;
+
+struct Int4VaDesc {
+  const uint8_t* W;
+  const float* s;
+  const float* x;
+  float* y;
+  int64_t N, K;
+  int64_t task_begin;  // first wave-task of this matrix in the launch
+  int64_t dw;          // dwords per lane for this matrix
+};
+
+template <int DW>
+__device__ __forceinline__ void int4_valu_task(const Int4VaDesc& d, int64_t wid, int lane) {
+  constexpr int P = kI4Passes;
+  const int64_t N = d.N, K = d.K;
+  const int L = int((K / 8) / DW), rpp = 64 / L;
+  const int s = lane & (L - 1), rg = lane / L;
+  const int64_t rb = K / 2;
+  const int64_t row0 = (wid - d.task_begin) * int64_t(P) * rpp;
+
+  uint32_t w[P][DW];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int64_t r = row0 + int64_t(p) * rpp + rg;
+    const uint32_t* src =
+        reinterpret_cast<const uint32_t*>(d.W + (r < N ? r : N - 1) * rb) + DW * s;
+#pragma unroll
+    for (int q = 0; q < DW; ++q) w[p][q] = gload_u32(src + q);
+  }
+  float4 xv[2 * DW];
+  const float4* xp = reinterpret_cast<const float4*>(d.x + 8 * DW * s);
+#pragma unroll
+  for (int q = 0; q < 2 * DW; ++q) xv[q] = gload_f4(xp + q);
+  float sc[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int64_t r = row0 + int64_t(p) * rpp + rg;
+    sc[p] = gload_f(d.s + (r < N ? r : N - 1));
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before any use
+
+  float xsum = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 2 * DW; ++q) xsum += (xv[q].x + xv[q].y) + (xv[q].z + xv[q].w);
+  float acc[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float t = 0.0f;
+#pragma unroll
+    for (int q = 0; q < DW; ++q) {
+      // dword q holds k = 8q .. 8q+7 of the lane's slice (low nibble even k)
+      const uint32_t ev = w[p][q] & 0x0F0F0F0Fu, od = (w[p][q] >> 4) & 0x0F0F0F0Fu;
+      const float4 xa = xv[2 * q], xb = xv[2 * q + 1];
+      t += ubyte<0>(ev) * xa.x;
+      t += ubyte<0>(od) * xa.y;
+      t += ubyte<1>(ev) * xa.z;
+      t += ubyte<1>(od) * xa.w;
+      t += ubyte<2>(ev) * xb.x;
+      t += ubyte<2>(od) * xb.y;
+      t += ubyte<3>(ev) * xb.z;
+      t += ubyte<3>(od) * xb.w;
+    }
+    acc[p] = t - 8.0f * xsum;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    if (o < L) {
+#pragma unroll
+      for (int p = 0; p < P; ++p) acc[p] += __shfl_xor(acc[p], o, 64);
+    }
+  }
+  if (s == 0) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int64_t r = row0 + int64_t(p) * rpp + rg;
+      if (r < N) gstore_f(d.y + r, sc[p] * acc[p]);
+    }
+  }
+}
+
+template <int DA, int DB>
+__global__ __launch_bounds__(kBlock) void int4_gemv_valu_kernel(const Int4VaDesc* __restrict__ tab,
+                                                               int n, int64_t n_waves) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = int64_t(blockIdx.x) * (kBlock / 64) +
+                      __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  if (wid >= n_waves) return;
+  int cnt = 0;  // this wave's matrix (task_begin ascends), one ballot per 64 entries
+  for (int base = 0; base < n; base += 64) {
+    const int j = base + lane;
+    const int c = __popcll(__ballot(j < n && gload_i64(&tab[j].task_begin) <= wid));
+    cnt += c;
+    if (c < 64) break;
+  }
+  const Int4VaDesc d = tab[__builtin_amdgcn_readfirstlane(cnt - 1)];
+  if (DA == DB || d.dw == DA)
+    int4_valu_task<DA>(d, wid, lane);
+  else
+    int4_valu_task<DB>(d, wid, lane);
+}
+
+// int4 GEMV on the int8 matrix cores, exact in integer arithmetic.
+//
+// The dequantised product is y[b][r] = s_r * sum_k (nib - 8) x[b][k]. The
+// kernel computes sum_k nib * x - 8 * sum_k x exactly:
+//   - nibbles (0..15) are int8 operands as they sit in memory, after one
+//     mask (even k) or shift+mask (odd k) per dword;
+//   - x[b] becomes a fixed-point integer X = rint(x * 2^F), with F chosen from
+//     max|x[b]| so that |X| < 2^30, split into four signed int8 limbs
+//     X = d0 + 2^8 d1 + 2^16 d2 + 2^24 d3;
+//   - v_mfma_i32_16x16x64_i8 multiplies 16 rows of nibbles with 16 columns of
+//     limbs (4 limbs x up to 4 batches) and accumulates exactly in int32;
+//   - each limb's integer sum (below 2^24) converts exactly to fp32 and is
+//     scaled by an exact power of two; y = s_r * (sum of the 4 limb terms).
+// The approximations are x's rounding to 2^-F (about 2^-30 of max|x[b]|) and
+// the last few fp32 roundings: the long sum over k itself is exact, closer
+// to the reference's double accumulation (int4_gemv_amx.cc:258-271) than an
+// fp32 dot product.
+//
+// Layout. A "unit" is 16 rows of one matrix. In step t (128 k) lane (r, g)
+// (r = lane%16, g = lane/16) loads the 16 bytes of row r at byte 64t + 16g:
+// 32 nibbles, 16 even-k and 16 odd-k, the A operands of two MFMAs. The MFMA
+// pairs A byte j of lane group g with B byte j of lane group g; B byte j of
+// lane (c, g) is limb c%4 of x[c/4][128t + 32g + 2j] (+1 for the odd MFMA).
+// The B operands depend only on x, so a block writes them to LDS once per
+// matrix and reuses them for every unit it streams.
+//
+// Scheduling. One launch per K (= 128*STEPS, so registers are sized
+// exactly). A block owns a few units and issues all of their weight loads
+// first; the x preparation then overlaps those loads. For long rows two
+// waves share a unit, each taking half of K, and add their exact partial
+// sums through LDS. The matrix descriptors live in a device table (uploaded
+// once, cached): a multi-kilobyte kernel argument would be copied by a blit
+// before every launch of a captured graph.
+constexpr int kI4MaxK = 3072;      // B operands in LDS: K * 16 bytes
+constexpr int kI4Batch = 4;        // batches per pass: 4 limbs x 4 = 16 columns
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+struct Int4MfDesc {
+  const uint8_t* W;
+  const float* s;
+  const float* x;  // [nb, K] (this pass's batches)
+  float* y;        // [nb, N]
+  int64_t N;
+  int64_t block_begin;  // first block of this matrix in the launch
+};
+
+// Work split for K = 128*STEPS. KS waves share a unit (16 rows), each taking
+// STEPS/KS of the steps, so long rows still give enough blocks; a wave group
+// owns RBW units. Rows per block = (4/KS) * RBW * 16.
+__host__ __device__ constexpr int i4_ks(int steps) { return steps >= 16 ? 2 : 1; }
+__host__ __device__ constexpr int i4_rbw(int steps) { return steps >= 6 ? 1 : steps >= 4 ? 2 : 4; }
+__host__ __device__ constexpr int i4_rows_per_block(int steps) {
+  return (kBlock / 64 / i4_ks(steps)) * i4_rbw(steps) * 16;
+}
+__host__ __device__ constexpr bool i4_steps_ok(int steps) {
+  return steps == 2 || steps == 4 || steps == 6 || steps == 8 || steps == 12 || steps == 16 ||
+         steps == 24;
+}
+
+struct I4Shared {
+  uint32_t bop[kI4MaxK * 4];  // B operands: [step][even/odd][lane][4 dwords]
+  float smax[kBlock / 64][kI4Batch];
+  i32x4_t part[kBlock / 64][64];  // K-split partial sums (one unit per wave)
+};
+
+// Quad-lane exchange (lanes 4i..4i+3) without LDS: DPP quad permutes.
+template <int XOR>
+__device__ __forceinline__ float quad_xor_f(float v) {
+  constexpr int ctrl = XOR == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+}
+
+template <int STEPS>
+__global__ __launch_bounds__(kBlock) void int4_gemv_mfma_kernel(const Int4MfDesc* __restrict__ tab,
+                                                               int n, int nb) {
+  constexpr int KS = i4_ks(STEPS), RBW = i4_rbw(STEPS), SPW = STEPS / KS;
+  constexpr int K = 128 * STEPS, KPT = K / kBlock;  // x values per thread per batch
+  static_assert(K % kBlock == 0, "K must split evenly over the block");
+  __shared__ __attribute__((aligned(16))) I4Shared sh;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave / KS, part = wave % KS;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t bid = blockIdx.x;
+  // This block's matrix: how many table entries start at or before bid
+  // (block_begin ascends), one ballot per 64 entries.
+  int cnt = 0;
+  for (int base = 0; base < n; base += 64) {
+    const int j = base + lane;
+    const int c = __popcll(__ballot(j < n && gload_i64(&tab[j].block_begin) <= bid));
+    cnt += c;
+    if (c < 64) break;
+  }
+  const Int4MfDesc d = tab[__builtin_amdgcn_readfirstlane(cnt - 1)];
+  const int64_t N = d.N;
+  const int64_t r0 = (bid - d.block_begin) * i4_rows_per_block(STEPS) + int64_t(grp) * RBW * 16;
+
+  // 1. every weight this wave needs, its rows' scales, this thread's x
+  uint4 w[RBW][SPW];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
+    const int64_t row = r0 + rb * 16 + r;
+    const uint8_t* rp = d.W + (row < N ? row : N - 1) * int64_t(K / 2);
+#pragma unroll
+    for (int t = 0; t < SPW; ++t)
+      w[rb][t] = gload_u4(reinterpret_cast<const uint4*>(rp + 64 * (part * SPW + t) + 16 * g));
+  }
+  float scv[RBW][4];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t row = r0 + rb * 16 + 4 * g + v;
+      scv[rb][v] = gload_f(d.s + (row < N ? row : N - 1));
+    }
+  float xr[kI4Batch][KPT];
+#pragma unroll
+  for (int b = 0; b < kI4Batch; ++b)
+#pragma unroll
+    for (int i = 0; i < KPT; ++i)
+      xr[b][i] = b < nb ? gload_f(d.x + int64_t(b) * K + tid + kBlock * i) : 0.0f;
+
+  // 2. x -> fixed-point limbs in the B-operand layout (overlaps the weights)
+  for (int i = tid; i < K; i += kBlock)  // unused columns stay zero
+    *reinterpret_cast<uint4*>(sh.bop + 4 * i) = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int b = 0; b < kI4Batch; ++b) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      // fmaxf would drop a NaN, so a non-finite |x| enters the maximum as inf
+      const float ax = fabsf(xr[b][i]);
+      m = ax <= 3.4028235e38f ? fmaxf(m, ax) : INFINITY;
+    }
+    m = wave_max(m);
+    if (lane == 0) sh.smax[wave][b] = m;
+  }
+  __syncthreads();
+  int F[kI4Batch];
+  bool finite[kI4Batch];
+#pragma unroll
+  for (int b = 0; b < kI4Batch; ++b) {
+    float m = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < kBlock / 64; ++w2) m = fmaxf(m, sh.smax[w2][b]);
+    finite[b] = m <= 3.4028235e38f;
+    if (!finite[b]) m = 0.0f;
+    int e = 0;
+    (void)frexpf(m, &e);  // m < 2^e
+    F[b] = m > 0.0f ? 30 - e : 0;
+  }
+  uint8_t* bb = reinterpret_cast<uint8_t*>(sh.bop);
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int k = tid + kBlock * i;
+    const int st = k >> 7, kk = k & 127, gg = kk >> 5, q = kk & 31;
+    const int eo = q & 1, j = q >> 1;
+#pragma unroll
+    for (int b = 0; b < kI4Batch; ++b) {
+      if (b >= nb) break;
+      int X = finite[b] ? int(rintf(ldexpf(xr[b][i], F[b]))) : 0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int dg = c < 3 ? ((X + 128) & 255) - 128 : X;  // balanced digit; top in [-64, 64]
+        X = (X - dg) >> 8;
+        bb[(((2 * st + eo) * 64 + (4 * b + c) + 16 * gg) * 16) + j] = uint8_t(int8_t(dg));
+      }
+    }
+  }
+  __syncthreads();
+
+  // 3. the fold term sum_k X per column: an MFMA with an all-ones A
+  const i32x4_t ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+  i32x4_t fold = {0, 0, 0, 0};
+#pragma unroll
+  for (int t = 0; t < STEPS; ++t) {
+    const i32x4_t be = *reinterpret_cast<const i32x4_t*>(sh.bop + ((2 * t) * 64 + lane) * 4);
+    const i32x4_t bo = *reinterpret_cast<const i32x4_t*>(sh.bop + ((2 * t + 1) * 64 + lane) * 4);
+    fold = __builtin_amdgcn_mfma_i32_16x16x64_i8(ones, be, fold, 0, 0, 0);
+    fold = __builtin_amdgcn_mfma_i32_16x16x64_i8(ones, bo, fold, 0, 0, 0);
+  }
+
+  // 4. this wave's steps of each of its units
+  i32x4_t acc[RBW];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
+    acc[rb] = i32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < SPW; ++t) {
+      const int st = part * SPW + t;
+      const uint4 q = w[rb][t];
+      const i32x4_t ev = {int(q.x & 0x0F0F0F0Fu), int(q.y & 0x0F0F0F0Fu), int(q.z & 0x0F0F0F0Fu),
+                          int(q.w & 0x0F0F0F0Fu)};
+      const i32x4_t od = {int((q.x >> 4) & 0x0F0F0F0Fu), int((q.y >> 4) & 0x0F0F0F0Fu),
+                          int((q.z >> 4) & 0x0F0F0F0Fu), int((q.w >> 4) & 0x0F0F0F0Fu)};
+      const i32x4_t be = *reinterpret_cast<const i32x4_t*>(sh.bop + ((2 * st) * 64 + lane) * 4);
+      const i32x4_t bo = *reinterpret_cast<const i32x4_t*>(sh.bop + ((2 * st + 1) * 64 + lane) * 4);
+      acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ev, be, acc[rb], 0, 0, 0);
+      acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(od, bo, acc[rb], 0, 0, 0);
+    }
+  }
+  if constexpr (KS > 1) {
+    static_assert(RBW == 1, "a K-split wave owns one unit");
+    // the other K parts hand their exact partial sums to part 0
+    if (part != 0) sh.part[wave][lane] = acc[0];
+    __syncthreads();
+    if (part != 0) return;
+#pragma unroll
+    for (int p2 = 1; p2 < KS; ++p2) acc[0] += sh.part[wave + p2][lane];
+  }
+
+  // 5. acc[rb][v]: row 4g+v of unit rb, column col = (batch cb, limb cl). Each
+  //    limb term acc - 8*fold is below 2^24 in magnitude, so it and its
+  //    power-of-two scaling are exact in fp32; a batch's 4 terms (a lane
+  //    quad) are summed in fp32.
+  const int col = lane & 15, cb = col >> 2, cl = col & 3;
+  int Fc = 0;
+  bool okc = true;
+#pragma unroll
+  for (int b = 0; b < kI4Batch; ++b) {
+    Fc = b == cb ? F[b] : Fc;
+    okc = b == cb ? finite[b] : okc;
+  }
+  const int sh_exp = 8 * cl - Fc;
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float t = ldexpf(float(acc[rb][v] - 8 * fold[v]), sh_exp);
+      t += quad_xor_f<1>(t);
+      t += quad_xor_f<2>(t);
+      const int64_t row = r0 + rb * 16 + 4 * g + v;
+      if (cl == 0 && cb < nb && row < N)
+        // a non-finite x makes the whole output non-finite, as in the reference
+        gstore_f(d.y + int64_t(cb) * N + row, okc ? scv[rb][v] * t : __int_as_float(0x7fc00000));
+    }
 }
 
 // Fallback for K not a multiple of 32: one thread per (b, row), exact formula.
@@ -473,27 +863,30 @@ namespace {
 
 // Device copies of recently used grouped-GEMV descriptor tables, keyed by
 // their bytes, so repeated calls with the same matrices skip the upload.
+template <class T>
 struct TableCache {
   struct Entry {
-    std::vector<Int4Mat> key;
-    Int4Mat* dev = nullptr;
+    std::vector<T> key;
+    T* dev = nullptr;
   };
   std::vector<Entry> entries;
 };
 
-TableCache& table_cache(inferc_hip_ctx* ctx) {
-  static thread_local std::vector<std::pair<inferc_hip_ctx*, TableCache>> caches;
+template <class T>
+TableCache<T>& table_cache(inferc_hip_ctx* ctx) {
+  static thread_local std::vector<std::pair<inferc_hip_ctx*, TableCache<T>>> caches;
   for (auto& c : caches)
     if (c.first == ctx) return c.second;
-  caches.emplace_back(ctx, TableCache{});
+  caches.emplace_back(ctx, TableCache<T>{});
   return caches.back().second;
 }
 
-const Int4Mat* upload_table(inferc_hip_ctx* ctx, const std::vector<Int4Mat>& mats) {
-  TableCache& tc = table_cache(ctx);
+template <class T>
+const T* upload_table(inferc_hip_ctx* ctx, const std::vector<T>& mats) {
+  TableCache<T>& tc = table_cache<T>(ctx);
   for (auto& e : tc.entries)
     if (e.key.size() == mats.size() &&
-        std::memcmp(e.key.data(), mats.data(), mats.size() * sizeof(Int4Mat)) == 0)
+        std::memcmp(e.key.data(), mats.data(), mats.size() * sizeof(T)) == 0)
       return e.dev;
   IH_REQUIRE(!ctx->capturing, INFERC_ERR_STATE,
              "int4 grouped GEMV: descriptor table must be uploaded before graph capture");
@@ -502,12 +895,118 @@ const Int4Mat* upload_table(inferc_hip_ctx* ctx, const std::vector<Int4Mat>& mat
     for (auto& e : tc.entries) (void)hipFree(e.dev);
     tc.entries.clear();
   }
-  TableCache::Entry e;
+  typename TableCache<T>::Entry e;
   e.key = mats;
-  IH_HIP(hipMalloc(&e.dev, mats.size() * sizeof(Int4Mat)));
-  IH_HIP(hipMemcpy(e.dev, mats.data(), mats.size() * sizeof(Int4Mat), hipMemcpyHostToDevice));
+  IH_HIP(hipMalloc(&e.dev, mats.size() * sizeof(T)));
+  IH_HIP(hipMemcpy(e.dev, mats.data(), mats.size() * sizeof(T), hipMemcpyHostToDevice));
   tc.entries.push_back(std::move(e));
   return tc.entries.back().dev;
+}
+
+struct Int4MfMat {
+  const uint8_t* W;
+  const float* s;
+  const float* x;
+  float* y;
+  int64_t N, K;
+};
+
+// Shapes the int8-MFMA kernel takes: K = 128*STEPS for a supported STEPS,
+// 16-byte aligned rows.
+bool int4_mfma_ok(int64_t K, const uint8_t* W) {
+  return K > 0 && K % 128 == 0 && K <= kI4MaxK && i4_steps_ok(int(K / 128)) && aligned16(W);
+}
+
+template <int STEPS>
+void launch_int4_mfma_k(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats, int64_t batch) {
+  if (mats.empty()) return;
+  for (int64_t b0 = 0; b0 < batch; b0 += kI4Batch) {
+    const int nb = int(std::min<int64_t>(kI4Batch, batch - b0));
+    std::vector<Int4MfDesc> tab;
+    int64_t blocks = 0;
+    for (const Int4MfMat& m : mats) {
+      Int4MfDesc dsc{};
+      dsc.W = m.W; dsc.s = m.s;
+      dsc.x = m.x + b0 * m.K;
+      dsc.y = m.y + b0 * m.N;
+      dsc.N = m.N;
+      dsc.block_begin = blocks;
+      blocks += ceil_div(m.N, int64_t(i4_rows_per_block(STEPS)));
+      tab.push_back(dsc);
+    }
+    IH_REQUIRE(blocks < (int64_t(1) << 31) && tab.size() < (size_t(1) << 20), INFERC_ERR_SHAPE,
+               "int4 gemv: launch too large");
+    const Int4MfDesc* dev = upload_table(ctx, tab);
+    hipLaunchKernelGGL(int4_gemv_mfma_kernel<STEPS>, dim3(unsigned(blocks)), dim3(kBlock), 0,
+                       ctx->stream, dev, int(tab.size()), nb);
+    check_launch("int4_gemv_mfma");
+  }
+}
+
+// Groups the matrices by K and launches each group.
+void launch_int4_mfma(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats, int64_t batch) {
+  std::vector<Int4MfMat> by_k[kI4MaxK / 128 + 1];
+  for (const Int4MfMat& m : mats) by_k[m.K / 128].push_back(m);
+  launch_int4_mfma_k<2>(ctx, by_k[2], batch);
+  launch_int4_mfma_k<4>(ctx, by_k[4], batch);
+  launch_int4_mfma_k<6>(ctx, by_k[6], batch);
+  launch_int4_mfma_k<8>(ctx, by_k[8], batch);
+  launch_int4_mfma_k<12>(ctx, by_k[12], batch);
+  launch_int4_mfma_k<16>(ctx, by_k[16], batch);
+  launch_int4_mfma_k<24>(ctx, by_k[24], batch);
+}
+
+// Dwords per lane for the VALU kernel: L = (K/8)/DW lanes per row must be a
+// power of two no larger than 64. 0 if none fits.
+int int4_valu_dw(int64_t K) {
+  if (K <= 0 || K % 8) return 0;
+  const int64_t dwords = K / 8;
+  for (int dw : {3, 6, 2, 4}) {
+    if (dwords % dw) continue;
+    const int64_t l = dwords / dw;
+    if (l >= 1 && l <= 64 && (l & (l - 1)) == 0) return dw;
+  }
+  return 0;
+}
+
+// One launch over matrices whose DW is DA or DB. The larger tasks go first
+// (wider DW = more bytes per wave-task), so the short ones fill the tail.
+template <int DA, int DB>
+void launch_int4_valu_pair(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& a,
+                           const std::vector<Int4MfMat>& b) {
+  if (a.empty() && b.empty()) return;
+  std::vector<Int4VaDesc> tab;
+  int64_t waves = 0;
+  auto add = [&](const std::vector<Int4MfMat>& mats, int dw) {
+    for (const Int4MfMat& m : mats) {
+      const int64_t L = (m.K / 8) / dw;
+      tab.push_back(Int4VaDesc{m.W, m.s, m.x, m.y, m.N, m.K, waves, dw});
+      waves += ceil_div(m.N, int64_t(kI4Passes) * (64 / L));
+    }
+  };
+  add(DA >= DB ? a : b, DA >= DB ? DA : DB);
+  if (DA != DB) add(DA >= DB ? b : a, DA >= DB ? DB : DA);
+  IH_REQUIRE(ceil_div(waves, kBlock / 64) < (int64_t(1) << 31), INFERC_ERR_SHAPE,
+             "int4 gemv: launch too large");
+  const Int4VaDesc* dev = upload_table(ctx, tab);
+  hipLaunchKernelGGL((int4_gemv_valu_kernel<DA, DB>), dim3(unsigned(ceil_div(waves, kBlock / 64))),
+                     dim3(kBlock), 0, ctx->stream, dev, int(tab.size()), waves);
+  check_launch("int4_gemv_valu");
+}
+
+void launch_int4_valu(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats) {
+  std::vector<Int4MfMat> by_dw[7];
+  for (const Int4MfMat& m : mats) by_dw[int4_valu_dw(m.K)].push_back(m);
+  static const std::vector<Int4MfMat> none;
+  // the pair a transformer's matrices form (K = 768 and 4 * 768) in one launch
+  if (!by_dw[3].empty() && !by_dw[6].empty()) {
+    launch_int4_valu_pair<6, 3>(ctx, by_dw[6], by_dw[3]);
+  } else {
+    launch_int4_valu_pair<3, 3>(ctx, by_dw[3], none);
+    launch_int4_valu_pair<6, 6>(ctx, by_dw[6], none);
+  }
+  launch_int4_valu_pair<2, 2>(ctx, by_dw[2], none);
+  launch_int4_valu_pair<4, 4>(ctx, by_dw[4], none);
 }
 
 void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const int64_t* Ks,
@@ -519,6 +1018,8 @@ void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const 
   if (n_mats == 0) return;
   IH_REQUIRE(Ns && Ks && W && scales && x && y, INFERC_ERR_ARG, "int4 gemv: null array");
   std::vector<Int4Mat> mats;
+  std::vector<Int4MfMat> mf;  // int8-MFMA form
+  std::vector<Int4MfMat> va;  // batch-1 VALU streaming form
   int64_t blocks = 0;
   for (int64_t i = 0; i < n_mats; ++i) {
     const int64_t N = Ns[i], K = Ks[i];
@@ -528,6 +1029,18 @@ void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const 
                "int4 gemv: null pointer");
     const bool fast = K > 0 && K % 32 == 0 && K / 32 <= kBlock && aligned16(W[i]) &&
                       aligned16(x[i]);
+    // batch 1: the VALU streaming kernel (read the fewest bytes per output);
+    // several batches: the int8 matrix-core kernel (VALU work would grow with
+    // the batch, matrix-core work barely does)
+    if (batch == 1 && int4_valu_dw(K) > 0 && aligned16(x[i]) &&
+        (reinterpret_cast<uintptr_t>(W[i]) & 3) == 0) {
+      va.push_back(Int4MfMat{W[i], scales[i], x[i], y[i], N, K});
+      continue;
+    }
+    if (int4_mfma_ok(K, W[i])) {
+      mf.push_back(Int4MfMat{W[i], scales[i], x[i], y[i], N, K});
+      continue;
+    }
     if (!fast) {
       // Odd shapes run alone through the exact per-row kernel.
       const int64_t t = N * batch;
@@ -545,6 +1058,8 @@ void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const 
     blocks += ceil_div(N, int64_t(m.groups) * kRowsPerThread);
     mats.push_back(m);
   }
+  launch_int4_valu(ctx, va);
+  launch_int4_mfma(ctx, mf, batch);
   if (mats.empty()) return;
   IH_REQUIRE(blocks < (int64_t(1) << 31), INFERC_ERR_SHAPE, "int4 gemv: launch too large");
   const Int4Mat* dev = upload_table(ctx, mats);

@@ -330,9 +330,44 @@ def test_int4_grouped_full_gpt2_volume(ctx):
             _int4_close(y.numpy(), W, s, x, K)
 
 
-def test_int4_deterministic(ctx):
+@pytest.mark.parametrize("scale", [1e-30, 1.0, 1e30])
+def test_int4_gemv_batches_and_x_scale(ctx, scale):
+    """Five batches (a pass of four plus one) and x spanning 60 decades: the
+    fixed-point exponent is chosen per batch from max|x|."""
+    N, K, B = 300, 768, 5
+    W, s = graphs.int4_weights(N, K, 98, "scale")
+    x = (rnd((B, K), 99) * np.float32(scale)).astype(np.float32)
+    x[3] *= np.float32(1e-3)  # batches of different magnitude in one pass
+    got = rt.Int4Gemv(T(ctx, W, np.uint8), T(ctx, s), T(ctx, x), K).numpy()
+    assert np.all(np.isfinite(got))
+    _int4_close(got, W, s, x, K)
+
+
+def test_int4_gemv_nan_propagates(ctx):
+    N, K = 64, 768
+    W, s = graphs.int4_weights(N, K, 100, "nan")
+    x = rnd((2, K), 101)
+    x[1, 17] = np.nan
+    got = rt.Int4Gemv(T(ctx, W, np.uint8), T(ctx, s), T(ctx, x), K).numpy()
+    assert np.all(np.isnan(got[1]))
+    _int4_close(got[:1], W, s, x[:1], K)
+
+
+def test_int4_reference_stand_in_shape(ctx):
+    """The reference's own benchmark matrix, N=60000 x K=2048 (int4_gemv_amx.cc:550),
+    batch 1; rows checked on a slice to keep the float64 bound cheap."""
+    N, K = 60000, 2048
+    W, s = graphs.int4_weights(N, K, 96, "standin")
+    x = rnd((1, K), 97)
+    got = rt.Int4Gemv(T(ctx, W, np.uint8), T(ctx, s), T(ctx, x), K).numpy()
+    for lo in (0, N - 4096):
+        _int4_close(got[:, lo:lo + 4096], W[lo:lo + 4096], s[lo:lo + 4096], x, K)
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_int4_deterministic(ctx, B):
     W, s = graphs.int4_weights(3072, 768, 94, "det")
-    x = rnd((8, 768), 95)
+    x = rnd((B, 768), 95)
     a, b, c = T(ctx, W, np.uint8), T(ctx, s), T(ctx, x)
     first = rt.Int4Gemv(a, b, c, 768).numpy()
     np.testing.assert_array_equal(rt.Int4Gemv(a, b, c, 768).numpy(), first)
