@@ -291,6 +291,16 @@ __device__ __forceinline__ float ubyte(uint32_t v) {
   return float((v >> (8 * N)) & 0xFFu);
 }
 
+// v & 0x0F0F0F0F with the result's known bits hidden from the optimiser: if
+// it sees that the high nibble of every byte is zero, it rewrites each
+// ubyte<N> of the result as a 4-bit field extract plus ubyte<0> (two
+// instructions where v_cvt_f32_ubyteN alone suffices).
+__device__ __forceinline__ uint32_t low_nibbles(uint32_t v) {
+  uint32_t r;
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
 // Layout of the work: thread t of a block owns chunk c = t % cpr of rows
 // r0 + t/cpr + groups*j (j < 4), so its 32 x values (fp32) are loaded once and
 // reused for 4 rows. Nibbles become floats with v_cvt_f32_ubyteN, and the
@@ -339,8 +349,8 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_kernel(const Int4Mat* __rest
 #pragma unroll
         for (int j = 0; j < kRowsPerThread; ++j) {
           const uint32_t word = (q == 0) ? w[j].x : (q == 1) ? w[j].y : (q == 2) ? w[j].z : w[j].w;
-          const uint32_t ev = word & 0x0F0F0F0Fu;         // nibbles of k = 8q + 0,2,4,6
-          const uint32_t od = (word >> 4) & 0x0F0F0F0Fu;  // nibbles of k = 8q + 1,3,5,7
+          const uint32_t ev = low_nibbles(word);       // nibbles of k = 8q + 0,2,4,6
+          const uint32_t od = low_nibbles(word >> 4);  // nibbles of k = 8q + 1,3,5,7
           float a = acc[j];
           a += ubyte<0>(ev) * xa.x;
           a += ubyte<0>(od) * xa.y;
@@ -379,15 +389,36 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_kernel(const Int4Mat* __rest
 // GEMV). Rows are contiguous in memory and L lanes share a row (L a power of
 // two, L * DW dwords = K/8): lane s owns dwords [DW*s, DW*s + DW) of every
 // row it visits, i.e. 8*DW consecutive weights, so one load instruction
-// covers 64/L whole consecutive rows and the lane's 8*DW x values are loaded
-// once per wave and reused for all of its rows. A wave-task is kI4Passes
-// passes of 64/L rows, all loads issued before any use. Row sums reduce over
-// the L lanes with a fixed butterfly (deterministic); the -8 offset is
-// folded: sum (nib-8) x = sum nib*x - 8*sum x. One launch serves two DW
-// values (the wave's matrix picks one, wave-uniformly), so matrices of two
-// row lengths overlap instead of running back to back; the descriptors live
-// in a device table.
+// covers 64/L whole consecutive rows. A chunk is kI4Passes passes of 64/L
+// rows. Each wave streams a run of consecutive chunks of one matrix (about
+// kI4RunKB of weights): it prepares its 8*DW x values once, then
+// software-pipelines the run, issuing the loads of chunk c+2 before it
+// computes chunk c+1 (a ring of two register buffers), so its memory
+// requests stay in flight while it computes. For the transformer row
+// lengths the run is fully unrolled; other shapes loop.
+//
+// Arithmetic per dword w (8 nibbles, low nibble = even k): with
+// e = w & 0x0F0F0F0F (even nibbles) and b_i = byte i of w = e_i + 16 o_i,
+//   sum_i e_i x[2i] + o_i x[2i+1] = sum_i e_i (x[2i] - x[2i+1]/16)
+//                                 + sum_i b_i (x[2i+1]/16),
+// i.e. one mask, eight v_cvt_f32_ubyteN and eight FMAs per 8 weights (the
+// x terms are prepared once per wave; x/16 is an exact power-of-two
+// scaling for normal x). The -8 offset is
+// folded: sum (nib-8) x = sum nib*x - 8*sum x.
+//
+// Reduction over the L lanes of a row, in a fixed order (deterministic).
+// For a compile-time L >= 4 it is a reduce-scatter: two exchanges spread
+// the chunk's 4 rows over the lanes (lane s ends up with row s / (L/4)),
+// then log2(L/4) DPP steps finish the sums; lane s keeps chunk s % (L/4)
+// of its run, so every result is stored once, after the loop (a store
+// inside the pipelined loop would tie up registers the next loads need).
+// Other L reduce all 4 rows over all L lanes and lane s keeps chunk s.
+// One launch serves two (DW, L) forms (the wave's matrix picks one,
+// wave-uniformly), so matrices of two row lengths overlap instead of
+// running back to back; the descriptors live in a device table.
 constexpr int kI4Passes = 4;
+constexpr int kI4RunKB = 12;  // weights per wave of the unrolled run
+constexpr int kI4Ring = 2;    // chunks in flight per wave
 
 struct Int4VaDesc {
   const uint8_t* W;
@@ -395,80 +426,224 @@ struct Int4VaDesc {
   const float* x;
   float* y;
   int64_t N, K;
-  int64_t task_begin;  // first wave-task of this matrix in the launch
+  int64_t task_begin;  // first wave of this matrix in the launch
   int64_t dw;          // dwords per lane for this matrix
+  int64_t chunks;      // chunks of this matrix
+  int64_t per_wave;    // chunks per wave (the last wave may get fewer)
 };
 
-template <int DW>
-__device__ __forceinline__ void int4_valu_task(const Int4VaDesc& d, int64_t wid, int lane) {
-  constexpr int P = kI4Passes;
-  const int64_t N = d.N, K = d.K;
-  const int L = int((K / 8) / DW), rpp = 64 / L;
-  const int s = lane & (L - 1), rg = lane / L;
-  const int64_t rb = K / 2;
-  const int64_t row0 = (wid - d.task_begin) * int64_t(P) * rpp;
-
-  uint32_t w[P][DW];
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int64_t r = row0 + int64_t(p) * rpp + rg;
-    const uint32_t* src =
-        reinterpret_cast<const uint32_t*>(d.W + (r < N ? r : N - 1) * rb) + DW * s;
-#pragma unroll
-    for (int q = 0; q < DW; ++q) w[p][q] = gload_u32(src + q);
+// Partner value across lane distance O (lane ^ O), for O < 16 by DPP. For
+// O = 4 and 8 the DPP mirrors stand in for the exchange, which is exact
+// only when the value is already uniform within groups of O lanes (true in
+// the reductions below, which go from the smallest distance up).
+template <int O>
+__device__ __forceinline__ float lane_partner(float v) {
+  if constexpr (O == 1 || O == 2) {
+    constexpr int ctrl = O == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+  } else if constexpr (O == 4 || O == 8) {
+    constexpr int ctrl = O == 4 ? 0x141 : 0x140;  // row_half_mirror / row_mirror
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+  } else {
+    return __shfl_xor(v, O, 64);
   }
+}
+
+template <int G, int O = 1>
+__device__ __forceinline__ float group_sum(float v) {  // sum over lane groups of G
+  if constexpr (O >= G) {
+    return v;
+  } else {
+    return group_sum<G, 2 * O>(v + lane_partner<O>(v));
+  }
+}
+
+template <int DW>
+struct I4Chunk {
+  uint32_t w[kI4Passes][DW];
+  float sc;                // compile-time L: scale of the row this lane reports
+  float sc4[kI4Passes];    // run-time L: scales of the chunk's 4 passes
+};
+
+// Loads one chunk. With keep = 0 (a chunk past the run's end) every lane
+// reads the matrix's first dwords instead: one cache line per instruction,
+// and the load stays unconditional so the wait counts stay exact (a branch
+// around it would make the compiler wait for every load at the join).
+template <int DW, int LT>
+__device__ __forceinline__ void i4_load_chunk(I4Chunk<DW>& b, const Int4VaDesc& d, int64_t chunk,
+                                              uint32_t keep, int rpp, int rg, int s) {
+  // rows fit in 32 bits (the host checks N < 2^31); clamped to the last row
+  const uint32_t rb = uint32_t(d.K / 2), last = uint32_t(d.N - 1);
+  const uint32_t r0 = uint32_t(chunk) * (kI4Passes * rpp) + rg;
+  const uint8_t* wl = d.W + ((4 * DW * s) & keep);
+#pragma unroll
+  for (int p = 0; p < kI4Passes; ++p) {
+    const uint32_t r = min(r0 + uint32_t(p * rpp), last) & keep;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(wl + uint64_t(r) * rb);
+#pragma unroll
+    for (int q = 0; q < DW; ++q) b.w[p][q] = gload_u32(src + q);
+  }
+  if constexpr (LT >= 4) {
+    const int p = s / (LT / 4);
+    b.sc = gload_f(d.s + (min(r0 + uint32_t(p * rpp), last) & keep));
+  } else {
+#pragma unroll
+    for (int p = 0; p < kI4Passes; ++p)
+      b.sc4[p] = gload_f(d.s + (min(r0 + uint32_t(p * rpp), last) & keep));
+  }
+}
+
+template <int DW, int LT>
+__device__ __forceinline__ void i4_chunk_rows(const I4Chunk<DW>& b, const float (&xe)[4 * DW],
+                                              const float (&xo)[4 * DW], float xsum8, int L, int s,
+                                              int j, float& res, float (&res4)[kI4Passes]) {
+  float acc[kI4Passes];
+#pragma unroll
+  for (int p = 0; p < kI4Passes; ++p) {
+    float t = -xsum8;
+#pragma unroll
+    for (int q = 0; q < DW; ++q) {
+      const uint32_t w = b.w[p][q], e = low_nibbles(w);
+      t += ubyte<0>(e) * xe[4 * q + 0];
+      t += ubyte<0>(w) * xo[4 * q + 0];
+      t += ubyte<1>(e) * xe[4 * q + 1];
+      t += ubyte<1>(w) * xo[4 * q + 1];
+      t += ubyte<2>(e) * xe[4 * q + 2];
+      t += ubyte<2>(w) * xo[4 * q + 2];
+      t += ubyte<3>(e) * xe[4 * q + 3];
+      t += ubyte<3>(w) * xo[4 * q + 3];
+    }
+    acc[p] = t;
+  }
+  if constexpr (LT >= 4) {
+    // reduce-scatter: distance L/2 splits rows {0,1} / {2,3}, L/4 splits again
+    const bool h1 = s & (LT / 2), h2 = s & (LT / 4);
+    float k0 = h1 ? acc[2] : acc[0], k1 = h1 ? acc[3] : acc[1];
+    const float g0 = h1 ? acc[0] : acc[2], g1 = h1 ? acc[1] : acc[3];
+    k0 += __shfl_xor(g0, LT / 2, 64);
+    k1 += __shfl_xor(g1, LT / 2, 64);
+    float k = h2 ? k1 : k0;
+    k += __shfl_xor(h2 ? k0 : k1, LT / 4, 64);
+    k = group_sum<LT / 4>(k);  // row s / (L/4) of this chunk, summed over its L lanes
+    res = s % (LT / 4) == j ? b.sc * k : res;
+  } else {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      if (o < L) {
+#pragma unroll
+        for (int p = 0; p < kI4Passes; ++p) acc[p] += __shfl_xor(acc[p], o, 64);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < kI4Passes; ++p) res4[p] = s == j ? b.sc4[p] * acc[p] : res4[p];
+  }
+}
+
+template <int DW, int LT>
+__device__ __forceinline__ void int4_valu_run(const Int4VaDesc& d, int64_t wid, int lane) {
+  const int L = LT ? LT : int((d.K / 8) / DW), rpp = 64 / L;
+  const int s = lane & (L - 1), rg = lane / L;
+  const int64_t c0 = (wid - d.task_begin) * d.per_wave;
+  const int64_t c1 = c0 + d.per_wave < d.chunks ? c0 + d.per_wave : d.chunks;
+  const int n = int(c1 - c0);  // chunks in this run (the host bounds it by the lanes that keep results)
+
+  auto keep = [&](int j) { return j < n ? ~0u : 0u; };
+  I4Chunk<DW> A, B;
+  i4_load_chunk<DW, LT>(A, d, c0, ~0u, rpp, rg, s);
+  i4_load_chunk<DW, LT>(B, d, c0 + 1, keep(1), rpp, rg, s);
   float4 xv[2 * DW];
   const float4* xp = reinterpret_cast<const float4*>(d.x + 8 * DW * s);
 #pragma unroll
   for (int q = 0; q < 2 * DW; ++q) xv[q] = gload_f4(xp + q);
-  float sc[P];
+  float xsum = 0.0f, xe[4 * DW], xo[4 * DW];
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int64_t r = row0 + int64_t(p) * rpp + rg;
-    sc[p] = gload_f(d.s + (r < N ? r : N - 1));
+  for (int q = 0; q < 2 * DW; ++q) {
+    xsum += (xv[q].x + xv[q].y) + (xv[q].z + xv[q].w);
+    xo[2 * q] = xv[q].y * 0.0625f;
+    xo[2 * q + 1] = xv[q].w * 0.0625f;
+    xe[2 * q] = xv[q].x - xo[2 * q];
+    xe[2 * q + 1] = xv[q].z - xo[2 * q + 1];
   }
-  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before any use
-
-  float xsum = 0.0f;
-#pragma unroll
-  for (int q = 0; q < 2 * DW; ++q) xsum += (xv[q].x + xv[q].y) + (xv[q].z + xv[q].w);
-  float acc[P];
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    float t = 0.0f;
-#pragma unroll
-    for (int q = 0; q < DW; ++q) {
-      // dword q holds k = 8q .. 8q+7 of the lane's slice (low nibble even k)
-      const uint32_t ev = w[p][q] & 0x0F0F0F0Fu, od = (w[p][q] >> 4) & 0x0F0F0F0Fu;
-      const float4 xa = xv[2 * q], xb = xv[2 * q + 1];
-      t += ubyte<0>(ev) * xa.x;
-      t += ubyte<0>(od) * xa.y;
-      t += ubyte<1>(ev) * xa.z;
-      t += ubyte<1>(od) * xa.w;
-      t += ubyte<2>(ev) * xb.x;
-      t += ubyte<2>(od) * xb.y;
-      t += ubyte<3>(ev) * xb.z;
-      t += ubyte<3>(od) * xb.w;
-    }
-    acc[p] = t - 8.0f * xsum;
+  const float xsum8 = 8.0f * xsum;
+  // Two chunks are in flight when the loop starts; each half-step computes
+  // the older one and refills its buffer with the chunk two ahead, so one
+  // chunk's loads are always outstanding while the other is computed.
+  float res = 0.0f, res4[kI4Passes] = {};
+  for (int j = 0; j < n; j += 2) {
+    i4_chunk_rows<DW, LT>(A, xe, xo, xsum8, L, s, j, res, res4);
+    if (j + 1 >= n) break;
+    __builtin_amdgcn_sched_barrier(0);
+    i4_load_chunk<DW, LT>(A, d, c0 + j + 2, keep(j + 2), rpp, rg, s);
+    __builtin_amdgcn_sched_barrier(0);
+    i4_chunk_rows<DW, LT>(B, xe, xo, xsum8, L, s, j + 1, res, res4);
+    __builtin_amdgcn_sched_barrier(0);
+    i4_load_chunk<DW, LT>(B, d, c0 + j + 3, keep(j + 3), rpp, rg, s);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  if (s < n) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    if (o < L) {
-#pragma unroll
-      for (int p = 0; p < P; ++p) acc[p] += __shfl_xor(acc[p], o, 64);
-    }
-  }
-  if (s == 0) {
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int64_t r = row0 + int64_t(p) * rpp + rg;
-      if (r < N) gstore_f(d.y + r, sc[p] * acc[p]);
+    for (int p = 0; p < kI4Passes; ++p) {
+      const int64_t r = ((c0 + s) * kI4Passes + p) * rpp + rg;
+      if (r < d.N) gstore_f(d.y + r, res4[p]);
     }
   }
 }
 
-template <int DA, int DB>
+// The run with a compile-time lane count L (>= 4) and NC chunks per wave,
+// fully unrolled: straight-line code lets the compiler count every wait
+// exactly (in a loop, copies of registers whose loads are still in flight
+// make it wait for all of them). A matrix's last run may hold fewer than NC
+// chunks; the missing ones load the broadcast line and are not stored.
+template <int DW, int LT, int NC>
+__device__ __forceinline__ void int4_valu_fixed(const Int4VaDesc& d, int64_t wid, int lane) {
+  static_assert(LT >= 4 && NC <= LT / 4, "a lane keeps one chunk's row");
+  constexpr int rpp = 64 / LT;
+  const int s = lane & (LT - 1), rg = lane / LT;
+  const int64_t c0 = (wid - d.task_begin) * NC;
+  const int n = int(d.chunks - c0 < NC ? d.chunks - c0 : NC);
+  auto keep = [&](int j) { return j < n ? ~0u : 0u; };
+  // x first: its preparation then waits for x alone, with both chunks'
+  // loads (issued after it) still in flight
+  float4 xv[2 * DW];
+  const float4* xp = reinterpret_cast<const float4*>(d.x + 8 * DW * s);
+#pragma unroll
+  for (int q = 0; q < 2 * DW; ++q) xv[q] = gload_f4(xp + q);
+  __builtin_amdgcn_sched_barrier(0);
+  constexpr int R = NC < kI4Ring ? NC : kI4Ring;
+  I4Chunk<DW> buf[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) i4_load_chunk<DW, LT>(buf[j], d, c0 + j, j ? keep(j) : ~0u, rpp, rg, s);
+  __builtin_amdgcn_sched_barrier(0);
+  float xsum = 0.0f, xe[4 * DW], xo[4 * DW];
+#pragma unroll
+  for (int q = 0; q < 2 * DW; ++q) {
+    xsum += (xv[q].x + xv[q].y) + (xv[q].z + xv[q].w);
+    xo[2 * q] = xv[q].y * 0.0625f;
+    xo[2 * q + 1] = xv[q].w * 0.0625f;
+    xe[2 * q] = xv[q].x - xo[2 * q];
+    xe[2 * q + 1] = xv[q].z - xo[2 * q + 1];
+  }
+  const float xsum8 = 8.0f * xsum;
+  float res = 0.0f, res4[kI4Passes];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    __builtin_amdgcn_sched_barrier(0);
+    i4_chunk_rows<DW, LT>(buf[j % R], xe, xo, xsum8, LT, s, j, res, res4);
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + R < NC) i4_load_chunk<DW, LT>(buf[j % R], d, c0 + j + R, keep(j + R), rpp, rg, s);
+  }
+  const int j = s % (LT / 4), p = s / (LT / 4);
+  const int64_t r = ((c0 + j) * kI4Passes + p) * rpp + rg;
+  if (j < n && r < d.N) gstore_f(d.y + r, res);
+}
+
+// Chunks per wave of the unrolled run: about 12 KB of weights.
+template <int DW>
+constexpr int i4_fixed_chunks() { return kI4RunKB / DW; }
+
+// (DA, LA) and (DB, LB): the two forms of one launch; L = 0 means the lanes
+// per row come from K at run time.
+template <int DA, int LA, int DB, int LB>
 __global__ __launch_bounds__(kBlock) void int4_gemv_valu_kernel(const Int4VaDesc* __restrict__ tab,
                                                                int n, int64_t n_waves) {
   const int lane = threadIdx.x & 63;
@@ -483,10 +658,17 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_valu_kernel(const Int4VaDesc
     if (c < 64) break;
   }
   const Int4VaDesc d = tab[__builtin_amdgcn_readfirstlane(cnt - 1)];
-  if (DA == DB || d.dw == DA)
-    int4_valu_task<DA>(d, wid, lane);
-  else
-    int4_valu_task<DB>(d, wid, lane);
+  if ((DA == DB && LA == LB) || d.dw == DA) {
+    if constexpr (LA >= 4)
+      int4_valu_fixed<DA, LA, i4_fixed_chunks<DA>()>(d, wid, lane);
+    else
+      int4_valu_run<DA, 0>(d, wid, lane);
+  } else {
+    if constexpr (LB >= 4)
+      int4_valu_fixed<DB, LB, i4_fixed_chunks<DB>()>(d, wid, lane);
+    else
+      int4_valu_run<DB, 0>(d, wid, lane);
+  }
 }
 
 // int4 GEMV on the int8 matrix cores, exact in integer arithmetic.
@@ -969,44 +1151,72 @@ int int4_valu_dw(int64_t K) {
   return 0;
 }
 
-// One launch over matrices whose DW is DA or DB. The larger tasks go first
-// (wider DW = more bytes per wave-task), so the short ones fill the tail.
-template <int DA, int DB>
+// Lanes per row of the VALU kernel for a given K and DW.
+int64_t int4_valu_lanes(int64_t K, int dw) { return (K / 8) / dw; }
+
+// One launch over matrices of two forms: a (DA, LA) and b (DB, LB); LA or
+// LB = 0 for a run-time lane count. Every wave streams about 12 KB of
+// weights; the larger chunks go first so the short ones fill the tail.
+template <int DA, int LA, int DB, int LB>
 void launch_int4_valu_pair(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& a,
                            const std::vector<Int4MfMat>& b) {
   if (a.empty() && b.empty()) return;
   std::vector<Int4VaDesc> tab;
   int64_t waves = 0;
-  auto add = [&](const std::vector<Int4MfMat>& mats, int dw) {
+  auto add = [&](const std::vector<Int4MfMat>& mats, int dw, int lt) {
     for (const Int4MfMat& m : mats) {
-      const int64_t L = (m.K / 8) / dw;
-      tab.push_back(Int4VaDesc{m.W, m.s, m.x, m.y, m.N, m.K, waves, dw});
-      waves += ceil_div(m.N, int64_t(kI4Passes) * (64 / L));
+      const int64_t L = int4_valu_lanes(m.K, dw);
+      const int64_t chunks = ceil_div(m.N, int64_t(kI4Passes) * (64 / L));
+      const int64_t chunk_bytes = int64_t(kI4Passes) * 64 * dw * 4;
+      // compile-time L: the unrolled run's fixed length; run-time L: about
+      // 12 KB, bounded by the lanes that keep a run's results
+      const int64_t per_wave =
+          lt >= 4 ? kI4RunKB / dw
+                  : std::min<int64_t>(L, std::max<int64_t>(1, kI4RunKB * 1024 / chunk_bytes));
+      tab.push_back(Int4VaDesc{m.W, m.s, m.x, m.y, m.N, m.K, waves, dw, chunks, per_wave});
+      waves += ceil_div(chunks, per_wave);
     }
   };
-  add(DA >= DB ? a : b, DA >= DB ? DA : DB);
-  if (DA != DB) add(DA >= DB ? b : a, DA >= DB ? DB : DA);
+  if (DA >= DB) {
+    add(a, DA, LA);
+    if (DA != DB || LA != LB) add(b, DB, LB);
+  } else {
+    add(b, DB, LB);
+    add(a, DA, LA);
+  }
   IH_REQUIRE(ceil_div(waves, kBlock / 64) < (int64_t(1) << 31), INFERC_ERR_SHAPE,
              "int4 gemv: launch too large");
   const Int4VaDesc* dev = upload_table(ctx, tab);
-  hipLaunchKernelGGL((int4_gemv_valu_kernel<DA, DB>), dim3(unsigned(ceil_div(waves, kBlock / 64))),
-                     dim3(kBlock), 0, ctx->stream, dev, int(tab.size()), waves);
+  hipLaunchKernelGGL((int4_gemv_valu_kernel<DA, LA, DB, LB>),
+                     dim3(unsigned(ceil_div(waves, kBlock / 64))), dim3(kBlock), 0, ctx->stream,
+                     dev, int(tab.size()), waves);
   check_launch("int4_gemv_valu");
 }
 
 void launch_int4_valu(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats) {
-  std::vector<Int4MfMat> by_dw[7];
-  for (const Int4MfMat& m : mats) by_dw[int4_valu_dw(m.K)].push_back(m);
-  static const std::vector<Int4MfMat> none;
-  // the pair a transformer's matrices form (K = 768 and 4 * 768) in one launch
-  if (!by_dw[3].empty() && !by_dw[6].empty()) {
-    launch_int4_valu_pair<6, 3>(ctx, by_dw[6], by_dw[3]);
-  } else {
-    launch_int4_valu_pair<3, 3>(ctx, by_dw[3], none);
-    launch_int4_valu_pair<6, 6>(ctx, by_dw[6], none);
+  // the transformer forms (K = 768: DW 3, L 32; K = 3072: DW 6, L 64) get
+  // compile-time lane counts and share one launch; the rest run per DW
+  std::vector<Int4MfMat> k768, k3072, by_dw[7];
+  for (const Int4MfMat& m : mats) {
+    const int dw = int4_valu_dw(m.K);
+    if (dw == 3 && int4_valu_lanes(m.K, 3) == 32)
+      k768.push_back(m);
+    else if (dw == 6 && int4_valu_lanes(m.K, 6) == 64)
+      k3072.push_back(m);
+    else
+      by_dw[dw].push_back(m);
   }
-  launch_int4_valu_pair<2, 2>(ctx, by_dw[2], none);
-  launch_int4_valu_pair<4, 4>(ctx, by_dw[4], none);
+  static const std::vector<Int4MfMat> none;
+  if (!k768.empty() && !k3072.empty())
+    launch_int4_valu_pair<6, 64, 3, 32>(ctx, k3072, k768);
+  else if (!k768.empty())
+    launch_int4_valu_pair<3, 32, 3, 32>(ctx, k768, none);
+  else if (!k3072.empty())
+    launch_int4_valu_pair<6, 64, 6, 64>(ctx, k3072, none);
+  launch_int4_valu_pair<2, 0, 2, 0>(ctx, by_dw[2], none);
+  launch_int4_valu_pair<3, 0, 3, 0>(ctx, by_dw[3], none);
+  launch_int4_valu_pair<4, 0, 4, 0>(ctx, by_dw[4], none);
+  launch_int4_valu_pair<6, 0, 6, 0>(ctx, by_dw[6], none);
 }
 
 void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const int64_t* Ks,
@@ -1032,7 +1242,7 @@ void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const 
     // batch 1: the VALU streaming kernel (read the fewest bytes per output);
     // several batches: the int8 matrix-core kernel (VALU work would grow with
     // the batch, matrix-core work barely does)
-    if (batch == 1 && int4_valu_dw(K) > 0 && aligned16(x[i]) &&
+    if (batch == 1 && int4_valu_dw(K) > 0 && N < (int64_t(1) << 31) && aligned16(x[i]) &&
         (reinterpret_cast<uintptr_t>(W[i]) & 3) == 0) {
       va.push_back(Int4MfMat{W[i], scales[i], x[i], y[i], N, K});
       continue;

@@ -364,6 +364,18 @@ def test_int4_reference_stand_in_shape(ctx):
         _int4_close(got[:, lo:lo + 4096], W[lo:lo + 4096], s[lo:lo + 4096], x, K)
 
 
+@pytest.mark.parametrize("N,K", [(1, 768), (7, 768), (65, 768), (97, 768), (1, 3072),
+                                 (5, 3072), (19, 3072), (40, 1536), (130, 512)])
+def test_int4_gemv_batch1_run_edges(ctx, N, K):
+    """Batch 1, row counts that end a wave's run early (fewer rows than one
+    chunk, a partial last chunk, a partial last run) and the row lengths that
+    take the looped form (K = 1536, 512)."""
+    W, s = graphs.int4_weights(N, K, 102, "edges")
+    x = rnd((1, K), 103)
+    got = rt.Int4Gemv(T(ctx, W, np.uint8), T(ctx, s), T(ctx, x), K).numpy()
+    _int4_close(got, W, s, x, K)
+
+
 @pytest.mark.parametrize("B", [1, 8])
 def test_int4_deterministic(ctx, B):
     W, s = graphs.int4_weights(3072, 768, 94, "det")
