@@ -910,6 +910,312 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_mfma_kernel(const Int4MfDesc
     }
 }
 
+// Streaming int4 GEMV on the int8 matrix cores, for K = 768 * S (S = 1, 2
+// or 4) and up to 8 batches. Same exact arithmetic as above (fixed-point x
+// split into 4 int8 limbs, integer MFMA sums, -8 fold); the work is split
+// differently so that the weights stream at full rate:
+//
+// 1. int4_xprep_kernel, one block per (matrix, 768-k slab q, column group
+//    gr of 4 batches), writes the slab's B operands to the workspace: record
+//    (t, eo, lane) of 16 bytes, byte j = limb c%4 of
+//    x[4gr + c/4][768q + 128t + 32g + 2j + eo] for lane = (c = lane%16,
+//    g = lane/16), plus the slab's fold (each column's sum of limbs) and
+//    F / finiteness per batch, F from max|x| over the slab (so a slab's
+//    limbs use its own fixed-point scale).
+// 2. int4_gemv_stream_kernel: each wave owns one slab for its lifetime, so
+//    its B operands load once into registers; it then streams T tiles of 16
+//    rows (16 x 768 k = 6 KB each), the loads of tile i+2 issued before tile
+//    i+1 is computed, fully unrolled so the waits count exactly. With S > 1
+//    the S waves of a tile group take the S slabs of the same tiles and add
+//    their scaled partial sums through LDS. Both column groups (batches 0-3,
+//    4-7) reuse each unpacked weight operand, so weights are read once for
+//    all 8 batches.
+constexpr int kI4SlabK = 768;
+constexpr int kI4SlabSteps = kI4SlabK / 128;  // 128 k (64 bytes of a row) per step
+
+struct I4Prep {  // one (matrix, slab, column group)
+  uint32_t bop[kI4SlabSteps * 2 * 64 * 4];  // [t][even/odd][lane][4 dwords]
+  int32_t fold[16];                         // per column: sum of its limbs over the slab
+  int32_t F[4];                             // per batch: x scaled by 2^F before rounding
+  int32_t finite[4];                        // per batch: 0 if x holds a NaN or inf
+};
+
+struct I4PrepDesc {
+  const float* x;  // [batch][K]
+  int64_t K;
+  int64_t slab_begin;  // first slab of this matrix in the launch
+  I4Prep* out;         // [group][slab]
+};
+
+__global__ __launch_bounds__(kBlock) void int4_xprep_kernel(const I4PrepDesc* __restrict__ tab,
+                                                            int batch) {
+  __shared__ float smax[kBlock / 64][4];
+  __shared__ int sfold[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = blockIdx.x, gr = blockIdx.z;  // slab, column group
+  const I4PrepDesc d = tab[blockIdx.y];       // matrix
+  const int64_t K = d.K;
+  const int S = int(K / kI4SlabK);
+  if (q >= S) return;  // grid.x covers the longest row
+  const int b0 = 4 * gr, nbg = min(4, batch - b0);
+  I4Prep* o = d.out + gr * S + q;
+  const float* xs = d.x + int64_t(b0) * K + kI4SlabK * q;  // this slab of batch b0
+  if (tid < 16) sfold[tid] = 0;
+
+  // Thread (t, eo, g, b) owns x[b][128t + 32g + 2j + eo], j < 16: it loads
+  // the 32 values x[b][128t + 32g + i] (its even/odd partner loads the same
+  // line), which together cover the slab for the maximum.
+  constexpr int kThreads = kI4SlabSteps * 2 * 4 * 4;  // 192
+  const bool active = tid < kThreads;
+  const int b = tid & 3, g = (tid >> 2) & 3, eo = (tid >> 4) & 1, t = tid >> 5;
+  float own[16];  // x[b][128t + 32g + 2j + eo]
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) own[j] = 0.0f;
+  if (active && b < nbg) {
+    const float4* xr = reinterpret_cast<const float4*>(xs + int64_t(b) * K + 128 * t + 32 * g);
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 v = gload_f4(xr + i);
+      const float a0 = fabsf(v.x), a1 = fabsf(v.y), a2 = fabsf(v.z), a3 = fabsf(v.w);
+      m = fmaxf(m, fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
+      bad |= !(a0 <= 3.4028235e38f && a1 <= 3.4028235e38f && a2 <= 3.4028235e38f &&
+               a3 <= 3.4028235e38f);
+      const float e0 = v.x, o0 = v.y, e1 = v.z, o1 = v.w;
+      own[2 * i] = eo ? o0 : e0;
+      own[2 * i + 1] = eo ? o1 : e1;
+    }
+    // fmaxf would drop a NaN, so a non-finite |x| enters the maximum as inf
+    m = bad ? INFINITY : m;
+  }
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb) {
+    const float w = wave_max(bb == b ? m : 0.0f);
+    if (lane == 0) smax[wave][bb] = w;
+  }
+  __syncthreads();
+  int F[4], fin[4];
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb) {
+    float mm = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < kBlock / 64; ++w2) mm = fmaxf(mm, smax[w2][bb]);
+    fin[bb] = mm <= 3.4028235e38f;
+    if (!fin[bb]) mm = 0.0f;
+    int e = 0;
+    (void)frexpf(mm, &e);  // mm < 2^e, so |x * 2^(30-e)| < 2^30
+    F[bb] = mm > 0.0f ? 30 - e : 0;
+  }
+
+  if (active) {
+    int Fb = 0, ok = 0;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      Fb = bb == b ? F[bb] : Fb;
+      ok = bb == b ? fin[bb] : ok;
+    }
+    // Balanced base-256 digits of X (three in [-128, 127], the top one in
+    // [-64, 64]): with Y = X + 0x808080 the low three are Y's bytes minus
+    // 128 and the top one is Y >> 24, so the digits' bytes are exactly the
+    // bytes of Z = Y ^ 0x808080 (byte - 128 = byte ^ 0x80 modulo 256).
+    uint32_t Z[16];
+    const bool use = b < nbg && ok;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int X = use ? int(rintf(ldexpf(own[j], Fb))) : 0;
+      Z[j] = uint32_t(X + 0x808080) ^ 0x808080u;
+    }
+    // Record of limb cl: byte j = byte cl of Z[j]. A 4x4 byte transpose per
+    // group of four values (v_perm_b32), and the limb's sum of signed bytes
+    // by a dot product with ones.
+    const int rec0 = (2 * t + eo) * 64 + 16 * g + 4 * b;
+    u32x4_t out[4];
+    int fsum[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t z0 = Z[4 * k], z1 = Z[4 * k + 1], z2 = Z[4 * k + 2], z3 = Z[4 * k + 3];
+      // lo01 = [z0.b0, z1.b0, z0.b1, z1.b1], hi01 = [z0.b2, z1.b2, z0.b3, z1.b3]
+      const uint32_t lo01 = __builtin_amdgcn_perm(z1, z0, 0x05010400u);
+      const uint32_t hi01 = __builtin_amdgcn_perm(z1, z0, 0x07030602u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(z3, z2, 0x05010400u);
+      const uint32_t hi23 = __builtin_amdgcn_perm(z3, z2, 0x07030602u);
+      // limb c: [z0.bc, z1.bc, z2.bc, z3.bc]
+      const uint32_t l0 = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+      const uint32_t l1 = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+      const uint32_t l2 = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+      const uint32_t l3 = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+      out[0][k] = l0;
+      out[1][k] = l1;
+      out[2][k] = l2;
+      out[3][k] = l3;
+      fsum[0] = __builtin_amdgcn_sdot4(int(l0), 0x01010101, fsum[0], false);
+      fsum[1] = __builtin_amdgcn_sdot4(int(l1), 0x01010101, fsum[1], false);
+      fsum[2] = __builtin_amdgcn_sdot4(int(l2), 0x01010101, fsum[2], false);
+      fsum[3] = __builtin_amdgcn_sdot4(int(l3), 0x01010101, fsum[3], false);
+    }
+#pragma unroll
+    for (int cl = 0; cl < 4; ++cl) {
+      *reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>(
+          reinterpret_cast<uintptr_t>(o->bop + 4 * (rec0 + cl))) = out[cl];
+      atomicAdd(&sfold[4 * b + cl], fsum[cl]);  // integer: exact in any order
+    }
+  }
+  __syncthreads();
+  if (tid < 16) o->fold[tid] = sfold[tid];
+  if (tid < 4) {
+    o->F[tid] = F[tid];
+    o->finite[tid] = tid < nbg ? fin[tid] : 1;
+  }
+}
+
+struct I4StreamDesc {
+  const uint8_t* W;
+  const float* s;
+  float* y;  // [batch][N]
+  int64_t N, K;
+  int64_t block_begin;  // first block of this matrix in the launch
+  const I4Prep* prep;   // [group][slab]
+};
+
+__device__ __forceinline__ i32x4_t gload_i32x4(const uint32_t* p) {
+  const u32x4_t v = *reinterpret_cast<const __attribute__((address_space(1))) u32x4_t*>(
+      reinterpret_cast<uintptr_t>(p));
+  return i32x4_t{int(v.x), int(v.y), int(v.z), int(v.w)};
+}
+
+template <int G, int T, int R>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(G == 1 && R <= 2 ? 3 : 2)))
+void int4_gemv_stream_kernel(
+    const I4StreamDesc* __restrict__ tab, int n, int batch) {
+  constexpr int NW = kBlock / 64;
+  __shared__ f32x4_t part[2][NW][G][64];  // S > 1: per-slab partial terms, by tile parity
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t bid = blockIdx.x;
+  int cnt = 0;  // this block's matrix (block_begin ascends)
+  for (int base = 0; base < n; base += 64) {
+    const int j = base + lane;
+    const int c = __popcll(__ballot(j < n && gload_i64(&tab[j].block_begin) <= bid));
+    cnt += c;
+    if (c < 64) break;
+  }
+  const I4StreamDesc d = tab[__builtin_amdgcn_readfirstlane(cnt - 1)];
+  const int64_t N = d.N, rb = d.K / 2;
+  const int S = int(d.K / kI4SlabK);
+  const int q = wave % S, tg = wave / S, tgs = NW / S;
+  const int64_t tile0 = ((bid - d.block_begin) * tgs + tg) * T;
+  const int r = lane & 15, g = lane >> 4, col = lane & 15, cl = col & 3;
+
+  // this wave's slab: B operands, fold, exponent and finiteness of its column
+  i32x4_t bo[kI4SlabSteps][2][G];
+  int fold[G], Fc[G], fin[G];
+#pragma unroll
+  for (int gr = 0; gr < G; ++gr) {
+    const I4Prep* pp = d.prep + gr * S + q;
+#pragma unroll
+    for (int t = 0; t < kI4SlabSteps; ++t)
+#pragma unroll
+      for (int eo = 0; eo < 2; ++eo) bo[t][eo][gr] = gload_i32x4(pp->bop + ((2 * t + eo) * 64 + lane) * 4);
+    fold[gr] = *reinterpret_cast<const __attribute__((address_space(1))) int32_t*>(
+        reinterpret_cast<uintptr_t>(pp->fold + col));
+    Fc[gr] = *reinterpret_cast<const __attribute__((address_space(1))) int32_t*>(
+        reinterpret_cast<uintptr_t>(pp->F + (col >> 2)));
+    fin[gr] = *reinterpret_cast<const __attribute__((address_space(1))) int32_t*>(
+        reinterpret_cast<uintptr_t>(pp->finite + (col >> 2)));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // tile i: lane (r, g) holds row 16i + r, bytes [384q + 64t + 16g, +16) for
+  // t < 6, and the scales of rows 16i + 4g + v (rows past N are clamped)
+  uint4 wb[R][kI4SlabSteps];
+  float sb[R][4];
+  auto load_tile = [&](int slot, int64_t tile) {
+    int64_t row = tile * 16 + r;
+    row = row < N ? row : N - 1;
+    const uint8_t* rp = d.W + row * rb + kI4SlabK / 2 * q + 16 * g;
+#pragma unroll
+    for (int t = 0; t < kI4SlabSteps; ++t)
+      wb[slot][t] = gload_u4(reinterpret_cast<const uint4*>(rp + 64 * t));
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      int64_t rw = tile * 16 + 4 * g + v;
+      sb[slot][v] = gload_f(d.s + (rw < N ? rw : N - 1));
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < (R < T ? R : T); ++j) load_tile(j, tile0 + j);
+  __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+  for (int i = 0; i < T; ++i) {
+    const int slot = i % R;
+    __builtin_amdgcn_sched_barrier(0);
+    i32x4_t acc[G];
+#pragma unroll
+    for (int gr = 0; gr < G; ++gr) acc[gr] = i32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < kI4SlabSteps; ++t) {
+      const uint4 w = wb[slot][t];
+      const i32x4_t ev = {int(low_nibbles(w.x)), int(low_nibbles(w.y)), int(low_nibbles(w.z)),
+                          int(low_nibbles(w.w))};
+      const i32x4_t od = {int(low_nibbles(w.x >> 4)), int(low_nibbles(w.y >> 4)),
+                          int(low_nibbles(w.z >> 4)), int(low_nibbles(w.w >> 4))};
+#pragma unroll
+      for (int gr = 0; gr < G; ++gr) {
+        acc[gr] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ev, bo[t][0][gr], acc[gr], 0, 0, 0);
+        acc[gr] = __builtin_amdgcn_mfma_i32_16x16x64_i8(od, bo[t][1][gr], acc[gr], 0, 0, 0);
+      }
+    }
+    float sc[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sc[v] = sb[slot][v];
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + R < T) load_tile(slot, tile0 + i + R);
+    __builtin_amdgcn_sched_barrier(0);
+    // acc[gr][v]: row 16i + 4g + v, column (batch 4gr + col/4, limb cl). Each
+    // limb term acc - 8*fold is below 2^24, so it and its power-of-two
+    // scaling are exact in fp32; a slab whose x is not finite gives NaN, so
+    // the whole output is non-finite, as in the reference.
+    f32x4_t tv[G];
+#pragma unroll
+    for (int gr = 0; gr < G; ++gr)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        tv[gr][v] = fin[gr] ? ldexpf(float(acc[gr][v] - 8 * fold[gr]), 8 * cl - Fc[gr])
+                            : __int_as_float(0x7fc00000);
+    bool report = true;
+    if (S > 1) {
+      // the S slabs' terms meet in LDS and add in slab order; slab 0 reports
+#pragma unroll
+      for (int gr = 0; gr < G; ++gr) part[i & 1][wave][gr][lane] = tv[gr];
+      __syncthreads();
+      report = q == 0;
+      if (report) {
+        for (int s2 = 1; s2 < S; ++s2)
+#pragma unroll
+          for (int gr = 0; gr < G; ++gr) tv[gr] += part[i & 1][wave + s2][gr][lane];
+      }
+    }
+    if (report) {
+      // a batch's 4 limb terms (a lane quad) add in fp32
+      const int64_t tile = tile0 + i;
+#pragma unroll
+      for (int gr = 0; gr < G; ++gr) {
+        const int b = 4 * gr + (col >> 2);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float t2 = tv[gr][v];
+          t2 += quad_xor_f<1>(t2);
+          t2 += quad_xor_f<2>(t2);
+          const int64_t row = tile * 16 + 4 * g + v;
+          if (cl == 0 && b < batch && row < N) gstore_f(d.y + int64_t(b) * N + row, sc[v] * t2);
+        }
+      }
+    }
+  }
+}
+
 // Fallback for K not a multiple of 32: one thread per (b, row), exact formula.
 __global__ __launch_bounds__(kBlock) void int4_gemv_generic(const uint8_t* __restrict__ W,
                                                             const float* __restrict__ s,
@@ -1138,6 +1444,56 @@ void launch_int4_mfma(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats, i
   launch_int4_mfma_k<24>(ctx, by_k[24], batch);
 }
 
+// Shapes of the streaming MFMA kernel: K = 768 * S with S = 1, 2 or 4 and
+// 16-byte aligned rows (x must be 16-byte aligned too).
+bool int4_stream_ok(int64_t K, const uint8_t* W) {
+  const int64_t S = K / kI4SlabK;
+  return K > 0 && K % kI4SlabK == 0 && (S == 1 || S == 2 || S == 4) && aligned16(W);
+}
+
+constexpr int kI4StreamTiles = 6;  // 16-row tiles per wave
+constexpr int kI4StreamRing = 2;   // tiles in flight per wave
+
+template <int G>
+void launch_int4_stream_g(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats, int batch) {
+  int64_t slabs = 0, blocks = 0;
+  for (const Int4MfMat& m : mats) slabs += m.K / kI4SlabK;
+  I4Prep* ws = static_cast<I4Prep*>(ctx->ws(size_t(slabs) * G * sizeof(I4Prep)));
+  std::vector<I4PrepDesc> ptab;
+  std::vector<I4StreamDesc> stab;
+  int64_t sb = 0;
+  for (const Int4MfMat& m : mats) {
+    const int64_t S = m.K / kI4SlabK;
+    I4Prep* out = ws + sb * G;  // this matrix's [group][slab] records
+    ptab.push_back(I4PrepDesc{m.x, m.K, sb, out});
+    stab.push_back(I4StreamDesc{m.W, m.s, m.y, m.N, m.K, blocks, out});
+    sb += S;
+    const int64_t tiles = ceil_div(m.N, 16);
+    blocks += ceil_div(tiles, (kBlock / 64 / S) * kI4StreamTiles);
+  }
+  IH_REQUIRE(blocks < (int64_t(1) << 31) && mats.size() <= 65535, INFERC_ERR_SHAPE,
+             "int4 gemv: launch too large");
+  const I4PrepDesc* pdev = upload_table(ctx, ptab);
+  const I4StreamDesc* sdev = upload_table(ctx, stab);
+  int64_t smax = 1;
+  for (const Int4MfMat& m : mats) smax = std::max<int64_t>(smax, m.K / kI4SlabK);
+  hipLaunchKernelGGL(int4_xprep_kernel, dim3(unsigned(smax), unsigned(ptab.size()), unsigned(G)),
+                     dim3(kBlock), 0, ctx->stream, pdev, batch);
+  check_launch("int4_xprep");
+  hipLaunchKernelGGL((int4_gemv_stream_kernel<G, kI4StreamTiles, kI4StreamRing>),
+                     dim3(unsigned(blocks)),
+                     dim3(kBlock), 0, ctx->stream, sdev, int(stab.size()), batch);
+  check_launch("int4_gemv_stream");
+}
+
+void launch_int4_stream(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats, int64_t batch) {
+  if (mats.empty()) return;
+  if (batch <= 4)
+    launch_int4_stream_g<1>(ctx, mats, int(batch));
+  else
+    launch_int4_stream_g<2>(ctx, mats, int(batch));
+}
+
 // Dwords per lane for the VALU kernel: L = (K/8)/DW lanes per row must be a
 // power of two no larger than 64. 0 if none fits.
 int int4_valu_dw(int64_t K) {
@@ -1230,6 +1586,7 @@ void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const 
   std::vector<Int4Mat> mats;
   std::vector<Int4MfMat> mf;  // int8-MFMA form
   std::vector<Int4MfMat> va;  // batch-1 VALU streaming form
+  std::vector<Int4MfMat> st;  // streaming int8-MFMA form (K = 768, 1536, 3072)
   int64_t blocks = 0;
   for (int64_t i = 0; i < n_mats; ++i) {
     const int64_t N = Ns[i], K = Ks[i];
@@ -1245,6 +1602,10 @@ void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const 
     if (batch == 1 && int4_valu_dw(K) > 0 && N < (int64_t(1) << 31) && aligned16(x[i]) &&
         (reinterpret_cast<uintptr_t>(W[i]) & 3) == 0) {
       va.push_back(Int4MfMat{W[i], scales[i], x[i], y[i], N, K});
+      continue;
+    }
+    if (int4_stream_ok(K, W[i]) && aligned16(x[i])) {
+      st.push_back(Int4MfMat{W[i], scales[i], x[i], y[i], N, K});
       continue;
     }
     if (int4_mfma_ok(K, W[i])) {
@@ -1269,6 +1630,7 @@ void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const 
     mats.push_back(m);
   }
   launch_int4_valu(ctx, va);
+  launch_int4_stream(ctx, st, batch);
   launch_int4_mfma(ctx, mf, batch);
   if (mats.empty()) return;
   IH_REQUIRE(blocks < (int64_t(1) << 31), INFERC_ERR_SHAPE, "int4 gemv: launch too large");

@@ -376,6 +376,17 @@ def test_int4_gemv_batch1_run_edges(ctx, N, K):
     _int4_close(got, W, s, x, K)
 
 
+@pytest.mark.parametrize("N,K,B", [(37, 1536, 3), (100, 3072, 2), (17, 768, 6), (1000, 768, 8),
+                                   (5, 3072, 7), (130, 1536, 5)])
+def test_int4_gemv_multi_batch_shapes(ctx, N, K, B):
+    """Several batches (one and two column groups of four), rows split over
+    2 or 4 waves (K = 1536, 3072) and tiles that end past the last row."""
+    W, s = graphs.int4_weights(N, K, 104, "multi")
+    x = rnd((B, K), 105)
+    got = rt.Int4Gemv(T(ctx, W, np.uint8), T(ctx, s), T(ctx, x), K).numpy()
+    _int4_close(got, W, s, x, K)
+
+
 @pytest.mark.parametrize("B", [1, 8])
 def test_int4_deterministic(ctx, B):
     W, s = graphs.int4_weights(3072, 768, 94, "det")
