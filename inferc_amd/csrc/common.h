@@ -124,6 +124,64 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// LayerNorm of one row by one wave64: the reference's two passes (mean, then
+// the centred second moment; activation.cc:103-150), with y = (d * inv) *
+// gamma + beta. x (+ res when given) is read once when the row fits 64*VPL
+// values, else re-read per pass.
+template <int VPL>
+__device__ __forceinline__ void ln_row(int lane, const float* __restrict__ xr,
+                                       const float* __restrict__ rr, const float* __restrict__ g,
+                                       const float* __restrict__ b, int64_t feat, float eps,
+                                       float* __restrict__ yr) {
+  const float inv_n = 1.0f / float(feat);
+  if (feat <= 64 * VPL) {
+    // gamma and beta are loaded with x, so the row costs one memory round
+    // trip before the reductions instead of a second one after them.
+    float v[VPL], gv[VPL], bv[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int64_t c = lane + 64 * i;
+      const bool in = c < feat;
+      v[i] = in ? (rr ? xr[c] + rr[c] : xr[c]) : 0.0f;
+      gv[i] = in ? g[c] : 0.0f;
+      bv[i] = in ? b[c] : 0.0f;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) s += v[i];
+    const float mean = wave_sum(s) * inv_n;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int64_t c = lane + 64 * i;
+      const float d = (c < feat) ? v[i] - mean : 0.0f;
+      v[i] = d;
+      q += d * d;
+    }
+    const float var = wave_sum(q) * inv_n;
+    const float inv = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int64_t c = lane + 64 * i;
+      if (c < feat) yr[c] = (v[i] * inv) * gv[i] + bv[i];
+    }
+    return;
+  }
+  float s = 0.0f;
+  for (int64_t c = lane; c < feat; c += 64) s += rr ? xr[c] + rr[c] : xr[c];
+  const float mean = wave_sum(s) * inv_n;
+  float q = 0.0f;
+  for (int64_t c = lane; c < feat; c += 64) {
+    const float d = (rr ? xr[c] + rr[c] : xr[c]) - mean;
+    q += d * d;
+  }
+  const float inv = 1.0f / sqrtf(wave_sum(q) * inv_n + eps);
+  for (int64_t c = lane; c < feat; c += 64) {
+    const float d = (rr ? xr[c] + rr[c] : xr[c]) - mean;
+    yr[c] = (d * inv) * g[c] + b[c];
+  }
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

@@ -114,14 +114,14 @@ __global__ __launch_bounds__(kBlock) void kv_append_attend_kernel(KvP p) {
   }
 }
 
-// Decode attention for head_dim 64, one block (4 waves) per head. The block
-// appends the token's K/V at *pos, then wave w walks key chunks w, w+4, ...
+// Decode attention for head_dim 64, one block (8 waves) per head. The block
+// appends the token's K/V at *pos, then wave w walks key chunks w, w+8, ...
 // of 32 keys. For a chunk every K and V load is issued before any is used
 // (indices past the last key are clamped to it and weighted by 0), so a
 // chunk costs one memory round trip. Per chunk: s_j = (q . k_j) / sqrt(64)
 // (the with-past graph's MatMul -> Div), m = max s_j, e_j = exp(s_j - m),
 // l = sum e_j, O = sum e_j v_j; chunks are merged online within a wave and
-// the four waves through LDS in wave order; out = O / L.
+// the eight waves through LDS in wave order; out = O / L.
 struct AttnDecP {
   int64_t T;
   const int64_t* pos;
@@ -133,7 +133,7 @@ struct AttnDecP {
   float* out;
 };
 
-constexpr int kDecWaves = 4;
+constexpr int kDecWaves = 8;
 
 __global__ __launch_bounds__(64 * kDecWaves) void attn_decode_d64(AttnDecP p) {
   constexpr int D = 64;

@@ -15,9 +15,9 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// One wave64 per row. Rows up to 64*VPL features stay in registers for the
-// two passes (mean, then the centred second moment, as the reference's
-// vDSP_meanv / vDSP_measqv sequence); wider rows fall back to re-reading.
+// One wave64 per row (ln_row): rows up to 64*VPL features stay in registers
+// for the two passes (mean, then the centred second moment, as the
+// reference's vDSP_meanv / vDSP_measqv sequence); wider rows are re-read.
 template <int VPL>
 __global__ __launch_bounds__(kBlock) void layernorm_kernel(int64_t rows, int64_t feat,
                                                            const float* __restrict__ x,
@@ -28,56 +28,8 @@ __global__ __launch_bounds__(kBlock) void layernorm_kernel(int64_t rows, int64_t
   const int lane = threadIdx.x & 63;
   const int64_t row = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const float* xr = x + row * feat;
-  const float* rr = res ? res + row * feat : nullptr;
-  float* yr = y + row * feat;
-  const float inv_n = 1.0f / float(feat);
-  if (feat <= 64 * VPL) {
-    // gamma and beta are loaded with x, so the row costs one memory round
-    // trip before the reductions instead of a second one after them.
-    float v[VPL], gv[VPL], bv[VPL];
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int64_t c = lane + 64 * i;
-      const bool in = c < feat;
-      v[i] = in ? (rr ? xr[c] + rr[c] : xr[c]) : 0.0f;
-      gv[i] = in ? g[c] : 0.0f;
-      bv[i] = in ? b[c] : 0.0f;
-    }
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) s += v[i];
-    const float mean = wave_sum(s) * inv_n;
-    float q = 0.0f;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int64_t c = lane + 64 * i;
-      const float d = (c < feat) ? v[i] - mean : 0.0f;
-      v[i] = d;
-      q += d * d;
-    }
-    const float var = wave_sum(q) * inv_n;
-    const float inv = 1.0f / sqrtf(var + eps);
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int64_t c = lane + 64 * i;
-      if (c < feat) yr[c] = (v[i] * inv) * gv[i] + bv[i];
-    }
-    return;
-  }
-  float s = 0.0f;
-  for (int64_t c = lane; c < feat; c += 64) s += rr ? xr[c] + rr[c] : xr[c];
-  const float mean = wave_sum(s) * inv_n;
-  float q = 0.0f;
-  for (int64_t c = lane; c < feat; c += 64) {
-    const float d = (rr ? xr[c] + rr[c] : xr[c]) - mean;
-    q += d * d;
-  }
-  const float inv = 1.0f / sqrtf(wave_sum(q) * inv_n + eps);
-  for (int64_t c = lane; c < feat; c += 64) {
-    const float d = (rr ? xr[c] + rr[c] : xr[c]) - mean;
-    yr[c] = (d * inv) * g[c] + b[c];
-  }
+  ln_row<VPL>(lane, x + row * feat, res ? res + row * feat : nullptr, g, b, feat, eps,
+              y + row * feat);
 }
 
 __global__ __launch_bounds__(kBlock) void activation_kernel(int64_t n, const float* __restrict__ x,
