@@ -235,7 +235,7 @@ def roofline_ffn_up_gemm(ctx, reps: int = 200):
         traffic = json.loads(tf.read_text()).get("gemm_ffn_up_b1")
     return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-            "traffic": traffic, "kernel": "gemm_f32_ksplit<32,64,8,3> (FusedMatMulAddGELU)",
+            "traffic": traffic, "kernel": "gemm_f32_ksplit<32,48,8,2> (FusedMatMulAddGELU)",
             "shape": [M, N, K], "algorithmic_flops_per_launch": flops,
             "avg_launch_us": round(ms * 1e3, 3)}
 

@@ -323,6 +323,9 @@ struct KsFrag {
         if constexpr (CB == 4) {
           const float4 t = *reinterpret_cast<const float4*>(src);
           b[e][0] = t.x; b[e][1] = t.y; b[e][2] = t.z; b[e][3] = t.w;
+        } else if constexpr (CB == 3) {
+          // (the host takes 48-wide tiles only when N % 48 == 0)
+          b[e][0] = src[0]; b[e][1] = src[1]; b[e][2] = src[2];
         } else if constexpr (CB == 2) {
           const float2 t = *reinterpret_cast<const float2*>(src);
           b[e][0] = t.x; b[e][1] = t.y;
@@ -460,13 +463,17 @@ void launch_ksplit(GemmParams p, int64_t slices, bool tb, hipStream_t s) {
     hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, false>), grid, dim3(64 * W), 0, s, p, tm, tn);
 }
 
-// Two shapes cover the small-M products (measured on MI355X at M=32..256,
-// N=768..3072, K=768..3072): 32x64 tiles with 8 waves when that alone gives
-// at least half as many blocks as CUs (the b=1 FFN-up and QKV), else 16x32
-// tiles with 16 waves (out-proj, FFN-down, prefill), trading operand reuse
-// for blocks to spread over the CUs. Ring depth 3 in both: deeper rings
-// measured no faster.
+// Three shapes cover the small-M products (measured on MI355X at M=32..256,
+// N=768..3072, K=768..3072). 32x48 tiles with 8 waves and a 2-deep ring when
+// N is a multiple of 48 and they give at least 3/4 as many blocks as CUs:
+// the b=1 FFN-up (256 blocks, 10.9 us vs 13.3 us for 32x64) and QKV (192
+// blocks, 10.4 us vs 12.7 us). Else 32x64 tiles with 8 waves when that
+// gives at least half as many blocks as CUs. Else 16x32 tiles with 16 waves
+// (out-proj, FFN-down, prefill), trading operand reuse for blocks to spread
+// over the CUs.
 KsCfg pick_ksplit(int64_t M, int64_t N, int64_t slices, int64_t cus) {
+  const int64_t b48 = ceil_div(M, 32) * ceil_div(N, 48) * slices;
+  if (N % 48 == 0 && 4 * b48 >= 3 * cus) return KsCfg{32, 48, 8, 2};
   const int64_t big_blocks = ceil_div(M, 32) * ceil_div(N, 64) * slices;
   if (2 * big_blocks >= cus) return KsCfg{32, 64, 8, 3};
   return KsCfg{16, 32, 16, 3};
@@ -481,7 +488,8 @@ bool ksplit_supported(const GemmParams& p, int64_t slices, bool ta, bool vec, in
 
 void run_ksplit(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool tb) {
   const KsCfg c = pick_ksplit(p.M, p.N, slices, ctx->num_cus);
-  if (c.wm == 32) launch_ksplit<32, 64, 8, 3>(p, slices, tb, ctx->stream);
+  if (c.wn == 48) launch_ksplit<32, 48, 8, 2>(p, slices, tb, ctx->stream);
+  else if (c.wm == 32) launch_ksplit<32, 64, 8, 3>(p, slices, tb, ctx->stream);
   else launch_ksplit<16, 32, 16, 3>(p, slices, tb, ctx->stream);
   check_launch("gemm_f32_ksplit");
 }

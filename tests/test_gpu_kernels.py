@@ -121,6 +121,21 @@ def test_gemm_epilogues(ctx, act):
     close(got, ref)
 
 
+@pytest.mark.parametrize("M,N,K,tb", [(100, 2304, 200, False), (128, 3072, 768, False),
+                                       (77, 2352, 52, True)])
+def test_gemm_small_m_48_wide_tiles(ctx, M, N, K, tb):
+    """Small-M products whose N is a multiple of 48 with enough tiles take
+    the 32x48 K-split kernel: partial row tiles, K not a multiple of the
+    per-wave k-groups, B plain and transposed."""
+    A = rnd((M, K), 94 + M)
+    B = rnd((N, K) if tb else (K, N), 95 + K, 0.05)
+    bias, res = rnd(N, 96), rnd((M, N), 97)
+    got = rt.Gemm(T(ctx, A), T(ctx, B), T(ctx, bias), 1.0, 1.0, trans_b=tb, residual=T(ctx, res),
+                  act=L.ACT_GELU_ERF).numpy()
+    Bd = (B.T if tb else B).astype(np.float64)
+    close(got, ref64.gelu_erf((A.astype(np.float64) @ Bd + bias) + res))
+
+
 @pytest.mark.parametrize("N,K", [(2, 768), (768, 768), (50, 3072), (33, 100)])
 def test_gemm_single_row_transb_epilogues(ctx, N, K):
     """M=1 with B^T takes the GEMV route (matmul.cc:207-216); bias, residual and
