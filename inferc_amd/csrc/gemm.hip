@@ -468,15 +468,19 @@ void launch_ksplit(GemmParams p, int64_t slices, bool tb, hipStream_t s) {
 // N is a multiple of 48 and they give at least 3/4 as many blocks as CUs:
 // the b=1 FFN-up (256 blocks, 10.9 us vs 13.3 us for 32x64) and QKV (192
 // blocks, 10.4 us vs 12.7 us). Else 32x64 tiles with 8 waves when that
-// gives at least half as many blocks as CUs. Else 16x32 tiles with 16 waves
-// (out-proj, FFN-down, prefill), trading operand reuse for blocks to spread
-// over the CUs.
+// gives at least half as many blocks as CUs. Else 16x32 tiles with 8 waves
+// (out-proj, FFN-down, prefill; 14.9 us for the b=1 FFN-down), trading
+// operand reuse for blocks to spread over the CUs, or 16x16 tiles when even
+// those give at most a quarter as many blocks as CUs (M=32, N=768 prefill:
+// 13.7 us vs 19.2 us).
 KsCfg pick_ksplit(int64_t M, int64_t N, int64_t slices, int64_t cus) {
   const int64_t b48 = ceil_div(M, 32) * ceil_div(N, 48) * slices;
   if (N % 48 == 0 && 4 * b48 >= 3 * cus) return KsCfg{32, 48, 8, 2};
   const int64_t big_blocks = ceil_div(M, 32) * ceil_div(N, 64) * slices;
   if (2 * big_blocks >= cus) return KsCfg{32, 64, 8, 3};
-  return KsCfg{16, 32, 16, 3};
+  const int64_t b16 = ceil_div(M, 16) * ceil_div(N, 32) * slices;
+  if (4 * b16 <= cus) return KsCfg{16, 16, 8, 2};
+  return KsCfg{16, 32, 8, 2};
 }
 
 bool ksplit_supported(const GemmParams& p, int64_t slices, bool ta, bool vec, int64_t cus,
@@ -490,7 +494,8 @@ void run_ksplit(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool tb) {
   const KsCfg c = pick_ksplit(p.M, p.N, slices, ctx->num_cus);
   if (c.wn == 48) launch_ksplit<32, 48, 8, 2>(p, slices, tb, ctx->stream);
   else if (c.wm == 32) launch_ksplit<32, 64, 8, 3>(p, slices, tb, ctx->stream);
-  else launch_ksplit<16, 32, 16, 3>(p, slices, tb, ctx->stream);
+  else if (c.wn == 16) launch_ksplit<16, 16, 8, 2>(p, slices, tb, ctx->stream);
+  else launch_ksplit<16, 32, 8, 2>(p, slices, tb, ctx->stream);
   check_launch("gemm_f32_ksplit");
 }
 
