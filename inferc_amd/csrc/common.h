@@ -239,6 +239,10 @@ void attention(inferc_hip_ctx* ctx, const AttnArgs& a);
 void layernorm(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
                const float* residual, const float* gamma, const float* beta, float eps,
                float* y);
+// As layernorm, with row r adding residual row r % res_rows.
+void layernorm_res_period(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
+                          const float* residual, int64_t res_rows, const float* gamma,
+                          const float* beta, float eps, float* y);
 void activation(inferc_hip_ctx* ctx, int64_t n, const float* x, int act, float* y);
 void add_bcast(inferc_hip_ctx* ctx, int64_t n, const float* a, const float* b, int64_t b_n,
                float* y);

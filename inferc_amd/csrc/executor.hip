@@ -385,6 +385,26 @@ void inferc_executor::peephole() {
       }
     }
   }
+  // Add(a, b) -> FusedLayerNorm (its only reader)  ==>  LayerNorm with a
+  // residual input: the embedding sum word + position goes straight into
+  // the LayerNorm kernel (activation.cc:103-150 on the summed rows).
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    inferc_graph::Node& n = nodes[i];
+    if (dead[i] || n.op != "Add" || n.in.size() != 2 || n.out.size() != 1 ||
+        uses[n.out[0]] != 1 || inits.count(n.in[0]) || inits.count(n.in[1]))
+      continue;
+    for (size_t j = i + 1; j < nodes.size(); ++j) {
+      if (dead[j]) continue;
+      inferc_graph::Node& ln = nodes[j];
+      if (std::find(ln.in.begin(), ln.in.end(), n.out[0]) == ln.in.end()) continue;
+      if (ln.op == "FusedLayerNorm" && ln.in.size() == 3 && ln.in[0] == n.out[0]) {
+        ln.in = {n.in[0], ln.in[1], ln.in[2], n.in[1]};
+        ln.name = n.name + "+" + ln.name;
+        dead[i] = true;
+      }
+      break;
+    }
+  }
   std::vector<inferc_graph::Node> kept;
   for (size_t i = 0; i < nodes.size(); ++i)
     if (!dead[i]) kept.push_back(std::move(nodes[i]));
@@ -572,17 +592,32 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "FusedLayerNorm") {
-    const Value x = in(0);
+    // optional 4th input: the other operand of an Add folded in front
+    // (y = LN(x + r), r repeated over leading dims as the Add broadcast it)
+    size_t xi = 0, ri = 3;
+    if (n.in.size() >= 4 && in(3).numel() > in(0).numel()) std::swap(xi, ri);
+    const Value x = in(xi);
     require_f32(x, "X");
     const int64_t feat = x.shape.back();
     IH_REQUIRE(in(1).numel() == feat && in(2).numel() == feat, INFERC_ERR_SHAPE,
                "LayerNorm: scale/bias size mismatch with feature dim");
     const float eps = attr_float(n, "epsilon", 1e-5f);
+    const float* res = nullptr;
+    int64_t res_rows = 1;
+    if (n.in.size() >= 4) {
+      const Value rv = in(ri);
+      require_f32(rv, "residual");
+      IH_REQUIRE(rv.numel() > 0 && rv.numel() % feat == 0 && x.numel() % rv.numel() == 0 &&
+                     (rv.shape.empty() || rv.shape.back() == feat),
+                 INFERC_ERR_UNSUPPORTED, "Add before LayerNorm: unsupported broadcast");
+      res = static_cast<const float*>(dev_of(n.in[ri]));
+      res_rows = rv.numel() / feat;
+    }
     float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, x.shape).dev);
     if (!dry) {
-      layernorm(ctx, x.numel() / feat, feat, static_cast<const float*>(dev_of(n.in[0])), nullptr,
-                static_cast<const float*>(dev_of(n.in[1])),
-                static_cast<const float*>(dev_of(n.in[2])), eps, y);
+      layernorm_res_period(ctx, x.numel() / feat, feat, static_cast<const float*>(dev_of(n.in[xi])),
+                           res, res_rows, static_cast<const float*>(dev_of(n.in[1])),
+                           static_cast<const float*>(dev_of(n.in[2])), eps, y);
     }
     return;
   }
@@ -692,8 +727,28 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     for (int64_t i = 0; i < axis; ++i) outer *= data.shape[size_t(i)];
     for (int64_t i = axis + 1; i < r; ++i) inner *= data.shape[size_t(i)];
     const int64_t ad = data.shape[size_t(axis)];
-    float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
     const float* dp = static_cast<const float*>(dev_of(n.in[0]));
+    if (idx.host && outer == 1 && idx.dtype == INFERC_DT_I64 && idx.numel() > 0) {
+      // Host-known consecutive indices k, k+1, ... with nothing outside the
+      // axis select one contiguous range (position ids from Range, the CLS
+      // row of a single sequence): the output is a view, no kernel runs.
+      const std::vector<int64_t> ix = host_i64(idx, "Gather");
+      const int64_t k0 = ix[0] < 0 ? ix[0] + ad : ix[0];
+      bool run = true;
+      for (size_t i = 0; i < ix.size() && run; ++i) {
+        const int64_t v = ix[i] < 0 ? ix[i] + ad : ix[i];
+        run = v >= 0 && v < ad && v == k0 + int64_t(i);
+      }
+      if (run) {
+        ih::Value v;
+        v.dtype = INFERC_DT_F32;
+        v.shape = os;
+        v.dev = const_cast<float*>(dp) + k0 * inner;
+        vals[n.out[0]] = v;
+        return;
+      }
+    }
+    float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
     // one device gather for any axis; host-known indices are validated here
     // and uploaded once (device indices are checked by the kernel's flag)
     if (idx.host) {

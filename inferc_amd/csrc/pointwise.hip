@@ -18,18 +18,21 @@ constexpr int kBlock = 256;
 // One wave64 per row (ln_row): rows up to 64*VPL features stay in registers
 // for the two passes (mean, then the centred second moment, as the
 // reference's vDSP_meanv / vDSP_measqv sequence); wider rows are re-read.
+// Row r adds residual row r % res_rows (a residual repeated over leading
+// dims, as a suffix-broadcast Add would).
 template <int VPL>
 __global__ __launch_bounds__(kBlock) void layernorm_kernel(int64_t rows, int64_t feat,
                                                            const float* __restrict__ x,
                                                            const float* __restrict__ res,
                                                            const float* __restrict__ g,
                                                            const float* __restrict__ b,
-                                                           float eps, float* __restrict__ y) {
+                                                           float eps, float* __restrict__ y,
+                                                           int64_t res_rows) {
   const int lane = threadIdx.x & 63;
   const int64_t row = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
   if (row >= rows) return;
-  ln_row<VPL>(lane, x + row * feat, res ? res + row * feat : nullptr, g, b, feat, eps,
-              y + row * feat);
+  ln_row<VPL>(lane, x + row * feat, res ? res + (row % res_rows) * feat : nullptr, g, b, feat,
+              eps, y + row * feat);
 }
 
 __global__ __launch_bounds__(kBlock) void activation_kernel(int64_t n, const float* __restrict__ x,
@@ -184,16 +187,24 @@ unsigned grid_for(int64_t n, int64_t per_block = kBlock, int64_t cap = 8192) {
 void layernorm(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
                const float* residual, const float* gamma, const float* beta, float eps,
                float* y) {
+  layernorm_res_period(ctx, rows, feat, x, residual, rows, gamma, beta, eps, y);
+}
+
+void layernorm_res_period(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
+                          const float* residual, int64_t res_rows, const float* gamma,
+                          const float* beta, float eps, float* y) {
   IH_REQUIRE(rows >= 0 && feat > 0, INFERC_ERR_SHAPE, "layernorm: bad shape");
+  IH_REQUIRE(residual == nullptr || (res_rows > 0 && rows % res_rows == 0), INFERC_ERR_SHAPE,
+             "layernorm: residual rows must divide the rows");
   if (rows == 0) return;
   IH_REQUIRE(x && gamma && beta && y, INFERC_ERR_ARG, "layernorm: null pointer");
   const unsigned blocks = unsigned(ceil_div(rows, kBlock / 64));
   if (feat <= 64 * 4)
     hipLaunchKernelGGL(layernorm_kernel<4>, dim3(blocks), dim3(kBlock), 0, ctx->stream, rows,
-                       feat, x, residual, gamma, beta, eps, y);
+                       feat, x, residual, gamma, beta, eps, y, residual ? res_rows : int64_t(1));
   else
     hipLaunchKernelGGL(layernorm_kernel<16>, dim3(blocks), dim3(kBlock), 0, ctx->stream, rows,
-                       feat, x, residual, gamma, beta, eps, y);
+                       feat, x, residual, gamma, beta, eps, y, residual ? res_rows : int64_t(1));
   check_launch("layernorm");
 }
 

@@ -25,9 +25,10 @@ def test_encoder_graph_shapes_and_fusion():
     g = graphs.encoder_graph(cfg, graphs.encoder_weights(cfg, 3))
     n_nodes = len(g.op_types)
     ex = Executor.dry(g)
-    # per layer the two MatMul->Add->Add chains fold into one GEMM each, and
-    # Gemm->Relu folds once: 4 nodes removed per layer + 1
-    assert ex.node_count() == n_nodes - 4 * cfg["layers"] - 1
+    # per layer the two MatMul->Add->Add chains fold into one GEMM each,
+    # Gemm->Relu folds once and the embedding Add joins its LayerNorm:
+    # 4 nodes removed per layer + 2
+    assert ex.node_count() == n_nodes - 4 * cfg["layers"] - 2
     ids, mask = graphs.encoder_inputs(cfg, 3, 21)
     ex.set_input("input_ids", ids)
     ex.set_input("attention_mask", mask)
@@ -109,3 +110,26 @@ def test_peephole_keeps_shared_intermediates():
     g.add_output("z")
     ex = Executor.dry(g)
     assert ex.node_count() == 3
+
+
+def test_peephole_folds_add_into_layernorm_with_broadcast():
+    """Add(x[B,S,H], p[1,S,H]) -> LayerNorm becomes one LayerNorm whose
+    residual repeats over the batch; a sum that is read twice stays an Add."""
+    def graph(sum_is_output: bool) -> Graph:
+        g = Graph()
+        g.add_initializer("gamma", np.ones(8, np.float32))
+        g.add_initializer("beta", np.zeros(8, np.float32))
+        g.add_node("Add", ["x", "p"], ["s"])
+        g.add_node("FusedLayerNorm", ["s", "gamma", "beta"], ["y"], epsilon=1e-12)
+        g.add_output("y")
+        if sum_is_output:
+            g.add_output("s")
+        return g
+
+    ex = Executor.dry(graph(False))
+    assert ex.node_count() == 1
+    ex.set_input("x", np.zeros((3, 5, 8), np.float32))
+    ex.set_input("p", np.zeros((1, 5, 8), np.float32))
+    ex.run_async()
+    assert ex.output_shape("y") == ((3, 5, 8), np.dtype(np.float32))
+    assert Executor.dry(graph(True)).node_count() == 2

@@ -50,6 +50,38 @@ def test_encoder_unsupported_op_raises(ctx):
         ex.run_async()
 
 
+def test_executor_folds_add_into_layernorm_and_gathers_by_view(ctx):
+    """Add(x[B,S,H], table[positions]) -> LayerNorm runs as one LayerNorm with
+    a residual repeated over the batch, and the Gather of rows 2..S+1 of the
+    table (host-known Range indices) is a view; checked against numpy."""
+    B, S, H = 3, 5, 96
+    rng = np.random.default_rng(120)
+    table = rng.standard_normal((16, H)).astype(np.float32)
+    gamma = rng.standard_normal(H).astype(np.float32)
+    beta = rng.standard_normal(H).astype(np.float32)
+    x = rng.standard_normal((B, S, H)).astype(np.float32)
+    g = rt.Graph()
+    g.add_initializer("table", table)
+    g.add_initializer("gamma", gamma)
+    g.add_initializer("beta", beta)
+    g.add_initializer("start", np.array(2, np.int64))
+    g.add_initializer("stop", np.array(S + 2, np.int64))
+    g.add_initializer("one", np.array(1, np.int64))
+    g.add_node("Range", ["start", "stop", "one"], ["pos"])
+    g.add_node("Unsqueeze", ["pos"], ["pos2"], axes=[0])
+    g.add_node("Gather", ["table", "pos2"], ["pe"], axis=0)
+    g.add_node("Add", ["x", "pe"], ["s"])
+    g.add_node("FusedLayerNorm", ["s", "gamma", "beta"], ["y"], epsilon=1e-12)
+    g.add_output("y")
+    ex = rt.Executor(ctx, g)
+    got = ex.run({"x": x}, ["y"])["y"]
+    s = x.astype(np.float64) + table[2:S + 2][None].astype(np.float64)
+    mu = s.mean(-1, keepdims=True)
+    var = ((s - mu) ** 2).mean(-1, keepdims=True)
+    ref = (s - mu) / np.sqrt(var + 1e-12) * gamma + beta
+    assert np.max(np.abs(got - ref)) <= 1e-4
+
+
 @pytest.mark.parametrize("B,ragged", [(1, False), (32, False), (32, True)])
 def test_distilbert_encoder_config1(ctx, B, ragged):
     """6 layers, H 768, 12x64, FFN 3072, S=128."""
