@@ -146,12 +146,16 @@ def bench_graph(ctx, g, inputs: dict, steps: int, warmup: int) -> float:
     return ms
 
 
-def bench_decode(ctx, max_tokens: int = 128, prompt_len: int = 32):
+def bench_decode(ctx, max_tokens: int = 128, prompt_len: int = 32, int4: bool = False):
+    """Config 4 (int4=False), or the same model switched to int4 weight-only
+    decode (inferc_gpt2_use_int4)."""
     from inferc_amd import graphs, rt
 
     cfg = graphs.GPT2_SMALL
     w = graphs.gpt2_weights(cfg, 2)
     dec = rt.Gpt2Decoder(ctx, cfg, w, max_t=prompt_len + max_tokens)
+    if int4:
+        dec.use_int4()
     prompt = graphs.gpt2_prompt(cfg, prompt_len)
     # One generate call: the step graph is captured before its first timed
     # step, and every post-prefill step is timed (main.cpp:863-872).
@@ -160,11 +164,14 @@ def bench_decode(ctx, max_tokens: int = 128, prompt_len: int = 32):
     return float(np.mean(steps)), float(np.median(steps)), float(np.min(steps)), toks, w, prompt
 
 
-def gpt2_bytes_per_token(cfg: dict, mean_ctx: float) -> float:
+def gpt2_bytes_per_token(cfg: dict, mean_ctx: float, int4: bool = False) -> float:
     H, F, V, L = cfg["hidden"], cfg["ffn"], cfg["vocab"], cfg["layers"]
     weights = L * (3 * H * H + H * H + 2 * H * F) + V * H
+    rows = L * (3 * H + H + F + H) + V  # one int4 scale per weight row
     small = L * (3 * H + H + F + H + 4 * H) + 2 * H + H * 2  # biases, LN, wpe row
     kv = L * 2 * H * mean_ctx
+    if int4:
+        return weights / 2.0 + 4.0 * (rows + small + kv + H)  # + the embedding row
     return 4.0 * (weights + small + kv)
 
 
@@ -372,6 +379,15 @@ def main(argv=None) -> int:
                "hbm_gbps": round(bpt / (d_mean * 1e-3) / 1e9, 1),
                "hbm_frac": round(bpt / (d_mean * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
         log(f"  {d_mean:.4f} ms/token")
+        log("gpt2 decode, int4 weight-only")
+        i_mean, i_p50, i_min, _, _, _ = bench_decode(ctx, int4=True)
+        ibpt = gpt2_bytes_per_token(graphs.GPT2_SMALL, 32 + 64, int4=True)
+        extra["gpt2_decode_int4"] = {
+            "ms_per_token": round(i_mean, 4), "p50": round(i_p50, 4), "min": round(i_min, 4),
+            "tokens_per_s": round(1e3 / i_mean, 1), "bytes_per_token": int(ibpt),
+            "hbm_gbps": round(ibpt / (i_mean * 1e-3) / 1e9, 1),
+            "hbm_frac": round(ibpt / (i_mean * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
+        log(f"  {i_mean:.4f} ms/token")
         for B in (1, 8):
             log(f"int4 grouped GEMV B={B}")
             r = bench_int4(ctx, B)

@@ -231,6 +231,14 @@ int inferc_hip_int4_unpack(inferc_hip_ctx* ctx, int64_t N, int64_t K,
 int inferc_hip_int4_gemv(inferc_hip_ctx* ctx, int64_t N, int64_t K,
                          const uint8_t* W, const float* scales,
                          int64_t batch, const float* x, float* y);
+/* Host-side symmetric per-row quantisation of w [N,K] (fp32) into the
+ * layout above: s_r = max_k |w[r,k]| / 7, q = clamp(rint(w[r,k] / s_r),
+ * -8, 7) (0 for an all-zero row), packed [N, K/2] with nibble q + 8;
+ * deq (nullable) receives s_r * q. The reference's int4 benchmark draws q
+ * at random (int4_gemv_amx.cc:520-535); this is the quantiser for real
+ * weights. No GPU is used. */
+int inferc_int4_quantize_rows(int64_t N, int64_t K, const float* w,
+                              uint8_t* packed, float* scales, float* deq);
 /* One launch over n_mats independent int4 GEMVs (all of a model's matrices).
  * Ns, Ks and the pointer arrays are HOST arrays of length n_mats holding
  * device pointers. x[i] is [batch, Ks[i]], y[i] is [batch, Ns[i]]. */
@@ -335,6 +343,16 @@ int inferc_gpt2_generate(inferc_gpt2* m, const int64_t* prompt,
 /* Full-sequence forward logits [n, V] (host) for every position. */
 int inferc_gpt2_forward(inferc_gpt2* m, const int64_t* ids, int64_t n,
                         float* logits);
+/* Switches the model to int4 weight-only decode, irreversibly: every
+ * projection and the tied LM head are quantised per output row with
+ * inferc_int4_quantize_rows (the int4 format of
+ * bench/amx/int4_gemv_amx.cc:249-250,264-267), the fp32 weights are replaced
+ * by their dequantised values (so prefill, embedding lookup and
+ * inferc_gpt2_forward run the same quantised model), and each decode step
+ * streams the packed weights through the int4 GEMV. The reference measures
+ * that GEMV only standalone; it never runs its decode loop on int4. Needs
+ * hidden 768 and ffn 3072. */
+int inferc_gpt2_use_int4(inferc_gpt2* m);
 
 #ifdef __cplusplus
 }

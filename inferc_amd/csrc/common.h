@@ -295,6 +295,19 @@ struct Gemv2Args {
   ValIdxPart* amax = nullptr;
 };
 bool gemv2_supported(int64_t K);
+// Batch-1 int4 GEMV for the decode step (K = 768 or 3072): optional
+// LayerNorm of x (K = 768), y = act(s_r*acc + bias + res), or with amax set
+// one first-max (value, row) partial per wave instead of y.
+int64_t int4_dec_waves(int64_t N, int64_t K);
+void int4_gemv_dec(inferc_hip_ctx* ctx, int64_t N, int64_t K, const uint8_t* W,
+                   const float* scales, const float* x, const float* ln_g, const float* ln_b,
+                   float ln_eps, const float* bias, const float* res, int act, float* y,
+                   ValIdxPart* amax);
+// Symmetric per-row int4 quantisation of an [N, K] fp32 matrix (host):
+// s_r = max|w_r| / 7, q = clamp(rint(w / s_r), -8, 7), packed nibble q + 8
+// (low nibble = even k); deq (optional) receives s_r * q.
+void int4_quantize_rows(int64_t N, int64_t K, const float* w, uint8_t* packed, float* scales,
+                        float* deq);
 int64_t gemv2_blocks(inferc_hip_ctx* ctx, int64_t N, int64_t K, bool argmax);
 void gemv2(inferc_hip_ctx* ctx, const Gemv2Args& a);
 

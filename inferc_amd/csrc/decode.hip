@@ -367,6 +367,9 @@ struct inferc_gpt2 {
   struct Layer {
     float *ln1_g, *ln1_b, *attn_w, *attn_b, *proj_w, *proj_b;
     float *ln2_g, *ln2_b, *fc_w, *fc_b, *fcproj_w, *fcproj_b;  // *_w are [N, K]
+    // int4 weight-only mode: packed [N, K/2] nibbles and per-row scales
+    uint8_t *attn_q = nullptr, *proj_q = nullptr, *fc_q = nullptr, *fcproj_q = nullptr;
+    float *attn_s = nullptr, *proj_s = nullptr, *fc_s = nullptr, *fcproj_s = nullptr;
   };
   std::vector<Layer> layers;
   float *lnf_g = nullptr, *lnf_b = nullptr;
@@ -377,6 +380,15 @@ struct inferc_gpt2 {
   void* argmax_ws = nullptr;  // model-owned, so the captured step never uses ctx->ws
   ih::ValIdxPart* amax = nullptr;  // LM-head block partials of the argmax
   int64_t amax_n = 0;
+  // int4 weight-only decode: every projection and the tied LM head are
+  // quantised per row; the fp32 copies hold the dequantised values (used by
+  // the prefill and the embedding lookup, so the whole model is the
+  // quantised one).
+  bool int4 = false;
+  uint8_t* wte_q = nullptr;
+  float* wte_s = nullptr;
+  ih::ValIdxPart* amax4 = nullptr;  // one partial per wave of the int4 LM head
+  int64_t amax4_n = 0;
   int64_t* ids = nullptr;     // [max_t]
   float *ph = nullptr, *pa = nullptr, *pqkv = nullptr, *patt = nullptr, *pf = nullptr;
   hipGraphExec_t step_exec = nullptr;
@@ -437,6 +449,26 @@ struct inferc_gpt2 {
                          dim3(ih::kBlock), 0, s, wte, wpe, state, Hh, h);
       ih::check_launch("embed_step");
     }
+    if (int4) {
+      // the same five launches per layer, weights streamed as int4
+      for (int64_t l = 0; l < cfg.layers; ++l) {
+        const Layer& L = layers[size_t(l)];
+        ih::int4_gemv_dec(ctx, 3 * Hh, Hh, L.attn_q, L.attn_s, h, L.ln1_g, L.ln1_b, cfg.eps,
+                          L.attn_b, nullptr, INFERC_ACT_NONE, qkv, nullptr);
+        ih::AttnDecP ap{max_t, state, qkv, qkv + Hh, qkv + 2 * Hh, kc_l(l), vc_l(l), att};
+        hipLaunchKernelGGL(ih::attn_decode_d64, dim3(unsigned(cfg.heads)),
+                           dim3(64 * ih::kDecWaves), 0, s, ap);
+        ih::check_launch("attn_decode");
+        ih::int4_gemv_dec(ctx, Hh, Hh, L.proj_q, L.proj_s, att, nullptr, nullptr, 0.0f, L.proj_b,
+                          h, INFERC_ACT_NONE, h, nullptr);
+        ih::int4_gemv_dec(ctx, F, Hh, L.fc_q, L.fc_s, h, L.ln2_g, L.ln2_b, cfg.eps, L.fc_b,
+                          nullptr, INFERC_ACT_GELU_TANH, f, nullptr);
+        ih::int4_gemv_dec(ctx, Hh, F, L.fcproj_q, L.fcproj_s, f, nullptr, nullptr, 0.0f,
+                          L.fcproj_b, h, INFERC_ACT_NONE, h, nullptr);
+      }
+      lm_head_finish(h);
+      return;
+    }
     for (int64_t l = 0; l < cfg.layers; ++l) {
       const Layer& L = layers[size_t(l)];
       ih::gemv(ctx, 3 * Hh, Hh, L.attn_w, h, L.ln1_g, L.ln1_b, cfg.eps, L.attn_b, nullptr,
@@ -466,6 +498,15 @@ struct inferc_gpt2 {
   // tokens[state[0]+1] = argmax (first max), state advanced by one position.
   void lm_head_finish(const float* hrow) {
     const int64_t Hh = H(), V = cfg.vocab;
+    if (int4) {
+      ih::int4_gemv_dec(ctx, V, Hh, wte_q, wte_s, hrow, lnf_g, lnf_b, cfg.eps, nullptr, nullptr,
+                        INFERC_ACT_NONE, logits, amax4);
+      hipLaunchKernelGGL(ih::decode_finish_kernel, dim3(1), dim3(ih::kFinishThreads), 0,
+                         ctx->stream, amax4, int(amax4_n), state, tokens, wte, wpe, h, Hh,
+                         cfg.max_pos);
+      ih::check_launch("decode_finish");
+      return;
+    }
     if (fast()) {
       ih::Gemv2Args a;
       a.N = V; a.K = Hh; a.W = wte; a.x = hrow; a.ln_g = lnf_g; a.ln_b = lnf_b;
@@ -538,6 +579,46 @@ struct inferc_gpt2 {
       g4.R = ph; g4.ldr = Hh; g4.Y = ph; g4.ldy = Hh;
       ih::gemm(ctx, g4);
     }
+  }
+
+  // Quantises the [N, K] matrix at dev (host round trip: read, quantise per
+  // row, write back the dequantised values) into packed nibbles and scales.
+  void quantize_matrix(float* dev, int64_t N, int64_t K, uint8_t** q, float** sc) {
+    const size_t nk = static_cast<size_t>(N * K);
+    std::vector<float> w(nk), deq(nk), s(static_cast<size_t>(N));
+    std::vector<uint8_t> packed(nk / 2);
+    IH_HIP(hipMemcpy(w.data(), dev, w.size() * sizeof(float), hipMemcpyDeviceToHost));
+    ih::int4_quantize_rows(N, K, w.data(), packed.data(), s.data(), deq.data());
+    *q = alloc<uint8_t>(packed.size());
+    *sc = alloc<float>(s.size());
+    IH_HIP(hipMemcpy(*q, packed.data(), packed.size(), hipMemcpyHostToDevice));
+    IH_HIP(hipMemcpy(*sc, s.data(), s.size() * sizeof(float), hipMemcpyHostToDevice));
+    IH_HIP(hipMemcpy(dev, deq.data(), deq.size() * sizeof(float), hipMemcpyHostToDevice));
+  }
+
+  void enable_int4() {
+    if (int4) return;
+    const int64_t Hh = H(), F = cfg.ffn, V = cfg.vocab;
+    IH_REQUIRE(fast() && Hh == 768 && F == 3072, INFERC_ERR_UNSUPPORTED,
+               "int4 decode: needs the GPT-2-small row lengths (hidden 768, ffn 3072)");
+    IH_HIP(hipStreamSynchronize(ctx->stream));
+    for (Layer& L : layers) {
+      quantize_matrix(L.attn_w, 3 * Hh, Hh, &L.attn_q, &L.attn_s);
+      quantize_matrix(L.proj_w, Hh, Hh, &L.proj_q, &L.proj_s);
+      quantize_matrix(L.fc_w, F, Hh, &L.fc_q, &L.fc_s);
+      quantize_matrix(L.fcproj_w, Hh, F, &L.fcproj_q, &L.fcproj_s);
+    }
+    quantize_matrix(wte, V, Hh, &wte_q, &wte_s);
+    amax4_n = ih::int4_dec_waves(V, Hh);
+    IH_REQUIRE(amax4_n <= ih::kFinishThreads * ih::kFinishPerThread, INFERC_ERR_UNSUPPORTED,
+               "int4 decode: vocabulary too large for the argmax tail");
+    amax4 = alloc<ih::ValIdxPart>(size_t(amax4_n));
+    // the captured step used the fp32 kernels: capture it again
+    if (step_exec) (void)hipGraphExecDestroy(step_exec);
+    if (step_graph) (void)hipGraphDestroy(step_graph);
+    step_exec = nullptr;
+    step_graph = nullptr;
+    int4 = true;
   }
 
   void capture_step() {
@@ -662,6 +743,13 @@ int inferc_gpt2_create(inferc_hip_ctx* ctx, const inferc_gpt2_config* cfg,
       throw;
     }
     *out = m;
+  });
+}
+
+int inferc_gpt2_use_int4(inferc_gpt2* m) {
+  return ih::guard([&] {
+    check_model(m);
+    m->enable_int4();
   });
 }
 

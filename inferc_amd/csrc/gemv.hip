@@ -671,6 +671,127 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_valu_kernel(const Int4VaDesc
   }
 }
 
+// Batch-1 int4 GEMV of one matrix for the decode step: the unrolled run of
+// int4_valu_fixed with the step's fusions around it.
+//   - LayerNorm prologue (ln_g set; the K = 768 form): every wave reduces
+//     the whole x row (mean, then the centred second moment, as LayerNorm)
+//     and normalises its own slice before the weight arithmetic.
+//   - Epilogue per row, in the fp32 GEMV's order: v = s_r*acc + bias +
+//     residual, then the activation; y may alias the residual (each row is
+//     read and written by the same lane).
+//   - amax set (the LM head): each wave also stores the first maximum
+//     (value, row) of its rows, for the step's finishing kernel (y may be
+//     null then).
+struct Int4DecP {
+  Int4VaDesc d;
+  const float* ln_g;
+  const float* ln_b;
+  float ln_eps;
+  const float* bias;
+  const float* res;
+  int act;
+  ValIdxPart* amax;
+};
+
+// One wave per block: a decode-step matrix (1.7 to 2.4 MB of int4) is a few
+// hundred waves, which then land on as many CUs.
+constexpr int kI4DecBlock = 64;
+
+template <int DW, int LT, int NC>
+__global__ __launch_bounds__(kI4DecBlock) void int4_gemv_dec_kernel(Int4DecP p, int64_t n_waves) {
+  static_assert(LT >= 4 && NC <= LT / 4, "a lane keeps one chunk's row");
+  constexpr int K = 8 * DW * LT, rpp = 64 / LT;
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = blockIdx.x;
+  if (wid >= n_waves) return;
+  const Int4VaDesc& d = p.d;
+  const int s = lane & (LT - 1), rg = lane / LT;
+  const int64_t c0 = wid * NC;
+  const int n = int(d.chunks - c0 < NC ? d.chunks - c0 : NC);
+  auto keep = [&](int j) { return j < n ? ~0u : 0u; };
+
+  float4 xv[2 * DW];
+  const float4* xp = reinterpret_cast<const float4*>(d.x + 8 * DW * s);
+#pragma unroll
+  for (int q = 0; q < 2 * DW; ++q) xv[q] = gload_f4(xp + q);
+  constexpr int PL = K / 64;  // x values per lane for the row statistics
+  float xs[PL];
+  if (p.ln_g) {
+#pragma unroll
+    for (int i = 0; i < PL; ++i) xs[i] = gload_f(d.x + lane + 64 * i);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  I4Chunk<DW> buf[2];
+  i4_load_chunk<DW, LT>(buf[0], d, c0, ~0u, rpp, rg, s);
+  if constexpr (NC > 1) i4_load_chunk<DW, LT>(buf[1], d, c0 + 1, keep(1), rpp, rg, s);
+  __builtin_amdgcn_sched_barrier(0);
+  if (p.ln_g) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) sum += xs[i];
+    const float mean = wave_sum(sum) / float(K);
+    float q2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const float dd = xs[i] - mean;
+      q2 += dd * dd;
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(q2) / float(K) + p.ln_eps);
+    const float4* gp = reinterpret_cast<const float4*>(p.ln_g + 8 * DW * s);
+    const float4* bp = reinterpret_cast<const float4*>(p.ln_b + 8 * DW * s);
+#pragma unroll
+    for (int q = 0; q < 2 * DW; ++q) {
+      const float4 g = gload_f4(gp + q), b = gload_f4(bp + q);
+      xv[q].x = ((xv[q].x - mean) * inv) * g.x + b.x;
+      xv[q].y = ((xv[q].y - mean) * inv) * g.y + b.y;
+      xv[q].z = ((xv[q].z - mean) * inv) * g.z + b.z;
+      xv[q].w = ((xv[q].w - mean) * inv) * g.w + b.w;
+    }
+  }
+  float xsum = 0.0f, xe[4 * DW], xo[4 * DW];
+#pragma unroll
+  for (int q = 0; q < 2 * DW; ++q) {
+    xsum += (xv[q].x + xv[q].y) + (xv[q].z + xv[q].w);
+    xo[2 * q] = xv[q].y * 0.0625f;
+    xo[2 * q + 1] = xv[q].w * 0.0625f;
+    xe[2 * q] = xv[q].x - xo[2 * q];
+    xe[2 * q + 1] = xv[q].z - xo[2 * q + 1];
+  }
+  const float xsum8 = 8.0f * xsum;
+  float res = 0.0f, res4[kI4Passes];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    __builtin_amdgcn_sched_barrier(0);
+    i4_chunk_rows<DW, LT>(buf[j & 1], xe, xo, xsum8, LT, s, j, res, res4);
+    __builtin_amdgcn_sched_barrier(0);
+    if (j + 2 < NC) i4_load_chunk<DW, LT>(buf[j & 1], d, c0 + j + 2, keep(j + 2), rpp, rg, s);
+  }
+  const int j = s % (LT / 4), pr = s / (LT / 4);
+  const int64_t r = ((c0 + j) * kI4Passes + pr) * rpp + rg;
+  const bool valid = j < n && r < d.N;
+  float v = res;
+  if (valid) {
+    if (p.bias) v += gload_f(p.bias + r);
+    if (p.res) v += gload_f(p.res + r);
+    v = apply_act(v, p.act);
+  }
+  if (valid && d.y) gstore_f(d.y + r, v);
+  if (p.amax == nullptr) return;
+  // first maximum of the wave's rows (a NaN never wins, as in the fp32 head)
+  float bv = valid ? v : -INFINITY;
+  int64_t bi = valid ? r : INT64_MAX;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float w = __shfl_xor(bv, o, 64);
+    const int64_t wi = __shfl_xor(bi, o, 64);
+    if (w > bv || (w == bv && wi < bi)) {
+      bv = w;
+      bi = wi;
+    }
+  }
+  if (lane == 0) p.amax[wid] = ValIdxPart{bv, bi};
+}
+
 // int4 GEMV on the int8 matrix cores, exact in integer arithmetic.
 //
 // The dequantised product is y[b][r] = s_r * sum_k (nib - 8) x[b][k]. The
@@ -1641,6 +1762,77 @@ void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const 
 }
 
 }  // namespace
+
+// Chunks per wave of the decode-step int4 GEMV: one (the least latency) for
+// the layers' matrices, a 12 KB run for the LM head (a 19 MB stream).
+int int4_dec_chunks(int64_t N, int64_t K) {
+  return N * K / 2 > (int64_t(8) << 20) ? kI4RunKB / (K == 768 ? 3 : 6) : 1;
+}
+
+// Waves of the decode-step int4 GEMV for an [N, K] matrix (also the number
+// of argmax partials it writes); 0 when K is not a supported row length.
+int64_t int4_dec_waves(int64_t N, int64_t K) {
+  if (K != 768 && K != 3072) return 0;
+  const int64_t rows_per_chunk = int64_t(kI4Passes) * (K == 768 ? 2 : 1);
+  return ceil_div(ceil_div(N, rows_per_chunk), int4_dec_chunks(N, K));
+}
+
+void int4_quantize_rows(int64_t N, int64_t K, const float* w, uint8_t* packed, float* scales,
+                        float* deq) {
+  IH_REQUIRE(N >= 0 && K >= 0 && K % 2 == 0, INFERC_ERR_SHAPE, "int4 quantize: K must be even");
+  IH_REQUIRE(N == 0 || K == 0 || (w && packed && scales), INFERC_ERR_ARG,
+             "int4 quantize: null pointer");
+  for (int64_t r = 0; r < N; ++r) {
+    const float* wr = w + r * K;
+    float m = 0.0f;
+    for (int64_t k = 0; k < K; ++k) m = std::max(m, std::fabs(wr[k]));
+    const float sc = m / 7.0f;
+    scales[r] = sc;
+    for (int64_t k = 0; k < K; k += 2) {
+      int q[2];
+      for (int e = 0; e < 2; ++e) {
+        const float t = sc > 0.0f ? std::nearbyint(wr[k + e] / sc) : 0.0f;
+        q[e] = int(std::min(7.0f, std::max(-8.0f, t)));
+        if (deq) deq[r * K + k + e] = sc * float(q[e]);
+      }
+      packed[r * (K / 2) + k / 2] = uint8_t((q[0] + 8) | ((q[1] + 8) << 4));
+    }
+  }
+}
+
+void int4_gemv_dec(inferc_hip_ctx* ctx, int64_t N, int64_t K, const uint8_t* W,
+                   const float* scales, const float* x, const float* ln_g, const float* ln_b,
+                   float ln_eps, const float* bias, const float* res, int act, float* y,
+                   ValIdxPart* amax) {
+  IH_REQUIRE(int4_dec_waves(N, K) > 0 && N > 0 && N < (int64_t(1) << 31), INFERC_ERR_UNSUPPORTED,
+             "int4 decode GEMV: K must be 768 or 3072");
+  IH_REQUIRE(W && scales && x && (y || amax), INFERC_ERR_ARG, "int4 decode GEMV: null pointer");
+  IH_REQUIRE((reinterpret_cast<uintptr_t>(W) & 3) == 0 && aligned16(x), INFERC_ERR_ARG,
+             "int4 decode GEMV: W must be 4-byte and x 16-byte aligned");
+  IH_REQUIRE(!ln_g || (K == 768 && ln_b && aligned16(ln_g) && aligned16(ln_b)), INFERC_ERR_ARG,
+             "int4 decode GEMV: LayerNorm needs K = 768 and aligned gamma/beta");
+  const int dw = K == 768 ? 3 : 6, nc = int4_dec_chunks(N, K);
+  const int64_t L = K / 8 / dw, chunks = ceil_div(N, int64_t(kI4Passes) * (64 / L));
+  const int64_t waves = int4_dec_waves(N, K);
+  Int4DecP p{};
+  p.d = Int4VaDesc{W, scales, x, y, N, K, 0, dw, chunks, nc};
+  p.ln_g = ln_g; p.ln_b = ln_b; p.ln_eps = ln_eps;
+  p.bias = bias; p.res = res; p.act = act; p.amax = amax;
+  const dim3 grid{unsigned(waves)}, block{unsigned(kI4DecBlock)};
+  if (dw == 3 && nc == 1)
+    hipLaunchKernelGGL((int4_gemv_dec_kernel<3, 32, 1>), grid, block, 0, ctx->stream, p, waves);
+  else if (dw == 3)
+    hipLaunchKernelGGL((int4_gemv_dec_kernel<3, 32, kI4RunKB / 3>), grid, block, 0, ctx->stream,
+                       p, waves);
+  else if (nc == 1)
+    hipLaunchKernelGGL((int4_gemv_dec_kernel<6, 64, 1>), grid, block, 0, ctx->stream, p, waves);
+  else
+    hipLaunchKernelGGL((int4_gemv_dec_kernel<6, 64, kI4RunKB / 6>), grid, block, 0, ctx->stream,
+                       p, waves);
+  check_launch("int4_gemv_dec");
+}
+
+
 }  // namespace ih
 
 extern "C" {
@@ -1676,6 +1868,11 @@ int inferc_hip_int4_gemv(inferc_hip_ctx* ctx, int64_t N, int64_t K, const uint8_
     ih::check_ctx(ctx)->make_current();
     ih::int4_grouped(ctx, 1, &N, &K, &W, &scales, batch, &x, &y);
   });
+}
+
+int inferc_int4_quantize_rows(int64_t N, int64_t K, const float* w, uint8_t* packed,
+                              float* scales, float* deq) {
+  return ih::guard([&] { ih::int4_quantize_rows(N, K, w, packed, scales, deq); });
 }
 
 int inferc_hip_int4_gemv_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns,

@@ -142,6 +142,36 @@ def gpt2_weights(cfg: dict, seed: int = 2) -> list[np.ndarray]:
     return w
 
 
+def int4_quantize_rows_np(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Per-row symmetric int4 quantisation in numpy (fp32 arithmetic):
+    s_r = max|w_r| / 7, q = clip(rint(w / s_r), -8, 7), 0 for an all-zero
+    row. Returns (q as int8 [N, K], s [N]); the dequantised row is s_r * q."""
+    w = np.ascontiguousarray(w, np.float32)
+    s = (np.abs(w).max(axis=1) / np.float32(7)).astype(np.float32)
+    safe = np.where(s > 0, s, np.float32(1))[:, None]
+    q = np.where(s[:, None] > 0, np.rint(w / safe), np.float32(0))
+    return np.clip(q, -8, 7).astype(np.int8), s
+
+
+def gpt2_int4_dequantized(cfg: dict, w: list[np.ndarray]) -> list[np.ndarray]:
+    """The weights of an int4 weight-only GPT-2 (inferc_gpt2_use_int4), as
+    fp32 values: every projection quantised per output feature (a column of
+    the [K, N] matrix) and the tied wte per vocabulary row; biases, LayerNorm
+    and wpe unchanged."""
+    out = [a.copy() for a in w]
+
+    def deq_rows(m):  # rows of m are the quantised rows
+        q, s = int4_quantize_rows_np(m)
+        return (s[:, None] * q.astype(np.float32)).astype(np.float32)
+
+    out[0] = deq_rows(w[0])
+    for l in range(cfg["layers"]):
+        base = 2 + 12 * l
+        for off in (2, 4, 8, 10):
+            out[base + off] = np.ascontiguousarray(deq_rows(w[base + off].T).T)
+    return out
+
+
 def gpt2_prompt(cfg: dict, n: int, seed: int = 3) -> np.ndarray:
     return rng_for(seed, f"prompt_{n}").integers(0, cfg["vocab"], size=n, dtype=np.int64)
 

@@ -103,6 +103,8 @@ _SIGS = {
     "inferc_executor_set_graph_mode": [vp, i32],
     "inferc_gpt2_create": [vp, vp, P(vp), i64, P(vp)],
     "inferc_gpt2_destroy": [vp],
+    "inferc_gpt2_use_int4": [vp],
+    "inferc_int4_quantize_rows": [i64, i64, vp, vp, vp, vp],
     "inferc_gpt2_generate": [vp, P(i64), i64, i64, P(i64), P(f32), P(f32)],
     "inferc_gpt2_forward": [vp, P(i64), i64, P(f32)],
 }

@@ -525,6 +525,21 @@ def Int4Gemv(w: Tensor, scales: Tensor, x: Tensor, K: int) -> Tensor:
     return out
 
 
+def int4_quantize_rows(w: np.ndarray, lib=None) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Per-row symmetric int4 quantisation of w [N, K] on the host (no GPU):
+    returns (packed [N, K/2] uint8, scales [N] fp32, dequantised [N, K] fp32)."""
+    from . import lib as L
+    w = _c_order(w, np.float32)
+    N, K = w.shape
+    packed = np.empty((N, K // 2), np.uint8)
+    scales = np.empty(N, np.float32)
+    deq = np.empty((N, K), np.float32)
+    lb = lib or L.load_library()
+    check(lb.inferc_int4_quantize_rows(N, K, w.ctypes.data, packed.ctypes.data,
+                                       scales.ctypes.data, deq.ctypes.data))
+    return packed, scales, deq
+
+
 def int4_gemv_grouped(ctx: Context, mats: Sequence[tuple[Tensor, Tensor, Tensor, Tensor, int]],
                       batch: int) -> None:
     """One launch over many int4 GEMVs; each entry is (W, scales, x, y, K)."""
@@ -722,6 +737,10 @@ class Gpt2Decoder:
             steps.ctypes.data_as(fp) if steps is not None else None,
             logits.ctypes.data_as(fp) if logits is not None else None))
         return toks, (steps[:max_tokens - 1] if steps is not None else None), logits
+
+    def use_int4(self) -> None:
+        """int4 weight-only decode (irreversible): see inferc_gpt2_use_int4."""
+        check(self.ctx._lib.inferc_gpt2_use_int4(self.handle))
 
     def forward(self, ids: np.ndarray) -> np.ndarray:
         i = _c_order(ids, np.int64)

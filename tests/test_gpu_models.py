@@ -131,6 +131,36 @@ def test_gpt2_forward_logits_config4(ctx, gpt2_full):
     assert np.max(np.abs(got - ref)) <= 1e-4, np.max(np.abs(got - ref))
 
 
+def test_gpt2_int4_decode_matches_oracle_on_dequantised_weights(ctx, gpt2_full):
+    """int4 weight-only decode (inferc_gpt2_use_int4) against the oracle GPT-2
+    run on the same weights dequantised by the numpy statement of the
+    quantiser: greedy tokens bit-exact, last logits and the prefill forward
+    within 1e-4."""
+    cfg, w = gpt2_full
+    wq = graphs.gpt2_int4_dequantized(cfg, w)
+    prompt = graphs.gpt2_prompt(cfg, 16)
+    dec = rt.Gpt2Decoder(ctx, cfg, w, max_t=64)
+    dec.use_int4()
+    dec.use_int4()  # a second call changes nothing
+    toks, steps, logits = dec.generate(prompt, 24, want_step_ms=True, want_logits=True)
+    ref_toks, ref_logits, margins = O.gpt2_generate(cfg, wq, prompt, 24)
+    print(f"int4: min top-2 margin {margins.min():.3e}; max |dlogit| "
+          f"{np.max(np.abs(logits - ref_logits)):.3e}; ms/token {steps.mean():.4f}")
+    np.testing.assert_array_equal(toks, ref_toks)
+    assert np.max(np.abs(logits - ref_logits)) <= 1e-4
+    got = dec.forward(prompt)
+    assert np.max(np.abs(got - O.gpt2_forward(cfg, wq, prompt))) <= 1e-4
+    toks2, _, _ = dec.generate(prompt, 24)
+    np.testing.assert_array_equal(toks2, toks)
+
+
+def test_gpt2_int4_rejects_other_shapes(ctx):
+    cfg = graphs.small_gpt2_cfg()
+    dec = rt.Gpt2Decoder(ctx, cfg, graphs.gpt2_weights(cfg, 23), max_t=16)
+    with pytest.raises(RuntimeError, match="hidden 768, ffn 3072"):
+        dec.use_int4()
+
+
 def test_gpt2_greedy_decode_config4_bit_exact(ctx, gpt2_full):
     """prompt 32, 128 generated tokens, sequence bit-exact."""
     cfg, w = gpt2_full
