@@ -291,6 +291,108 @@ def cpu_baseline_encoder(weights, budget_s: float = 12.0):
     return el / n * 1e3, n, O.num_threads()
 
 
+def cpu_profile_encoder(weights, B: int = 1, S: int = 128, iters: int = 3):
+    """The CPU baseline's per-op profile in the same JSON schema: the oracle's
+    encoder forward replayed op by op through the oracle's per-op functions
+    under the native profiler's host clock, one op record per op of the
+    executor's fused graph (embedding Gathers, the embedding Add folded into
+    its LayerNorm, per layer FusedQKV, FusedAttention, the MatMul + bias +
+    residual epilogue GEMMs, LayerNorms and FusedMatMulAddGELU, then the two
+    classifier Gemms). The last pass's logits are checked against the
+    oracle's own encoder forward."""
+    import oracle as O
+    from inferc_amd import graphs
+    from inferc_amd.profiler import Profiler
+
+    cfg = graphs.DISTILBERT
+    H, L, nh = cfg["hidden"], cfg["layers"], cfg["heads"]
+    eps = cfg["eps"]
+    w = [np.ascontiguousarray(t, np.float32) for t in weights]
+    ids, amask = graphs.encoder_inputs(cfg, B, S)
+    p = Profiler()
+    p.set_track_activation_bytes(False)
+
+    def op(kind, name, fn, *a):
+        p.begin_op(kind, name)
+        r = fn(*a)
+        p.end_op(0)
+        return r
+
+    def gemm_res(x, wt, b, res):
+        return O.add_bcast(O.add_bcast(O.sgemm(x, wt), b), res)
+
+    for _ in range(iters):
+        p.begin_iteration()
+        tok = op("Gather", "word_embeddings", O.gather_rows, w[0], ids.reshape(-1))
+        pos = op("Gather", "position_embeddings", O.gather_rows, w[1], np.arange(S))
+        h = op("FusedLayerNorm", "embeddings.LayerNorm",
+               lambda: O.layernorm(O.add_bcast(tok.reshape(B, S, H), pos), w[2], w[3], eps))
+        mask = (amask == 0).reshape(B, 1, 1, S)
+        for l in range(L):
+            lw = w[4 + 16 * l: 4 + 16 * (l + 1)]
+            x2 = h.reshape(B * S, H)
+            q, k, v = op("FusedQKV", f"l{l}.qkv", O.fused_qkv, x2, *lw[0:6])
+            c = op("FusedAttention", f"l{l}.attn", O.fused_attention, q.reshape(B, S, H),
+                   k.reshape(B, S, H), v.reshape(B, S, H), mask, H // nh, -3.4028234663852886e38)
+            t = op("FusedGemmEpilogue", f"l{l}.out_lin", gemm_res, c.reshape(B * S, H), lw[6],
+                   lw[7], x2)
+            h1 = op("FusedLayerNorm", f"l{l}.sa_layer_norm", O.layernorm, t, lw[8], lw[9], eps)
+            f = op("FusedMatMulAddGELU", f"l{l}.ffn.lin1", O.fused_matmul_add_gelu, h1, lw[10],
+                   lw[11])
+            t = op("FusedGemmEpilogue", f"l{l}.ffn.lin2", gemm_res, f, lw[12], lw[13], h1)
+            h = op("FusedLayerNorm", f"l{l}.output_layer_norm", O.layernorm, t, lw[14], lw[15],
+                   eps).reshape(B, S, H)
+        tw = w[4 + 16 * L:]
+        cls = np.ascontiguousarray(h[:, 0, :])
+        pre = op("Gemm", "pre_classifier", lambda: np.maximum(
+            O.gemm(cls, tw[0], tw[1], trans_b=True), np.float32(0)))
+        logits = op("Gemm", "classifier", O.gemm, pre, tw[2], tw[3], 1.0, 1.0, False, True)
+        p.end_iteration()
+    p.snapshot_peak_rss()
+    ref = O.encoder_forward(cfg, weights, ids, amask)
+    err = float(np.max(np.abs(logits - ref)))
+    if err > 1e-5:
+        raise RuntimeError(f"per-op CPU replay differs from the oracle encoder by {err}")
+    return p.report(f"oracle-cpu-{O.num_threads()}t", "distilbert_encoder_b1_s128")
+
+
+def write_profiles(ctx, out_dir: str, enc_w) -> None:
+    """--profile-dir: per-op profiles in the reference's JSON schema of the
+    encoder (b1 s128, executor, device times per node), its CPU baseline
+    replay, and the GPT-2 decode steps; plus the `inferc compare` table of
+    the two encoder profiles."""
+    from inferc_amd import graphs, rt
+    from inferc_amd.profiler import Profiler, compare_table
+
+    d = Path(out_dir)
+    d.mkdir(parents=True, exist_ok=True)
+    cfg = graphs.DISTILBERT
+    ex = rt.Executor(ctx, graphs.encoder_graph(cfg, enc_w))
+    ids, mask = graphs.encoder_inputs(cfg, 1, 128)
+    hip = ex.profile({"input_ids": ids, "attention_mask": mask}, iters=20, warmup=3,
+                     backend="inferc-hip-gfx950", model="distilbert_encoder_b1_s128")
+    ex.close()
+    (d / "encoder_b1_s128.hip.json").write_text(json.dumps(hip, indent=2, sort_keys=True))
+    log("  encoder profile written")
+    cpu = cpu_profile_encoder(enc_w)
+    (d / "encoder_b1_s128.cpu.json").write_text(json.dumps(cpu, indent=2, sort_keys=True))
+    table = compare_table(hip, cpu)
+    (d / "encoder_b1_s128.compare.txt").write_text(table)
+    log(table)
+    gcfg = graphs.GPT2_SMALL
+    dec = rt.Gpt2Decoder(ctx, gcfg, graphs.gpt2_weights(gcfg, 2), max_t=160)
+    for int4 in (False, True):
+        if int4:
+            dec.use_int4()
+        p = Profiler()
+        dec.generate_profiled(graphs.gpt2_prompt(gcfg, 32), 33, p)
+        name = "gpt2_decode_int4" if int4 else "gpt2_decode"
+        rep = p.report("inferc-decode-hip" + ("-int4" if int4 else ""), name)
+        (d / f"{name}.hip.json").write_text(json.dumps(rep, indent=2, sort_keys=True))
+        log(f"  {name} profile written")
+    dec.close()
+
+
 def cpu_baseline_decode(weights, prompt, tokens: int = 6):
     import oracle as O
     from inferc_amd import graphs
@@ -314,6 +416,8 @@ def main(argv=None) -> int:
     ap.add_argument("--quick", action="store_true", help="primary workload and roofline only")
     ap.add_argument("--roofline-only", action="store_true",
                     help="roofline kernel + calibration copy only (for rocprofv3 --pmc runs)")
+    ap.add_argument("--profile-dir", default=None,
+                    help="also write per-op profiles (reference JSON schema) to this folder")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -406,6 +510,10 @@ def main(argv=None) -> int:
             cpu["gpt2_decode_ms_per_token"] = round(cdec, 3)
             cpu["sample"] += "; GPT-2 decode 6 tokens after an 8-token prompt"
         log(f"  {cms:.2f} ms/forward on {thr} threads")
+
+    if args.profile_dir:
+        log(f"per-op profiles -> {args.profile_dir}")
+        write_profiles(ctx, args.profile_dir, enc_w)
 
     line = {
         "metric": METRIC,

@@ -312,6 +312,54 @@ int inferc_executor_get_output(inferc_executor* ex, const char* name,
 /* 0 = eager dispatch every run, 1 = capture/replay HIP graphs (default). */
 int inferc_executor_set_graph_mode(inferc_executor* ex, int enabled);
 
+/* ---------------- Profiler (src/profiler/profiler.h:40-89) ---------------- */
+
+/* prof::Profiler: per-op records over a sequence of inference passes
+ * ("iterations") and the JSON report of profiler.cc:138-176. The host-clock
+ * calls mirror BeginIteration/EndIteration/BeginOp/EndOp
+ * (profiler.h:42-47): BeginOp while an op is in flight and EndOp without
+ * BeginOp fail with INFERC_ERR_STATE (profiler.cc:68-90). Records made by
+ * inferc_executor_run_profiled and inferc_gpt2_generate_profiled carry
+ * device times instead. */
+typedef struct inferc_profiler inferc_profiler;
+int inferc_profiler_create(inferc_profiler** out);
+int inferc_profiler_destroy(inferc_profiler* p);
+int inferc_profiler_begin_iteration(inferc_profiler* p);
+int inferc_profiler_end_iteration(inferc_profiler* p);
+int inferc_profiler_begin_op(inferc_profiler* p, const char* op_type,
+                             const char* node_name);
+int inferc_profiler_end_op(inferc_profiler* p, int64_t activation_bytes_after);
+/* Records a finished op whose time the caller measured itself (no
+ * counterpart in the reference, whose ops are always timed by the host clock
+ * between BeginOp and EndOp); fails while an op is in flight. */
+int inferc_profiler_record_op(inferc_profiler* p, const char* op_type,
+                              const char* node_name, double ms,
+                              int64_t activation_bytes_after);
+/* SetTrackActivationBytes (profiler.h:53): with 0, profiled executor runs
+ * record 0 activation bytes and skip the O(tape) sum per node. Default 1. */
+int inferc_profiler_set_track_activation_bytes(inferc_profiler* p, int on);
+/* SnapshotPeakRss (profiler.h:57): the process's peak resident set. */
+int inferc_profiler_snapshot_peak_rss(inferc_profiler* p);
+int inferc_profiler_iteration_count(inferc_profiler* p, int64_t* n);
+/* TotalStats (profiler.h:64): out5 = {mean, p50, p95, min, max} in ms. */
+int inferc_profiler_total_stats(inferc_profiler* p, double* out5);
+/* ToJson (profiler.h:75-76). *len receives the length without the NUL;
+ * buf == NULL only queries it; capacity must be at least *len + 1. */
+int inferc_profiler_to_json(inferc_profiler* p, const char* backend,
+                            const char* model, char* buf, size_t capacity,
+                            size_t* len);
+/* Percentile (profiler.h:87): linear interpolation between closest ranks
+ * (numpy's default); 0 for an empty sample. */
+int inferc_profile_percentile(const double* v, int64_t n, double p, double* out);
+/* StatsFrom (profiler.h:88): out5 = {mean, p50, p95, min, max}. */
+int inferc_profile_stats(const double* v, int64_t n, double* out5);
+/* Executor::Run(inputs, profiler) (src/runtime/executor.cc:98-125,349-354):
+ * one eager pass recorded as one iteration, one op record per node. An op's
+ * time is the device time between HIP events recorded on the stream around
+ * the node; the iteration total is the host wall clock from the first
+ * node's enqueue until the stream drains. Synchronises the stream. */
+int inferc_executor_run_profiled(inferc_executor* ex, inferc_profiler* p);
+
 /* ---------------- GPT-2 greedy decode (inferc decode) ---------------- */
 
 typedef struct {
@@ -340,6 +388,15 @@ int inferc_gpt2_generate(inferc_gpt2* m, const int64_t* prompt,
                          int64_t n_prompt, int64_t max_tokens,
                          int64_t* tokens_out, float* step_ms,
                          float* last_logits);
+/* generate() with per-op profiling of the decode steps (main.cpp:846-872,
+ * 914-934): each of the max_tokens-1 steps is enqueued eagerly and recorded
+ * as one iteration whose ops are the step's fused launch groups
+ * ("LayerNorm+QKV", "AttentionDecode", "MatMul+Bias+Residual",
+ * "LayerNorm+MatMulAddGELU" per layer, then "LayerNorm+LMHead+ArgMax"),
+ * each timed between HIP events. Tokens equal generate()'s. */
+int inferc_gpt2_generate_profiled(inferc_gpt2* m, const int64_t* prompt,
+                                  int64_t n_prompt, int64_t max_tokens,
+                                  int64_t* tokens_out, inferc_profiler* p);
 /* Full-sequence forward logits [n, V] (host) for every position. */
 int inferc_gpt2_forward(inferc_gpt2* m, const int64_t* ids, int64_t n,
                         float* logits);

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "common.h"
+#include "profiler.h"
 
 namespace ih {
 namespace {
@@ -357,6 +358,20 @@ void kv_append_attend(inferc_hip_ctx* ctx, int64_t nH, int64_t D, int64_t T,
 
 // ---------------------------------------------------------------- GPT-2 model
 
+// Op types of a profiled decode step's launch groups. Each group is one
+// fused launch standing for a run of the reference's with-past graph ops:
+// LayerNorm -> MatMul -> Add (qkv), the attention over past + new K/V,
+// MatMul -> Add -> Add (projection, bias, residual), LayerNorm -> MatMul ->
+// Add -> GELU (MLP up), and the final LayerNorm -> LM-head MatMul -> argmax.
+namespace {
+constexpr const char* kOpEmbed = "Embedding";
+constexpr const char* kOpLnQkv = "LayerNorm+QKV";
+constexpr const char* kOpAttn = "AttentionDecode";
+constexpr const char* kOpProjRes = "MatMul+Bias+Residual";
+constexpr const char* kOpLnFcGelu = "LayerNorm+MatMulAddGELU";
+constexpr const char* kOpHead = "LayerNorm+LMHead+ArgMax";
+}  // namespace
+
 struct inferc_gpt2 {
   inferc_hip_ctx* ctx = nullptr;
   inferc_gpt2_config cfg{};
@@ -394,6 +409,11 @@ struct inferc_gpt2 {
   hipGraphExec_t step_exec = nullptr;
   hipGraph_t step_graph = nullptr;
   std::vector<hipEvent_t> events;
+  // Profiled steps run eagerly: mark() records an event on the stream before
+  // each launch group and remembers the op type and name that group starts.
+  bool profiling = false;
+  std::vector<hipEvent_t> pev;
+  std::vector<std::pair<const char*, std::string>> pops;
 
   template <class T>
   T* alloc(size_t n) {
@@ -406,9 +426,11 @@ struct inferc_gpt2 {
     if (step_exec) (void)hipGraphExecDestroy(step_exec);
     if (step_graph) (void)hipGraphDestroy(step_graph);
     for (auto e : events) (void)hipEventDestroy(e);
+    for (auto e : pev) (void)hipEventDestroy(e);
     for (void* p : allocs) (void)hipFree(p);
     allocs.clear();
     events.clear();
+    pev.clear();
     step_exec = nullptr;
     step_graph = nullptr;
   }
@@ -438,6 +460,19 @@ struct inferc_gpt2 {
     return D() == 64 && H() == 768 && ih::gemv2_supported(cfg.ffn);
   }
 
+  // Records the start of a launch group when profiling; `op` == nullptr
+  // records the end of the last group.
+  void mark(const char* op, int64_t layer = -1, const char* part = "") {
+    if (!profiling) return;
+    if (pev.size() < pops.size() + 1) {
+      hipEvent_t e;
+      IH_HIP(hipEventCreate(&e));
+      pev.push_back(e);
+    }
+    IH_HIP(hipEventRecord(pev[pops.size()], ctx->stream));
+    if (op) pops.emplace_back(op, layer >= 0 ? "h." + std::to_string(layer) + part : part);
+  }
+
   // One decode step for the token in state[1] at position state[0]. On the
   // fast path the step's input embedding h was written by the previous
   // step's LM-head tail (or the prefill's), so the step starts with layer 0.
@@ -445,6 +480,7 @@ struct inferc_gpt2 {
     hipStream_t s = ctx->stream;
     const int64_t Hh = H(), F = cfg.ffn;
     if (!fast()) {
+      mark(kOpEmbed, -1, "embed");
       hipLaunchKernelGGL(ih::embed_step_kernel, dim3(unsigned(ih::ceil_div(Hh, ih::kBlock))),
                          dim3(ih::kBlock), 0, s, wte, wpe, state, Hh, h);
       ih::check_launch("embed_step");
@@ -453,16 +489,21 @@ struct inferc_gpt2 {
       // the same five launches per layer, weights streamed as int4
       for (int64_t l = 0; l < cfg.layers; ++l) {
         const Layer& L = layers[size_t(l)];
+        mark(kOpLnQkv, l, ".attn.qkv");
         ih::int4_gemv_dec(ctx, 3 * Hh, Hh, L.attn_q, L.attn_s, h, L.ln1_g, L.ln1_b, cfg.eps,
                           L.attn_b, nullptr, INFERC_ACT_NONE, qkv, nullptr);
+        mark(kOpAttn, l, ".attn");
         ih::AttnDecP ap{max_t, state, qkv, qkv + Hh, qkv + 2 * Hh, kc_l(l), vc_l(l), att};
         hipLaunchKernelGGL(ih::attn_decode_d64, dim3(unsigned(cfg.heads)),
                            dim3(64 * ih::kDecWaves), 0, s, ap);
         ih::check_launch("attn_decode");
+        mark(kOpProjRes, l, ".attn.proj");
         ih::int4_gemv_dec(ctx, Hh, Hh, L.proj_q, L.proj_s, att, nullptr, nullptr, 0.0f, L.proj_b,
                           h, INFERC_ACT_NONE, h, nullptr);
+        mark(kOpLnFcGelu, l, ".mlp.fc");
         ih::int4_gemv_dec(ctx, F, Hh, L.fc_q, L.fc_s, h, L.ln2_g, L.ln2_b, cfg.eps, L.fc_b,
                           nullptr, INFERC_ACT_GELU_TANH, f, nullptr);
+        mark(kOpProjRes, l, ".mlp.proj");
         ih::int4_gemv_dec(ctx, Hh, F, L.fcproj_q, L.fcproj_s, f, nullptr, nullptr, 0.0f,
                           L.fcproj_b, h, INFERC_ACT_NONE, h, nullptr);
       }
@@ -471,23 +512,26 @@ struct inferc_gpt2 {
     }
     for (int64_t l = 0; l < cfg.layers; ++l) {
       const Layer& L = layers[size_t(l)];
+      mark(kOpLnQkv, l, ".attn.qkv");
       ih::gemv(ctx, 3 * Hh, Hh, L.attn_w, h, L.ln1_g, L.ln1_b, cfg.eps, L.attn_b, nullptr,
                INFERC_ACT_NONE, qkv);
+      mark(kOpAttn, l, ".attn");
       if (fast()) {
         ih::AttnDecP ap{max_t, state, qkv, qkv + Hh, qkv + 2 * Hh, kc_l(l), vc_l(l), att};
         hipLaunchKernelGGL(ih::attn_decode_d64, dim3(unsigned(cfg.heads)),
                            dim3(64 * ih::kDecWaves), 0, s, ap);
         ih::check_launch("attn_decode");
-        ih::gemv(ctx, Hh, Hh, L.proj_w, att, nullptr, nullptr, 0.0f, L.proj_b, h,
-                 INFERC_ACT_NONE, h);
       } else {
         ih::kv_append_attend(ctx, cfg.heads, D(), max_t, state, qkv, qkv + Hh, qkv + 2 * Hh,
                              kc_l(l), vc_l(l), att);
-        ih::gemv(ctx, Hh, Hh, L.proj_w, att, nullptr, nullptr, 0.0f, L.proj_b, h,
-                 INFERC_ACT_NONE, h);
       }
+      mark(kOpProjRes, l, ".attn.proj");
+      ih::gemv(ctx, Hh, Hh, L.proj_w, att, nullptr, nullptr, 0.0f, L.proj_b, h, INFERC_ACT_NONE,
+               h);
+      mark(kOpLnFcGelu, l, ".mlp.fc");
       ih::gemv(ctx, F, Hh, L.fc_w, h, L.ln2_g, L.ln2_b, cfg.eps, L.fc_b, nullptr,
                INFERC_ACT_GELU_TANH, f);
+      mark(kOpProjRes, l, ".mlp.proj");
       ih::gemv(ctx, Hh, F, L.fcproj_w, f, nullptr, nullptr, 0.0f, L.fcproj_b, h, INFERC_ACT_NONE,
                h);
     }
@@ -498,6 +542,7 @@ struct inferc_gpt2 {
   // tokens[state[0]+1] = argmax (first max), state advanced by one position.
   void lm_head_finish(const float* hrow) {
     const int64_t Hh = H(), V = cfg.vocab;
+    mark(kOpHead, -1, "lm_head");
     if (int4) {
       ih::int4_gemv_dec(ctx, V, Hh, wte_q, wte_s, hrow, lnf_g, lnf_b, cfg.eps, nullptr, nullptr,
                         INFERC_ACT_NONE, logits, amax4);
@@ -656,6 +701,26 @@ void upload_ids(inferc_gpt2* m, const int64_t* ids, int64_t n) {
                         m->ctx->stream));
 }
 
+// Checks the request, then enqueues the prefill and the first greedy token:
+// state = {pos = n_prompt - 1} lets the prefill's last row play the role of
+// a step input, so the LM-head tail records the first generated token at
+// position n_prompt and leaves the state at the first decode step
+// (main.cpp:820-828).
+void start_generation(inferc_gpt2* m, const int64_t* prompt, int64_t n_prompt,
+                      int64_t max_tokens, const int64_t* tokens_out) {
+  check_model(m);
+  IH_REQUIRE(n_prompt > 0, INFERC_ERR_ARG, "inferc decode: empty prompt");
+  IH_REQUIRE(max_tokens > 0, INFERC_ERR_ARG, "inferc decode: max_tokens must be > 0");
+  IH_REQUIRE(tokens_out != nullptr, INFERC_ERR_ARG, "null tokens_out");
+  IH_REQUIRE(n_prompt + max_tokens - 1 <= m->max_t, INFERC_ERR_SHAPE,
+             "prompt + generated tokens exceed the KV cache (max_t)");
+  const int64_t init[4] = {n_prompt - 1, 0, 0, 0};
+  IH_HIP(hipMemcpyAsync(m->state, init, sizeof(init), hipMemcpyHostToDevice, m->ctx->stream));
+  upload_ids(m, prompt, n_prompt);
+  m->enqueue_prefill_blocks(n_prompt);
+  m->lm_head_finish(m->ph + (n_prompt - 1) * m->H());
+}
+
 }  // namespace
 
 extern "C" {
@@ -769,24 +834,10 @@ int inferc_gpt2_generate(inferc_gpt2* m, const int64_t* prompt, int64_t n_prompt
                          int64_t max_tokens, int64_t* tokens_out, float* step_ms,
                          float* last_logits) {
   return ih::guard([&] {
-    check_model(m);
-    IH_REQUIRE(n_prompt > 0, INFERC_ERR_ARG, "inferc decode: empty prompt");
-    IH_REQUIRE(max_tokens > 0, INFERC_ERR_ARG, "inferc decode: max_tokens must be > 0");
-    IH_REQUIRE(tokens_out != nullptr, INFERC_ERR_ARG, "null tokens_out");
-    IH_REQUIRE(n_prompt + max_tokens - 1 <= m->max_t, INFERC_ERR_SHAPE,
-               "prompt + generated tokens exceed the KV cache (max_t)");
+    start_generation(m, prompt, n_prompt, max_tokens, tokens_out);
     inferc_hip_ctx* ctx = m->ctx;
     hipStream_t s = ctx->stream;
-    const int64_t H = m->H(), V = m->cfg.vocab;
-    // state = {pos = n_prompt - 1}: the prefill's last row plays the role of
-    // a step input, so finish_token() records the first generated token at
-    // position n_prompt and leaves the state at the first decode step.
-    const int64_t init[4] = {n_prompt - 1, 0, 0, 0};
-    IH_HIP(hipMemcpyAsync(m->state, init, sizeof(init), hipMemcpyHostToDevice, s));
-    upload_ids(m, prompt, n_prompt);
-    m->enqueue_prefill_blocks(n_prompt);
-    // First token: final LN + LM head on the last prompt row (main.cpp:820-828).
-    m->lm_head_finish(m->ph + (n_prompt - 1) * H);
+    const int64_t V = m->cfg.vocab;
     m->capture_step();
     const int64_t steps = max_tokens - 1;
     if (step_ms && steps > 0) {
@@ -810,6 +861,48 @@ int inferc_gpt2_generate(inferc_gpt2* m, const int64_t* prompt, int64_t n_prompt
     if (last_logits)
       IH_HIP(hipMemcpy(last_logits, m->logits, size_t(V) * sizeof(float),
                        hipMemcpyDeviceToHost));
+  });
+}
+
+// generate() with each decode step recorded as one profiler iteration
+// (main.cpp:849-872): the step is enqueued eagerly rather than replayed from
+// its graph, an event opens each launch group, and an op's time is the device
+// time to the next event. The iteration total is the host wall clock of the
+// step from enqueue until the stream has drained. Activation bytes are not
+// tracked (main.cpp:850).
+int inferc_gpt2_generate_profiled(inferc_gpt2* m, const int64_t* prompt, int64_t n_prompt,
+                                  int64_t max_tokens, int64_t* tokens_out,
+                                  inferc_profiler* p) {
+  return ih::guard([&] {
+    IH_REQUIRE(p != nullptr, INFERC_ERR_ARG, "null profiler");
+    start_generation(m, prompt, n_prompt, max_tokens, tokens_out);
+    hipStream_t s = m->ctx->stream;
+    struct Off {
+      inferc_gpt2* m;
+      ~Off() { m->profiling = false; }
+    } off{m};
+    for (int64_t i = 0; i + 1 < max_tokens; ++i) {
+      IH_HIP(hipStreamSynchronize(s));
+      m->pops.clear();
+      m->profiling = true;
+      p->begin_iteration();
+      m->enqueue_step();
+      m->mark(nullptr);
+      m->profiling = false;
+      const size_t n_ops = m->pops.size();
+      IH_HIP(hipEventSynchronize(m->pev[n_ops]));
+      std::vector<float> ms(n_ops, 0.0f);
+      for (size_t k = 0; k < n_ops; ++k)
+        IH_HIP(hipEventElapsedTime(&ms[k], m->pev[k], m->pev[k + 1]));
+      const double total = std::chrono::duration<double, std::milli>(
+                               inferc_profiler::clock::now() - p->iter_t0).count();
+      for (size_t k = 0; k < n_ops; ++k)
+        p->add_op(m->pops[k].first, m->pops[k].second, double(ms[k]), 0);
+      p->end_iteration(total);
+    }
+    IH_HIP(hipStreamSynchronize(s));
+    IH_HIP(hipMemcpy(tokens_out, m->tokens + n_prompt, size_t(max_tokens) * sizeof(int64_t),
+                     hipMemcpyDeviceToHost));
   });
 }
 

@@ -26,6 +26,7 @@
 #include <vector>
 
 #include "common.h"
+#include "profiler.h"
 
 struct inferc_graph {
   struct Init {
@@ -154,10 +155,12 @@ struct inferc_executor {
   hipGraphExec_t exec = nullptr;
   std::string graph_sig;
   uint64_t graph_ws_gen = 0;
+  std::vector<hipEvent_t> prof_ev;  // one per node boundary of a profiled pass
 
   ~inferc_executor() {
     if (dry) return;
     drop_graph();
+    for (hipEvent_t e : prof_ev) (void)hipEventDestroy(e);
     for (auto& kv : arena) (void)hipFree(kv.second.p);
     for (auto& kv : inputs)
       if (kv.second.from_host && kv.second.v.dev) (void)hipFree(kv.second.v.dev);
@@ -263,11 +266,25 @@ struct inferc_executor {
     vals[out] = v;
   }
 
+  // Bytes of every non-initializer tensor on the tape (inputs and node
+  // outputs, views counted at their logical size), the reference's
+  // live_activation_bytes (src/runtime/executor.cc:112-119).
+  int64_t live_activation_bytes() const {
+    int64_t b = 0;
+    for (const auto& kv : vals)
+      if (!inits.count(kv.first)) b += int64_t(kv.second.bytes());
+    return b;
+  }
+
   void peephole();
   void exec_node(const inferc_graph::Node& n);
-  void walk();
+  // With `act`, records an event before each node and after the last on the
+  // stream, and appends each node's activation bytes (0 unless `track`).
+  void walk(std::vector<int64_t>* act = nullptr, bool track = false);
   std::string signature() const;
+  void stage_inputs();
   void run();
+  void run_profiled(inferc_profiler* p);
 };
 
 namespace ih {
@@ -910,17 +927,22 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
   fail(INFERC_ERR_UNSUPPORTED, "Executor: unsupported op '" + op + "' (node: " + n.name + ")");
 }
 
-void inferc_executor::walk() {
+void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
   vals = inits;
   for (auto& kv : inputs) vals[kv.first] = kv.second.v;
-  for (const auto& n : nodes) {
+  const bool events = act != nullptr && !dry;
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    const inferc_graph::Node& n = nodes[i];
+    if (events) IH_HIP(hipEventRecord(prof_ev[i], ctx->stream));
     try {
       exec_node(n);
     } catch (ih::Error& e) {
       e.msg += " [node '" + n.name + "', op " + n.op + "]";
       throw;
     }
+    if (act) act->push_back(track ? live_activation_bytes() : 0);
   }
+  if (events) IH_HIP(hipEventRecord(prof_ev[nodes.size()], ctx->stream));
   for (const auto& o : outputs) get(o);  // every graph output must exist
 }
 
@@ -934,19 +956,23 @@ std::string inferc_executor::signature() const {
   return o.str();
 }
 
-void inferc_executor::run() {
-  if (dry) {
-    walk();
-    return;
-  }
-  ctx->make_current();
-  // stage host inputs into their device buffers (outside any graph)
+// Host inputs are copied into their device buffers outside any graph.
+void inferc_executor::stage_inputs() {
   for (auto& kv : inputs) {
     Input& in = kv.second;
     if (!in.from_host) continue;
     const size_t bytes = in.v.bytes();
     IH_HIP(hipMemcpyAsync(in.v.dev, in.staged.data(), bytes, hipMemcpyHostToDevice, ctx->stream));
   }
+}
+
+void inferc_executor::run() {
+  if (dry) {
+    walk();
+    return;
+  }
+  ctx->make_current();
+  stage_inputs();
   const std::string sig = signature();
   if (graph_mode && exec && graph_sig == sig && graph_ws_gen == ctx->ws_generation) {
     IH_HIP(hipGraphLaunch(exec, ctx->stream));
@@ -979,6 +1005,48 @@ void inferc_executor::run() {
   graph_sig = sig;
   graph_ws_gen = gen;
   IH_HIP(hipGraphLaunch(exec, ctx->stream));
+}
+
+// One eager pass recorded as a profiler iteration (executor.cc:121-125,
+// 145-160, 349-354): each node's time is the device time between HIP events
+// recorded on the stream before and after it (host-only shape nodes read
+// about 0 ms); the iteration total is the host wall clock from the first
+// node's enqueue until the stream has drained, so it includes launch and
+// host work. A dry executor records 0 ms per node. The captured graph of
+// this input signature, if any, stays valid: the pass reuses its buffers.
+void inferc_executor::run_profiled(inferc_profiler* p) {
+  std::vector<int64_t> act;
+  act.reserve(nodes.size());
+  if (dry) {
+    p->begin_iteration();
+    walk(&act, p->track_activation_bytes);
+    for (size_t i = 0; i < nodes.size(); ++i) p->add_op(nodes[i].op, nodes[i].name, 0.0, act[i]);
+    p->end_iteration();
+    return;
+  }
+  ctx->make_current();
+  IH_REQUIRE(!ctx->capturing, INFERC_ERR_STATE, "executor: profiled run during graph capture");
+  while (prof_ev.size() < nodes.size() + 1) {
+    hipEvent_t e;
+    IH_HIP(hipEventCreate(&e));
+    prof_ev.push_back(e);
+  }
+  stage_inputs();
+  const std::string sig = signature();
+  if (sig != last_sig) {
+    drop_graph();  // buffers may be reallocated for the new shapes
+    last_sig = sig;
+  }
+  IH_HIP(hipStreamSynchronize(ctx->stream));
+  p->begin_iteration();
+  walk(&act, p->track_activation_bytes);
+  IH_HIP(hipEventSynchronize(prof_ev[nodes.size()]));
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    float ms = 0.0f;
+    IH_HIP(hipEventElapsedTime(&ms, prof_ev[i], prof_ev[i + 1]));
+    p->add_op(nodes[i].op, nodes[i].name, double(ms), act[i]);
+  }
+  p->end_iteration();
 }
 
 namespace {
@@ -1185,6 +1253,13 @@ int inferc_executor_set_input_device(inferc_executor* ex, const char* name, int 
 
 int inferc_executor_run(inferc_executor* ex) {
   return ih::guard([&] { check_ex(ex)->run(); });
+}
+
+int inferc_executor_run_profiled(inferc_executor* ex, inferc_profiler* p) {
+  return ih::guard([&] {
+    IH_REQUIRE(p != nullptr, INFERC_ERR_ARG, "null profiler");
+    check_ex(ex)->run_profiled(p);
+  });
 }
 
 int inferc_executor_output_info(inferc_executor* ex, const char* name, int* dtype, int* rank,

@@ -101,12 +101,28 @@ _SIGS = {
     "inferc_executor_output_info": [vp, C.c_char_p, P(i32), P(i32), P(i64)],
     "inferc_executor_get_output": [vp, C.c_char_p, vp, sz],
     "inferc_executor_set_graph_mode": [vp, i32],
+    "inferc_executor_run_profiled": [vp, vp],
+    "inferc_profiler_create": [P(vp)],
+    "inferc_profiler_destroy": [vp],
+    "inferc_profiler_begin_iteration": [vp],
+    "inferc_profiler_end_iteration": [vp],
+    "inferc_profiler_begin_op": [vp, C.c_char_p, C.c_char_p],
+    "inferc_profiler_end_op": [vp, i64],
+    "inferc_profiler_record_op": [vp, C.c_char_p, C.c_char_p, C.c_double, i64],
+    "inferc_profiler_set_track_activation_bytes": [vp, i32],
+    "inferc_profiler_snapshot_peak_rss": [vp],
+    "inferc_profiler_iteration_count": [vp, P(i64)],
+    "inferc_profiler_total_stats": [vp, P(C.c_double)],
+    "inferc_profiler_to_json": [vp, C.c_char_p, C.c_char_p, vp, sz, P(sz)],
+    "inferc_profile_percentile": [P(C.c_double), i64, C.c_double, P(C.c_double)],
+    "inferc_profile_stats": [P(C.c_double), i64, P(C.c_double)],
     "inferc_gpt2_create": [vp, vp, P(vp), i64, P(vp)],
     "inferc_gpt2_destroy": [vp],
     "inferc_gpt2_use_int4": [vp],
     "inferc_int4_quantize_rows": [i64, i64, vp, vp, vp, vp],
     "inferc_gpt2_generate": [vp, P(i64), i64, i64, P(i64), P(f32), P(f32)],
     "inferc_gpt2_forward": [vp, P(i64), i64, P(f32)],
+    "inferc_gpt2_generate_profiled": [vp, P(i64), i64, i64, P(i64), vp],
 }
 
 EXPORTED = sorted(list(_SIGS) + ["inferc_hip_last_error"])

@@ -687,6 +687,30 @@ class Executor:
         self.run_async()
         return {o: self.output(o) for o in outputs}
 
+    def run_profiled(self, profiler) -> None:
+        """Executor::Run(inputs, profiler) (src/runtime/executor.cc:98-125,
+        349-354): one eager pass recorded as one profiler iteration, each
+        node's time measured between HIP events on the stream."""
+        check(self.ctx._lib.inferc_executor_run_profiled(self.handle, profiler.handle))
+
+    def profile(self, inputs: dict[str, np.ndarray], iters: int = 10, warmup: int = 3,
+                backend: str = "inferc-hip", model: str = "",
+                track_activation_bytes: bool = False) -> dict:
+        """The profiled loop of `inferc run --profile` (src/cli/main.cpp:355-424):
+        `warmup` unprofiled runs, `iters` profiled ones, peak RSS, then the
+        report in the reference's JSON schema (as a dict)."""
+        from .profiler import Profiler
+        for k, v in inputs.items():
+            self.set_input(k, v)
+        for _ in range(warmup):
+            self.run_async()
+        p = Profiler()
+        p.set_track_activation_bytes(track_activation_bytes)
+        for _ in range(iters):
+            self.run_profiled(p)
+        p.snapshot_peak_rss()
+        return p.report(backend, model)
+
     def close(self) -> None:
         if getattr(self, "handle", None):
             self.ctx._lib.inferc_executor_destroy(self.handle)
@@ -737,6 +761,18 @@ class Gpt2Decoder:
             steps.ctypes.data_as(fp) if steps is not None else None,
             logits.ctypes.data_as(fp) if logits is not None else None))
         return toks, (steps[:max_tokens - 1] if steps is not None else None), logits
+
+    def generate_profiled(self, prompt: np.ndarray, max_tokens: int, profiler) -> np.ndarray:
+        """generate() with every decode step recorded as one profiler
+        iteration of fused launch groups (main.cpp:846-872); the steps run
+        eagerly, so their totals include launch overhead that the replayed
+        step graph of generate() avoids. Returns the tokens."""
+        p = _c_order(prompt, np.int64)
+        toks = np.empty(max_tokens, np.int64)
+        check(self.ctx._lib.inferc_gpt2_generate_profiled(
+            self.handle, p.ctypes.data_as(C.POINTER(C.c_int64)), p.size, max_tokens,
+            toks.ctypes.data_as(C.POINTER(C.c_int64)), profiler.handle))
+        return toks
 
     def use_int4(self) -> None:
         """int4 weight-only decode (irreversible): see inferc_gpt2_use_int4."""

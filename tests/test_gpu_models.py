@@ -9,6 +9,7 @@ import pytest
 
 import oracle as O
 from inferc_amd import graphs, rt
+from inferc_amd.profiler import Profiler
 
 pytestmark = pytest.mark.gpu
 
@@ -82,6 +83,79 @@ def test_executor_folds_add_into_layernorm_and_gathers_by_view(ctx):
     assert np.max(np.abs(got - ref)) <= 1e-4
 
 
+def _check_device_profile(rep, iters):
+    assert rep["iterations"] == iters
+    per = rep["per_op_type"]
+    # device op times sit inside the iteration's wall clock
+    assert sum(v["total_ms"]["mean_ms"] for v in per.values()) <= rep["total"]["mean_ms"]
+    assert rep["total"]["min_ms"] > 0
+
+
+def test_executor_profiled_runs(ctx):
+    """Profiled eager passes (Executor::Run with a profiler): device time per
+    node, the node counts of the fused graph, the dry run's activation bytes,
+    and outputs that still match the oracle; the graph captured before the
+    profiled passes and one captured after a new shape both replay correctly."""
+    cfg = graphs.small_encoder_cfg()
+    w, ex = _encoder(ctx, cfg, 31)
+    ids, mask = graphs.encoder_inputs(cfg, 3, 40, ragged=True)
+    feeds = {"input_ids": ids, "attention_mask": mask}
+    ref = O.encoder_forward(cfg, w, ids, mask)
+    first = [ex.run(feeds, ["logits"])["logits"] for _ in range(2)]  # eager, capture
+    rep = ex.profile(feeds, iters=5, warmup=1, backend="inferc-hip", model="small-encoder",
+                     track_activation_bytes=True)
+    print({k: round(v["total_ms"]["mean_ms"], 4) for k, v in rep["per_op_type"].items()},
+          "total", round(rep["total"]["mean_ms"], 4))
+    np.testing.assert_array_equal(ex.output("logits"), first[0])
+    np.testing.assert_allclose(first[0], ref, atol=1e-4)
+    np.testing.assert_array_equal(ex.run(feeds, ["logits"])["logits"], first[0])  # replay
+    _check_device_profile(rep, 5)
+    assert rep["peak_rss_bytes"] > 0  # snapshot taken by profile() (main.cpp:382)
+    assert sum(rep["op_counts"].values()) == ex.node_count()
+    for op in ("FusedQKV", "FusedAttention", "FusedMatMulAddGELU", "FusedGemmEpilogue"):
+        assert rep["per_op_type"][op]["total_ms"]["min_ms"] > 0, op
+    assert rep["per_op_type"]["Shape"]["total_ms"]["max_ms"] < 0.05
+    dry = rt.Executor.dry(graphs.encoder_graph(cfg, w))
+    for k, v in feeds.items():
+        dry.set_input(k, v)
+    pd = Profiler()
+    dry.run_profiled(pd)
+    assert rep["activation_bytes_peak"] == pd.report("d")["activation_bytes_peak"] > 0
+    # a new input shape, profiled first, then eager + capture + replay
+    ids2, mask2 = graphs.encoder_inputs(cfg, 2, 17, seed=5)
+    feeds2 = {"input_ids": ids2, "attention_mask": mask2}
+    rep2 = ex.profile(feeds2, iters=2, warmup=0)
+    _check_device_profile(rep2, 2)
+    ref2 = O.encoder_forward(cfg, w, ids2, mask2)
+    for _ in range(3):
+        np.testing.assert_allclose(ex.run(feeds2, ["logits"])["logits"], ref2, atol=1e-4)
+
+
+def _decode_counts(layers, embed):
+    c = {"LayerNorm+QKV": layers, "AttentionDecode": layers,
+         "MatMul+Bias+Residual": 2 * layers, "LayerNorm+MatMulAddGELU": layers,
+         "LayerNorm+LMHead+ArgMax": 1}
+    if embed:
+        c["Embedding"] = 1
+    return c
+
+
+def test_gpt2_small_generate_profiled(ctx):
+    cfg = graphs.small_gpt2_cfg()
+    w = graphs.gpt2_weights(cfg, 24)
+    prompt = graphs.gpt2_prompt(cfg, 7)
+    dec = rt.Gpt2Decoder(ctx, cfg, w, max_t=32)
+    p = Profiler()
+    toks_p = dec.generate_profiled(prompt, 12, p)
+    toks, _, _ = dec.generate(prompt, 12)
+    np.testing.assert_array_equal(toks_p, toks)
+    np.testing.assert_array_equal(toks, O.gpt2_generate(cfg, w, prompt, 12)[0])
+    rep = p.report("inferc-decode-hip")
+    _check_device_profile(rep, 11)
+    assert rep["op_counts"] == _decode_counts(cfg["layers"], embed=True)
+    assert all(v["total_ms"]["min_ms"] > 0 for v in rep["per_op_type"].values())
+
+
 @pytest.mark.parametrize("B,ragged", [(1, False), (32, False), (32, True)])
 def test_distilbert_encoder_config1(ctx, B, ragged):
     """6 layers, H 768, 12x64, FFN 3072, S=128."""
@@ -152,6 +226,11 @@ def test_gpt2_int4_decode_matches_oracle_on_dequantised_weights(ctx, gpt2_full):
     assert np.max(np.abs(got - O.gpt2_forward(cfg, wq, prompt))) <= 1e-4
     toks2, _, _ = dec.generate(prompt, 24)
     np.testing.assert_array_equal(toks2, toks)
+    p = Profiler()
+    np.testing.assert_array_equal(dec.generate_profiled(prompt, 8, p), toks[:8])
+    rep = p.report("inferc-decode-int4")
+    _check_device_profile(rep, 7)
+    assert rep["op_counts"] == _decode_counts(cfg["layers"], embed=False)
 
 
 def test_gpt2_int4_rejects_other_shapes(ctx):
@@ -159,6 +238,23 @@ def test_gpt2_int4_rejects_other_shapes(ctx):
     dec = rt.Gpt2Decoder(ctx, cfg, graphs.gpt2_weights(cfg, 23), max_t=16)
     with pytest.raises(RuntimeError, match="hidden 768, ffn 3072"):
         dec.use_int4()
+
+
+def test_gpt2_generate_profiled_config4(ctx, gpt2_full):
+    """Profiled decode steps of GPT-2 small (fp32 GEMV path): tokens equal
+    generate()'s, one iteration per step, the step's fused launch groups."""
+    cfg, w = gpt2_full
+    prompt = graphs.gpt2_prompt(cfg, 32)
+    dec = rt.Gpt2Decoder(ctx, cfg, w, max_t=64)
+    p = Profiler()
+    toks_p = dec.generate_profiled(prompt, 10, p)
+    toks, _, _ = dec.generate(prompt, 10)
+    np.testing.assert_array_equal(toks_p, toks)
+    rep = p.report("inferc-decode-hip", "gpt2")
+    print({k: round(v["total_ms"]["mean_ms"], 4) for k, v in rep["per_op_type"].items()},
+          "total", round(rep["total"]["mean_ms"], 4))
+    _check_device_profile(rep, 9)
+    assert rep["op_counts"] == _decode_counts(cfg["layers"], embed=False)
 
 
 def test_gpt2_greedy_decode_config4_bit_exact(ctx, gpt2_full):
