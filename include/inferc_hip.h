@@ -276,6 +276,58 @@ int inferc_graph_add_node(inferc_graph* g, const char* op_type,
                           const char* const* inputs, int n_outputs,
                           const char* const* outputs, const char* attrs);
 int inferc_graph_add_output(inferc_graph* g, const char* name);
+/* A declared graph input (Graph::inputs, src/ir/graph.h:80): dtype and
+ * shape, -1 for a symbolic dim (onnx_to_ir.cc:10-23). */
+int inferc_graph_add_input(inferc_graph* g, const char* name, int dtype,
+                           int rank, const int64_t* shape);
+/* A tensor-valued attribute (AttributeProto TENSOR, e.g. Constant's
+ * "value", graph.h:69-72) on the most recently added node. */
+int inferc_graph_add_tensor_attr(inferc_graph* g, const char* attr, int dtype,
+                                 int rank, const int64_t* shape,
+                                 const void* host_data);
+/* The graph as JSON: name, inputs, outputs, initializers (name, dtype, shape,
+ * bytes) and nodes (op, name, domain, inputs, outputs, attrs as text,
+ * tensor_attrs). *len is the length without the NUL; buf == NULL queries it.
+ * No counterpart in the reference (its IR is inspected in C++ directly). */
+int inferc_graph_to_json(const inferc_graph* g, char* buf, size_t capacity,
+                         size_t* len);
+/* Copies an initializer's dtype, shape (room for 8 dims) and, when host_dst is
+ * not NULL, its bytes (Graph::GetTensor, graph.h:90-92). */
+int inferc_graph_get_initializer(const inferc_graph* g, const char* name,
+                                 int* dtype, int* rank, int64_t* shape,
+                                 void* host_dst, size_t capacity_bytes);
+
+/* ---------------- ONNX reader and fusion passes ---------------- */
+
+/* LoadOnnx + ConvertOnnxToIR (src/frontend/onnx_loader.cc:107-111,
+ * onnx_to_ir.cc:87-144) without libprotobuf: the ModelProto subset inferc
+ * reads (opset imports, graph name, nodes with INT/FLOAT/STRING/TENSOR/
+ * INTS/FLOATS/STRINGS attributes, initializers from raw_data or typed
+ * fields, inputs/outputs with dtype and shape). A malformed or truncated
+ * file fails with INFERC_ERR_ARG; external tensor data and graph-valued
+ * attributes with INFERC_ERR_UNSUPPORTED. The result feeds
+ * inferc_graph_optimize and inferc_executor_create. */
+int inferc_onnx_load(const char* path, inferc_graph** out);
+int inferc_onnx_load_bytes(const void* data, size_t n, inferc_graph** out);
+/* SummarizeModel as JSON (as_text = 0) or PrintSummary's text (as_text = 1)
+ * (onnx_loader.cc:113-210); buffer protocol as inferc_graph_to_json. */
+int inferc_onnx_summary(const void* data, size_t n, int as_text, char* buf,
+                        size_t capacity, size_t* len);
+/* OnnxElementBytes (onnx_loader.cc:69-86): 0 for variable-width types. */
+int inferc_onnx_element_bytes(int onnx_dtype, int64_t* bytes);
+/* One pass by name: "fold_constant_transpose" (constant_fold.cc:12-54),
+ * "recognize_attention" (recognize_attention.cc:49-165),
+ * "recognize_attention_additive" (no reference counterpart: the same block
+ * with an additive float mask), "fuse_qkv_projection"
+ * (recognize_attention.cc:167-237), "recognize_layernorm"
+ * (recognize_layernorm.cc:46-187), "recognize_gelu" (recognize_gelu.cc:
+ * 57-163), "recognize_gelu_tanh" (:165-296), "fuse_matmul_add_gelu"
+ * (fuse_matmul_add_gelu.cc:20-122). *count = patterns folded. */
+int inferc_graph_run_pass(inferc_graph* g, const char* pass, int* count);
+/* All eight in the order of `inferc optimize` (src/cli/main.cpp:265-271),
+ * the additive attention form right after the reference's; counts (nullable)
+ * receives the eight match counts in that order. */
+int inferc_graph_optimize(inferc_graph* g, int* counts);
 
 /* Executor: uploads every initializer once (src/runtime/executor.cc:89-96);
  * run() walks the nodes in order and dispatches each op to a kernel

@@ -17,6 +17,7 @@
 //  - Activation buffers live in a per-executor arena keyed by tensor name, so
 //    repeated runs with the same input shapes touch no allocator; the second
 //    such run is captured into a HIP graph that later runs replay.
+#include <cstdio>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -26,24 +27,9 @@
 #include <vector>
 
 #include "common.h"
+#include "graph.h"
 #include "profiler.h"
 
-struct inferc_graph {
-  struct Init {
-    std::string name;
-    int dtype;
-    std::vector<int64_t> shape;
-    std::vector<uint8_t> data;
-  };
-  struct Node {
-    std::string op, name;
-    std::vector<std::string> in, out;
-    std::map<std::string, std::string> attrs;
-  };
-  std::vector<Init> inits;
-  std::vector<Node> nodes;
-  std::vector<std::string> outputs;
-};
 
 namespace ih {
 namespace {
@@ -1133,6 +1119,124 @@ int inferc_graph_add_output(inferc_graph* g, const char* name) {
     check_graph(g);
     IH_REQUIRE(name != nullptr, INFERC_ERR_ARG, "null output name");
     g->outputs.push_back(name);
+  });
+}
+
+int inferc_graph_add_input(inferc_graph* g, const char* name, int dtype, int rank,
+                           const int64_t* shape) {
+  return ih::guard([&] {
+    check_graph(g);
+    IH_REQUIRE(name != nullptr && *name, INFERC_ERR_ARG, "input needs a name");
+    IH_REQUIRE(rank >= 0 && rank <= 8 && (rank == 0 || shape != nullptr), INFERC_ERR_SHAPE,
+               "rank must be in [0, 8]");
+    inferc_graph::IO io;
+    io.name = name;
+    io.dtype = dtype;
+    io.shape.assign(shape, shape + rank);  // -1 marks a symbolic dim
+    g->inputs.push_back(io);
+  });
+}
+
+int inferc_graph_add_tensor_attr(inferc_graph* g, const char* attr, int dtype, int rank,
+                                 const int64_t* shape, const void* host_data) {
+  return ih::guard([&] {
+    check_graph(g);
+    IH_REQUIRE(!g->nodes.empty(), INFERC_ERR_STATE, "no node to attach the attribute to");
+    IH_REQUIRE(attr != nullptr && *attr, INFERC_ERR_ARG, "attribute needs a name");
+    inferc_graph::Init t;
+    t.name = attr;
+    t.dtype = dtype;
+    t.shape = read_shape(rank, shape);
+    const size_t bytes = size_t(ih::numel_of(t.shape)) * ih::dtype_size(dtype);
+    IH_REQUIRE(bytes == 0 || host_data != nullptr, INFERC_ERR_ARG, "null attribute data");
+    t.data.assign(static_cast<const uint8_t*>(host_data),
+                  static_cast<const uint8_t*>(host_data) + bytes);
+    g->nodes.back().tattrs[attr] = std::move(t);
+  });
+}
+
+int inferc_graph_to_json(const inferc_graph* g, char* buf, size_t capacity, size_t* len) {
+  return ih::guard([&] {
+    IH_REQUIRE(g != nullptr && len != nullptr, INFERC_ERR_ARG, "null argument");
+    auto q = [](const std::string& s) {
+      std::string o = "\"";
+      for (unsigned char c : s) {
+        if (c == '"' || c == '\\') {
+          o += '\\';
+          o += char(c);
+        } else if (c < 0x20) {
+          char u[8];
+          std::snprintf(u, sizeof u, "\\u%04x", c);
+          o += u;
+        } else {
+          o += char(c);
+        }
+      }
+      return o + "\"";
+    };
+    auto shape = [](const std::vector<int64_t>& s) {
+      std::string o = "[";
+      for (size_t i = 0; i < s.size(); ++i) o += (i ? ", " : "") + std::to_string(s[i]);
+      return o + "]";
+    };
+    auto names = [&](const std::vector<std::string>& v) {
+      std::string o = "[";
+      for (size_t i = 0; i < v.size(); ++i) o += (i ? ", " : "") + q(v[i]);
+      return o + "]";
+    };
+    std::string o = "{\"name\": " + q(g->name) + ", \"inputs\": [";
+    for (size_t i = 0; i < g->inputs.size(); ++i)
+      o += std::string(i ? ", " : "") + "{\"name\": " + q(g->inputs[i].name) +
+           ", \"dtype\": " + std::to_string(g->inputs[i].dtype) +
+           ", \"shape\": " + shape(g->inputs[i].shape) + "}";
+    o += "], \"outputs\": " + names(g->outputs) + ", \"initializers\": [";
+    for (size_t i = 0; i < g->inits.size(); ++i)
+      o += std::string(i ? ", " : "") + "{\"name\": " + q(g->inits[i].name) +
+           ", \"dtype\": " + std::to_string(g->inits[i].dtype) +
+           ", \"shape\": " + shape(g->inits[i].shape) +
+           ", \"bytes\": " + std::to_string(g->inits[i].data.size()) + "}";
+    o += "], \"nodes\": [";
+    for (size_t i = 0; i < g->nodes.size(); ++i) {
+      const inferc_graph::Node& n = g->nodes[i];
+      o += std::string(i ? ", " : "") + "{\"op\": " + q(n.op) + ", \"name\": " + q(n.name) +
+           ", \"domain\": " + q(n.domain) + ", \"inputs\": " + names(n.in) +
+           ", \"outputs\": " + names(n.out) + ", \"attrs\": {";
+      size_t k = 0;
+      for (const auto& kv : n.attrs) o += std::string(k++ ? ", " : "") + q(kv.first) + ": " + q(kv.second);
+      o += "}, \"tensor_attrs\": {";
+      k = 0;
+      for (const auto& kv : n.tattrs)
+        o += std::string(k++ ? ", " : "") + q(kv.first) + ": {\"dtype\": " +
+             std::to_string(kv.second.dtype) + ", \"shape\": " + shape(kv.second.shape) + "}";
+      o += "}}";
+    }
+    o += "]}";
+    *len = o.size();
+    if (buf == nullptr) return;
+    IH_REQUIRE(capacity > o.size(), INFERC_ERR_ARG,
+               "buffer too small: need " + std::to_string(o.size() + 1) + " bytes");
+    std::memcpy(buf, o.c_str(), o.size() + 1);
+  });
+}
+
+int inferc_graph_get_initializer(const inferc_graph* g, const char* name, int* dtype, int* rank,
+                                 int64_t* shape, void* host_dst, size_t capacity_bytes) {
+  return ih::guard([&] {
+    IH_REQUIRE(g != nullptr && name != nullptr && dtype && rank && shape, INFERC_ERR_ARG,
+               "null argument");
+    for (const auto& t : g->inits) {
+      if (t.name != name) continue;
+      IH_REQUIRE(t.shape.size() <= 8, INFERC_ERR_SHAPE, "initializer rank > 8");
+      *dtype = t.dtype;
+      *rank = int(t.shape.size());
+      for (size_t i = 0; i < t.shape.size(); ++i) shape[i] = t.shape[i];
+      if (host_dst) {
+        IH_REQUIRE(capacity_bytes >= t.data.size(), INFERC_ERR_ARG, "buffer too small");
+        if (!t.data.empty()) std::memcpy(host_dst, t.data.data(), t.data.size());
+      }
+      return;
+    }
+    ih::fail(INFERC_ERR_ARG, std::string("no initializer '") + name + "'");
   });
 }
 

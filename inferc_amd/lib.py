@@ -91,6 +91,16 @@ _SIGS = {
     "inferc_graph_add_node": [vp, C.c_char_p, C.c_char_p, i32, P(C.c_char_p), i32,
                               P(C.c_char_p), C.c_char_p],
     "inferc_graph_add_output": [vp, C.c_char_p],
+    "inferc_graph_add_input": [vp, C.c_char_p, i32, i32, P(i64)],
+    "inferc_graph_add_tensor_attr": [vp, C.c_char_p, i32, i32, P(i64), vp],
+    "inferc_graph_to_json": [vp, vp, sz, P(sz)],
+    "inferc_graph_get_initializer": [vp, C.c_char_p, P(i32), P(i32), P(i64), vp, sz],
+    "inferc_graph_run_pass": [vp, C.c_char_p, P(i32)],
+    "inferc_graph_optimize": [vp, P(i32)],
+    "inferc_onnx_load": [C.c_char_p, P(vp)],
+    "inferc_onnx_load_bytes": [C.c_char_p, sz, P(vp)],
+    "inferc_onnx_summary": [C.c_char_p, sz, i32, vp, sz, P(sz)],
+    "inferc_onnx_element_bytes": [i32, P(i64)],
     "inferc_executor_create": [vp, vp, P(vp)],
     "inferc_executor_destroy": [vp],
     "inferc_executor_create_dry": [vp, P(vp)],

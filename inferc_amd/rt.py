@@ -565,6 +565,26 @@ def KvAppendAttend(q: Tensor, k_new: Tensor, v_new: Tensor, k_cache: Tensor, v_c
 
 # ----------------------------------------------------------------- executor
 
+# inferc_graph_optimize's pass order and count slots
+PASSES = ("fold_constant_transpose", "recognize_attention", "recognize_attention_additive",
+          "fuse_qkv_projection", "recognize_layernorm", "recognize_gelu", "recognize_gelu_tanh",
+          "fuse_matmul_add_gelu")
+
+
+def onnx_summary(src, text: bool = False):
+    """SummarizeModel (dict) or PrintSummary (text) of an ONNX model
+    (src/frontend/onnx_loader.cc:113-210), from a path or bytes."""
+    import json
+    lib = L.load_library()
+    b = bytes(src) if isinstance(src, (bytes, bytearray, memoryview)) else open(src, "rb").read()
+    n = C.c_size_t()
+    check(lib.inferc_onnx_summary(b, len(b), int(text), None, 0, C.byref(n)))
+    buf = C.create_string_buffer(n.value + 1)
+    check(lib.inferc_onnx_summary(b, len(b), int(text), buf, n.value + 1, C.byref(n)))
+    s = buf.value.decode()
+    return s if text else json.loads(s)
+
+
 class Graph:
     """Host IR of (fused) nodes as the reference's passes leave it
     (src/ir/graph.h:45-97)."""
@@ -602,6 +622,78 @@ class Graph:
 
     def add_output(self, name: str) -> None:
         check(self._lib.inferc_graph_add_output(self.handle, name.encode()))
+
+    def add_input(self, name: str, dtype, shape: Sequence[int]) -> None:
+        """A declared graph input (-1 for a symbolic dim)."""
+        check(self._lib.inferc_graph_add_input(self.handle, name.encode(),
+                                               _NP2DT[np.dtype(dtype)], len(shape),
+                                               _i64_array(list(shape))))
+
+    def add_tensor_attr(self, attr: str, arr: np.ndarray) -> None:
+        """A tensor-valued attribute on the most recently added node."""
+        a = _c_order(arr)
+        check(self._lib.inferc_graph_add_tensor_attr(self.handle, attr.encode(), _NP2DT[a.dtype],
+                                                     a.ndim, _i64_array(list(a.shape)),
+                                                     a.ctypes.data if a.nbytes else None))
+
+    def add_constant(self, out: str, arr, name: str = "") -> None:
+        """An ONNX Constant node whose `value` attribute holds `arr`."""
+        self.add_node("Constant", [], [out], name=name)
+        self.add_tensor_attr("value", np.asarray(arr))
+
+    @classmethod
+    def from_onnx(cls, src) -> "Graph":
+        """LoadOnnx + ConvertOnnxToIR (src/frontend/onnx_loader.cc:107-111,
+        onnx_to_ir.cc:87-144) from a path or the model's bytes."""
+        g = cls.__new__(cls)
+        g._lib = L.load_library()
+        g.op_types = []
+        h = C.c_void_p()
+        if isinstance(src, (bytes, bytearray, memoryview)):
+            b = bytes(src)
+            check(g._lib.inferc_onnx_load_bytes(b, len(b), C.byref(h)))
+        else:
+            check(g._lib.inferc_onnx_load(str(src).encode(), C.byref(h)))
+        g.handle = h.value
+        g.op_types = [n["op"] for n in g.to_dict()["nodes"]]
+        return g
+
+    def to_dict(self) -> dict:
+        """The graph's structure: name, inputs, outputs, initializers (name,
+        dtype, shape, bytes) and nodes (op, name, domain, inputs, outputs,
+        attrs as text, tensor_attrs)."""
+        import json
+        n = C.c_size_t()
+        check(self._lib.inferc_graph_to_json(self.handle, None, 0, C.byref(n)))
+        buf = C.create_string_buffer(n.value + 1)
+        check(self._lib.inferc_graph_to_json(self.handle, buf, n.value + 1, C.byref(n)))
+        return json.loads(buf.value.decode(errors="replace"))
+
+    def initializer(self, name: str) -> np.ndarray:
+        dt, rank = C.c_int(), C.c_int()
+        shape = (C.c_int64 * 8)()
+        check(self._lib.inferc_graph_get_initializer(self.handle, name.encode(), C.byref(dt),
+                                                     C.byref(rank), shape, None, 0))
+        out = np.empty(tuple(shape[i] for i in range(rank.value)), dtype=_DT2NP[dt.value])
+        check(self._lib.inferc_graph_get_initializer(self.handle, name.encode(), C.byref(dt),
+                                                     C.byref(rank), shape, out.ctypes.data,
+                                                     out.nbytes))
+        return out
+
+    def run_pass(self, name: str) -> int:
+        """One fusion pass by name (see PASSES); returns its match count."""
+        c = C.c_int()
+        check(self._lib.inferc_graph_run_pass(self.handle, name.encode(), C.byref(c)))
+        self.op_types = [n["op"] for n in self.to_dict()["nodes"]]
+        return c.value
+
+    def optimize(self) -> dict[str, int]:
+        """The pass pipeline of `inferc optimize` (src/cli/main.cpp:265-271);
+        returns each pass's match count."""
+        counts = (C.c_int * len(PASSES))()
+        check(self._lib.inferc_graph_optimize(self.handle, counts))
+        self.op_types = [n["op"] for n in self.to_dict()["nodes"]]
+        return dict(zip(PASSES, counts))
 
     def close(self) -> None:
         if getattr(self, "handle", None):

@@ -1,0 +1,125 @@
+"""Writes the exported-model fixtures of the ONNX reader / pass / executor
+tests:
+
+  distilbert_tiny.onnx + distilbert_tiny_io.npz
+      DistilBertForSequenceClassification (2 layers, dim 64, 4 heads, FFN 128,
+      vocab 97), eager attention, exported by torch.onnx (TorchScript
+      exporter, opset 13, dynamic batch/sequence) as transformers exports
+      DistilBERT; the npz holds two input sets (one with padding) and the
+      logits torch computes for them in float32.
+  gpt2_tiny.onnx + gpt2_tiny_io.npz
+      GPT2LMHeadModel (2 layers, dim 64, 4 heads, vocab 101), eager
+      attention, no KV cache, inputs input_ids + attention_mask as the
+      reference's GPT-2 decoder model takes them, dynamic batch/sequence; the
+      npz holds token ids, masks and torch's float32 logits.
+
+Every parameter is drawn at random (biases and LayerNorm weights included),
+so the exporter's deduplication of equal initializers does not fire.
+The exporter's only use of the `onnx` package (absent here) is inserting
+custom-op functions, which these models do not have; that step is skipped.
+
+Usage: python tests/golden/make_onnx_fixtures.py
+"""
+from __future__ import annotations
+
+import io
+from pathlib import Path
+
+import numpy as np
+import torch
+
+OUT = Path(__file__).resolve().parent
+
+
+def _export(model, args, input_names, output_names, dynamic_axes) -> bytes:
+    from torch.onnx._internal.torchscript_exporter import onnx_proto_utils as opu
+
+    opu._add_onnxscript_fn = lambda model_bytes, custom_opsets: model_bytes
+    f = io.BytesIO()
+    torch.onnx.export(model, args, f, input_names=input_names, output_names=output_names,
+                      dynamic_axes=dynamic_axes, opset_version=13, dynamo=False,
+                      do_constant_folding=True)
+    return f.getvalue()
+
+
+def _randomize(model, seed: int) -> None:
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.2)
+        for name, p in model.named_parameters():
+            if "LayerNorm" in name or "layer_norm" in name or ".ln_" in name:
+                if name.endswith("weight"):
+                    p.add_(1.0)
+
+
+def distilbert() -> None:
+    from transformers import DistilBertConfig, DistilBertForSequenceClassification
+
+    cfg = DistilBertConfig(vocab_size=97, dim=64, n_layers=2, n_heads=4, hidden_dim=128,
+                           max_position_embeddings=64, num_labels=2)
+    cfg._attn_implementation = "eager"
+    m = DistilBertForSequenceClassification(cfg).eval()
+    _randomize(m, 11)
+    rng = np.random.default_rng(5)
+    ids_a = rng.integers(0, 97, (2, 16)).astype(np.int64)
+    mask_a = np.ones((2, 16), np.int64)
+    mask_a[1, 11:] = 0  # a padded row
+    ids_b = rng.integers(0, 97, (3, 9)).astype(np.int64)
+    mask_b = np.ones((3, 9), np.int64)
+    mask_b[0, 5:] = 0
+    data = _export(m, (torch.from_numpy(ids_a), torch.from_numpy(mask_a)),
+                   ["input_ids", "attention_mask"], ["logits"],
+                   {"input_ids": {0: "batch", 1: "sequence"},
+                    "attention_mask": {0: "batch", 1: "sequence"}, "logits": {0: "batch"}})
+    (OUT / "distilbert_tiny.onnx").write_bytes(data)
+    with torch.no_grad():
+        la = m(torch.from_numpy(ids_a), attention_mask=torch.from_numpy(mask_a)).logits.numpy()
+        lb = m(torch.from_numpy(ids_b), attention_mask=torch.from_numpy(mask_b)).logits.numpy()
+    np.savez(OUT / "distilbert_tiny_io.npz", ids_a=ids_a, mask_a=mask_a, logits_a=la,
+             ids_b=ids_b, mask_b=mask_b, logits_b=lb)
+
+
+def gpt2() -> None:
+    from transformers import GPT2Config, GPT2LMHeadModel
+
+    cfg = GPT2Config(vocab_size=101, n_positions=64, n_embd=64, n_layer=2, n_head=4,
+                     use_cache=False)
+    cfg._attn_implementation = "eager"
+    m = GPT2LMHeadModel(cfg).eval()
+    _randomize(m, 12)
+    rng = np.random.default_rng(6)
+    ids = rng.integers(0, 101, (1, 12)).astype(np.int64)
+    ids2 = rng.integers(0, 101, (2, 7)).astype(np.int64)
+
+    class Logits(torch.nn.Module):
+        def __init__(self, inner):
+            super().__init__()
+            self.inner = inner
+
+        def forward(self, input_ids, attention_mask):
+            return self.inner(input_ids=input_ids, attention_mask=attention_mask,
+                              use_cache=False).logits
+
+    w = Logits(m).eval()
+    mask = np.ones_like(ids)
+    mask2 = np.ones_like(ids2)
+    data = _export(w, (torch.from_numpy(ids), torch.from_numpy(mask)),
+                   ["input_ids", "attention_mask"], ["logits"],
+                   {"input_ids": {0: "batch", 1: "sequence"},
+                    "attention_mask": {0: "batch", 1: "sequence"},
+                    "logits": {0: "batch", 1: "sequence"}})
+    (OUT / "gpt2_tiny.onnx").write_bytes(data)
+    with torch.no_grad():
+        la = w(torch.from_numpy(ids), torch.from_numpy(mask)).numpy()
+        lb = w(torch.from_numpy(ids2), torch.from_numpy(mask2)).numpy()
+    np.savez(OUT / "gpt2_tiny_io.npz", ids_a=ids, mask_a=mask, logits_a=la, ids_b=ids2,
+             mask_b=mask2, logits_b=lb)
+
+
+if __name__ == "__main__":
+    torch.manual_seed(0)
+    distilbert()
+    gpt2()
+    for p in sorted(OUT.glob("*_tiny*")):
+        print(p.name, p.stat().st_size)
