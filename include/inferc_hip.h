@@ -358,7 +358,9 @@ int inferc_executor_run(inferc_executor* ex);
 /* Shape and dtype of a graph output after run(); shape has room for 8 dims. */
 int inferc_executor_output_info(inferc_executor* ex, const char* name,
                                 int* dtype, int* rank, int64_t* shape);
-/* Copy an output to host memory (synchronises the stream). */
+/* Copy an output to host memory (synchronises the stream). A dry-run
+ * executor returns outputs whose values are known on the host (constants and
+ * shape arithmetic folded while planning) and fails for the rest. */
 int inferc_executor_get_output(inferc_executor* ex, const char* name,
                                void* host_dst, size_t capacity_bytes);
 /* 0 = eager dispatch every run, 1 = capture/replay HIP graphs (default). */

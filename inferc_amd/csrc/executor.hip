@@ -27,6 +27,7 @@
 #include <vector>
 
 #include "common.h"
+#include "ew.h"
 #include "graph.h"
 #include "profiler.h"
 
@@ -49,14 +50,6 @@ int64_t numel_of(const std::vector<int64_t>& s) {
   int64_t n = 1;
   for (int64_t d : s) n *= d;
   return n;
-}
-
-std::string shape_str(const std::vector<int64_t>& s) {
-  std::ostringstream o;
-  o << "[";
-  for (size_t i = 0; i < s.size(); ++i) o << (i ? "," : "") << s[i];
-  o << "]";
-  return o.str();
 }
 
 // A tensor during a run: device data and/or a host copy (initializers and
@@ -243,6 +236,30 @@ struct inferc_executor {
     return vals[name];
   }
 
+  // A host value of the given shape, zero-filled; returns its bytes.
+  void* make_host_buf(const std::string& name, int dtype, std::vector<int64_t> shape) {
+    ih::Value v;
+    v.dtype = dtype;
+    v.shape = std::move(shape);
+    v.host = std::make_shared<std::vector<uint8_t>>(v.bytes());
+    vals[name] = v;
+    return vals[name].host->data();
+  }
+
+  // Every input of `n` is known on the host and the result is small: the
+  // node is folded on the host (values derived from shapes and constants
+  // only; graph inputs are always on the device).
+  bool host_foldable(const inferc_graph::Node& n, int64_t out_numel) const {
+    if (out_numel > (int64_t(1) << 16)) return false;
+    for (const auto& i : n.in) {
+      if (i.empty()) continue;
+      auto it = vals.find(i);
+      if (it == vals.end() || !it->second.host) return false;
+    }
+    return true;
+  }
+  const void* host_of(const std::string& name) const { return vals.at(name).host->data(); }
+
   void alias(const std::string& out, const ih::Value& in, std::vector<int64_t> shape) {
     ih::Value v = in;
     IH_REQUIRE(ih::numel_of(shape) == in.numel(), INFERC_ERR_SHAPE,
@@ -264,6 +281,8 @@ struct inferc_executor {
 
   void peephole();
   void exec_node(const inferc_graph::Node& n);
+  void generic_binary(const inferc_graph::Node& n, int ewop);
+  bool exec_generic(const inferc_graph::Node& n);
   // With `act`, records an event before each node and after the last on the
   // stream, and appends each node's activation bytes (0 unless `track`).
   void walk(std::vector<int64_t>* act = nullptr, bool track = false);
@@ -412,6 +431,24 @@ void inferc_executor::peephole() {
   for (size_t i = 0; i < nodes.size(); ++i)
     if (!dead[i]) kept.push_back(std::move(nodes[i]));
   nodes = std::move(kept);
+  // Nodes none of whose outputs is read or returned are not run (e.g. the
+  // float mask an attention fusion left behind). A graph that declares no
+  // outputs keeps every node.
+  for (bool changed = !outputs.empty(); changed;) {
+    changed = false;
+    std::unordered_map<std::string, int> used;
+    for (const auto& n : nodes)
+      for (const auto& i : n.in) ++used[i];
+    for (const auto& o : outputs) ++used[o];
+    std::vector<inferc_graph::Node> live;
+    for (auto& n : nodes) {
+      bool read = n.out.empty();
+      for (const auto& o : n.out) read = read || used.count(o) > 0;
+      if (read) live.push_back(std::move(n));
+      else changed = true;
+    }
+    nodes = std::move(live);
+  }
 }
 
 void inferc_executor::exec_node(const inferc_graph::Node& n) {
@@ -665,8 +702,13 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       make_host(n.out[0], INFERC_DT_I64, a0.shape, r.data());
       return;
     }
-    require_f32(a0, "A");
-    require_f32(b0, "B");
+    if (a0.dtype != INFERC_DT_F32 || b0.dtype != INFERC_DT_F32 ||
+        (a0.host && b0.host && a0.numel() <= 65536 && b0.numel() <= 65536) ||
+        !(a0.numel() == b0.numel() || suffix_broadcast(a0.shape, b0.shape) ||
+          suffix_broadcast(b0.shape, a0.shape))) {
+      generic_binary(n, kEwAdd);
+      return;
+    }
     // the larger operand carries the output shape; the other broadcasts as a suffix
     const bool swap = b0.numel() > a0.numel();
     const std::string& an = swap ? n.in[1] : n.in[0];
@@ -691,10 +733,12 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
   if (op == "Equal") {
     const Value a = in(0);
     const Value b = in(1);
-    IH_REQUIRE(a.dtype == INFERC_DT_I64 && b.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED,
-               "Equal: int64 operands only");
-    IH_REQUIRE(b.numel() == a.numel() || b.numel() == 1 || suffix_broadcast(a.shape, b.shape),
-               INFERC_ERR_UNSUPPORTED, "Equal: unsupported broadcast");
+    if (a.dtype != INFERC_DT_I64 || b.dtype != INFERC_DT_I64 || (a.host && b.host) ||
+        !(b.numel() == a.numel() || b.numel() == 1 || suffix_broadcast(a.shape, b.shape)) ||
+        b.numel() > a.numel()) {
+      generic_binary(n, kEwEqual);
+      return;
+    }
     uint8_t* y = static_cast<uint8_t*>(make_dev(n.out[0], INFERC_DT_BOOL, a.shape).dev);
     if (!dry) {
       equal_i64(ctx, a.numel(), static_cast<const int64_t*>(dev_of(n.in[0])),
@@ -712,9 +756,9 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     std::vector<int64_t> os(data.shape.begin(), data.shape.begin() + axis);
     for (int64_t d : idx.shape) os.push_back(d);
     for (int64_t i = axis + 1; i < r; ++i) os.push_back(data.shape[size_t(i)]);
-    if (data.host && (data.dtype == INFERC_DT_I64 || data.dtype == INFERC_DT_I32)) {
+    if (data.host && idx.host && (data.dtype == INFERC_DT_I64 || data.dtype == INFERC_DT_I32) &&
+        axis == 0 && r == 1) {
       // host shape plumbing (e.g. Gather(Shape(x), 1))
-      IH_REQUIRE(axis == 0 && r == 1, INFERC_ERR_UNSUPPORTED, "Gather: host data must be 1-D");
       std::vector<int64_t> d = host_i64(data, "Gather"), ix = host_i64(idx, "Gather");
       std::vector<int64_t> res;
       for (int64_t i : ix) {
@@ -723,6 +767,34 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
         res.push_back(d[size_t(i)]);
       }
       make_host(n.out[0], INFERC_DT_I64, os, res.data());
+      return;
+    }
+    if (data.dtype != INFERC_DT_F32 || host_foldable(n, numel_of(os))) {
+      // any element type: on the host when everything is known there, else
+      // on the device with host-validated or device indices
+      int64_t outer = 1, inner = 1;
+      for (int64_t i = 0; i < axis; ++i) outer *= data.shape[size_t(i)];
+      for (int64_t i = axis + 1; i < r; ++i) inner *= data.shape[size_t(i)];
+      const int64_t ad = data.shape[size_t(axis)];
+      IH_REQUIRE(idx.dtype == INFERC_DT_I64 || idx.dtype == INFERC_DT_I32, INFERC_ERR_UNSUPPORTED,
+                 "Gather: integer indices only");
+      if (host_foldable(n, numel_of(os))) {
+        const std::vector<int64_t> ix = host_i64(idx, "Gather");
+        void* y = make_host_buf(n.out[0], data.dtype, os);
+        ew_gather(nullptr, data.dtype, outer, ad, inner, host_of(n.in[0]), ix.data(),
+                  int64_t(ix.size()), y);
+        return;
+      }
+      if (idx.host) {
+        for (int64_t i : host_i64(idx, "Gather"))
+          IH_REQUIRE(i >= -ad && i < ad, INFERC_ERR_ARG, "Gather: index out of range");
+      }
+      IH_REQUIRE(idx.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED,
+                 "Gather: device indices must be int64");
+      const void* xp = dev_of(n.in[0]);
+      const int64_t* ip = static_cast<const int64_t*>(dev_of(n.in[1]));
+      void* y = make_dev(n.out[0], data.dtype, os).dev;
+      if (!dry) ew_gather(ctx, data.dtype, outer, ad, inner, xp, ip, idx.numel(), y);
       return;
     }
     require_f32(data, "data");
@@ -884,6 +956,24 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       sizes.push_back(p.shape[size_t(axis)]);
       os[size_t(axis)] += p.shape[size_t(axis)];
     }
+    if (host_foldable(n, numel_of(os)) && (x0.dtype != INFERC_DT_I64 || r != 1)) {
+      // any element type on the host: parts laid side by side along `axis`
+      const size_t eb = dtype_size(x0.dtype);
+      int64_t outer = 1, inner = 1;
+      for (int64_t i = 0; i < axis; ++i) outer *= os[size_t(i)];
+      for (int64_t i = axis + 1; i < r; ++i) inner *= os[size_t(i)];
+      uint8_t* y = static_cast<uint8_t*>(make_host_buf(n.out[0], x0.dtype, os));
+      int64_t at = 0;
+      for (size_t i = 0; i < n.in.size(); ++i) {
+        const uint8_t* src = static_cast<const uint8_t*>(host_of(n.in[i]));
+        const int64_t w = sizes[i] * inner;
+        for (int64_t o = 0; o < outer; ++o)
+          std::memcpy(y + size_t((o * os[size_t(axis)] * inner + at * inner)) * eb,
+                      src + size_t(o * w) * eb, size_t(w) * eb);
+        at += sizes[i];
+      }
+      return;
+    }
     if (x0.dtype == INFERC_DT_I64) {
       bool all_host = true;
       for (size_t i = 0; i < n.in.size(); ++i) all_host = all_host && in(i).host != nullptr;
@@ -910,7 +1000,269 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     }
     return;
   }
+  if (exec_generic(n)) return;
   fail(INFERC_ERR_UNSUPPORTED, "Executor: unsupported op '" + op + "' (node: " + n.name + ")");
+}
+
+// Binary op with numpy broadcasting: folded on the host when every input is
+// host-known and the result small, else one device kernel.
+void inferc_executor::generic_binary(const inferc_graph::Node& n, int ewop) {
+  using namespace ih;
+  IH_REQUIRE(n.in.size() == 2, INFERC_ERR_ARG, n.op + ": needs two inputs");
+  Value a = get(n.in[0]);
+  Value b = get(n.in[1]);
+  std::string bn = n.in[1];
+  if (ewop == kEwPow && b.dtype != a.dtype) {
+    // a float base with an integer exponent: the exponent as float32
+    IH_REQUIRE(b.host != nullptr, INFERC_ERR_UNSUPPORTED, "Pow: exponent type differs");
+    std::vector<float> e(size_t(b.numel()));
+    ew_cast(nullptr, b.dtype, INFERC_DT_F32, b.numel(), b.host->data(), e.data());
+    bn = n.out[0] + "__exp";
+    make_host(bn, INFERC_DT_F32, b.shape, e.data());
+    b = get(bn);
+  }
+  IH_REQUIRE(a.dtype == b.dtype, INFERC_ERR_UNSUPPORTED,
+             n.op + ": operand types differ (" + std::to_string(a.dtype) + " vs " +
+                 std::to_string(b.dtype) + ")");
+  const std::vector<int64_t> os = ew_broadcast_shape({a.shape, b.shape});
+  const int odt = ew_binary_out_dtype(ewop, a.dtype);
+  if (a.host && b.host && numel_of(os) <= (int64_t(1) << 16)) {
+    void* y = make_host_buf(n.out[0], odt, os);
+    ew_binary(nullptr, ewop, a.dtype, os, a.host->data(), a.shape, b.host->data(), b.shape, y);
+    return;
+  }
+  const void* ap = dev_of(n.in[0]);
+  const void* bp = dev_of(bn);
+  void* y = make_dev(n.out[0], odt, os).dev;
+  if (!dry) ew_binary(ctx, ewop, a.dtype, os, ap, a.shape, bp, b.shape, y);
+}
+
+// The ops of exported graphs outside the fused set: Constant,
+// ConstantOfShape, Cast, unary math, binary arithmetic / comparison /
+// logic, Where, Expand, Transpose, Slice and ReduceMean
+// (src/runtime/executor.cc:226-339). Returns false for an op it does not
+// know.
+bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
+  using namespace ih;
+  const std::string& op = n.op;
+  static const std::map<std::string, int> binary = {
+      {"Sub", kEwSub}, {"Mul", kEwMul}, {"Div", kEwDiv}, {"Pow", kEwPow}, {"Max", kEwMax},
+      {"Min", kEwMin}, {"Less", kEwLess}, {"LessOrEqual", kEwLessOrEqual},
+      {"Greater", kEwGreater}, {"GreaterOrEqual", kEwGreaterOrEqual}, {"And", kEwAnd},
+      {"Or", kEwOr}, {"Xor", kEwXor}};
+  static const std::map<std::string, int> unary = {
+      {"Sqrt", kEwSqrt}, {"Erf", kEwErf}, {"Tanh", kEwTanh}, {"Neg", kEwNeg},
+      {"Abs", kEwAbs}, {"Exp", kEwExp}, {"Log", kEwLog}, {"Reciprocal", kEwReciprocal},
+      {"Sigmoid", kEwSigmoid}, {"Floor", kEwFloor}, {"Ceil", kEwCeil}, {"Not", kEwNot}};
+  auto bi = binary.find(op);
+  if (bi != binary.end()) {
+    generic_binary(n, bi->second);
+    return true;
+  }
+  auto ui = unary.find(op);
+  if (ui != unary.end()) {
+    const Value x = get(n.in.at(0));
+    if (host_foldable(n, x.numel())) {
+      void* y = make_host_buf(n.out[0], x.dtype, x.shape);
+      ew_unary(nullptr, ui->second, x.dtype, x.numel(), x.host->data(), y);
+    } else {
+      const void* xp = dev_of(n.in[0]);
+      void* y = make_dev(n.out[0], x.dtype, x.shape).dev;
+      if (!dry) ew_unary(ctx, ui->second, x.dtype, x.numel(), xp, y);
+    }
+    return true;
+  }
+  if (op == "Constant") {
+    auto tv = n.tattrs.find("value");
+    if (tv != n.tattrs.end()) {
+      (void)dtype_size(tv->second.dtype);
+      make_host(n.out[0], tv->second.dtype, tv->second.shape, tv->second.data.data());
+      return true;
+    }
+    if (n.attrs.count("value_float")) {
+      const float f = attr_float(n, "value_float", 0.0f);
+      make_host(n.out[0], INFERC_DT_F32, {}, &f);
+    } else if (n.attrs.count("value_int")) {
+      const int64_t i = attr_int(n, "value_int", 0);
+      make_host(n.out[0], INFERC_DT_I64, {}, &i);
+    } else if (n.attrs.count("value_ints")) {
+      const std::vector<int64_t> v = attr_ints(n, "value_ints");
+      make_host(n.out[0], INFERC_DT_I64, {int64_t(v.size())}, v.data());
+    } else {
+      fail(INFERC_ERR_UNSUPPORTED, "Constant '" + n.name + "': unsupported value attribute");
+    }
+    return true;
+  }
+  if (op == "ConstantOfShape") {
+    const std::vector<int64_t> shape = host_i64(get(n.in.at(0)), "ConstantOfShape");
+    int dt = INFERC_DT_F32;
+    std::vector<uint8_t> one(4, 0);
+    auto tv = n.tattrs.find("value");
+    if (tv != n.tattrs.end()) {
+      dt = tv->second.dtype;
+      one = tv->second.data;
+      IH_REQUIRE(one.size() == dtype_size(dt), INFERC_ERR_ARG,
+                 "ConstantOfShape: value must hold one element");
+    }
+    const int64_t cnt = numel_of(shape);
+    IH_REQUIRE(cnt <= (int64_t(1) << 24), INFERC_ERR_UNSUPPORTED, "ConstantOfShape: too large");
+    uint8_t* y = static_cast<uint8_t*>(make_host_buf(n.out[0], dt, shape));
+    for (int64_t i = 0; i < cnt; ++i) std::memcpy(y + size_t(i) * one.size(), one.data(), one.size());
+    return true;
+  }
+  if (op == "Cast") {
+    const Value x = get(n.in.at(0));
+    const int to = int(attr_int(n, "to", 0));
+    (void)dtype_size(to);
+    if (to == x.dtype) {
+      alias(n.out[0], x, x.shape);
+      return true;
+    }
+    if (host_foldable(n, x.numel())) {
+      void* y = make_host_buf(n.out[0], to, x.shape);
+      ew_cast(nullptr, x.dtype, to, x.numel(), x.host->data(), y);
+    } else {
+      const void* xp = dev_of(n.in[0]);
+      void* y = make_dev(n.out[0], to, x.shape).dev;
+      if (!dry) ew_cast(ctx, x.dtype, to, x.numel(), xp, y);
+    }
+    return true;
+  }
+  if (op == "Where") {
+    const Value c = get(n.in.at(0)), a = get(n.in.at(1)), b = get(n.in.at(2));
+    IH_REQUIRE(c.dtype == INFERC_DT_BOOL || c.dtype == INFERC_DT_U8, INFERC_ERR_UNSUPPORTED,
+               "Where: condition must be bool");
+    IH_REQUIRE(a.dtype == b.dtype, INFERC_ERR_UNSUPPORTED, "Where: branch types differ");
+    const std::vector<int64_t> os = ew_broadcast_shape({c.shape, a.shape, b.shape});
+    if (host_foldable(n, numel_of(os))) {
+      void* y = make_host_buf(n.out[0], a.dtype, os);
+      ew_where(nullptr, a.dtype, os, c.host->data(), c.shape, a.host->data(), a.shape,
+               b.host->data(), b.shape, y);
+    } else {
+      const void* cp = dev_of(n.in[0]);
+      const void* ap = dev_of(n.in[1]);
+      const void* bp = dev_of(n.in[2]);
+      void* y = make_dev(n.out[0], a.dtype, os).dev;
+      if (!dry) ew_where(ctx, a.dtype, os, cp, c.shape, ap, a.shape, bp, b.shape, y);
+    }
+    return true;
+  }
+  if (op == "Expand") {
+    const Value x = get(n.in.at(0));
+    const std::vector<int64_t> target = host_i64(get(n.in.at(1)), "Expand");
+    const std::vector<int64_t> os = ew_broadcast_shape({x.shape, target});
+    if (os == x.shape) {
+      alias(n.out[0], x, os);
+      return true;
+    }
+    if (host_foldable(n, numel_of(os))) {
+      void* y = make_host_buf(n.out[0], x.dtype, os);
+      ew_expand(nullptr, x.dtype, os, x.host->data(), x.shape, y);
+    } else {
+      const void* xp = dev_of(n.in[0]);
+      void* y = make_dev(n.out[0], x.dtype, os).dev;
+      if (!dry) ew_expand(ctx, x.dtype, os, xp, x.shape, y);
+    }
+    return true;
+  }
+  if (op == "Transpose") {
+    const Value x = get(n.in.at(0));
+    std::vector<int64_t> perm = attr_ints(n, "perm");
+    const int64_t r = int64_t(x.shape.size());
+    if (perm.empty())
+      for (int64_t k = r - 1; k >= 0; --k) perm.push_back(k);
+    IH_REQUIRE(int64_t(perm.size()) == r, INFERC_ERR_SHAPE, "Transpose: perm rank mismatch");
+    std::vector<int64_t> os;
+    for (int64_t p : perm) {
+      IH_REQUIRE(p >= 0 && p < r, INFERC_ERR_SHAPE, "Transpose: perm out of range");
+      os.push_back(x.shape[size_t(p)]);
+    }
+    if (host_foldable(n, x.numel())) {
+      void* y = make_host_buf(n.out[0], x.dtype, os);
+      ew_transpose(nullptr, x.dtype, x.shape, perm, x.host->data(), y);
+    } else {
+      const void* xp = dev_of(n.in[0]);
+      void* y = make_dev(n.out[0], x.dtype, os).dev;
+      if (!dry) ew_transpose(ctx, x.dtype, x.shape, perm, xp, y);
+    }
+    return true;
+  }
+  if (op == "Slice") {
+    // opset 10+: data, starts, ends[, axes[, steps]]; clamping as ONNX
+    // specifies (start to [0, d] / [0, d-1] for negative steps, end to
+    // [0, d] / [-1, d-1])
+    const Value x = get(n.in.at(0));
+    const int64_t r = int64_t(x.shape.size());
+    const std::vector<int64_t> starts = host_i64(get(n.in.at(1)), "Slice");
+    const std::vector<int64_t> ends = host_i64(get(n.in.at(2)), "Slice");
+    std::vector<int64_t> axes, steps;
+    if (n.in.size() > 3 && !n.in[3].empty()) axes = host_i64(get(n.in[3]), "Slice");
+    if (n.in.size() > 4 && !n.in[4].empty()) steps = host_i64(get(n.in[4]), "Slice");
+    if (axes.empty())
+      for (size_t i = 0; i < starts.size(); ++i) axes.push_back(int64_t(i));
+    if (steps.empty()) steps.assign(starts.size(), 1);
+    IH_REQUIRE(ends.size() == starts.size() && axes.size() == starts.size() &&
+                   steps.size() == starts.size(),
+               INFERC_ERR_SHAPE, "Slice: starts/ends/axes/steps lengths differ");
+    std::vector<int64_t> st(size_t(r), 0), sp(size_t(r), 1), os = x.shape;
+    for (size_t k = 0; k < starts.size(); ++k) {
+      int64_t a = axes[k] < 0 ? axes[k] + r : axes[k];
+      IH_REQUIRE(a >= 0 && a < r, INFERC_ERR_ARG, "Slice: axis out of range");
+      const int64_t d = x.shape[size_t(a)], step = steps[k];
+      IH_REQUIRE(step != 0, INFERC_ERR_ARG, "Slice: step must be non-zero");
+      int64_t b = starts[k] < 0 ? starts[k] + d : starts[k];
+      int64_t e = ends[k] < 0 ? ends[k] + d : ends[k];
+      if (step > 0) {
+        b = b < 0 ? 0 : (b > d ? d : b);
+        e = e < 0 ? 0 : (e > d ? d : e);
+      } else {
+        b = b < 0 ? 0 : (b > d - 1 ? d - 1 : b);
+        e = e < -1 ? -1 : (e > d - 1 ? d - 1 : e);
+      }
+      const int64_t len = step > 0 ? (e - b + step - 1) / step : (b - e + (-step) - 1) / (-step);
+      st[size_t(a)] = b;
+      sp[size_t(a)] = step;
+      os[size_t(a)] = len > 0 ? len : 0;
+    }
+    if (host_foldable(n, numel_of(os))) {
+      void* y = make_host_buf(n.out[0], x.dtype, os);
+      ew_slice(nullptr, x.dtype, x.shape, st, sp, os, x.host->data(), y);
+    } else {
+      const void* xp = dev_of(n.in[0]);
+      void* y = make_dev(n.out[0], x.dtype, os).dev;
+      if (!dry) ew_slice(ctx, x.dtype, x.shape, st, sp, os, xp, y);
+    }
+    return true;
+  }
+  if (op == "ReduceMean") {
+    const Value x = get(n.in.at(0));
+    IH_REQUIRE(x.dtype == INFERC_DT_F32, INFERC_ERR_UNSUPPORTED, "ReduceMean: float32 only");
+    const int64_t r = int64_t(x.shape.size());
+    std::vector<int64_t> axes = attr_ints(n, "axes");
+    if (n.in.size() > 1 && !n.in[1].empty()) axes = host_i64(get(n.in[1]), "ReduceMean");
+    const bool keep = attr_int(n, "keepdims", 1) != 0;
+    std::vector<bool> red(size_t(r), axes.empty());
+    for (int64_t a : axes) {
+      const int64_t aa = a < 0 ? a + r : a;
+      IH_REQUIRE(aa >= 0 && aa < r, INFERC_ERR_ARG, "ReduceMean: axis out of range");
+      red[size_t(aa)] = true;
+    }
+    std::vector<int64_t> os;
+    for (int64_t d = 0; d < r; ++d) {
+      if (!red[size_t(d)]) os.push_back(x.shape[size_t(d)]);
+      else if (keep) os.push_back(1);
+    }
+    if (host_foldable(n, numel_of(os))) {
+      float* y = static_cast<float*>(make_host_buf(n.out[0], INFERC_DT_F32, os));
+      ew_reduce_mean(nullptr, x.shape, red, reinterpret_cast<const float*>(x.host->data()), y);
+    } else {
+      const float* xp = static_cast<const float*>(dev_of(n.in[0]));
+      float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
+      if (!dry) ew_reduce_mean(ctx, x.shape, red, xp, y);
+    }
+    return true;
+  }
+  return false;
 }
 
 void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
@@ -1384,9 +1736,14 @@ int inferc_executor_get_output(inferc_executor* ex, const char* name, void* host
   return ih::guard([&] {
     check_ex(ex);
     IH_REQUIRE(name && host_dst, INFERC_ERR_ARG, "null argument");
-    IH_REQUIRE(!ex->dry, INFERC_ERR_STATE, "a dry-run executor has no output data");
     const ih::Value& v = ex->get(name);
+    IH_REQUIRE(!ex->dry || v.host, INFERC_ERR_STATE,
+               "a dry-run executor has no output data (only host-known values)");
     IH_REQUIRE(capacity_bytes >= v.bytes(), INFERC_ERR_ARG, "output buffer too small");
+    if (ex->dry) {
+      std::memcpy(host_dst, v.host->data(), v.bytes());
+      return;
+    }
     IH_HIP(hipStreamSynchronize(ex->ctx->stream));
     if (v.dev) {
       IH_HIP(hipMemcpy(host_dst, v.dev, v.bytes(), hipMemcpyDeviceToHost));
