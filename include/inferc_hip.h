@@ -365,6 +365,25 @@ int inferc_executor_get_output(inferc_executor* ex, const char* name,
                                void* host_dst, size_t capacity_bytes);
 /* 0 = eager dispatch every run, 1 = capture/replay HIP graphs (default). */
 int inferc_executor_set_graph_mode(inferc_executor* ex, int enabled);
+/* Device KV cache for decode over an exported with-past graph: the
+ * FusedAttentionPast nodes (GPT-2's attention over Concat(past, new), made
+ * by the additive-attention pass) keep K/V in a persistent [B, nH, max_t, dh]
+ * cache. Each run appends the new rows at the past length P (the past
+ * input's dim 2); a past input set with data seeds rows [0, P), one set by
+ * inferc_executor_set_input_shape means the cache already holds them. The
+ * present.* outputs are views of the cache, copied out by get_output. This
+ * replaces the reference's present -> past renaming through host tensors
+ * (src/cli/main.cpp:831-836, 883-888). max_t = 0 unbinds. */
+int inferc_executor_bind_kv_cache(inferc_executor* ex, int64_t max_t);
+/* An input that carries only a shape (no data): a past the KV cache holds.
+ * A node that needs its data fails with INFERC_ERR_STATE. */
+int inferc_executor_set_input_shape(inferc_executor* ex, const char* name,
+                                    int dtype, int rank, const int64_t* shape);
+/* Index of the first maximum of the last row (last dim) of a float32
+ * output, computed on the device: the greedy token of `inferc decode`
+ * (main.cpp:875-879). Synchronises the stream. */
+int inferc_executor_output_argmax(inferc_executor* ex, const char* name,
+                                  int64_t* index);
 
 /* ---------------- Profiler (src/profiler/profiler.h:40-89) ---------------- */
 

@@ -1,0 +1,143 @@
+// Attention over a key/value cache: the FusedAttentionPast node that the
+// additive-attention pass makes of GPT-2's with-past decoder block
+// (present = Concat(past, new); softmax(q K^T * scale + mask) V; the
+// reference runs this block unfused and renames present.* to past.* between
+// decode steps, src/cli/main.cpp:831-888).
+//
+// Cache layout: head-major [B, nH, max_t, dh] floats, the layout of the
+// GPT-2 decoder's device cache. S new query rows attend over T = P + S keys
+// (P cached before the call).
+//
+// cache_attention: one 64-lane wave per (batch, head, query row), four rows
+// per 256-thread block. Keys are taken 64 at a time: each lane scores one key
+// (dot product over dh with the query row held in LDS), a first sweep finds
+// the row maximum, a second recomputes the scores, turns them into
+// exp(s - max) and accumulates sum_j e_j V[j] with lanes over dh (coalesced
+// rows of V), and the result is scaled by 1/sum at the end. Masked scores
+// take `fill` as in FusedAttention (src/kernels/attention.cc:77-91).
+#include "common.h"
+#include "ew.h"
+
+namespace ih {
+
+namespace {
+
+constexpr int kCaWaves = 4;
+constexpr int kCaMaxDh = 256;
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__global__ __launch_bounds__(64 * kCaWaves) void cache_attn_kernel(CacheAttnArgs p, float scale) {
+  __shared__ float qs[kCaWaves][kCaMaxDh];
+  __shared__ float es[kCaWaves][64];
+  const int wave = int(threadIdx.x) / 64, lane = int(threadIdx.x) % 64;
+  const int64_t rows = p.B * p.nH * p.S;
+  const int64_t row = int64_t(blockIdx.x) * kCaWaves + wave;
+  const bool live = row < rows;
+  const int64_t r = live ? row : 0;
+  const int64_t i = r % p.S, h = (r / p.S) % p.nH, b = r / (p.S * p.nH);
+  const int dh = int(p.dh);
+  const float* qrow = p.q + (b * p.S + i) * p.ldq + h * p.dh;
+  for (int d = lane; d < dh; d += 64) qs[wave][d] = live ? qrow[d] : 0.0f;
+  __syncthreads();
+  const float* kbase = p.kc + (b * p.nH + h) * p.max_t * p.dh;
+  const float* vbase = p.vc + (b * p.nH + h) * p.max_t * p.dh;
+  const uint8_t* mrow = p.mask ? p.mask + b * p.ms[0] + h * p.ms[1] + i * p.ms[2] : nullptr;
+  auto score = [&](int64_t j) {
+    const float* kr = kbase + j * p.dh;
+    float s = 0.0f;
+    for (int d = 0; d < dh; ++d) s += qs[wave][d] * kr[d];
+    s *= scale;
+    if (mrow && mrow[j * p.ms[3]]) s = p.fill;
+    return s;
+  };
+  float mx = -INFINITY;
+  for (int64_t j0 = 0; j0 < p.T; j0 += 64) {
+    const int64_t j = j0 + lane;
+    if (live && j < p.T) mx = fmaxf(mx, score(j));
+  }
+  mx = wave_max(mx);
+  float part = 0.0f;
+  float acc[kCaMaxDh / 64] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int64_t j0 = 0; j0 < p.T; j0 += 64) {
+    const int64_t j = j0 + lane;
+    const float e = (live && j < p.T) ? expf(score(j) - mx) : 0.0f;
+    part += e;
+    es[wave][lane] = e;
+    __syncthreads();
+    const int n = int(p.T - j0 < 64 ? p.T - j0 : 64);
+    if (live) {
+      for (int k = 0; k < n; ++k) {
+        const float ek = es[wave][k];
+        const float* vr = vbase + (j0 + k) * p.dh;
+#pragma unroll
+        for (int c = 0; c < kCaMaxDh / 64; ++c) {
+          const int d = lane + 64 * c;
+          if (d < dh) acc[c] += ek * vr[d];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const float inv = 1.0f / wave_sum(part);
+  if (!live) return;
+  float* orow = p.out + (b * p.S + i) * p.ldo + h * p.dh;
+#pragma unroll
+  for (int c = 0; c < kCaMaxDh / 64; ++c) {
+    const int d = lane + 64 * c;
+    if (d < dh) orow[d] = acc[c] * inv;
+  }
+}
+
+// cache[b, h, t0 + s, :] = src[b, s, h*dh : (h+1)*dh] (token-major rows).
+__global__ __launch_bounds__(256) void cache_write_tokens_kernel(int64_t B, int64_t S, int64_t nH,
+                                                                 int64_t dh, int64_t max_t,
+                                                                 int64_t t0,
+                                                                 const float* __restrict__ src,
+                                                                 int64_t ld,
+                                                                 float* __restrict__ cache) {
+  const int64_t total = B * S * nH * dh;
+  for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < total;
+       e += int64_t(gridDim.x) * 256) {
+    const int64_t d = e % dh, h = (e / dh) % nH, s = (e / (dh * nH)) % S, b = e / (dh * nH * S);
+    cache[((b * nH + h) * max_t + t0 + s) * dh + d] = src[(b * S + s) * ld + h * dh + d];
+  }
+}
+
+}  // namespace
+
+void cache_attention(inferc_hip_ctx* ctx, const CacheAttnArgs& a) {
+  IH_REQUIRE(a.dh > 0 && a.dh <= kCaMaxDh, INFERC_ERR_UNSUPPORTED,
+             "attention over a cache: head_dim must be in [1, 256]");
+  IH_REQUIRE(a.T >= 1 && a.T <= a.max_t && a.S >= 1 && a.S <= a.T, INFERC_ERR_SHAPE,
+             "attention over a cache: bad lengths");
+  IH_REQUIRE(a.ldq >= a.nH * a.dh && a.ldo >= a.nH * a.dh, INFERC_ERR_SHAPE,
+             "attention over a cache: row stride smaller than the hidden size");
+  const int64_t rows = a.B * a.nH * a.S;
+  if (rows == 0) return;
+  const float scale = 1.0f / sqrtf(float(a.dh));
+  hipLaunchKernelGGL(cache_attn_kernel, dim3(unsigned(ceil_div(rows, kCaWaves))),
+                     dim3(64 * kCaWaves), 0, ctx->stream, a, scale);
+  check_launch("cache attention");
+}
+
+void cache_write_tokens(inferc_hip_ctx* ctx, int64_t B, int64_t S, int64_t nH, int64_t dh,
+                        int64_t max_t, int64_t t0, const float* src, int64_t ld, float* cache) {
+  IH_REQUIRE(t0 >= 0 && t0 + S <= max_t, INFERC_ERR_SHAPE, "KV cache: append past max_t");
+  const int64_t total = B * S * nH * dh;
+  if (total == 0) return;
+  const int64_t blocks = ceil_div(total, 256);
+  hipLaunchKernelGGL(cache_write_tokens_kernel, dim3(unsigned(blocks > 8192 ? 8192 : blocks)),
+                     dim3(256), 0, ctx->stream, B, S, nH, dh, max_t, t0, src, ld, cache);
+  check_launch("cache write");
+}
+
+}  // namespace ih

@@ -52,4 +52,24 @@ void ew_gather(inferc_hip_ctx* ctx, int dtype, int64_t outer, int64_t rows, int6
 
 std::string shape_str(const std::vector<int64_t>& s);
 
+// Attention of S query rows ([B, S, nH*dh], row stride ldq) over T keys of a
+// head-major cache [B, nH, max_t, dh] (attention_cache.hip).
+struct CacheAttnArgs {
+  int64_t B = 0, S = 0, nH = 0, dh = 0;
+  int64_t T = 0, max_t = 0;
+  const float* q = nullptr;
+  int64_t ldq = 0;
+  const float* kc = nullptr;
+  const float* vc = nullptr;
+  const uint8_t* mask = nullptr;
+  int64_t ms[4] = {0, 0, 0, 0};  // strides over [B, nH, S, T]; 0 on broadcast dims
+  float fill = -3.0e38f;
+  float* out = nullptr;
+  int64_t ldo = 0;
+};
+void cache_attention(inferc_hip_ctx* ctx, const CacheAttnArgs& a);
+// cache[b, h, t0 + s, :] = src[b, s, h*dh : (h+1)*dh] for s < S.
+void cache_write_tokens(inferc_hip_ctx* ctx, int64_t B, int64_t S, int64_t nH, int64_t dh,
+                        int64_t max_t, int64_t t0, const float* src, int64_t ld, float* cache);
+
 }  // namespace ih

@@ -135,10 +135,34 @@ struct inferc_executor {
   std::string graph_sig;
   uint64_t graph_ws_gen = 0;
   std::vector<hipEvent_t> prof_ev;  // one per node boundary of a profiled pass
+  // Device KV caches of FusedAttentionPast nodes (bind_kv_cache): per node,
+  // K and V as [B, nH, kv_max_t, dh] and the number of positions held.
+  int64_t kv_max_t = 0;
+  struct KvCache {
+    float* k = nullptr;
+    float* v = nullptr;
+    int64_t B = 0, nH = 0, dh = 0, len = 0;
+  };
+  std::map<std::string, KvCache> kv;  // keyed by the node's name
+  // present.* outputs that live in a KV cache: name -> (cache, rows held)
+  struct CacheView {
+    const float* base = nullptr;
+    int64_t rows = 0, T = 0, dh = 0, max_t = 0;
+  };
+  std::map<std::string, CacheView> cache_views;
+
+  void free_kv() {
+    for (auto& c : kv) {
+      if (c.second.k) (void)hipFree(c.second.k);
+      if (c.second.v) (void)hipFree(c.second.v);
+    }
+    kv.clear();
+  }
 
   ~inferc_executor() {
     if (dry) return;
     drop_graph();
+    free_kv();
     for (hipEvent_t e : prof_ev) (void)hipEventDestroy(e);
     for (auto& kv : arena) (void)hipFree(kv.second.p);
     for (auto& kv : inputs)
@@ -282,6 +306,7 @@ struct inferc_executor {
   void peephole();
   void exec_node(const inferc_graph::Node& n);
   void generic_binary(const inferc_graph::Node& n, int ewop);
+  void exec_attention_past(const inferc_graph::Node& n);
   bool exec_generic(const inferc_graph::Node& n);
   // With `act`, records an event before each node and after the last on the
   // stream, and appends each node's activation bytes (0 unless `track`).
@@ -517,6 +542,10 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     if (!dry) {
       attention(ctx, a);
     }
+    return;
+  }
+  if (op == "FusedAttentionPast") {
+    exec_attention_past(n);
     return;
   }
   if (op == "FusedMatMulAddGELU" || op == "FusedGemmEpilogue" || op == "MatMul") {
@@ -937,6 +966,11 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     }
     return;
   }
+  if (op == "Concat" && n.in.size() == 1) {
+    const Value x0 = in(0);
+    alias(n.out[0], x0, x0.shape);
+    return;
+  }
   if (op == "Concat") {
     int64_t axis = attr_int(n, "axis", 0);
     const Value x0 = in(0);
@@ -1035,6 +1069,126 @@ void inferc_executor::generic_binary(const inferc_graph::Node& n, int ewop) {
   const void* bp = dev_of(bn);
   void* y = make_dev(n.out[0], odt, os).dev;
   if (!dry) ew_binary(ctx, ewop, a.dtype, os, ap, a.shape, bp, b.shape, y);
+}
+
+// FusedAttentionPast(q, k, v, past_k, past_v, mask) -> (ctx, present_k,
+// present_v): q/k/v [B,S,H] new rows, past_* [B,nH,P,dh], present_* =
+// Concat(past, heads of k/v) along the position axis, ctx = attention of
+// the S new rows over the T = P + S present keys.
+//  - Unbound: present_* are materialised (past rows copied, new rows
+//    written) and attention reads them.
+//  - Bound to a KV cache (bind_kv_cache): the node keeps K/V in a
+//    persistent [B, nH, max_t, dh] cache. A past input with data seeds rows
+//    [0, P); a shape-only past input says the cache already holds them. The
+//    new rows are appended at P, attention reads the cache, and present_*
+//    are views of its first T rows, copied out only when asked for.
+void inferc_executor::exec_attention_past(const inferc_graph::Node& n) {
+  using namespace ih;
+  IH_REQUIRE(n.in.size() >= 5 && n.out.size() == 3, INFERC_ERR_ARG,
+             "FusedAttentionPast: needs q, k, v, past_k, past_v[, mask] and three outputs");
+  const Value q = get(n.in[0]);
+  IH_REQUIRE(q.dtype == INFERC_DT_F32 && q.shape.size() == 3, INFERC_ERR_SHAPE,
+             "FusedAttentionPast: q must be float32 [B,S,H]");
+  IH_REQUIRE(get(n.in[1]).shape == q.shape && get(n.in[2]).shape == q.shape, INFERC_ERR_SHAPE,
+             "FusedAttentionPast: q/k/v shapes differ");
+  const Value pk = get(n.in[3]);
+  const Value pv = get(n.in[4]);
+  const int64_t B = q.shape[0], S = q.shape[1], H = q.shape[2];
+  const int64_t dh = attr_int(n, "head_dim", 64);
+  IH_REQUIRE(dh > 0 && H % dh == 0, INFERC_ERR_SHAPE, "FusedAttentionPast: H % head_dim != 0");
+  const int64_t nH = H / dh;
+  IH_REQUIRE(pk.shape.size() == 4 && pk.shape[0] == B && pk.shape[1] == nH && pk.shape[3] == dh &&
+                 pv.shape == pk.shape,
+             INFERC_ERR_SHAPE, "FusedAttentionPast: past must be [B, nH, P, head_dim]");
+  const int64_t P = pk.shape[2], T = P + S;
+  CacheAttnArgs a;
+  a.B = B; a.S = S; a.nH = nH; a.dh = dh; a.T = T;
+  a.fill = attr_float(n, "fill", -3.0e38f);
+  a.q = static_cast<const float*>(dev_of(n.in[0]));
+  a.ldq = a.ldo = H;
+  if (n.in.size() >= 6 && !n.in[5].empty()) {
+    const Value m = get(n.in[5]);
+    IH_REQUIRE(m.dtype == INFERC_DT_BOOL || m.dtype == INFERC_DT_U8, INFERC_ERR_UNSUPPORTED,
+               "FusedAttentionPast: mask must be bool");
+    IH_REQUIRE(m.shape.size() <= 4, INFERC_ERR_SHAPE, "FusedAttentionPast: mask rank > 4");
+    const std::vector<int64_t> full = {B, nH, S, T};
+    for (size_t i = 0; i < m.shape.size(); ++i) {
+      const int64_t d = m.shape[i], f = full[4 - m.shape.size() + i];
+      IH_REQUIRE(d == f || d == 1, INFERC_ERR_SHAPE,
+                 "FusedAttentionPast: mask " + shape_str(m.shape) + " does not broadcast to " +
+                     shape_str(full));
+    }
+    a.mask = static_cast<const uint8_t*>(dev_of(n.in[5]));
+    mask_strides(m.shape, a.ms);
+  }
+  const float* kn = static_cast<const float*>(dev_of(n.in[1]));
+  const float* vn = static_cast<const float*>(dev_of(n.in[2]));
+  a.out = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, q.shape).dev);
+  const std::vector<int64_t> present = {B, nH, T, dh};
+  auto has_data = [&](const Value& v) { return v.dev != nullptr || v.host != nullptr; };
+  if (kv_max_t == 0) {
+    IH_REQUIRE(P == 0 || (has_data(pk) && has_data(pv)), INFERC_ERR_STATE,
+               "FusedAttentionPast: past has no data and no KV cache is bound");
+    float* ko = static_cast<float*>(make_dev(n.out[1], INFERC_DT_F32, present).dev);
+    float* vo = static_cast<float*>(make_dev(n.out[2], INFERC_DT_F32, present).dev);
+    const float* pkp = P ? static_cast<const float*>(dev_of(n.in[3])) : nullptr;
+    const float* pvp = P ? static_cast<const float*>(dev_of(n.in[4])) : nullptr;
+    a.kc = ko;
+    a.vc = vo;
+    a.max_t = T;
+    if (!dry) {
+      if (P) {
+        copy2d(ctx, ko, T * dh, pkp, P * dh, P * dh, B * nH);
+        copy2d(ctx, vo, T * dh, pvp, P * dh, P * dh, B * nH);
+      }
+      cache_write_tokens(ctx, B, S, nH, dh, T, P, kn, H, ko);
+      cache_write_tokens(ctx, B, S, nH, dh, T, P, vn, H, vo);
+      cache_attention(ctx, a);
+    }
+    return;
+  }
+  IH_REQUIRE(T <= kv_max_t, INFERC_ERR_SHAPE,
+             "FusedAttentionPast: " + std::to_string(T) + " positions exceed the KV cache (" +
+                 std::to_string(kv_max_t) + ")");
+  KvCache& c = kv[n.name];
+  if (c.k == nullptr || c.B != B || c.nH != nH || c.dh != dh) {
+    IH_REQUIRE(!dry, INFERC_ERR_STATE, "a dry-run executor has no KV cache");
+    IH_REQUIRE(!ctx->capturing, INFERC_ERR_STATE, "KV cache allocation during graph capture");
+    if (c.k) {
+      IH_HIP(hipStreamSynchronize(ctx->stream));
+      (void)hipFree(c.k);
+      (void)hipFree(c.v);
+    }
+    c = KvCache{};
+    const size_t bytes = size_t(B * nH * kv_max_t * dh) * sizeof(float);
+    IH_HIP(hipMalloc(&c.k, bytes));
+    IH_HIP(hipMalloc(&c.v, bytes));
+    c.B = B; c.nH = nH; c.dh = dh;
+  }
+  const bool seed = P > 0 && has_data(pk) && has_data(pv);
+  IH_REQUIRE(seed || P <= c.len, INFERC_ERR_STATE,
+             "FusedAttentionPast: the KV cache holds " + std::to_string(c.len) +
+                 " positions, the past says " + std::to_string(P));
+  a.kc = c.k;
+  a.vc = c.v;
+  a.max_t = kv_max_t;
+  if (seed) {
+    const float* pkp = static_cast<const float*>(dev_of(n.in[3]));
+    const float* pvp = static_cast<const float*>(dev_of(n.in[4]));
+    copy2d(ctx, c.k, kv_max_t * dh, pkp, P * dh, P * dh, B * nH);
+    copy2d(ctx, c.v, kv_max_t * dh, pvp, P * dh, P * dh, B * nH);
+  }
+  cache_write_tokens(ctx, B, S, nH, dh, kv_max_t, P, kn, H, c.k);
+  cache_write_tokens(ctx, B, S, nH, dh, kv_max_t, P, vn, H, c.v);
+  cache_attention(ctx, a);
+  c.len = T;
+  for (int o = 1; o <= 2; ++o) {
+    Value v;
+    v.dtype = INFERC_DT_F32;
+    v.shape = present;
+    vals[n.out[size_t(o)]] = v;  // no contiguous data: read through the view
+    cache_views[n.out[size_t(o)]] = CacheView{o == 1 ? c.k : c.v, B * nH, T, dh, kv_max_t};
+  }
 }
 
 // The ops of exported graphs outside the fused set: Constant,
@@ -1267,6 +1421,7 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
 
 void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
   vals = inits;
+  cache_views.clear();
   for (auto& kv : inputs) vals[kv.first] = kv.second.v;
   const bool events = act != nullptr && !dry;
   for (size_t i = 0; i < nodes.size(); ++i) {
@@ -1745,6 +1900,15 @@ int inferc_executor_get_output(inferc_executor* ex, const char* name, void* host
       return;
     }
     IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+    auto cv = ex->cache_views.find(name);
+    if (!v.dev && !v.host && cv != ex->cache_views.end()) {
+      const auto& w = cv->second;
+      const size_t row = size_t(w.T * w.dh) * sizeof(float);
+      IH_HIP(hipMemcpy2D(host_dst, row, w.base, size_t(w.max_t * w.dh) * sizeof(float), row,
+                         size_t(w.rows), hipMemcpyDeviceToHost));
+      return;
+    }
+    IH_REQUIRE(v.dev || v.host, INFERC_ERR_STATE, std::string("tensor '") + name + "' has no data");
     if (v.dev) {
       IH_HIP(hipMemcpy(host_dst, v.dev, v.bytes(), hipMemcpyDeviceToHost));
     } else if (v.host) {
@@ -1758,6 +1922,56 @@ int inferc_executor_set_graph_mode(inferc_executor* ex, int enabled) {
     check_ex(ex);
     ex->graph_mode = enabled != 0;
     if (!ex->graph_mode) ex->drop_graph();
+  });
+}
+
+int inferc_executor_bind_kv_cache(inferc_executor* ex, int64_t max_t) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(max_t >= 0, INFERC_ERR_ARG, "max_t must be >= 0");
+    IH_REQUIRE(!ex->dry, INFERC_ERR_STATE, "a dry-run executor has no KV cache");
+    IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+    ex->drop_graph();
+    ex->free_kv();
+    ex->kv_max_t = max_t;
+    ex->last_sig.clear();
+  });
+}
+
+int inferc_executor_set_input_shape(inferc_executor* ex, const char* name, int dtype, int rank,
+                                    const int64_t* shape) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(name != nullptr, INFERC_ERR_ARG, "null input name");
+    inferc_executor::Input& in = ex->inputs[name];
+    if (in.from_host && in.v.dev && !ex->dry) {
+      IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+      IH_HIP(hipFree(in.v.dev));
+    }
+    in.from_host = false;
+    in.staged.clear();
+    in.v.dtype = dtype;
+    (void)ih::dtype_size(dtype);
+    in.v.shape = read_shape(rank, shape);
+    in.v.dev = nullptr;
+    in.v.host.reset();
+  });
+}
+
+int inferc_executor_output_argmax(inferc_executor* ex, const char* name, int64_t* index) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(name != nullptr && index != nullptr, INFERC_ERR_ARG, "null argument");
+    IH_REQUIRE(!ex->dry, INFERC_ERR_STATE, "a dry-run executor has no output data");
+    const ih::Value& v = ex->get(name);
+    IH_REQUIRE(v.dtype == INFERC_DT_F32 && v.dev && !v.shape.empty() && v.shape.back() > 0,
+               INFERC_ERR_ARG, "argmax: needs a float32 device output");
+    const int64_t n = v.shape.back();
+    const float* last = static_cast<const float*>(v.dev) + (v.numel() - n);
+    int64_t* d = static_cast<int64_t*>(ex->buf("__argmax__", sizeof(int64_t)));
+    ih::argmax(ex->ctx, n, last, d, nullptr);
+    IH_HIP(hipMemcpyAsync(index, d, sizeof(int64_t), hipMemcpyDeviceToHost, ex->ctx->stream));
+    IH_HIP(hipStreamSynchronize(ex->ctx->stream));
   });
 }
 

@@ -25,6 +25,7 @@
 // fill))) instead of selecting with Where(mask, fill, scores); it produces
 // the same FusedAttention node, with a Not in front of the mask when the
 // Where keeps positions where its condition holds.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -590,14 +591,56 @@ int recognize_attention(inferc_graph& g) {
 // finite score gives the fill (|score| is far below the fill's ulp), so the
 // sum equals the Where-select form. The projections' transposes must be the
 // head split (perm 0,2,1,3; K: 0,2,3,1) and the context's the merge
-// (0,2,1,3). When M keeps positions where cond holds, a Not(cond) node is
-// added once per distinct cond.
+// (0,2,1,3); a Cast to float32 may sit between Softmax and the context
+// MatMul (GPT-2 exports). When M keeps positions where cond holds, a Not(cond)
+// node is added once per distinct cond.
+//
+// With a KV cache in the graph (GPT-2's with-past decoder: K = Transpose
+// (0,1,3,2) of Concat(past_k, head split of k, axis 2), V = Concat(past_v,
+// head split of v, axis 2), the Concats being the present.* outputs) the
+// block becomes FusedAttentionPast(q, k, v, past_k, past_v, mask) with
+// outputs (ctx, present_k, present_v).
 int recognize_attention_additive(inferc_graph& g) {
   View v(g);
   std::set<int> removed;
   std::map<int, std::vector<Node>> inserts;
   std::map<std::string, std::string> negated;  // cond -> its Not output
-  const std::vector<int64_t> split = {0, 2, 1, 3}, split_t = {0, 2, 3, 1};
+  const std::vector<int64_t> split = {0, 2, 1, 3}, split_t = {0, 2, 3, 1}, last2 = {0, 1, 3, 2};
+  auto concat_axis2 = [&](const Node* c) {
+    if (!c || c->in.size() != 2) return false;
+    auto it = c->attrs.find("axis");
+    if (it == c->attrs.end()) return false;
+    const int64_t a = std::stoll(it->second);
+    return a == 2 || a == -2;
+  };
+  // K operand of the scores MatMul -> (k projection, past_k or "", Concat)
+  auto key_src = [&](const std::string& t, std::set<int>* rm, std::string* x, std::string* past,
+                     const Node** cat) {
+    *x = proj_behind(v, t, rm, &split_t);
+    if (!x->empty()) return true;
+    const Node* tr = v.producer_op(t, "Transpose");
+    if (!tr || tr->in.empty() || ints_attr(*tr, "perm") != last2) return false;
+    const Node* c = v.producer_op(tr->in[0], "Concat");
+    if (!concat_axis2(c)) return false;
+    *x = proj_behind(v, c->in[1], rm, &split);
+    if (x->empty()) return false;
+    rm->insert(v.index_of(tr));
+    *past = c->in[0];
+    *cat = c;
+    return true;
+  };
+  auto value_src = [&](const std::string& t, std::set<int>* rm, std::string* x, std::string* past,
+                       const Node** cat) {
+    *x = proj_behind(v, t, rm, &split);
+    if (!x->empty()) return true;
+    const Node* c = v.producer_op(t, "Concat");
+    if (!concat_axis2(c)) return false;
+    *x = proj_behind(v, c->in[1], rm, &split);
+    if (x->empty()) return false;
+    *past = c->in[0];
+    *cat = c;
+    return true;
+  };
   for (int i = 0; i < int(g.nodes.size()); ++i) {
     const Node& sm = g.nodes[size_t(i)];
     if (sm.op != "Softmax" || sm.in.size() != 1 || sm.out.empty()) continue;
@@ -637,19 +680,88 @@ int recognize_attention_additive(inferc_graph& g) {
       std::string cond = where->in[0];
       if (const Node* ex = v.producer_op(cond, "Expand")) cond = ex->in[0];
       const std::string q = proj_behind(v, smm->in[0], &rm, &split);
-      const std::string k = proj_behind(v, smm->in[1], &rm, &split_t);
-      if (q.empty() || k.empty()) break;
+      std::string k, past_k, vv, past_v;
+      const Node *kcat = nullptr, *vcat = nullptr;
+      if (q.empty() || !key_src(smm->in[1], &rm, &k, &past_k, &kcat)) break;
       const Node* cmm = v.unique_consumer(sm.out[0]);
-      if (!cmm || cmm->op != "MatMul" || cmm->in.size() != 2 || cmm->in[0] != sm.out[0]) break;
-      const std::string vv = proj_behind(v, cmm->in[1], &rm, &split);
-      if (vv.empty()) break;
+      const Node* cst = nullptr;
+      if (cmm && cmm->op == "Cast" && cmm->attrs.count("to") &&
+          std::stoll(cmm->attrs.at("to")) == INFERC_DT_F32) {
+        cst = cmm;
+        cmm = v.unique_consumer(cst->out[0]);
+      }
+      const std::string probs = cst ? cst->out[0] : sm.out[0];
+      if (!cmm || cmm->op != "MatMul" || cmm->in.size() != 2 || cmm->in[0] != probs) break;
+      if (!value_src(cmm->in[1], &rm, &vv, &past_v, &vcat)) break;
+      if ((kcat == nullptr) != (vcat == nullptr)) break;  // both cached or neither
       const Node* ctr = v.unique_consumer(cmm->out[0]);
       if (!ctr || ctr->op != "Transpose" || ints_attr(*ctr, "perm") != split) break;
-      const Node* crs = v.unique_consumer(ctr->out[0]);
-      if (!crs || crs->op != "Reshape" || crs->out.empty()) break;
-      for (const Node* n : {smm, scale, add, &sm, cmm, ctr, crs}) rm.insert(v.index_of(n));
+      // the merged context feeds one Reshape, plus Shape nodes that compute
+      // that Reshape's target (GPT-2 exports)
+      const Node* crs = nullptr;
+      std::vector<int> shape_readers;
+      bool other = false;
+      for (int j = 0; j < int(g.nodes.size()); ++j) {
+        const Node& n = g.nodes[size_t(j)];
+        if (std::find(n.in.begin(), n.in.end(), ctr->out[0]) == n.in.end()) continue;
+        if (n.op == "Reshape" && n.in[0] == ctr->out[0] && !crs) crs = &n;
+        else if (n.op == "Shape") shape_readers.push_back(j);
+        else other = true;
+      }
+      if (!crs || other || crs->out.empty()) break;
+      for (const Node* n : {smm, scale, add, &sm, cst, cmm, ctr, crs}) rm.insert(v.index_of(n));
       if (v.unique_consumer(cc->out[0]) == scale) rm.insert(v.index_of(cc));
+      if (kcat) {
+        rm.insert(v.index_of(kcat));
+        rm.insert(v.index_of(vcat));
+      }
+      rm.insert(shape_readers.begin(), shape_readers.end());
       rm.erase(-1);
+      // nodes whose every output is read only by removed nodes go too (the
+      // shape arithmetic of the removed Reshapes), except the producers of
+      // the fused node's own inputs
+      const std::set<std::string> needed = {q, k, vv, past_k, past_v, cond};
+      for (bool grew = true; grew;) {
+        grew = false;
+        for (int j = 0; j < int(g.nodes.size()); ++j) {
+          if (rm.count(j)) continue;
+          const Node& n = g.nodes[size_t(j)];
+          bool feeds_only_removed = !n.out.empty();
+          for (const auto& o : n.out) feeds_only_removed = feeds_only_removed && !needed.count(o);
+          for (const auto& o : n.out) {
+            bool read = false;
+            for (int r = 0; r < int(g.nodes.size()) && feeds_only_removed; ++r) {
+              const auto& rin = g.nodes[size_t(r)].in;
+              if (std::find(rin.begin(), rin.end(), o) == rin.end()) continue;
+              read = true;
+              feeds_only_removed = rm.count(r) > 0;
+            }
+            feeds_only_removed = feeds_only_removed && read && !v.is_output(o);
+          }
+          if (feeds_only_removed) {
+            rm.insert(j);
+            grew = true;
+          }
+        }
+      }
+      // nothing kept may read a removed node's output, except the tensors the
+      // fused node itself produces
+      std::set<std::string> produced = {crs->out[0]};
+      if (kcat) {
+        produced.insert(kcat->out[0]);
+        produced.insert(vcat->out[0]);
+      }
+      std::set<std::string> gone;
+      for (int j : rm)
+        for (const auto& o : g.nodes[size_t(j)].out)
+          if (!produced.count(o)) gone.insert(o);
+      bool ok = true;
+      for (int j = 0; j < int(g.nodes.size()) && ok; ++j) {
+        if (rm.count(j)) continue;
+        for (const auto& in : g.nodes[size_t(j)].in) ok = ok && !gone.count(in);
+      }
+      for (const auto& o : g.outputs) ok = ok && !gone.count(o);
+      if (!ok) break;
       std::string mask = cond;
       std::vector<Node>& slot = inserts[i];
       if (keep_if_true) {
@@ -666,13 +778,20 @@ int recognize_attention_additive(inferc_graph& g) {
         mask = it->second;
       }
       removed.insert(rm.begin(), rm.end());
-      slot.push_back(attention_node(i, q, k, vv, mask, head_dim, fill, crs->out[0]));
+      Node fa = attention_node(i, q, k, vv, mask, head_dim, fill, crs->out[0]);
+      if (kcat) {
+        fa.op = "FusedAttentionPast";
+        fa.name = "FusedAttentionPast_" + std::to_string(i);
+        fa.in = {q, k, vv, past_k, past_v, mask};
+        fa.out = {crs->out[0], kcat->out[0], vcat->out[0]};
+      }
+      slot.push_back(std::move(fa));
       break;
     }
   }
   int found = 0;
   for (const auto& kv : inserts)
-    for (const auto& n : kv.second) found += n.op == "FusedAttention";
+    for (const auto& n : kv.second) found += n.op == "FusedAttention" || n.op == "FusedAttentionPast";
   if (found) rebuild(g, removed, inserts);
   return found;
 }

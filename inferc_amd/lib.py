@@ -112,6 +112,9 @@ _SIGS = {
     "inferc_executor_get_output": [vp, C.c_char_p, vp, sz],
     "inferc_executor_set_graph_mode": [vp, i32],
     "inferc_executor_run_profiled": [vp, vp],
+    "inferc_executor_bind_kv_cache": [vp, i64],
+    "inferc_executor_set_input_shape": [vp, C.c_char_p, i32, i32, P(i64)],
+    "inferc_executor_output_argmax": [vp, C.c_char_p, P(i64)],
     "inferc_profiler_create": [P(vp)],
     "inferc_profiler_destroy": [vp],
     "inferc_profiler_begin_iteration": [vp],

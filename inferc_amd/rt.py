@@ -779,6 +779,24 @@ class Executor:
         self.run_async()
         return {o: self.output(o) for o in outputs}
 
+    def bind_kv_cache(self, max_t: int) -> None:
+        """Keeps the K/V of every FusedAttentionPast node in a device cache of
+        max_t positions (0 unbinds); see inferc_executor_bind_kv_cache."""
+        check(self.ctx._lib.inferc_executor_bind_kv_cache(self.handle, max_t))
+
+    def set_input_shape(self, name: str, dtype, shape: Sequence[int]) -> None:
+        """An input that carries only its shape (a past the KV cache holds)."""
+        check(self.ctx._lib.inferc_executor_set_input_shape(
+            self.handle, name.encode(), _NP2DT[np.dtype(dtype)], len(shape),
+            _i64_array(list(shape))))
+
+    def output_argmax(self, name: str) -> int:
+        """Index of the first maximum of the output's last row, on the device."""
+        idx = C.c_int64()
+        check(self.ctx._lib.inferc_executor_output_argmax(self.handle, name.encode(),
+                                                          C.byref(idx)))
+        return idx.value
+
     def run_profiled(self, profiler) -> None:
         """Executor::Run(inputs, profiler) (src/runtime/executor.cc:98-125,
         349-354): one eager pass recorded as one profiler iteration, each
@@ -816,6 +834,57 @@ class Executor:
 
 
 # -------------------------------------------------------------------- GPT-2
+
+class OnnxDecoder:
+    """Greedy decode over an exported GPT-2 with-past graph (`inferc decode`,
+    src/cli/main.cpp:700-936) with the KV cache on the device.
+
+    The reference runs two graphs and, between steps, renames every
+    present.* output to the next step's past_key_values.* input (main.cpp:
+    831-836, 883-888), so each step copies the whole cache through the host.
+    Here the pass pipeline turns each layer's attention into a
+    FusedAttentionPast node, the executor keeps its K/V in a device cache
+    (bind_kv_cache), and each step passes the past inputs by shape only: the
+    prompt is the first step (past length 0), then one token per step.
+    Argmax (first maximum, main.cpp:875-879) runs on the device."""
+
+    def __init__(self, ctx: Context, with_past, max_t: int, optimize: bool = True):
+        self.graph = with_past if isinstance(with_past, Graph) else Graph.from_onnx(with_past)
+        self.counts = self.graph.optimize() if optimize else None
+        d = self.graph.to_dict()
+        self.past = [i for i in d["inputs"] if i["name"].startswith("past_key_values.")]
+        if not self.past:
+            raise HipError(L.ERR_ARG, "graph has no past_key_values.* inputs")
+        for i in self.past:
+            if len(i["shape"]) != 4 or i["shape"][1] <= 0 or i["shape"][3] <= 0:
+                raise HipError(L.ERR_SHAPE, f"{i['name']}: expected [batch, heads, past, head_dim]")
+        self.max_t = max_t
+        self.ex = Executor(ctx, self.graph)
+        self.ex.bind_kv_cache(max_t)
+
+    def _step(self, ids: np.ndarray, total: int) -> int:
+        self.ex.set_input("input_ids", ids)
+        self.ex.set_input("attention_mask", np.ones((1, total), np.int64))
+        past = total - ids.shape[1]
+        for i in self.past:
+            self.ex.set_input_shape(i["name"], np.float32,
+                                    [1, i["shape"][1], past, i["shape"][3]])
+        self.ex.run_async()
+        return self.ex.output_argmax("logits")
+
+    def generate(self, prompt: np.ndarray, max_tokens: int) -> np.ndarray:
+        p = np.asarray(prompt, np.int64).reshape(1, -1)
+        n = p.shape[1]
+        if n + max_tokens - 1 > self.max_t:
+            raise HipError(L.ERR_SHAPE, "prompt + generated tokens exceed the KV cache (max_t)")
+        toks = [self._step(p, n)]
+        for k in range(1, max_tokens):
+            toks.append(self._step(np.array([[toks[-1]]], np.int64), n + k))
+        return np.array(toks, np.int64)
+
+    def logits(self) -> np.ndarray:
+        return self.ex.output("logits")
+
 
 class Gpt2Config(C.Structure):
     _fields_ = [("layers", C.c_int64), ("hidden", C.c_int64), ("heads", C.c_int64),

@@ -12,6 +12,13 @@ tests:
       attention, no KV cache, inputs input_ids + attention_mask as the
       reference's GPT-2 decoder model takes them, dynamic batch/sequence; the
       npz holds token ids, masks and torch's float32 logits.
+  gpt2_tiny_past.onnx + gpt2_tiny_past_io.npz
+      The same GPT-2 as a with-past decoder: inputs input_ids, attention_mask
+      and past_key_values.{i}.key/value [batch, heads, past, head_dim];
+      outputs logits and present.{i}.key/value. The npz holds one step over a
+      7-token prompt's cache (past tensors, step logits and presents) and
+      torch's greedy generation of 12 tokens from that prompt with its KV
+      cache (first-maximum argmax) and the last step's logits.
 
 Every parameter is drawn at random (biases and LayerNorm weights included),
 so the exporter's deduplication of equal initializers does not fire.
@@ -115,6 +122,78 @@ def gpt2() -> None:
         lb = w(torch.from_numpy(ids2), torch.from_numpy(mask2)).numpy()
     np.savez(OUT / "gpt2_tiny_io.npz", ids_a=ids, mask_a=mask, logits_a=la, ids_b=ids2,
              mask_b=mask2, logits_b=lb)
+    gpt2_past(m, cfg)
+
+
+def gpt2_past(m, cfg) -> None:
+    from transformers.cache_utils import DynamicCache
+
+    L = cfg.n_layer
+
+    class Past(torch.nn.Module):
+        def __init__(self, inner):
+            super().__init__()
+            self.inner = inner
+
+        def forward(self, input_ids, attention_mask, *past):
+            cache = DynamicCache()
+            for i in range(L):
+                cache.update(past[2 * i], past[2 * i + 1], i)
+            out = self.inner(input_ids=input_ids, attention_mask=attention_mask,
+                             past_key_values=cache, use_cache=True)
+            pres = []
+            for i in range(L):
+                pres += [out.past_key_values.layers[i].keys, out.past_key_values.layers[i].values]
+            return (out.logits, *pres)
+
+    w = Past(m).eval()
+    nh, dh = cfg.n_head, cfg.n_embd // cfg.n_head
+    names_in = ["input_ids", "attention_mask"] + [
+        f"past_key_values.{i}.{kv}" for i in range(L) for kv in ("key", "value")]
+    names_out = ["logits"] + [f"present.{i}.{kv}" for i in range(L) for kv in ("key", "value")]
+    dyn = {"input_ids": {0: "batch", 1: "sequence"},
+           "attention_mask": {0: "batch", 1: "total_sequence"}, "logits": {0: "batch", 1: "sequence"}}
+    for nm in names_in[2:]:
+        dyn[nm] = {0: "batch", 2: "past_sequence"}
+    for nm in names_out[1:]:
+        dyn[nm] = {0: "batch", 2: "total_sequence"}
+    ex_ids = torch.tensor([[5]], dtype=torch.int64)
+    ex_mask = torch.ones(1, 4, dtype=torch.int64)
+    ex_past = [torch.zeros(1, nh, 3, dh) for _ in range(2 * L)]
+    data = _export(w, (ex_ids, ex_mask, *ex_past), names_in, names_out, dyn)
+    (OUT / "gpt2_tiny_past.onnx").write_bytes(data)
+
+    rng = np.random.default_rng(7)
+    prompt = rng.integers(0, cfg.vocab_size, (1, 7)).astype(np.int64)
+    out = {}
+    with torch.no_grad():
+        # one step over the prompt's cache
+        r = m(input_ids=torch.from_numpy(prompt), use_cache=True)
+        past = []
+        for i in range(L):
+            past += [r.past_key_values.layers[i].keys.clone(),
+                     r.past_key_values.layers[i].values.clone()]
+        step = np.array([[int(rng.integers(0, cfg.vocab_size))]], np.int64)
+        res = w(torch.from_numpy(step), torch.ones(1, 8, dtype=torch.int64), *past)
+        out["step_ids"] = step
+        for k in range(2 * L):
+            out[f"past_{k}"] = past[k].numpy()
+            out[f"present_{k}"] = res[1 + k].numpy()
+        out["step_logits"] = res[0].numpy()
+        # greedy generation with the KV cache
+        toks = []
+        r = m(input_ids=torch.from_numpy(prompt), use_cache=True)
+        cache = r.past_key_values
+        nxt = int(np.argmax(r.logits[0, -1].numpy()))
+        toks.append(nxt)
+        for _ in range(11):
+            r = m(input_ids=torch.tensor([[nxt]]), past_key_values=cache, use_cache=True)
+            cache = r.past_key_values
+            nxt = int(np.argmax(r.logits[0, -1].numpy()))
+            toks.append(nxt)
+        out["gen_tokens"] = np.array(toks, np.int64)
+        out["gen_last_logits"] = r.logits[0, -1].numpy()
+    np.savez(OUT / "gpt2_tiny_past_io.npz", prompt=prompt, **out)
 
 
 if __name__ == "__main__":

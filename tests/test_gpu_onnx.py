@@ -47,3 +47,59 @@ def test_exported_distilbert(ctx, optimize):
 @pytest.mark.parametrize("optimize", [False, True])
 def test_exported_gpt2(ctx, optimize):
     _run_model(ctx, "gpt2_tiny", optimize, ["a", "b"])
+
+
+def _past_feeds(io):
+    feeds = {"input_ids": io["step_ids"], "attention_mask": np.ones((1, 8), np.int64)}
+    for k in range(4):
+        feeds[f"past_key_values.{k // 2}.{'key' if k % 2 == 0 else 'value'}"] = io[f"past_{k}"]
+    return feeds
+
+
+@pytest.mark.parametrize("optimize,bound", [(False, False), (True, False), (True, True)])
+def test_exported_gpt2_with_past_step(ctx, optimize, bound):
+    """One decode step of the with-past graph over torch's 7-token cache:
+    logits and present.* against torch (1e-4). Bound to a KV cache (which
+    holds the FusedAttentionPast nodes the passes make) the past data seeds
+    the cache and present.* are read back through the cache."""
+    io = np.load(GOLDEN / "gpt2_tiny_past_io.npz")
+    g = rt.Graph.from_onnx(GOLDEN / "gpt2_tiny_past.onnx")
+    if optimize:
+        assert g.optimize()["recognize_attention_additive"] == 2
+    ex = rt.Executor(ctx, g)
+    if bound:
+        ex.bind_kv_cache(32)
+    outs = ["logits"] + [f"present.{k // 2}.{'key' if k % 2 == 0 else 'value'}" for k in range(4)]
+    got = ex.run(_past_feeds(io), outs)
+    err = float(np.max(np.abs(got["logits"] - io["step_logits"])))
+    print(f"with-past step optimize={optimize} bound={bound}: max|dlogit| {err:.3e}")
+    assert err <= 1e-4
+    for k in range(4):
+        ref = io[f"present_{k}"]
+        assert got[outs[1 + k]].shape == ref.shape
+        np.testing.assert_allclose(got[outs[1 + k]], ref, atol=1e-4)
+
+
+def test_onnx_decoder_greedy_tokens_match_torch(ctx):
+    """`inferc decode` over the exported with-past graph with the device KV
+    cache: the 12 greedy tokens equal torch's generation with its own cache
+    (bit-exact), the last step's logits within 1e-4."""
+    io = np.load(GOLDEN / "gpt2_tiny_past_io.npz")
+    dec = rt.OnnxDecoder(ctx, GOLDEN / "gpt2_tiny_past.onnx", max_t=32)
+    toks = dec.generate(io["prompt"], 12)
+    np.testing.assert_array_equal(toks, io["gen_tokens"])
+    err = float(np.max(np.abs(dec.logits()[0, -1] - io["gen_last_logits"])))
+    print(f"onnx decode: tokens {toks.tolist()}; last max|dlogit| {err:.3e}")
+    assert err <= 1e-4
+    # a second generation restarts at past length 0 and repeats itself
+    np.testing.assert_array_equal(dec.generate(io["prompt"], 12), toks)
+    with pytest.raises(RuntimeError, match="exceed the KV cache"):
+        dec.generate(io["prompt"], 40)
+    # a shape-only past longer than what the cache holds is refused
+    ex = dec.ex
+    ex.set_input("input_ids", np.array([[1]], np.int64))
+    ex.set_input("attention_mask", np.ones((1, 30), np.int64))
+    for i in dec.past:
+        ex.set_input_shape(i["name"], np.float32, [1, 4, 29, 16])
+    with pytest.raises(RuntimeError, match="KV cache holds"):
+        ex.run_async()
