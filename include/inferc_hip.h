@@ -379,6 +379,12 @@ int inferc_executor_bind_kv_cache(inferc_executor* ex, int64_t max_t);
  * A node that needs its data fails with INFERC_ERR_STATE. */
 int inferc_executor_set_input_shape(inferc_executor* ex, const char* name,
                                     int dtype, int rank, const int64_t* shape);
+/* Device address of an output computed on the device (valid until the next
+ * run of this executor), e.g. to hand a prefill's present.* to a with-past
+ * executor through inferc_executor_set_input_device without a host copy.
+ * No counterpart in the reference, whose tensors live on the host. */
+int inferc_executor_output_device(inferc_executor* ex, const char* name,
+                                  const void** ptr);
 /* Index of the first maximum of the last row (last dim) of a float32
  * output, computed on the device: the greedy token of `inferc decode`
  * (main.cpp:875-879). Synchronises the stream. */

@@ -1091,12 +1091,19 @@ void inferc_executor::exec_attention_past(const inferc_graph::Node& n) {
              "FusedAttentionPast: q must be float32 [B,S,H]");
   IH_REQUIRE(get(n.in[1]).shape == q.shape && get(n.in[2]).shape == q.shape, INFERC_ERR_SHAPE,
              "FusedAttentionPast: q/k/v shapes differ");
-  const Value pk = get(n.in[3]);
-  const Value pv = get(n.in[4]);
   const int64_t B = q.shape[0], S = q.shape[1], H = q.shape[2];
   const int64_t dh = attr_int(n, "head_dim", 64);
   IH_REQUIRE(dh > 0 && H % dh == 0, INFERC_ERR_SHAPE, "FusedAttentionPast: H % head_dim != 0");
   const int64_t nH = H / dh;
+  const bool has_past = !n.in[3].empty() && !n.in[4].empty();
+  Value pk, pv;
+  if (has_past) {
+    pk = get(n.in[3]);
+    pv = get(n.in[4]);
+  } else {
+    pk.dtype = pv.dtype = INFERC_DT_F32;
+    pk.shape = pv.shape = {B, nH, 0, dh};
+  }
   IH_REQUIRE(pk.shape.size() == 4 && pk.shape[0] == B && pk.shape[1] == nH && pk.shape[3] == dh &&
                  pv.shape == pk.shape,
              INFERC_ERR_SHAPE, "FusedAttentionPast: past must be [B, nH, P, head_dim]");
@@ -1955,6 +1962,17 @@ int inferc_executor_set_input_shape(inferc_executor* ex, const char* name, int d
     in.v.shape = read_shape(rank, shape);
     in.v.dev = nullptr;
     in.v.host.reset();
+  });
+}
+
+int inferc_executor_output_device(inferc_executor* ex, const char* name, const void** ptr) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(name != nullptr && ptr != nullptr, INFERC_ERR_ARG, "null argument");
+    const ih::Value& v = ex->get(name);
+    IH_REQUIRE(v.dev != nullptr, INFERC_ERR_STATE,
+               std::string("output '") + name + "' has no contiguous device buffer");
+    *ptr = v.dev;
   });
 }
 

@@ -597,9 +597,10 @@ int recognize_attention(inferc_graph& g) {
 //
 // With a KV cache in the graph (GPT-2's with-past decoder: K = Transpose
 // (0,1,3,2) of Concat(past_k, head split of k, axis 2), V = Concat(past_v,
-// head split of v, axis 2), the Concats being the present.* outputs) the
+// head split of v, axis 2), the Concats being the present.* outputs; or the
+// prefill decoder, whose present.* are the head splits themselves) the
 // block becomes FusedAttentionPast(q, k, v, past_k, past_v, mask) with
-// outputs (ctx, present_k, present_v).
+// outputs (ctx, present_k, present_v), past_* "" when there is none.
 int recognize_attention_additive(inferc_graph& g) {
   View v(g);
   std::set<int> removed;
@@ -607,38 +608,44 @@ int recognize_attention_additive(inferc_graph& g) {
   std::map<std::string, std::string> negated;  // cond -> its Not output
   const std::vector<int64_t> split = {0, 2, 1, 3}, split_t = {0, 2, 3, 1}, last2 = {0, 1, 3, 2};
   auto concat_axis2 = [&](const Node* c) {
-    if (!c || c->in.size() != 2) return false;
+    if (!c || c->in.empty() || c->in.size() > 2) return false;
     auto it = c->attrs.find("axis");
     if (it == c->attrs.end()) return false;
     const int64_t a = std::stoll(it->second);
     return a == 2 || a == -2;
   };
-  // K operand of the scores MatMul -> (k projection, past_k or "", Concat)
+  // The per-head K/V "present" tensor [B, nH, T, dh]: Concat(past, head
+  // split of x, axis 2), or the head split of x alone. Returns x, the past
+  // ("" without one) and the present's name.
+  auto present_src = [&](const std::string& t, std::set<int>* rm, std::string* x,
+                         std::string* past) {
+    const Node* c = v.producer_op(t, "Concat");
+    if (concat_axis2(c)) {  // Concat(past, new), or a one-input Concat(new)
+      *x = proj_behind(v, c->in.back(), rm, &split);
+      if (x->empty()) return false;
+      if (c->in.size() == 2) *past = c->in[0];
+      else past->clear();
+      rm->insert(v.index_of(c));
+      return true;
+    }
+    *x = proj_behind(v, t, rm, &split);
+    past->clear();
+    return !x->empty();
+  };
+  // K operand of the scores MatMul: the head split transposed for the
+  // product (0,2,3,1), or a present tensor transposed (0,1,3,2). `present`
+  // gets the present's name in the second case.
   auto key_src = [&](const std::string& t, std::set<int>* rm, std::string* x, std::string* past,
-                     const Node** cat) {
+                     std::string* present) {
+    present->clear();
+    past->clear();
     *x = proj_behind(v, t, rm, &split_t);
     if (!x->empty()) return true;
     const Node* tr = v.producer_op(t, "Transpose");
     if (!tr || tr->in.empty() || ints_attr(*tr, "perm") != last2) return false;
-    const Node* c = v.producer_op(tr->in[0], "Concat");
-    if (!concat_axis2(c)) return false;
-    *x = proj_behind(v, c->in[1], rm, &split);
-    if (x->empty()) return false;
+    if (!present_src(tr->in[0], rm, x, past)) return false;
     rm->insert(v.index_of(tr));
-    *past = c->in[0];
-    *cat = c;
-    return true;
-  };
-  auto value_src = [&](const std::string& t, std::set<int>* rm, std::string* x, std::string* past,
-                       const Node** cat) {
-    *x = proj_behind(v, t, rm, &split);
-    if (!x->empty()) return true;
-    const Node* c = v.producer_op(t, "Concat");
-    if (!concat_axis2(c)) return false;
-    *x = proj_behind(v, c->in[1], rm, &split);
-    if (x->empty()) return false;
-    *past = c->in[0];
-    *cat = c;
+    *present = tr->in[0];
     return true;
   };
   for (int i = 0; i < int(g.nodes.size()); ++i) {
@@ -680,9 +687,8 @@ int recognize_attention_additive(inferc_graph& g) {
       std::string cond = where->in[0];
       if (const Node* ex = v.producer_op(cond, "Expand")) cond = ex->in[0];
       const std::string q = proj_behind(v, smm->in[0], &rm, &split);
-      std::string k, past_k, vv, past_v;
-      const Node *kcat = nullptr, *vcat = nullptr;
-      if (q.empty() || !key_src(smm->in[1], &rm, &k, &past_k, &kcat)) break;
+      std::string k, past_k, vv, past_v, present_k, present_v;
+      if (q.empty() || !key_src(smm->in[1], &rm, &k, &past_k, &present_k)) break;
       const Node* cmm = v.unique_consumer(sm.out[0]);
       const Node* cst = nullptr;
       if (cmm && cmm->op == "Cast" && cmm->attrs.count("to") &&
@@ -692,8 +698,15 @@ int recognize_attention_additive(inferc_graph& g) {
       }
       const std::string probs = cst ? cst->out[0] : sm.out[0];
       if (!cmm || cmm->op != "MatMul" || cmm->in.size() != 2 || cmm->in[0] != probs) break;
-      if (!value_src(cmm->in[1], &rm, &vv, &past_v, &vcat)) break;
-      if ((kcat == nullptr) != (vcat == nullptr)) break;  // both cached or neither
+      if (present_k.empty()) {
+        vv = proj_behind(v, cmm->in[1], &rm, &split);
+        if (vv.empty()) break;
+      } else {
+        // with K as a present tensor, V is one too, with or without a past
+        if (!present_src(cmm->in[1], &rm, &vv, &past_v)) break;
+        present_v = cmm->in[1];
+        if (past_k.empty() != past_v.empty()) break;
+      }
       const Node* ctr = v.unique_consumer(cmm->out[0]);
       if (!ctr || ctr->op != "Transpose" || ints_attr(*ctr, "perm") != split) break;
       // the merged context feeds one Reshape, plus Shape nodes that compute
@@ -711,10 +724,6 @@ int recognize_attention_additive(inferc_graph& g) {
       if (!crs || other || crs->out.empty()) break;
       for (const Node* n : {smm, scale, add, &sm, cst, cmm, ctr, crs}) rm.insert(v.index_of(n));
       if (v.unique_consumer(cc->out[0]) == scale) rm.insert(v.index_of(cc));
-      if (kcat) {
-        rm.insert(v.index_of(kcat));
-        rm.insert(v.index_of(vcat));
-      }
       rm.insert(shape_readers.begin(), shape_readers.end());
       rm.erase(-1);
       // nodes whose every output is read only by removed nodes go too (the
@@ -747,9 +756,9 @@ int recognize_attention_additive(inferc_graph& g) {
       // nothing kept may read a removed node's output, except the tensors the
       // fused node itself produces
       std::set<std::string> produced = {crs->out[0]};
-      if (kcat) {
-        produced.insert(kcat->out[0]);
-        produced.insert(vcat->out[0]);
+      if (!present_k.empty()) {
+        produced.insert(present_k);
+        produced.insert(present_v);
       }
       std::set<std::string> gone;
       for (int j : rm)
@@ -779,11 +788,11 @@ int recognize_attention_additive(inferc_graph& g) {
       }
       removed.insert(rm.begin(), rm.end());
       Node fa = attention_node(i, q, k, vv, mask, head_dim, fill, crs->out[0]);
-      if (kcat) {
+      if (!present_k.empty()) {
         fa.op = "FusedAttentionPast";
         fa.name = "FusedAttentionPast_" + std::to_string(i);
         fa.in = {q, k, vv, past_k, past_v, mask};
-        fa.out = {crs->out[0], kcat->out[0], vcat->out[0]};
+        fa.out = {crs->out[0], present_k, present_v};
       }
       slot.push_back(std::move(fa));
       break;

@@ -115,6 +115,7 @@ _SIGS = {
     "inferc_executor_bind_kv_cache": [vp, i64],
     "inferc_executor_set_input_shape": [vp, C.c_char_p, i32, i32, P(i64)],
     "inferc_executor_output_argmax": [vp, C.c_char_p, P(i64)],
+    "inferc_executor_output_device": [vp, C.c_char_p, P(vp)],
     "inferc_profiler_create": [P(vp)],
     "inferc_profiler_destroy": [vp],
     "inferc_profiler_begin_iteration": [vp],

@@ -790,6 +790,14 @@ class Executor:
             self.handle, name.encode(), _NP2DT[np.dtype(dtype)], len(shape),
             _i64_array(list(shape))))
 
+    def output_device(self, name: str) -> "Tensor":
+        """A borrowed device view of an output (valid until the next run)."""
+        shape, dt = self.output_shape(name)
+        p = C.c_void_p()
+        check(self.ctx._lib.inferc_executor_output_device(self.handle, name.encode(),
+                                                          C.byref(p)))
+        return Tensor(self.ctx, shape, dt, ptr=p.value, owned=False)
+
     def output_argmax(self, name: str) -> int:
         """Index of the first maximum of the output's last row, on the device."""
         idx = C.c_int64()
@@ -848,9 +856,15 @@ class OnnxDecoder:
     prompt is the first step (past length 0), then one token per step.
     Argmax (first maximum, main.cpp:875-879) runs on the device."""
 
-    def __init__(self, ctx: Context, with_past, max_t: int, optimize: bool = True):
+    def __init__(self, ctx: Context, with_past, max_t: int, prefill=None, optimize: bool = True):
         self.graph = with_past if isinstance(with_past, Graph) else Graph.from_onnx(with_past)
         self.counts = self.graph.optimize() if optimize else None
+        self.prefill_ex = None
+        if prefill is not None:
+            pg = prefill if isinstance(prefill, Graph) else Graph.from_onnx(prefill)
+            if optimize:
+                pg.optimize()
+            self.prefill_ex = Executor(ctx, pg)
         d = self.graph.to_dict()
         self.past = [i for i in d["inputs"] if i["name"].startswith("past_key_values.")]
         if not self.past:
@@ -862,24 +876,47 @@ class OnnxDecoder:
         self.ex = Executor(ctx, self.graph)
         self.ex.bind_kv_cache(max_t)
 
-    def _step(self, ids: np.ndarray, total: int) -> int:
+    def _step(self, ids: np.ndarray, total: int, seed=None, profiler=None) -> int:
         self.ex.set_input("input_ids", ids)
         self.ex.set_input("attention_mask", np.ones((1, total), np.int64))
         past = total - ids.shape[1]
         for i in self.past:
-            self.ex.set_input_shape(i["name"], np.float32,
-                                    [1, i["shape"][1], past, i["shape"][3]])
-        self.ex.run_async()
+            if seed is not None:
+                self.ex.set_input_device(i["name"], seed[i["name"]])
+            else:
+                self.ex.set_input_shape(i["name"], np.float32,
+                                        [1, i["shape"][1], past, i["shape"][3]])
+        if profiler is not None:
+            self.ex.run_profiled(profiler)
+        else:
+            self.ex.run_async()
         return self.ex.output_argmax("logits")
 
-    def generate(self, prompt: np.ndarray, max_tokens: int) -> np.ndarray:
+    def generate(self, prompt: np.ndarray, max_tokens: int, profiler=None) -> np.ndarray:
+        """Greedy tokens. With a prefill graph the prompt runs there
+        (main.cpp:786-828) and its present.* seed the cache on the first
+        step, device to device; without one the prompt is the with-past
+        graph's first step. `profiler` records each post-prompt step as one
+        iteration (main.cpp:846-872)."""
         p = np.asarray(prompt, np.int64).reshape(1, -1)
         n = p.shape[1]
         if n + max_tokens - 1 > self.max_t:
             raise HipError(L.ERR_SHAPE, "prompt + generated tokens exceed the KV cache (max_t)")
-        toks = [self._step(p, n)]
+        seed = None
+        if self.prefill_ex is not None:
+            pe = self.prefill_ex
+            pe.set_input("input_ids", p)
+            pe.set_input("attention_mask", np.ones((1, n), np.int64))
+            pe.run_async()
+            toks = [pe.output_argmax("logits")]
+            seed = {i["name"]: pe.output_device(i["name"].replace("past_key_values.", "present."))
+                    for i in self.past}
+        else:
+            toks = [self._step(p, n)]
         for k in range(1, max_tokens):
-            toks.append(self._step(np.array([[toks[-1]]], np.int64), n + k))
+            toks.append(self._step(np.array([[toks[-1]]], np.int64), n + k, seed=seed,
+                                   profiler=profiler))
+            seed = None
         return np.array(toks, np.int64)
 
     def logits(self) -> np.ndarray:

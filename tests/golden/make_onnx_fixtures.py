@@ -19,6 +19,10 @@ tests:
       7-token prompt's cache (past tensors, step logits and presents) and
       torch's greedy generation of 12 tokens from that prompt with its KV
       cache (first-maximum argmax) and the last step's logits.
+  gpt2_tiny_prefill.onnx
+      The same GPT-2 as the reference's prefill decoder model: inputs
+      input_ids and attention_mask, outputs logits and present.{i}.key/value
+      (the first graph of `inferc decode --model`).
 
 Every parameter is drawn at random (biases and LayerNorm weights included),
 so the exporter's deduplication of equal initializers does not fire.
@@ -162,6 +166,26 @@ def gpt2_past(m, cfg) -> None:
     ex_past = [torch.zeros(1, nh, 3, dh) for _ in range(2 * L)]
     data = _export(w, (ex_ids, ex_mask, *ex_past), names_in, names_out, dyn)
     (OUT / "gpt2_tiny_past.onnx").write_bytes(data)
+
+    class Prefill(torch.nn.Module):
+        def __init__(self, inner):
+            super().__init__()
+            self.inner = inner
+
+        def forward(self, input_ids, attention_mask):
+            out = self.inner(input_ids=input_ids, attention_mask=attention_mask, use_cache=True)
+            pres = []
+            for i in range(L):
+                pres += [out.past_key_values.layers[i].keys, out.past_key_values.layers[i].values]
+            return (out.logits, *pres)
+
+    dyn_p = {"input_ids": {0: "batch", 1: "sequence"}, "attention_mask": {0: "batch", 1: "sequence"},
+             "logits": {0: "batch", 1: "sequence"}}
+    for nm in names_out[1:]:
+        dyn_p[nm] = {0: "batch", 2: "sequence"}
+    data = _export(Prefill(m).eval(), (torch.tensor([[1, 2, 3]]), torch.ones(1, 3, dtype=torch.int64)),
+                   ["input_ids", "attention_mask"], names_out, dyn_p)
+    (OUT / "gpt2_tiny_prefill.onnx").write_bytes(data)
 
     rng = np.random.default_rng(7)
     prompt = rng.integers(0, cfg.vocab_size, (1, 7)).astype(np.int64)
