@@ -194,6 +194,19 @@ __device__ __forceinline__ float wave_max(float v) {
 // ctx->stream and throw ih::Error on bad arguments).
 namespace ih {
 
+// LayerNorm of a GEMM operand's rows, applied as the operand is read:
+// x' = (x - mean) * rstd * gamma + beta over the row's D features, with mean
+// and rstd combined from per-16-column partials [rows][D/16][2] = (mean, M2
+// = sum of squared deviations) that the GEMM producing the rows wrote
+// (GemmArgs::stats_out). Only the small-M GEMM path reads rows this way,
+// for D <= 1024.
+struct RowNorm {
+  const float* stats = nullptr;
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  float eps = 1e-5f;
+};
+
 struct GemmArgs {
   int trans_a = 0, trans_b = 0;
   int64_t M = 0, N = 0, K = 0;
@@ -212,14 +225,26 @@ struct GemmArgs {
   int64_t ldy = 0;
   // batching: blockIdx.z selects slice b; strides in elements (0 broadcasts)
   int64_t batch = 1, stride_a = 0, stride_b = 0, stride_y = 0, stride_r = 0;
+  // small-M path only: A's rows (over K) and R's rows (over N) normalized
+  // as read, and Y's per-16-column (mean, M2) written to stats_out
+  // [M][N/16][2] for a later GEMM that reads Y through a RowNorm
+  RowNorm norm_a, norm_r;
+  float* stats_out = nullptr;
 };
 
 void gemm(inferc_hip_ctx* ctx, const GemmArgs& a);
 
-// Three projections that share X in one launch: Y_i = X*W_i + b_i.
+// Three projections that share X in one launch: Y_i = X*W_i + b_i (X's rows
+// normalized as read when norm_a is given).
 void gemm_qkv(inferc_hip_ctx* ctx, int64_t M, int64_t K, int64_t N, const float* X,
               const float* const w[3], const float* const b[3], float* const y[3],
-              int64_t ldy);
+              int64_t ldy, const RowNorm* norm_a = nullptr);
+
+// Whether an unbatched, untransposed product with 16-byte aligned operands
+// (M x K times K x N, `slices` such products sharing A) takes the small-M
+// path, the one that supports RowNorm operands and stats_out.
+bool gemm_small_m_path(const inferc_hip_ctx* ctx, int64_t M, int64_t N, int64_t K,
+                       int64_t slices);
 
 struct AttnArgs {
   int64_t B = 0, S = 0, H = 0, head_dim = 0;

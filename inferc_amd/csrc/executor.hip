@@ -133,6 +133,19 @@ struct inferc_executor {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   std::string graph_sig;
+  // A LayerNorm whose input h comes from a FusedGemmEpilogue and whose
+  // readers are all GEMM operands (A of FusedQKV / FusedMatMulAddGELU, the
+  // residual of a FusedGemmEpilogue): peephole lists the readers by h, and
+  // each run decides at the producer whether they read h through the
+  // LayerNorm (the small-M GEMM path for every product involved) instead of
+  // the LayerNorm kernel writing its output.
+  struct LnRead {
+    std::string gamma, beta;
+    float eps = 1e-5f;
+    std::vector<std::pair<size_t, char>> readers;  // node index, 'a' (A) or 'r' (R)
+  };
+  std::unordered_map<std::string, LnRead> ln_reads;  // by h
+  std::unordered_map<std::string, bool> ln_on;       // this run, by h
   uint64_t graph_ws_gen = 0;
   std::vector<hipEvent_t> prof_ev;  // one per node boundary of a profiled pass
   // Device KV caches of FusedAttentionPast nodes (bind_kv_cache): per node,
@@ -305,6 +318,8 @@ struct inferc_executor {
 
   void peephole();
   void exec_node(const inferc_graph::Node& n);
+  bool ln_read_ok(const std::string& h, int64_t M, int64_t N, int64_t K);
+  bool ln_read_of(const inferc_graph::Node& n, char role, std::string* h, ih::RowNorm* rn);
   void generic_binary(const inferc_graph::Node& n, int ewop);
   void exec_attention_past(const inferc_graph::Node& n);
   bool exec_generic(const inferc_graph::Node& n);
@@ -474,6 +489,90 @@ void inferc_executor::peephole() {
     }
     nodes = std::move(live);
   }
+  // LayerNorms that their readers can apply as they read (final node
+  // order, so the reader indices stay valid)
+  ln_reads.clear();
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    const inferc_graph::Node& ln = nodes[i];
+    if (ln.op != "FusedLayerNorm" || ln.in.size() != 3 || ln.out.size() != 1) continue;
+    const std::string& h = ln.in[0];
+    const std::string& x = ln.out[0];
+    if (!inits.count(ln.in[1]) || !inits.count(ln.in[2]) || inits.count(h) ||
+        std::find(outputs.begin(), outputs.end(), x) != outputs.end())
+      continue;
+    int pi = -1;
+    for (size_t j = 0; j < i; ++j)
+      if (std::find(nodes[j].out.begin(), nodes[j].out.end(), h) != nodes[j].out.end())
+        pi = int(j);
+    if (pi < 0 || nodes[size_t(pi)].op != "FusedGemmEpilogue") continue;
+    LnRead lr;
+    lr.gamma = ln.in[1];
+    lr.beta = ln.in[2];
+    lr.eps = ih::attr_float(ln, "epsilon", 1e-5f);
+    bool ok = true;
+    for (size_t j = i + 1; j < nodes.size() && ok; ++j) {
+      const inferc_graph::Node& c = nodes[j];
+      for (size_t k = 0; k < c.in.size(); ++k) {
+        if (c.in[k] != x) continue;
+        const bool a = k == 0 && (c.op == "FusedQKV" || c.op == "FusedMatMulAddGELU");
+        const bool r = k == 3 && c.op == "FusedGemmEpilogue";
+        if (!(a || r) || !inits.count(c.in[1])) ok = false;
+        else lr.readers.emplace_back(j, a ? 'a' : 'r');
+      }
+    }
+    if (ok && !lr.readers.empty()) ln_reads[h] = std::move(lr);
+  }
+}
+
+// Whether this run's readers of h apply its LayerNorm as they read (decided
+// at h's producer, which then writes h's row statistics): every product
+// involved takes the small-M GEMM path, and the operands are 16-byte aligned.
+bool inferc_executor::ln_read_ok(const std::string& h, int64_t M, int64_t N, int64_t K) {
+  auto it = ln_reads.find(h);
+  if (it == ln_reads.end() || dry || N % 16 != 0 || N > 1024) return false;
+  if (!ih::gemm_small_m_path(ctx, M, N, K, 1)) return false;
+  const LnRead& lr = it->second;
+  auto aligned = [&](const std::string& t) {
+    return (reinterpret_cast<uintptr_t>(inits.at(t).dev) & 15) == 0;
+  };
+  if (inits.at(lr.gamma).numel() != N || inits.at(lr.beta).numel() != N || !aligned(lr.gamma) ||
+      !aligned(lr.beta))
+    return false;
+  for (const auto& rd : lr.readers) {
+    const inferc_graph::Node& c = nodes[rd.first];
+    const ih::Value& w = inits.at(c.in[1]);
+    if (w.shape.size() != 2 || !aligned(c.in[1])) return false;
+    if (rd.second == 'a') {
+      const int64_t slices = c.op == "FusedQKV" ? 3 : 1;
+      if (w.shape[0] != N || !ih::gemm_small_m_path(ctx, M, w.shape[1], N, slices)) return false;
+    } else if (w.shape[1] != N || !ih::gemm_small_m_path(ctx, M, N, w.shape[0], 1)) {
+      return false;
+    }
+  }
+  return true;
+}
+
+// The LayerNorm a reader applies to operand `role` ('a' or 'r') of node n
+// this run, if any: the tensor h it reads instead of the LayerNorm output,
+// and the normalization.
+bool inferc_executor::ln_read_of(const inferc_graph::Node& n, char role, std::string* h,
+                                 ih::RowNorm* rn) {
+  const size_t k = role == 'a' ? 0 : 3;
+  if (n.in.size() <= k) return false;
+  for (const auto& kv : ln_reads) {
+    auto on = ln_on.find(kv.first);
+    if (on == ln_on.end() || !on->second) continue;
+    for (const auto& rd : kv.second.readers) {
+      if (rd.second != role || &nodes[rd.first] != &n) continue;
+      *h = kv.first;
+      rn->stats = static_cast<const float*>(arena.at("__lnstats:" + kv.first).p);
+      rn->gamma = static_cast<const float*>(dev_of(kv.second.gamma));
+      rn->beta = static_cast<const float*>(dev_of(kv.second.beta));
+      rn->eps = kv.second.eps;
+      return true;
+    }
+  }
+  return false;
 }
 
 void inferc_executor::exec_node(const inferc_graph::Node& n) {
@@ -490,7 +589,10 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
   IH_REQUIRE(!n.out.empty(), INFERC_ERR_ARG, op + ": node has no outputs");
 
   if (op == "FusedQKV") {
-    const Value x = in(0);
+    std::string ha;
+    RowNorm rna;
+    const bool lna = ln_read_of(n, 'a', &ha, &rna);
+    const Value x = lna ? get(ha) : in(0);
     require_f32(x, "X");
     const int64_t K = x.shape.back(), M = x.numel() / K;
     const Value wq = in(1);
@@ -512,7 +614,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       y[i] = static_cast<float*>(make_dev(n.out[size_t(i)], INFERC_DT_F32, os).dev);
     }
     if (!dry) {
-      gemm_qkv(ctx, M, K, N, static_cast<const float*>(dev_of(n.in[0])), w, b, y, N);
+      gemm_qkv(ctx, M, K, N, static_cast<const float*>(dev_of(lna ? ha : n.in[0])), w, b, y, N,
+               lna ? &rna : nullptr);
     }
     return;
   }
@@ -549,7 +652,11 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "FusedMatMulAddGELU" || op == "FusedGemmEpilogue" || op == "MatMul") {
-    const Value x = in(0);
+    std::string ha, hr;
+    RowNorm rna, rnr;
+    const bool lna = op != "MatMul" && ln_read_of(n, 'a', &ha, &rna);
+    const bool lnr = op == "FusedGemmEpilogue" && ln_read_of(n, 'r', &hr, &rnr);
+    const Value x = lna ? get(ha) : in(0);
     const Value w = in(1);
     require_f32(x, "A");
     require_f32(w, "B");
@@ -594,9 +701,10 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     os.back() = N;
     GemmArgs g;
     g.M = M; g.N = N; g.K = K;
-    g.A = static_cast<const float*>(dev_of(n.in[0])); g.lda = K;
+    g.A = static_cast<const float*>(dev_of(lna ? ha : n.in[0])); g.lda = K;
     g.B = static_cast<const float*>(dev_of(n.in[1])); g.ldb = N;
     g.ldy = N;
+    if (lna) g.norm_a = rna;
     if (op != "MatMul") {
       IH_REQUIRE(in(2).numel() == N, INFERC_ERR_SHAPE, op + ": bias size must equal N");
       g.beta = 1.0f;
@@ -605,13 +713,24 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     }
     if (op == "FusedMatMulAddGELU") g.act = INFERC_ACT_GELU_ERF;
     if (op == "FusedGemmEpilogue" && n.in.size() >= 4) {
-      const Value r = in(3);
+      const Value r = lnr ? get(hr) : in(3);
       IH_REQUIRE(r.numel() == M * N, INFERC_ERR_UNSUPPORTED,
                  "fused residual must match the product's shape");
-      g.R = static_cast<const float*>(dev_of(n.in[3]));
+      g.R = static_cast<const float*>(dev_of(lnr ? hr : n.in[3]));
       g.ldr = N;
+      if (lnr) g.norm_r = rnr;
     }
     g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
+    if (op == "FusedGemmEpilogue" && ln_reads.count(n.out[0])) {
+      // the producer of a LayerNorm read by its readers: decide for this
+      // run, and write the row statistics they combine
+      const bool on = ln_read_ok(n.out[0], M, N, K);
+      ln_on[n.out[0]] = on;
+      // (an arena buffer, not a tensor of the graph)
+      if (on)
+        g.stats_out = static_cast<float*>(
+            buf("__lnstats:" + n.out[0], size_t(M) * size_t(N / 16) * 2 * sizeof(float)));
+    }
     if (!dry) {
       gemm(ctx, g);
     }
@@ -661,6 +780,18 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "FusedLayerNorm") {
+    if (n.in.size() == 3) {
+      auto on = ln_on.find(n.in[0]);
+      if (on != ln_on.end() && on->second && ln_reads.count(n.in[0])) {
+        // its readers apply it: the output is a tensor of the tape at its
+        // logical size with no data (a non-reader asking for it fails)
+        ih::Value v;
+        v.dtype = INFERC_DT_F32;
+        v.shape = get(n.in[0]).shape;
+        vals[n.out[0]] = v;
+        return;
+      }
+    }
     // optional 4th input: the other operand of an Add folded in front
     // (y = LN(x + r), r repeated over leading dims as the Add broadcast it)
     size_t xi = 0, ri = 3;

@@ -57,11 +57,95 @@ struct GemmParams {
   int splits;
   int64_t k_per_split;
   float* partial;  // [slices][splits][M][N] when splits > 1
+  // small-M path: LayerNorm of A's rows (over K) and R's rows (over N) as
+  // read, from producer partials; Y's per-16-column (mean, M2) out
+  const float* na_stats;
+  const float* na_g;
+  const float* na_b;
+  float na_eps;
+  const float* nr_stats;
+  const float* nr_g;
+  const float* nr_b;
+  float nr_eps;
+  float* st_out;
 };
 
-__device__ __forceinline__ float epilogue(const GemmParams& p, const float* C,
-                                          const float* R, float acc,
-                                          int64_t row, int64_t col) {
+// Merges the (count, mean, M2) summary b into a (Chan et al.'s pairwise
+// update); an empty side leaves the other unchanged. The counts are small
+// integers, so a hardware reciprocal stands in for the divisions.
+__device__ __forceinline__ void merge_moments(float& na, float& ma, float& sa, float nb, float mb,
+                                              float sb) {
+  const float n = na + nb;
+  const float inv = n > 0.0f ? __builtin_amdgcn_rcpf(n) : 0.0f;
+  const float d = mb - ma;
+  ma = fmaf(d, nb * inv, ma);
+  sa = sa + sb + d * d * (na * nb * inv);
+  na = n;
+}
+
+// Value of the lane R places further on within its row of 16 lanes (DPP
+// row_ror).
+template <int R>
+__device__ __forceinline__ float row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + R, 0xF, 0xF, false));
+}
+
+// LayerNorm row statistics from per-16-column partials st[row][c] =
+// (mean_c, M2_c), c < nc <= 64 (D = 16 * nc <= 1024 features): a group of 16
+// lanes per row, lane l of the group holding columns l, l + 16, ... The
+// loads come first (row_stats_load), so the merge (row_stats_merge) can run
+// while later loads are still in flight.
+struct RowStatLoads {
+  float2 v[4];
+};
+
+// Unconditional loads from columns clamped into the row (nc >= 1); the
+// merge masks the columns past nc, so the wait for these loads counts them
+// exactly.
+__device__ __forceinline__ void row_stats_load(RowStatLoads& r, const float* __restrict__ st,
+                                               int64_t row, int64_t nc, int lane) {
+  const float2* p = reinterpret_cast<const float2*>(st) + row * nc;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t c = (lane & 15) + 16 * u;
+    r.v[u] = p[c < nc ? c : nc - 1];
+  }
+}
+
+// (mean, 1/sqrt(var + eps)) of the group's row: the lane's columns, then
+// rotations by 8, 4, 2 and 1 within the 16 lanes, after which every lane has
+// merged all 16 (in its own order; lane 0 of the group gives the row's
+// values). var = M2 / D, the biased variance LayerNorm uses.
+template <int R>
+__device__ __forceinline__ void merge_rotated(float& n, float& mean, float& m2) {
+  const float nb = row_ror<R>(n), mb = row_ror<R>(mean), sb = row_ror<R>(m2);
+  merge_moments(n, mean, m2, nb, mb, sb);
+}
+
+__device__ __forceinline__ float2 row_stats_merge(const RowStatLoads& r, int64_t nc, float eps,
+                                                  int lane) {
+  float n = 0.0f, mean = 0.0f, m2 = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const bool in = (lane & 15) + 16 * u < nc;
+    merge_moments(n, mean, m2, in ? 16.0f : 0.0f, r.v[u].x, in ? r.v[u].y : 0.0f);
+  }
+  merge_rotated<8>(n, mean, m2);
+  merge_rotated<4>(n, mean, m2);
+  merge_rotated<2>(n, mean, m2);
+  merge_rotated<1>(n, mean, m2);
+  return make_float2(mean, 1.0f / sqrtf(m2 / n + eps));  // as the LayerNorm kernel
+}
+
+// Workgroup barrier for LDS data only: unlike __syncthreads it does not make
+// the wave wait for its global loads still in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// alpha * acc + beta * C: the epilogue up to the residual
+__device__ __forceinline__ float epilogue_pre(const GemmParams& p, const float* C, float acc,
+                                              int64_t row, int64_t col) {
   float v = p.alpha * acc;
   if (C != nullptr && p.beta != 0.0f) {
     float c = 0.0f;
@@ -70,6 +154,13 @@ __device__ __forceinline__ float epilogue(const GemmParams& p, const float* C,
     else if (p.c_kind == INFERC_C_SCALAR) c = C[0];
     v = v + p.beta * c;
   }
+  return v;
+}
+
+__device__ __forceinline__ float epilogue(const GemmParams& p, const float* C,
+                                          const float* R, float acc,
+                                          int64_t row, int64_t col) {
+  float v = epilogue_pre(p, C, acc, row, col);
   if (R != nullptr) v = v + R[row * p.ldr + col];
   return apply_act(v, p.act);
 }
@@ -278,11 +369,12 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(GemmParams p) {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 
-template <int WM, int WN, bool TB>
+template <int WM, int WN, bool TB, bool LNA>
 struct KsFrag {
   static constexpr int RA = WM / 16, CB = WN / 16;
   float4 a[RA];
   float b[4][CB];  // b[e][j]: B operand of MFMA step e, column block j
+  int kc;          // LNA: first k of this lane group (clamped into K)
   bool kin;        // this lane group's 4 k lie inside the wave's K range
 
   // Loads are unconditional, from addresses clamped into the operands. A row
@@ -298,12 +390,14 @@ struct KsFrag {
     const int64_t kq = k0 + 4 * g;  // first k of this lane group (a multiple of 4)
     kin = kq < ke;
     const int64_t kc = kq < K - 4 ? kq : K - 4;  // K % 4 == 0 and K >= 4
+    this->kc = int(kc);
 #pragma unroll
     for (int i = 0; i < RA; ++i) {
       const int64_t row = m0 + 16 * i + r;
       const int64_t rc = row < M ? row : M - 1;
       a[i] = *reinterpret_cast<const float4*>(A + rc * lda + kc);
     }
+
     if constexpr (TB) {
 #pragma unroll
       for (int j = 0; j < CB; ++j) {
@@ -338,13 +432,29 @@ struct KsFrag {
 
   // Both operands of a masked k are zeroed, so a non-finite value at the
   // clamped address cannot leak into the sum.
-  __device__ __forceinline__ void mma(floatx4 (&acc)[RA][CB]) const {
+  // LNA: the A value x of row i becomes (x - mu[i]) * rs[i] * gamma + beta,
+  // as the LayerNorm kernel computes it; gamma and beta (interleaved as
+  // float2 per k) come from LDS.
+  __device__ __forceinline__ void mma(floatx4 (&acc)[RA][CB], const float (&mu)[RA],
+                                      const float (&rs)[RA], const float2* lgb) const {
+    float4 ga, ba;
+    if constexpr (LNA) {
+      const float4 u = *reinterpret_cast<const float4*>(lgb + kc);
+      const float4 v = *reinterpret_cast<const float4*>(lgb + kc + 2);
+      ga = make_float4(u.x, u.z, v.x, v.z);
+      ba = make_float4(u.y, u.w, v.y, v.w);
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float av[RA], bv[CB];
 #pragma unroll
       for (int i = 0; i < RA; ++i) {
-        const float x = e == 0 ? a[i].x : e == 1 ? a[i].y : e == 2 ? a[i].z : a[i].w;
+        float x = e == 0 ? a[i].x : e == 1 ? a[i].y : e == 2 ? a[i].z : a[i].w;
+        if constexpr (LNA) {
+          const float gk = e == 0 ? ga.x : e == 1 ? ga.y : e == 2 ? ga.z : ga.w;
+          const float bk = e == 0 ? ba.x : e == 1 ? ba.y : e == 2 ? ba.z : ba.w;
+          x = fmaf((x - mu[i]) * rs[i], gk, bk);
+        }
         av[i] = kin ? x : 0.0f;
       }
 #pragma unroll
@@ -359,12 +469,14 @@ struct KsFrag {
 };
 
 // P is the register ring depth: k-groups in flight per wave.
-template <int WM, int WN, int W, int P, bool TB>
+template <int WM, int WN, int W, int P, bool TB, bool LNA>
 __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t tiles_m,
                                                           int64_t tiles_n) {
   constexpr int RA = WM / 16, CB = WN / 16;
   static_assert(W * WM * WN * 4 <= 65536, "partial tiles must fit the LDS of one block");
   __shared__ __attribute__((aligned(16))) float red[W * WM * WN];
+  __shared__ float2 nstat[2][WM];  // LayerNorm (mean, rstd) of the tile's rows: A, R
+  __shared__ __attribute__((aligned(16))) float2 lgb[LNA ? 1024 : 2];  // (gamma, beta) per k
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
@@ -395,11 +507,52 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
 #pragma unroll
     for (int j = 0; j < CB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  KsFrag<WM, WN, TB> f[P];
-  if (kb < ke) {
+  KsFrag<WM, WN, TB, LNA> f[P];
+  const bool has_k = kb < ke;
+  // LayerNorm statistics of the tile's rows (row 4 * wave + lane / 16 per
+  // lane group): their loads go out before the operands', and the merge
+  // then waits for them alone
+  static_assert(WM <= 4 * W, "a lane group per row of the tile");
+  const bool nr = p.nr_stats != nullptr;
+  const int si = 4 * wave + (lane >> 4);
+  const int64_t srow = m0 + si < p.M ? m0 + si : p.M - 1;
+  RowStatLoads sla, slr;
+  float4 g4, b4;  // LNA: gamma and beta of k = 4 * tid .. 4 * tid + 3, for LDS
+  if (LNA) {
+    row_stats_load(sla, p.na_stats, srow, p.K / 16, lane);
+    const int64_t k4 = 4 * tid < p.K ? 4 * tid : p.K - 4;
+    g4 = *reinterpret_cast<const float4*>(p.na_g + k4);
+    b4 = *reinterpret_cast<const float4*>(p.na_b + k4);
+  }
+  // without R statistics the loads read A's first element instead: no
+  // branch around them, so no use of their results is hoisted next to them
+  row_stats_load(slr, nr ? p.nr_stats : A, nr ? srow : 0, nr ? p.N / 16 : 1, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  // (unconditional: a wave without a K range loads clamped addresses that
+  // mma() masks, and no branch joins before the merge, whose wait then
+  // counts the statistics loads alone)
 #pragma unroll
-    for (int q = 0; q < P; ++q)
-      f[q].load(A, p.lda, B, p.ldb, p.M, p.N, p.K, m0, n0, kb + 16 * q, ke, r, g);
+  for (int q = 0; q < P; ++q)
+    f[q].load(A, p.lda, B, p.ldb, p.M, p.N, p.K, m0, n0, kb + 16 * q, ke, r, g);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (LNA) {
+    const float2 v = row_stats_merge(sla, p.K / 16, p.na_eps, lane);
+    if ((lane & 15) == 0 && si < WM) nstat[0][si] = v;
+    if (4 * tid < p.K) {
+      float4* d = reinterpret_cast<float4*>(lgb + 4 * tid);
+      d[0] = make_float4(g4.x, b4.x, g4.y, b4.y);
+      d[1] = make_float4(g4.z, b4.z, g4.w, b4.w);
+    }
+    lds_barrier();
+  }
+  float mu_a[RA], rs_a[RA];
+#pragma unroll
+  for (int i = 0; i < RA; ++i) {
+    const float2 v = LNA ? nstat[0][16 * i + r] : make_float2(0.0f, 1.0f);
+    mu_a[i] = v.x;
+    rs_a[i] = v.y;
+  }
+  if (has_k) {
     for (int64_t ring = 1; ring < rings; ++ring) {
       const int64_t k_next = kb + 16 * P * ring;
 #pragma unroll
@@ -408,17 +561,23 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
         // group waits only for its own loads and the refill of slot q goes
         // out as soon as slot q has been consumed.
         __builtin_amdgcn_sched_barrier(0);
-        f[q].mma(acc);
+        f[q].mma(acc, mu_a, rs_a, lgb);
         f[q].load(A, p.lda, B, p.ldb, p.M, p.N, p.K, m0, n0, k_next + 16 * q, ke, r, g);
       }
     }
 #pragma unroll
     for (int q = 0; q < P; ++q) {
       __builtin_amdgcn_sched_barrier(0);
-      f[q].mma(acc);
+      f[q].mma(acc, mu_a, rs_a, lgb);
     }
   }
 
+  // The residual rows' statistics, needed only by the epilogue: merged
+  // after the K loop, behind the barrier that publishes the partial tiles.
+  if (nr) {
+    const float2 v = row_stats_merge(slr, p.N / 16, p.nr_eps, lane);
+    if ((lane & 15) == 0 && si < WM) nstat[1][si] = v;
+  }
   // Partial tiles to LDS in [row][col] order of the block's output tile.
   float* mine = red + wave * (WM * WN);
 #pragma unroll
@@ -439,7 +598,44 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
 #pragma unroll
     for (int w = 1; w < W; ++w) s += red[w * (WM * WN) + e];
     const int64_t row = m0 + e / WN, col = n0 + e % WN;
-    if (row < p.M && col < p.N) Y[row * p.ldy + col] = epilogue(p, C, R, s, row, col);
+    if (row < p.M && col < p.N) {
+      float y;
+      if (nr && R != nullptr) {
+        // the residual row read through its LayerNorm
+        const float2 st = nstat[1][e / WN];
+        const float rv = fmaf((R[row * p.ldr + col] - st.x) * st.y, p.nr_g[col], p.nr_b[col]);
+        y = apply_act(epilogue_pre(p, C, s, row, col) + rv, p.act);
+      } else {
+        y = epilogue(p, C, R, s, row, col);
+      }
+      Y[row * p.ldy + col] = y;
+      red[e] = y;  // only this thread reads red[e]
+    }
+  }
+  if (p.st_out != nullptr) {
+    // (mean, M2) of each row's 16-column chunks of Y, two-pass over the
+    // stored values (N % 16 == 0, so a chunk is all in or all out)
+    __syncthreads();
+    constexpr int NCH = WN / 16;
+    for (int idx = tid; idx < WM * NCH; idx += 64 * W) {
+      const int i = idx / NCH, c = idx % NCH;
+      const int64_t row = m0 + i, col0 = n0 + 16 * c;
+      if (row >= p.M || col0 >= p.N) continue;
+      const float* v = red + i * WN + 16 * c;
+      float mean = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) mean += v[k];
+      mean *= 1.0f / 16.0f;
+      float m2 = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const float d = v[k] - mean;
+        m2 += d * d;
+      }
+      float* o = p.st_out + (int64_t(slice) * p.M * (p.N / 16) + row * (p.N / 16) + col0 / 16) * 2;
+      o[0] = mean;
+      o[1] = m2;
+    }
   }
 }
 
@@ -457,10 +653,16 @@ void launch_ksplit(GemmParams p, int64_t slices, bool tb, hipStream_t s) {
   p.k_per_split = ks_k_per_wave(p.K, W, P);
   const int64_t tm = ceil_div(p.M, WM), tn = ceil_div(p.N, WN);
   const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(slices));
-  if (tb)
-    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, true>), grid, dim3(64 * W), 0, s, p, tm, tn);
+  const dim3 block(64 * W);
+  const bool lna = p.na_stats != nullptr;
+  if (tb && lna)
+    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, true, true>), grid, block, 0, s, p, tm, tn);
+  else if (tb)
+    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, true, false>), grid, block, 0, s, p, tm, tn);
+  else if (lna)
+    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, false, true>), grid, block, 0, s, p, tm, tn);
   else
-    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, false>), grid, dim3(64 * W), 0, s, p, tm, tn);
+    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, false, false>), grid, block, 0, s, p, tm, tn);
 }
 
 // Three shapes cover the small-M products (measured on MI355X at M=32..256,
@@ -530,6 +732,9 @@ void run(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool ta, bool tb, bo
   const Cfg big{128, 128, 16}, wide{128, 64, 16}, small{64, 64, 32};
   auto tiles = [&](const Cfg& c) { return ceil_div(p.M, c.bm) * ceil_div(p.N, c.bn) * slices; };
   if (ksplit_supported(p, slices, ta, vec, cus, tiles(big))) return run_ksplit(ctx, p, slices, tb);
+  IH_REQUIRE(p.na_stats == nullptr && p.nr_stats == nullptr && p.st_out == nullptr,
+             INFERC_ERR_UNSUPPORTED,
+             "gemm: LayerNorm-on-read operands and row statistics need the small-M path");
   // 128x128 tiles hold 3 blocks per CU (164 VGPRs). Between one and three
   // tiles per CU a round leaves CUs idle, and 128x64 tiles balance better
   // (the b=32 fused QKV, M=4096 N=3x768 K=768: 175 us against 196 us).
@@ -570,7 +775,35 @@ void validate_common(const GemmArgs& a) {
   IH_REQUIRE(a.batch >= 1, INFERC_ERR_SHAPE, "gemm: batch must be >= 1");
 }
 
+// Copies the LayerNorm-on-read operands and the statistics output into the
+// launch parameters, checking the dimensions they need (D % 16 == 0).
+void set_row_norms(GemmParams& p, const RowNorm& na, const RowNorm& nr, float* st_out) {
+  if (na.stats) {
+    IH_REQUIRE(na.gamma && na.beta && p.K % 16 == 0 && p.K <= 1024, INFERC_ERR_ARG,
+               "gemm: LayerNorm of A needs gamma, beta and K % 16 == 0, K <= 1024");
+    p.na_stats = na.stats; p.na_g = na.gamma; p.na_b = na.beta; p.na_eps = na.eps;
+  }
+  if (nr.stats) {
+    IH_REQUIRE(nr.gamma && nr.beta && p.R && p.N % 16 == 0 && p.N <= 1024, INFERC_ERR_ARG,
+               "gemm: LayerNorm of R needs R, gamma, beta and N % 16 == 0, N <= 1024");
+    p.nr_stats = nr.stats; p.nr_g = nr.gamma; p.nr_b = nr.beta; p.nr_eps = nr.eps;
+  }
+  if (st_out) {
+    IH_REQUIRE(p.N % 16 == 0, INFERC_ERR_ARG, "gemm: row statistics need N % 16 == 0");
+    p.st_out = st_out;
+  }
+}
+
 }  // namespace
+
+bool gemm_small_m_path(const inferc_hip_ctx* ctx, int64_t M, int64_t N, int64_t K,
+                       int64_t slices) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 4 || N % 4) return false;
+  GemmParams p{};
+  p.M = M; p.N = N; p.K = K;
+  const int64_t big_tiles = ceil_div(M, 128) * ceil_div(N, 128) * slices;
+  return ksplit_supported(p, slices, false, true, ctx->num_cus, big_tiles);
+}
 
 void gemm(inferc_hip_ctx* ctx, const GemmArgs& a) {
   validate_common(a);
@@ -591,7 +824,9 @@ void gemm(inferc_hip_ctx* ctx, const GemmArgs& a) {
   // One row times a [N,K] row-major B^T is the batch-1 GEMV, which the
   // reference also sends to sgemv (src/kernels/matmul.cc:207-216). The GEMV
   // applies bias, residual and act in the GEMM's order.
-  if (a.M == 1 && a.batch == 1 && !a.trans_a && a.trans_b && a.alpha == 1.0f && a.ldb == a.K &&
+  const bool row_norms = a.norm_a.stats || a.norm_r.stats || a.stats_out;
+  if (!row_norms && a.M == 1 && a.batch == 1 && !a.trans_a && a.trans_b && a.alpha == 1.0f &&
+      a.ldb == a.K &&
       a.K > 0 && a.K <= 16384 &&
       (a.c_kind == INFERC_C_NONE || a.beta == 0.0f ||
        ((a.c_kind == INFERC_C_ROW || a.c_kind == INFERC_C_FULL) && a.beta == 1.0f))) {
@@ -612,6 +847,12 @@ void gemm(inferc_hip_ctx* ctx, const GemmArgs& a) {
   p.act = a.act;
   p.Y = a.Y; p.ldy = a.ldy; p.sy = a.stride_y;
   p.use_table = 0;
+  if (row_norms) {
+    IH_REQUIRE(a.batch == 1 && !a.trans_a && a.lda == a.K && a.ldy == a.N &&
+                   (a.R == nullptr || a.ldr == a.N),
+               INFERC_ERR_UNSUPPORTED, "gemm: LayerNorm-on-read needs dense unbatched rows");
+    set_row_norms(p, a.norm_a, a.norm_r, a.stats_out);
+  }
 
   // float4 global loads need 16-byte aligned rows and a contiguous extent
   // that is a multiple of 4.
@@ -624,7 +865,7 @@ void gemm(inferc_hip_ctx* ctx, const GemmArgs& a) {
 
 void gemm_qkv(inferc_hip_ctx* ctx, int64_t M, int64_t K, int64_t N, const float* X,
               const float* const w[3], const float* const b[3], float* const y[3],
-              int64_t ldy) {
+              int64_t ldy, const RowNorm* norm_a) {
   IH_REQUIRE(M >= 0 && K >= 0 && N >= 0, INFERC_ERR_SHAPE, "qkv: negative dimension");
   if (M == 0 || N == 0) return;
   IH_REQUIRE(X && w[0] && w[1] && w[2] && b[0] && b[1] && b[2] && y[0] && y[1] && y[2],
@@ -644,6 +885,7 @@ void gemm_qkv(inferc_hip_ctx* ctx, int64_t M, int64_t K, int64_t N, const float*
     vec = vec && aligned16(w[i]);
   }
   p.C = b[0];  // non-null marker; the table supplies the per-slice bias
+  if (norm_a) set_row_norms(p, *norm_a, RowNorm{}, nullptr);
   run(ctx, p, 3, false, false, vec);
 }
 
