@@ -195,15 +195,19 @@ __device__ __forceinline__ float wave_max(float v) {
 namespace ih {
 
 // LayerNorm of a GEMM operand's rows, applied as the operand is read:
-// x' = (x - mean) * rstd * gamma + beta over the row's D features, with mean
-// and rstd combined from per-16-column partials [rows][D/16][2] = (mean, M2
-// = sum of squared deviations) that the GEMM producing the rows wrote
-// (GemmArgs::stats_out). Only the small-M GEMM path reads rows this way,
-// for D <= 1024.
+// x' = (x - mean) * rstd * gamma + beta over the row's D <= 1024 features,
+// with mean and rstd combined from per-16-column partials [rows][D/16][2] =
+// (mean, M2 = sum of squared deviations) that the GEMM producing the rows
+// wrote (GemmArgs::stats_out). Only the small-M GEMM path reads rows this
+// way. For A the caller folds gamma into B (B'_kn = gamma_k B_kn) and beta
+// into the bias (C_n + sum_k beta_k B_kn) and passes colsum_n = sum_k B'_kn
+// per slice; the product is then rstd * (sum_k x_k B'_kn - mean * colsum_n),
+// applied in the epilogue. For R, gamma and beta are applied as read.
 struct RowNorm {
   const float* stats = nullptr;
-  const float* gamma = nullptr;
-  const float* beta = nullptr;
+  const float* gamma = nullptr;              // R
+  const float* beta = nullptr;               // R
+  const float* colsum[3] = {nullptr, nullptr, nullptr};  // A, per slice
   float eps = 1e-5f;
 };
 

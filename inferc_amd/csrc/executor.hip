@@ -319,7 +319,12 @@ struct inferc_executor {
   void peephole();
   void exec_node(const inferc_graph::Node& n);
   bool ln_read_ok(const std::string& h, int64_t M, int64_t N, int64_t K);
-  bool ln_read_of(const inferc_graph::Node& n, char role, std::string* h, ih::RowNorm* rn);
+  bool ln_read_of(const inferc_graph::Node& n, char role, std::string* h, ih::RowNorm* rn,
+                  size_t* reader = nullptr);
+  void fold_ln_weights();
+  static std::string ln_fold_name(size_t reader, char what, int slice) {
+    return "__lnfold:" + std::to_string(reader) + ":" + what + std::to_string(slice);
+  }
   void generic_binary(const inferc_graph::Node& n, int ewop);
   void exec_attention_past(const inferc_graph::Node& n);
   bool exec_generic(const inferc_graph::Node& n);
@@ -545,6 +550,8 @@ bool inferc_executor::ln_read_ok(const std::string& h, int64_t M, int64_t N, int
     if (rd.second == 'a') {
       const int64_t slices = c.op == "FusedQKV" ? 3 : 1;
       if (w.shape[0] != N || !ih::gemm_small_m_path(ctx, M, w.shape[1], N, slices)) return false;
+      for (int i = 0; i < int(slices); ++i)
+        if (!inits.count(ln_fold_name(rd.first, 'w', i))) return false;
     } else if (w.shape[1] != N || !ih::gemm_small_m_path(ctx, M, N, w.shape[0], 1)) {
       return false;
     }
@@ -556,7 +563,7 @@ bool inferc_executor::ln_read_ok(const std::string& h, int64_t M, int64_t N, int
 // this run, if any: the tensor h it reads instead of the LayerNorm output,
 // and the normalization.
 bool inferc_executor::ln_read_of(const inferc_graph::Node& n, char role, std::string* h,
-                                 ih::RowNorm* rn) {
+                                 ih::RowNorm* rn, size_t* reader) {
   const size_t k = role == 'a' ? 0 : 3;
   if (n.in.size() <= k) return false;
   for (const auto& kv : ln_reads) {
@@ -565,14 +572,102 @@ bool inferc_executor::ln_read_of(const inferc_graph::Node& n, char role, std::st
     for (const auto& rd : kv.second.readers) {
       if (rd.second != role || &nodes[rd.first] != &n) continue;
       *h = kv.first;
+      if (reader) *reader = rd.first;
       rn->stats = static_cast<const float*>(arena.at("__lnstats:" + kv.first).p);
-      rn->gamma = static_cast<const float*>(dev_of(kv.second.gamma));
-      rn->beta = static_cast<const float*>(dev_of(kv.second.beta));
       rn->eps = kv.second.eps;
+      if (role == 'r') {
+        rn->gamma = static_cast<const float*>(dev_of(kv.second.gamma));
+        rn->beta = static_cast<const float*>(dev_of(kv.second.beta));
+      } else {
+        const int slices = n.op == "FusedQKV" ? 3 : 1;
+        for (int i = 0; i < slices; ++i)
+          rn->colsum[i] = static_cast<const float*>(dev_of(ln_fold_name(rd.first, 'c', i)));
+      }
       return true;
     }
   }
   return false;
+}
+
+// For every reader that takes a LayerNorm's output as its A operand: the
+// folded operands that let it read the LayerNorm's input instead,
+// B'_kn = gamma_k B_kn, colsum_n = sum_k B'_kn and C'_n = C_n + sum_k
+// beta_k B_kn (sums in double), kept as device initializers beside the
+// originals, which the LayerNorm-kernel path still uses. A LayerNorm whose
+// readers' operands cannot be folded (not float32 initializers of the
+// expected shapes) is left to the kernel.
+void inferc_executor::fold_ln_weights() {
+  for (auto it = ln_reads.begin(); it != ln_reads.end();) {
+    const LnRead& lr = it->second;
+    const ih::Value& gv = inits.at(lr.gamma);
+    const ih::Value& bv = inits.at(lr.beta);
+    const int64_t D = gv.numel();
+    bool ok = gv.dtype == INFERC_DT_F32 && bv.dtype == INFERC_DT_F32 && gv.host && bv.host &&
+              bv.numel() == D;
+    struct Fold {
+      std::string name;
+      std::vector<int64_t> shape;
+      std::vector<float> v;
+    };
+    std::vector<Fold> folds;
+    for (const auto& rd : lr.readers) {
+      if (!ok || rd.second != 'a') continue;
+      const inferc_graph::Node& c = nodes[rd.first];
+      const int slices = c.op == "FusedQKV" ? 3 : 1;
+      for (int i = 0; i < slices && ok; ++i) {
+        const size_t wi = size_t(1 + 2 * i), bi = size_t(2 + 2 * i);
+        if (c.in.size() <= bi || !inits.count(c.in[wi]) || !inits.count(c.in[bi])) {
+          ok = false;
+          break;
+        }
+        const ih::Value& W = inits.at(c.in[wi]);
+        const ih::Value& B = inits.at(c.in[bi]);
+        if (W.dtype != INFERC_DT_F32 || B.dtype != INFERC_DT_F32 || !W.host || !B.host ||
+            W.shape.size() != 2 || W.shape[0] != D || B.numel() != W.shape[1]) {
+          ok = false;
+          break;
+        }
+        const int64_t N = W.shape[1];
+        const float* w = reinterpret_cast<const float*>(W.host->data());
+        const float* b = reinterpret_cast<const float*>(B.host->data());
+        const float* gam = reinterpret_cast<const float*>(gv.host->data());
+        const float* bet = reinterpret_cast<const float*>(bv.host->data());
+        Fold fw{ln_fold_name(rd.first, 'w', i), {D, N}, std::vector<float>(size_t(D * N))};
+        std::vector<double> cs(size_t(N), 0.0), ds(size_t(N), 0.0);
+        for (int64_t k = 0; k < D; ++k)
+          for (int64_t n = 0; n < N; ++n) {
+            const float wk = gam[k] * w[k * N + n];
+            fw.v[size_t(k * N + n)] = wk;
+            cs[size_t(n)] += double(wk);
+            ds[size_t(n)] += double(bet[k]) * double(w[k * N + n]);
+          }
+        Fold fc{ln_fold_name(rd.first, 'c', i), {N}, std::vector<float>(size_t(N))};
+        Fold fb{ln_fold_name(rd.first, 'b', i), {N}, std::vector<float>(size_t(N))};
+        for (int64_t n = 0; n < N; ++n) {
+          fc.v[size_t(n)] = float(cs[size_t(n)]);
+          fb.v[size_t(n)] = float(double(b[n]) + ds[size_t(n)]);
+        }
+        folds.push_back(std::move(fw));
+        folds.push_back(std::move(fc));
+        folds.push_back(std::move(fb));
+      }
+    }
+    if (!ok) {
+      it = ln_reads.erase(it);
+      continue;
+    }
+    for (Fold& f : folds) {
+      ih::Value v;
+      v.dtype = INFERC_DT_F32;
+      v.shape = f.shape;
+      const size_t bytes = f.v.size() * sizeof(float);
+      IH_HIP(hipMalloc(&v.dev, bytes));
+      init_allocs.push_back(v.dev);
+      IH_HIP(hipMemcpy(v.dev, f.v.data(), bytes, hipMemcpyHostToDevice));
+      inits[f.name] = v;
+    }
+    ++it;
+  }
 }
 
 void inferc_executor::exec_node(const inferc_graph::Node& n) {
@@ -591,7 +686,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
   if (op == "FusedQKV") {
     std::string ha;
     RowNorm rna;
-    const bool lna = ln_read_of(n, 'a', &ha, &rna);
+    size_t rdr = 0;
+    const bool lna = ln_read_of(n, 'a', &ha, &rna, &rdr);
     const Value x = lna ? get(ha) : in(0);
     require_f32(x, "X");
     const int64_t K = x.shape.back(), M = x.numel() / K;
@@ -608,8 +704,10 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       const Value bi = in(size_t(2 + 2 * i));
       IH_REQUIRE(wi.shape == wq.shape && bi.numel() == N, INFERC_ERR_SHAPE,
                  "FusedQKV: projections must share shapes");
-      w[i] = static_cast<const float*>(dev_of(n.in[size_t(1 + 2 * i)]));
-      b[i] = static_cast<const float*>(dev_of(n.in[size_t(2 + 2 * i)]));
+      w[i] = static_cast<const float*>(
+          dev_of(lna ? ln_fold_name(rdr, 'w', i) : n.in[size_t(1 + 2 * i)]));
+      b[i] = static_cast<const float*>(
+          dev_of(lna ? ln_fold_name(rdr, 'b', i) : n.in[size_t(2 + 2 * i)]));
       IH_REQUIRE(i < int(n.out.size()), INFERC_ERR_ARG, "FusedQKV: needs three outputs");
       y[i] = static_cast<float*>(make_dev(n.out[size_t(i)], INFERC_DT_F32, os).dev);
     }
@@ -654,7 +752,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
   if (op == "FusedMatMulAddGELU" || op == "FusedGemmEpilogue" || op == "MatMul") {
     std::string ha, hr;
     RowNorm rna, rnr;
-    const bool lna = op != "MatMul" && ln_read_of(n, 'a', &ha, &rna);
+    size_t rdr = 0;
+    const bool lna = op != "MatMul" && ln_read_of(n, 'a', &ha, &rna, &rdr);
     const bool lnr = op == "FusedGemmEpilogue" && ln_read_of(n, 'r', &hr, &rnr);
     const Value x = lna ? get(ha) : in(0);
     const Value w = in(1);
@@ -702,13 +801,14 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     GemmArgs g;
     g.M = M; g.N = N; g.K = K;
     g.A = static_cast<const float*>(dev_of(lna ? ha : n.in[0])); g.lda = K;
-    g.B = static_cast<const float*>(dev_of(n.in[1])); g.ldb = N;
+    g.B = static_cast<const float*>(dev_of(lna ? ln_fold_name(rdr, 'w', 0) : n.in[1]));
+    g.ldb = N;
     g.ldy = N;
     if (lna) g.norm_a = rna;
     if (op != "MatMul") {
       IH_REQUIRE(in(2).numel() == N, INFERC_ERR_SHAPE, op + ": bias size must equal N");
       g.beta = 1.0f;
-      g.C = static_cast<const float*>(dev_of(n.in[2]));
+      g.C = static_cast<const float*>(dev_of(lna ? ln_fold_name(rdr, 'b', 0) : n.in[2]));
       g.c_kind = INFERC_C_ROW;
     }
     if (op == "FusedMatMulAddGELU") g.act = INFERC_ACT_GELU_ERF;
@@ -1907,6 +2007,7 @@ int inferc_executor_create(inferc_hip_ctx* ctx, const inferc_graph* g, inferc_ex
       ex->inits[in.name] = v;
     }
     ex->peephole();
+    ex->fold_ln_weights();
     *out = ex.release();
   });
 }

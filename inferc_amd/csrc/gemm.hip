@@ -60,8 +60,7 @@ struct GemmParams {
   // small-M path: LayerNorm of A's rows (over K) and R's rows (over N) as
   // read, from producer partials; Y's per-16-column (mean, M2) out
   const float* na_stats;
-  const float* na_g;
-  const float* na_b;
+  const float* na_c[kMaxSlices];  // per slice: column sums of the gamma-scaled B
   float na_eps;
   const float* nr_stats;
   const float* nr_g;
@@ -369,12 +368,11 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(GemmParams p) {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 
-template <int WM, int WN, bool TB, bool LNA>
+template <int WM, int WN, bool TB>
 struct KsFrag {
   static constexpr int RA = WM / 16, CB = WN / 16;
   float4 a[RA];
   float b[4][CB];  // b[e][j]: B operand of MFMA step e, column block j
-  int kc;          // LNA: first k of this lane group (clamped into K)
   bool kin;        // this lane group's 4 k lie inside the wave's K range
 
   // Loads are unconditional, from addresses clamped into the operands. A row
@@ -390,7 +388,6 @@ struct KsFrag {
     const int64_t kq = k0 + 4 * g;  // first k of this lane group (a multiple of 4)
     kin = kq < ke;
     const int64_t kc = kq < K - 4 ? kq : K - 4;  // K % 4 == 0 and K >= 4
-    this->kc = int(kc);
 #pragma unroll
     for (int i = 0; i < RA; ++i) {
       const int64_t row = m0 + 16 * i + r;
@@ -432,29 +429,13 @@ struct KsFrag {
 
   // Both operands of a masked k are zeroed, so a non-finite value at the
   // clamped address cannot leak into the sum.
-  // LNA: the A value x of row i becomes (x - mu[i]) * rs[i] * gamma + beta,
-  // as the LayerNorm kernel computes it; gamma and beta (interleaved as
-  // float2 per k) come from LDS.
-  __device__ __forceinline__ void mma(floatx4 (&acc)[RA][CB], const float (&mu)[RA],
-                                      const float (&rs)[RA], const float2* lgb) const {
-    float4 ga, ba;
-    if constexpr (LNA) {
-      const float4 u = *reinterpret_cast<const float4*>(lgb + kc);
-      const float4 v = *reinterpret_cast<const float4*>(lgb + kc + 2);
-      ga = make_float4(u.x, u.z, v.x, v.z);
-      ba = make_float4(u.y, u.w, v.y, v.w);
-    }
+  __device__ __forceinline__ void mma(floatx4 (&acc)[RA][CB]) const {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float av[RA], bv[CB];
 #pragma unroll
       for (int i = 0; i < RA; ++i) {
-        float x = e == 0 ? a[i].x : e == 1 ? a[i].y : e == 2 ? a[i].z : a[i].w;
-        if constexpr (LNA) {
-          const float gk = e == 0 ? ga.x : e == 1 ? ga.y : e == 2 ? ga.z : ga.w;
-          const float bk = e == 0 ? ba.x : e == 1 ? ba.y : e == 2 ? ba.z : ba.w;
-          x = fmaf((x - mu[i]) * rs[i], gk, bk);
-        }
+        const float x = e == 0 ? a[i].x : e == 1 ? a[i].y : e == 2 ? a[i].z : a[i].w;
         av[i] = kin ? x : 0.0f;
       }
 #pragma unroll
@@ -469,14 +450,13 @@ struct KsFrag {
 };
 
 // P is the register ring depth: k-groups in flight per wave.
-template <int WM, int WN, int W, int P, bool TB, bool LNA>
+template <int WM, int WN, int W, int P, bool TB, bool LNA, bool LNR>
 __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t tiles_m,
                                                           int64_t tiles_n) {
   constexpr int RA = WM / 16, CB = WN / 16;
   static_assert(W * WM * WN * 4 <= 65536, "partial tiles must fit the LDS of one block");
   __shared__ __attribute__((aligned(16))) float red[W * WM * WN];
   __shared__ float2 nstat[2][WM];  // LayerNorm (mean, rstd) of the tile's rows: A, R
-  __shared__ __attribute__((aligned(16))) float2 lgb[LNA ? 1024 : 2];  // (gamma, beta) per k
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
@@ -507,51 +487,49 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
 #pragma unroll
     for (int j = 0; j < CB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  KsFrag<WM, WN, TB, LNA> f[P];
+  KsFrag<WM, WN, TB> f[P];
   const bool has_k = kb < ke;
-  // LayerNorm statistics of the tile's rows (row 4 * wave + lane / 16 per
-  // lane group): their loads go out before the operands', and the merge
-  // then waits for them alone
-  static_assert(WM <= 4 * W, "a lane group per row of the tile");
-  const bool nr = p.nr_stats != nullptr;
-  const int si = 4 * wave + (lane >> 4);
-  const int64_t srow = m0 + si < p.M ? m0 + si : p.M - 1;
-  RowStatLoads sla, slr;
-  float4 g4, b4;  // LNA: gamma and beta of k = 4 * tid .. 4 * tid + 3, for LDS
-  if (LNA) {
-    row_stats_load(sla, p.na_stats, srow, p.K / 16, lane);
-    const int64_t k4 = 4 * tid < p.K ? 4 * tid : p.K - 4;
-    g4 = *reinterpret_cast<const float4*>(p.na_g + k4);
-    b4 = *reinterpret_cast<const float4*>(p.na_b + k4);
-  }
-  // without R statistics the loads read A's first element instead: no
-  // branch around them, so no use of their results is hoisted next to them
-  row_stats_load(slr, nr ? p.nr_stats : A, nr ? srow : 0, nr ? p.N / 16 : 1, lane);
-  __builtin_amdgcn_sched_barrier(0);
-  // (unconditional: a wave without a K range loads clamped addresses that
-  // mma() masks, and no branch joins before the merge, whose wait then
-  // counts the statistics loads alone)
+  // The operands' first ring (unconditional: a wave without a K range
+  // loads clamped addresses that mma() masks, and no branch joins before
+  // the loads below, whose waits are then counted exactly).
 #pragma unroll
   for (int q = 0; q < P; ++q)
     f[q].load(A, p.lda, B, p.ldb, p.M, p.N, p.K, m0, n0, kb + 16 * q, ke, r, g);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (LNA) {
-    const float2 v = row_stats_merge(sla, p.K / 16, p.na_eps, lane);
-    if ((lane & 15) == 0 && si < WM) nstat[0][si] = v;
-    if (4 * tid < p.K) {
-      float4* d = reinterpret_cast<float4*>(lgb + 4 * tid);
-      d[0] = make_float4(g4.x, b4.x, g4.y, b4.y);
-      d[1] = make_float4(g4.z, b4.z, g4.w, b4.w);
-    }
-    lds_barrier();
-  }
-  float mu_a[RA], rs_a[RA];
+  // LayerNorm statistics of the tile's rows (row 4 * wave + lane / 16 per
+  // lane group), needed only by the epilogue: loaded behind the first ring
+  // and merged after the K loop.
+  static_assert(WM <= 4 * W, "a lane group per row of the tile");
+  const int si = 4 * wave + (lane >> 4);
+  const int64_t srow = m0 + si < p.M ? m0 + si : p.M - 1;
+  RowStatLoads sla, slr;
+  if (LNA) row_stats_load(sla, p.na_stats, srow, p.K / 16, lane);
+  if (LNR) row_stats_load(slr, p.nr_stats, srow, p.N / 16, lane);
+  // This thread's epilogue operands (elements e = tid + 64 W k of the tile),
+  // fetched now so the epilogue after the K loop waits on no memory: C, R,
+  // the column sums (LNA) and R's gamma and beta (LNR). The loads are
+  // unconditional; an absent C or R reads A's first element instead, and
+  // indices are clamped into the tile's valid rows and columns.
+  constexpr int EPT = (WM * WN + 64 * W - 1) / (64 * W);
+  const float* C = p.use_table ? p.Ct[slice] : p.C;
+  const float* R = p.R ? p.R + slice * p.sr : nullptr;
+  const bool has_c = C != nullptr && p.beta != 0.0f;
+  float pc[EPT], pr[EPT], pcs[EPT], pg[EPT], pbt[EPT];
 #pragma unroll
-  for (int i = 0; i < RA; ++i) {
-    const float2 v = LNA ? nstat[0][16 * i + r] : make_float2(0.0f, 1.0f);
-    mu_a[i] = v.x;
-    rs_a[i] = v.y;
+  for (int k = 0; k < EPT; ++k) {
+    const int e = tid + 64 * W * k < WM * WN ? tid + 64 * W * k : 0;
+    const int64_t row = m0 + e / WN < p.M ? m0 + e / WN : p.M - 1;
+    const int64_t col = n0 + e % WN < p.N ? n0 + e % WN : p.N - 1;
+    const int64_t ci = p.c_kind == INFERC_C_ROW ? col
+                       : p.c_kind == INFERC_C_FULL ? row * p.ldc + col
+                                                   : 0;
+    pc[k] = (has_c ? C : A)[has_c ? ci : 0];
+    pr[k] = (R ? R : A)[R ? row * p.ldr + col : 0];
+    pg[k] = LNR ? p.nr_g[col] : 1.0f;
+    pbt[k] = LNR ? p.nr_b[col] : 0.0f;
+    pcs[k] = LNA ? p.na_c[slice][col] : 0.0f;
   }
+  __builtin_amdgcn_sched_barrier(0);
   if (has_k) {
     for (int64_t ring = 1; ring < rings; ++ring) {
       const int64_t k_next = kb + 16 * P * ring;
@@ -561,20 +539,24 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
         // group waits only for its own loads and the refill of slot q goes
         // out as soon as slot q has been consumed.
         __builtin_amdgcn_sched_barrier(0);
-        f[q].mma(acc, mu_a, rs_a, lgb);
+        f[q].mma(acc);
         f[q].load(A, p.lda, B, p.ldb, p.M, p.N, p.K, m0, n0, k_next + 16 * q, ke, r, g);
       }
     }
 #pragma unroll
     for (int q = 0; q < P; ++q) {
       __builtin_amdgcn_sched_barrier(0);
-      f[q].mma(acc, mu_a, rs_a, lgb);
+      f[q].mma(acc);
     }
   }
 
-  // The residual rows' statistics, needed only by the epilogue: merged
-  // after the K loop, behind the barrier that publishes the partial tiles.
-  if (nr) {
+  // The rows' statistics, merged after the K loop, behind the barrier that
+  // publishes the partial tiles.
+  if constexpr (LNA) {
+    const float2 v = row_stats_merge(sla, p.K / 16, p.na_eps, lane);
+    if ((lane & 15) == 0 && si < WM) nstat[0][si] = v;
+  }
+  if constexpr (LNR) {
     const float2 v = row_stats_merge(slr, p.N / 16, p.nr_eps, lane);
     if ((lane & 15) == 0 && si < WM) nstat[1][si] = v;
   }
@@ -590,24 +572,35 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
     }
   __syncthreads();
 
-  const float* C = p.use_table ? p.Ct[slice] : p.C;
-  const float* R = p.R ? p.R + slice * p.sr : nullptr;
   float* Y = p.use_table ? p.Yt[slice] : p.Y + slice * p.sy;
-  for (int e = tid; e < WM * WN; e += 64 * W) {
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int e = tid + 64 * W * k;
+    if (e >= WM * WN) break;
     float s = red[e];
 #pragma unroll
     for (int w = 1; w < W; ++w) s += red[w * (WM * WN) + e];
     const int64_t row = m0 + e / WN, col = n0 + e % WN;
     if (row < p.M && col < p.N) {
-      float y;
-      if (nr && R != nullptr) {
-        // the residual row read through its LayerNorm
-        const float2 st = nstat[1][e / WN];
-        const float rv = fmaf((R[row * p.ldr + col] - st.x) * st.y, p.nr_g[col], p.nr_b[col]);
-        y = apply_act(epilogue_pre(p, C, s, row, col) + rv, p.act);
-      } else {
-        y = epilogue(p, C, R, s, row, col);
+      if constexpr (LNA) {
+        // A read through its LayerNorm with gamma folded into B:
+        // rstd * (sum_k a_k B'_kn - mean * colsum_n); beta's share is in C
+        const float2 st = nstat[0][e / WN];
+        s = (s - st.x * pcs[k]) * st.y;
       }
+      // the epilogue's order: alpha * acc + beta * C, + R, then act
+      float v = p.alpha * s;
+      if (has_c) v = v + p.beta * pc[k];
+      if (R != nullptr) {
+        float rv = pr[k];
+        if constexpr (LNR) {
+          // the residual row read through its LayerNorm
+          const float2 st = nstat[1][e / WN];
+          rv = fmaf((rv - st.x) * st.y, pg[k], pbt[k]);
+        }
+        v = v + rv;
+      }
+      const float y = apply_act(v, p.act);
       Y[row * p.ldy + col] = y;
       red[e] = y;  // only this thread reads red[e]
     }
@@ -654,15 +647,22 @@ void launch_ksplit(GemmParams p, int64_t slices, bool tb, hipStream_t s) {
   const int64_t tm = ceil_div(p.M, WM), tn = ceil_div(p.N, WN);
   const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(slices));
   const dim3 block(64 * W);
-  const bool lna = p.na_stats != nullptr;
-  if (tb && lna)
-    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, true, true>), grid, block, 0, s, p, tm, tn);
-  else if (tb)
-    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, true, false>), grid, block, 0, s, p, tm, tn);
-  else if (lna)
-    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, false, true>), grid, block, 0, s, p, tm, tn);
-  else
-    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, false, false>), grid, block, 0, s, p, tm, tn);
+  const bool lna = p.na_stats != nullptr, lnr = p.nr_stats != nullptr;
+#define IH_KS(TB_, LNA_, LNR_)                                                           \
+  if (tb == TB_ && lna == LNA_ && lnr == LNR_) {                                         \
+    hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, TB_, LNA_, LNR_>), grid, block, 0, s, \
+                       p, tm, tn);                                                        \
+    return;                                                                               \
+  }
+  IH_KS(false, false, false)
+  IH_KS(false, true, false)
+  IH_KS(false, false, true)
+  IH_KS(false, true, true)
+  IH_KS(true, false, false)
+  IH_KS(true, true, false)
+  IH_KS(true, false, true)
+  IH_KS(true, true, true)
+#undef IH_KS
 }
 
 // Three shapes cover the small-M products (measured on MI355X at M=32..256,
@@ -777,11 +777,16 @@ void validate_common(const GemmArgs& a) {
 
 // Copies the LayerNorm-on-read operands and the statistics output into the
 // launch parameters, checking the dimensions they need (D % 16 == 0).
-void set_row_norms(GemmParams& p, const RowNorm& na, const RowNorm& nr, float* st_out) {
+void set_row_norms(GemmParams& p, int slices, const RowNorm& na, const RowNorm& nr,
+                   float* st_out) {
   if (na.stats) {
-    IH_REQUIRE(na.gamma && na.beta && p.K % 16 == 0 && p.K <= 1024, INFERC_ERR_ARG,
-               "gemm: LayerNorm of A needs gamma, beta and K % 16 == 0, K <= 1024");
-    p.na_stats = na.stats; p.na_g = na.gamma; p.na_b = na.beta; p.na_eps = na.eps;
+    IH_REQUIRE(p.K % 16 == 0 && p.K <= 1024, INFERC_ERR_ARG,
+               "gemm: LayerNorm of A needs K % 16 == 0, K <= 1024");
+    for (int i = 0; i < slices; ++i) {
+      IH_REQUIRE(na.colsum[i] != nullptr, INFERC_ERR_ARG, "gemm: LayerNorm of A needs column sums");
+      p.na_c[i] = na.colsum[i];
+    }
+    p.na_stats = na.stats; p.na_eps = na.eps;
   }
   if (nr.stats) {
     IH_REQUIRE(nr.gamma && nr.beta && p.R && p.N % 16 == 0 && p.N <= 1024, INFERC_ERR_ARG,
@@ -851,7 +856,7 @@ void gemm(inferc_hip_ctx* ctx, const GemmArgs& a) {
     IH_REQUIRE(a.batch == 1 && !a.trans_a && a.lda == a.K && a.ldy == a.N &&
                    (a.R == nullptr || a.ldr == a.N),
                INFERC_ERR_UNSUPPORTED, "gemm: LayerNorm-on-read needs dense unbatched rows");
-    set_row_norms(p, a.norm_a, a.norm_r, a.stats_out);
+    set_row_norms(p, 1, a.norm_a, a.norm_r, a.stats_out);
   }
 
   // float4 global loads need 16-byte aligned rows and a contiguous extent
@@ -885,7 +890,7 @@ void gemm_qkv(inferc_hip_ctx* ctx, int64_t M, int64_t K, int64_t N, const float*
     vec = vec && aligned16(w[i]);
   }
   p.C = b[0];  // non-null marker; the table supplies the per-slice bias
-  if (norm_a) set_row_norms(p, *norm_a, RowNorm{}, nullptr);
+  if (norm_a) set_row_norms(p, 3, *norm_a, RowNorm{}, nullptr);
   run(ctx, p, 3, false, false, vec);
 }
 
