@@ -134,8 +134,9 @@ struct inferc_executor {
   hipGraphExec_t exec = nullptr;
   std::string graph_sig;
   // A LayerNorm whose input h comes from a FusedGemmEpilogue and whose
-  // readers are all GEMM operands (A of FusedQKV / FusedMatMulAddGELU, the
-  // residual of a FusedGemmEpilogue): peephole lists the readers by h, and
+  // readers are all GEMM operands (A of FusedQKV / FusedMatMulAddGELU /
+  // FusedGemmEpilogue, the residual of a FusedGemmEpilogue): peephole lists
+  // the readers by h, and
   // each run decides at the producer whether they read h through the
   // LayerNorm (the small-M GEMM path for every product involved) instead of
   // the LayerNorm kernel writing its output.
@@ -519,7 +520,8 @@ void inferc_executor::peephole() {
       const inferc_graph::Node& c = nodes[j];
       for (size_t k = 0; k < c.in.size(); ++k) {
         if (c.in[k] != x) continue;
-        const bool a = k == 0 && (c.op == "FusedQKV" || c.op == "FusedMatMulAddGELU");
+        const bool a = k == 0 && (c.op == "FusedQKV" || c.op == "FusedMatMulAddGELU" ||
+                                  c.op == "FusedGemmEpilogue");
         const bool r = k == 3 && c.op == "FusedGemmEpilogue";
         if (!(a || r) || !inits.count(c.in[1])) ok = false;
         else lr.readers.emplace_back(j, a ? 'a' : 'r');

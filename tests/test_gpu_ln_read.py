@@ -1,7 +1,7 @@
 """LayerNorms applied by their readers (executor): a FusedGemmEpilogue
 writes the row statistics of its output h, and the GEMMs that read the
-LayerNorm of h (A of FusedQKV and FusedMatMulAddGELU, the residual of a
-FusedGemmEpilogue) normalize h as they read it, so the LayerNorm kernel does
+LayerNorm of h (A of FusedQKV, FusedMatMulAddGELU or FusedGemmEpilogue, the
+residual of a FusedGemmEpilogue) normalize h as they read it, so the LayerNorm kernel does
 not run. That holds while every product takes the small-M path (M <= 512);
 above it the LayerNorm kernel runs as before. Both against a float64
 statement of the unfused graph (src/kernels/activation.cc:103-150 for the
@@ -25,15 +25,15 @@ def _w(rng, *shape, std=0.05):
 
 
 def _graph(rng):
-    """out-proj(+x0) -> LN1 -> {QKV, FFN-up -> FFN-down(+LN1)} -> LN2 ->
-    out-proj(+LN2) -> LN3. LN1 and LN2 are read by GEMMs only; LN3 is an
-    output and stays a kernel."""
+    """out-proj(+x0) -> LN1 -> {QKV, FFN-up -> FFN-down(+LN1), a plain
+    projection} -> LN2 -> out-proj(+LN2) -> LN3. LN1 and LN2 are read by GEMMs
+    only; LN3 is an output and stays a kernel."""
     g = rt.Graph()
     p = {}
     for nm, shape in [("wo", (H, H)), ("bo", (H,)), ("wq", (H, H)), ("bq", (H,)),
                       ("wk", (H, H)), ("bk", (H,)), ("wv", (H, H)), ("bv", (H,)),
                       ("w1", (H, F)), ("c1", (F,)), ("w2", (F, H)), ("c2", (H,)),
-                      ("wo2", (H, H)), ("bo2", (H,))]:
+                      ("wo2", (H, H)), ("bo2", (H,)), ("wz", (H, 2 * H)), ("bz", (2 * H,))]:
         p[nm] = _w(rng, *shape)
     for i in (1, 2, 3):
         p[f"g{i}"] = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
@@ -44,11 +44,12 @@ def _graph(rng):
     g.add_node("FusedLayerNorm", ["h1", "g1", "b1"], ["x1"], epsilon=1e-12)
     g.add_node("FusedQKV", ["x1", "wq", "bq", "wk", "bk", "wv", "bv"], ["q", "k", "v"])
     g.add_node("FusedMatMulAddGELU", ["x1", "w1", "c1"], ["f"])
+    g.add_node("FusedGemmEpilogue", ["x1", "wz", "bz"], ["z"])
     g.add_node("FusedGemmEpilogue", ["f", "w2", "c2", "x1"], ["h2"])
     g.add_node("FusedLayerNorm", ["h2", "g2", "b2"], ["x2"], epsilon=1e-5)
     g.add_node("FusedGemmEpilogue", ["a2", "wo2", "bo2", "x2"], ["h3"])
     g.add_node("FusedLayerNorm", ["h3", "g3", "b3"], ["x3"], epsilon=1e-5)
-    for o in ("q", "k", "v", "x3"):
+    for o in ("q", "k", "v", "z", "x3"):
         g.add_output(o)
     return g, p
 
@@ -65,12 +66,13 @@ def _reference(p, x0, a, a2):
     h1 = a @ d["wo"] + d["bo"] + x0
     x1 = _ln(h1, d["g1"], d["b1"], 1e-12)
     q, k, v = (x1 @ d["w" + t] + d["b" + t] for t in "qkv")
+    z = x1 @ d["wz"] + d["bz"]
     u = x1 @ d["w1"] + d["c1"]
     f = 0.5 * u * (1.0 + erf(u / math.sqrt(2.0)))
     h2 = f @ d["w2"] + d["c2"] + x1
     x2 = _ln(h2, d["g2"], d["b2"], 1e-5)
     h3 = a2 @ d["wo2"] + d["bo2"] + x2
-    return {"q": q, "k": k, "v": v, "x3": _ln(h3, d["g3"], d["b3"], 1e-5)}
+    return {"q": q, "k": k, "v": v, "z": z, "x3": _ln(h3, d["g3"], d["b3"], 1e-5)}
 
 
 @pytest.mark.parametrize("M", [1, 7, 128, 512, 600])
@@ -84,7 +86,7 @@ def test_layernorm_read_by_gemms(ctx, M):
     # shift the rows off zero mean so the statistics carry real offsets
     feeds["x0"] += np.float32(3.0)
     ref = _reference(p, *(feeds[k].astype(np.float64) for k in ("x0", "a", "a2")))
-    names = ["q", "k", "v", "x3"]
+    names = ["q", "k", "v", "z", "x3"]
     runs = [ex.run(feeds, names) for _ in range(3)]  # eager, capture, replay
     for nm in names:
         err = float(np.max(np.abs(runs[0][nm] - ref[nm])))
