@@ -234,7 +234,15 @@ struct GemmArgs {
   // [M][N/16][2] for a later GEMM that reads Y through a RowNorm
   RowNorm norm_a, norm_r;
   float* stats_out = nullptr;
+  // one-row GEMV route only (gemm_gemv_route): LayerNorm of the A row first
+  const float* gemv_ln_g = nullptr;
+  const float* gemv_ln_b = nullptr;
+  float gemv_ln_eps = 1e-5f;
 };
+
+// Whether gemm() sends `a` to the batch-1 GEMV (one row of A times a [N,K]
+// B^T), the route that can apply a LayerNorm to the A row (gemv_ln_*).
+bool gemm_gemv_route(const GemmArgs& a);
 
 void gemm(inferc_hip_ctx* ctx, const GemmArgs& a);
 

@@ -473,6 +473,35 @@ void inferc_executor::peephole() {
       break;
     }
   }
+  // FusedLayerNorm (x) -> Gather(x, constant indices) -> Gemm(transB), each
+  // result read once: the Gather takes the LayerNorm's input and the Gemm
+  // normalizes its A rows (LayerNorm acts row by row, so the two commute; the
+  // classifier head of an encoder). On the one-row GEMV route the GEMV's
+  // LayerNorm prologue does it, else a LayerNorm of the gathered rows.
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    inferc_graph::Node& gt = nodes[i];
+    if (dead[i] || gt.op != "Gather" || gt.in.size() != 2 || !inits.count(gt.in[1]) ||
+        uses[gt.in[0]] != 1 || uses[gt.out[0]] != 1)
+      continue;
+    const int li = producer(gt.in[0]);
+    if (li < 0 || dead[size_t(li)]) continue;
+    const inferc_graph::Node& ln = nodes[size_t(li)];
+    if (ln.op != "FusedLayerNorm" || ln.in.size() != 3 || !inits.count(ln.in[1]) ||
+        !inits.count(ln.in[2]))
+      continue;
+    for (size_t j = i + 1; j < nodes.size(); ++j) {
+      inferc_graph::Node& c = nodes[j];
+      if (dead[j] || c.in.empty() || c.in[0] != gt.out[0]) continue;
+      if (c.op == "Gemm" && ih::attr_int(c, "transB", 0) == 1 && ih::attr_int(c, "transA", 0) == 0) {
+        c.attrs["__ln_g"] = ln.in[1];
+        c.attrs["__ln_b"] = ln.in[2];
+        c.attrs["__ln_eps"] = std::to_string(ih::attr_float(ln, "epsilon", 1e-5f));
+        gt.in[0] = ln.in[0];
+        dead[size_t(li)] = true;
+      }
+      break;
+    }
+  }
   std::vector<inferc_graph::Node> kept;
   for (size_t i = 0; i < nodes.size(); ++i)
     if (!dead[i]) kept.push_back(std::move(nodes[i]));
@@ -876,6 +905,25 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     g.act = int(attr_int(n, "__act", INFERC_ACT_NONE));
     g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, {g.M, g.N}).dev);
     g.ldy = g.N;
+    auto ln = n.attrs.find("__ln_g");
+    if (ln != n.attrs.end()) {
+      // A's rows through the LayerNorm that preceded the Gather (peephole)
+      const float* lg = static_cast<const float*>(dev_of(ln->second));
+      const float* lb = static_cast<const float*>(dev_of(n.attrs.at("__ln_b")));
+      const float eps = std::stof(n.attrs.at("__ln_eps"));
+      IH_REQUIRE(!g.trans_a && inits.at(ln->second).numel() == g.K, INFERC_ERR_SHAPE,
+                 "Gemm: LayerNorm of A: scale size must equal K");
+      if (gemm_gemv_route(g)) {
+        g.gemv_ln_g = lg;
+        g.gemv_ln_b = lb;
+        g.gemv_ln_eps = eps;
+      } else {
+        float* t = static_cast<float*>(buf("__lnrows:" + n.out[0], size_t(g.M * g.K) * 4));
+        IH_REQUIRE(g.lda == g.K, INFERC_ERR_SHAPE, "Gemm: LayerNorm of A needs dense rows");
+        if (!dry) layernorm_res_period(ctx, g.M, g.K, g.A, nullptr, 1, lg, lb, eps, t);
+        g.A = t;
+      }
+    }
     if (!dry) {
       gemm(ctx, g);
     }

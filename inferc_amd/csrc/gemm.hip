@@ -810,6 +810,14 @@ bool gemm_small_m_path(const inferc_hip_ctx* ctx, int64_t M, int64_t N, int64_t 
   return ksplit_supported(p, slices, false, true, ctx->num_cus, big_tiles);
 }
 
+bool gemm_gemv_route(const GemmArgs& a) {
+  const bool row_norms = a.norm_a.stats || a.norm_r.stats || a.stats_out;
+  return !row_norms && a.M == 1 && a.batch == 1 && !a.trans_a && a.trans_b && a.alpha == 1.0f &&
+         a.ldb == a.K && a.K > 0 && a.K <= 16384 &&
+         (a.c_kind == INFERC_C_NONE || a.beta == 0.0f ||
+          ((a.c_kind == INFERC_C_ROW || a.c_kind == INFERC_C_FULL) && a.beta == 1.0f));
+}
+
 void gemm(inferc_hip_ctx* ctx, const GemmArgs& a) {
   validate_common(a);
   if (a.M == 0 || a.N == 0) return;
@@ -829,18 +837,16 @@ void gemm(inferc_hip_ctx* ctx, const GemmArgs& a) {
   // One row times a [N,K] row-major B^T is the batch-1 GEMV, which the
   // reference also sends to sgemv (src/kernels/matmul.cc:207-216). The GEMV
   // applies bias, residual and act in the GEMM's order.
-  const bool row_norms = a.norm_a.stats || a.norm_r.stats || a.stats_out;
-  if (!row_norms && a.M == 1 && a.batch == 1 && !a.trans_a && a.trans_b && a.alpha == 1.0f &&
-      a.ldb == a.K &&
-      a.K > 0 && a.K <= 16384 &&
-      (a.c_kind == INFERC_C_NONE || a.beta == 0.0f ||
-       ((a.c_kind == INFERC_C_ROW || a.c_kind == INFERC_C_FULL) && a.beta == 1.0f))) {
+  if (gemm_gemv_route(a)) {
     // with one row, a full C is a row of N values like a bias
     const bool has_c = (a.c_kind == INFERC_C_ROW || a.c_kind == INFERC_C_FULL) && a.beta != 0.0f;
     const float* bias = has_c ? a.C : nullptr;
-    gemv(ctx, a.N, a.K, a.B, a.A, nullptr, nullptr, 0.0f, bias, a.R, a.act, a.Y);
+    gemv(ctx, a.N, a.K, a.B, a.A, a.gemv_ln_g, a.gemv_ln_b, a.gemv_ln_eps, bias, a.R, a.act, a.Y);
     return;
   }
+  IH_REQUIRE(a.gemv_ln_g == nullptr, INFERC_ERR_UNSUPPORTED,
+             "gemm: a LayerNorm of A needs the one-row GEMV route");
+  const bool row_norms = a.norm_a.stats || a.norm_r.stats || a.stats_out;
 
   GemmParams p{};
   p.M = a.M; p.N = a.N; p.K = a.K;
