@@ -141,6 +141,7 @@ struct inferc_executor {
   // LayerNorm (the small-M GEMM path for every product involved) instead of
   // the LayerNorm kernel writing its output.
   struct LnRead {
+    std::string out;  // the LayerNorm's output
     std::string gamma, beta;
     float eps = 1e-5f;
     std::vector<std::pair<size_t, char>> readers;  // node index, 'a' (A) or 'r' (R)
@@ -527,12 +528,16 @@ void inferc_executor::peephole() {
   // LayerNorms that their readers can apply as they read (final node
   // order, so the reader indices stay valid)
   ln_reads.clear();
+  std::unordered_map<std::string, int> ln_of;  // LayerNorms per input
+  for (const auto& n : nodes)
+    if (n.op == "FusedLayerNorm" && !n.in.empty()) ++ln_of[n.in[0]];
   for (size_t i = 0; i < nodes.size(); ++i) {
     const inferc_graph::Node& ln = nodes[i];
     if (ln.op != "FusedLayerNorm" || ln.in.size() != 3 || ln.out.size() != 1) continue;
     const std::string& h = ln.in[0];
     const std::string& x = ln.out[0];
-    if (!inits.count(ln.in[1]) || !inits.count(ln.in[2]) || inits.count(h) ||
+    // (an h with two LayerNorms keeps both as kernels)
+    if (!inits.count(ln.in[1]) || !inits.count(ln.in[2]) || inits.count(h) || ln_of[h] != 1 ||
         std::find(outputs.begin(), outputs.end(), x) != outputs.end())
       continue;
     int pi = -1;
@@ -541,6 +546,7 @@ void inferc_executor::peephole() {
         pi = int(j);
     if (pi < 0 || nodes[size_t(pi)].op != "FusedGemmEpilogue") continue;
     LnRead lr;
+    lr.out = x;
     lr.gamma = ln.in[1];
     lr.beta = ln.in[2];
     lr.eps = ih::attr_float(ln, "epsilon", 1e-5f);
@@ -932,7 +938,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
   if (op == "FusedLayerNorm") {
     if (n.in.size() == 3) {
       auto on = ln_on.find(n.in[0]);
-      if (on != ln_on.end() && on->second && ln_reads.count(n.in[0])) {
+      auto lr = ln_reads.find(n.in[0]);
+      if (on != ln_on.end() && on->second && lr != ln_reads.end() && lr->second.out == n.out[0]) {
         // its readers apply it: the output is a tensor of the tape at its
         // logical size with no data (a non-reader asking for it fails)
         ih::Value v;

@@ -94,3 +94,38 @@ def test_layernorm_read_by_gemms(ctx, M):
         assert err <= 1e-4, nm
         for r in runs[1:]:
             np.testing.assert_array_equal(r[nm], runs[0][nm])
+
+
+def test_two_layernorms_of_one_input_stay_kernels(ctx):
+    """Two LayerNorms (different gamma/beta) of one GEMM output, each read by
+    a GEMM: both are computed by the LayerNorm kernel."""
+    rng = np.random.default_rng(5)
+    M = 32
+    p = {"wo": _w(rng, H, H), "bo": _w(rng, H), "w1": _w(rng, H, F), "c1": _w(rng, F),
+         "wz": _w(rng, H, H), "bz": _w(rng, H)}
+    for i in (1, 2):
+        p[f"g{i}"] = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+        p[f"b{i}"] = (0.1 * rng.standard_normal(H)).astype(np.float32)
+    g = rt.Graph()
+    for nm, v in p.items():
+        g.add_initializer(nm, v)
+    g.add_node("FusedGemmEpilogue", ["a", "wo", "bo", "x0"], ["h"])
+    g.add_node("FusedLayerNorm", ["h", "g1", "b1"], ["x1"], epsilon=1e-5)
+    g.add_node("FusedLayerNorm", ["h", "g2", "b2"], ["x2"], epsilon=1e-5)
+    g.add_node("FusedMatMulAddGELU", ["x1", "w1", "c1"], ["f"])
+    g.add_node("FusedGemmEpilogue", ["x2", "wz", "bz"], ["z"])
+    g.add_output("f")
+    g.add_output("z")
+    feeds = {"x0": rng.standard_normal((M, H)).astype(np.float32),
+             "a": rng.standard_normal((M, H)).astype(np.float32)}
+    d = {k: v.astype(np.float64) for k, v in p.items()}
+    h = feeds["a"].astype(np.float64) @ d["wo"] + d["bo"] + feeds["x0"]
+    u = _ln(h, d["g1"], d["b1"], 1e-5) @ d["w1"] + d["c1"]
+    erf = np.vectorize(math.erf)
+    ref = {"f": 0.5 * u * (1.0 + erf(u / math.sqrt(2.0))),
+           "z": _ln(h, d["g2"], d["b2"], 1e-5) @ d["wz"] + d["bz"]}
+    ex = rt.Executor(ctx, g)
+    for _ in range(3):
+        got = ex.run(feeds, ["f", "z"])
+        for nm in ("f", "z"):
+            assert float(np.max(np.abs(got[nm] - ref[nm]))) <= 1e-4, nm
