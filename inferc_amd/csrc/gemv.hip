@@ -204,8 +204,8 @@ __global__ __launch_bounds__(kBlock) void gemv2_kernel(Gemv2P p) {
     const int64_t r = r0 + i;
     if (r < p.N) {
       float v = acc[i];
-      if (p.bias) v = v + p.bias[r];
-      if (p.res) v = v + p.res[r];
+      if (p.bias) v = v + p.bias[r0 + i];
+      if (p.res) v = v + p.res[r0 + i];
       v = apply_act(v, p.act);
       if (lane == i) p.y[r] = v;
       if (ARGMAX && v > bv) {  // rows ascend: strict '>' keeps the first max
@@ -738,6 +738,15 @@ __global__ __launch_bounds__(kI4DecBlock) void int4_gemv_dec_kernel(Int4DecP p, 
   i4_load_chunk<DW, LT>(buf[0], d, c0, ~0u, rpp, rg, s);
   if constexpr (NC > 1) i4_load_chunk<DW, LT>(buf[1], d, c0 + 1, keep(1), rpp, rg, s);
   __builtin_amdgcn_sched_barrier(0);
+  // the row this lane reports, and its bias and residual, fetched behind the
+  // weights so the epilogue waits on no memory (unconditional: an absent
+  // operand reads the scales instead)
+  const int jr = s % (LT / 4), pr = s / (LT / 4);
+  const int64_t r = ((c0 + jr) * kI4Passes + pr) * rpp + rg;
+  const int64_t rc = r < d.N ? r : d.N - 1;
+  const float bpre = gload_f((p.bias ? p.bias : d.s) + (p.bias ? rc : 0));
+  const float rpre = gload_f((p.res ? p.res : d.s) + (p.res ? rc : 0));
+  __builtin_amdgcn_sched_barrier(0);
   if (p.ln_g) {
     float sum = 0.0f;
 #pragma unroll
@@ -779,13 +788,11 @@ __global__ __launch_bounds__(kI4DecBlock) void int4_gemv_dec_kernel(Int4DecP p, 
     __builtin_amdgcn_sched_barrier(0);
     if (j + 2 < NC) i4_load_chunk<DW, LT>(buf[j & 1], d, c0 + j + 2, keep(j + 2), rpp, rg, s);
   }
-  const int j = s % (LT / 4), pr = s / (LT / 4);
-  const int64_t r = ((c0 + j) * kI4Passes + pr) * rpp + rg;
-  const bool valid = j < n && r < d.N;
+  const bool valid = jr < n && r < d.N;
   float v = res;
   if (valid) {
-    if (p.bias) v += gload_f(p.bias + r);
-    if (p.res) v += gload_f(p.res + r);
+    if (p.bias) v += bpre;
+    if (p.res) v += rpre;
     v = apply_act(v, p.act);
   }
   if (valid && d.y) gstore_f(d.y + r, v);
