@@ -428,6 +428,9 @@ def main(argv=None) -> int:
     ap.add_argument("--quick", action="store_true", help="primary workload and roofline only")
     ap.add_argument("--roofline-only", action="store_true",
                     help="roofline kernel + calibration copy only (for rocprofv3 --pmc runs)")
+    ap.add_argument("--decode-only", nargs="?", const="both", choices=["fp32", "int4", "both"],
+                    help="GPT-2 decode only (fp32 weights, int4 weights or both), one "
+                         "generate each, printed as text (for rocprofv3 --kernel-trace runs)")
     ap.add_argument("--profile-dir", default=None,
                     help="also write per-op profiles (reference JSON schema) to this folder")
     args = ap.parse_args(argv)
@@ -444,6 +447,13 @@ def main(argv=None) -> int:
     ctx = rt.Context(0)
     if args.roofline_only:
         print(json.dumps(roofline_only(ctx)), flush=True)
+        ctx.close()
+        return 0
+    if args.decode_only:
+        for int4 in {"fp32": (False,), "int4": (True,), "both": (False, True)}[args.decode_only]:
+            mean, p50, _, _, _, _ = bench_decode(ctx, int4=int4)
+            print(f"gpt2 decode {'int4' if int4 else 'fp32'}: {mean:.4f} ms/token "
+                  f"(p50 {p50:.4f})", flush=True)
         ctx.close()
         return 0
     extra = {}

@@ -434,3 +434,30 @@ def test_kv_append_attend_vs_numpy(ctx):
         close(out, ref)
         np.testing.assert_array_equal(kcd.numpy()[:, pos], kn.reshape(nH, D))
         np.testing.assert_array_equal(vcd.numpy()[:, pos], vn.reshape(nH, D))
+
+
+@pytest.mark.parametrize("pos", [0, 31, 255, 256, 299])
+def test_kv_append_attend_ignores_rows_past_pos(ctx, pos):
+    """Cache rows at and past pos hold NaN/Inf (the kernel reads its first
+    key chunk before the position, clamped to the cache, not to pos): the
+    output depends on rows [0, pos) of the cache and the new row only. T=300
+    spans two rounds of key chunks (8 waves x 32 keys)."""
+    nH, D, T_ = 12, 64, 300
+    rng = np.random.default_rng(200 + pos)
+    kc = rng.standard_normal((nH, T_, D)).astype(np.float32)
+    vc = rng.standard_normal((nH, T_, D)).astype(np.float32)
+    kc[:, pos:, ::2], kc[:, pos:, 1::2] = np.nan, np.inf
+    vc[:, pos:, ::2], vc[:, pos:, 1::2] = -np.inf, np.nan
+    q, kn, vn = (rng.standard_normal(nH * D).astype(np.float32) for _ in range(3))
+    kcd, vcd = T(ctx, kc), T(ctx, vc)
+    out = rt.KvAppendAttend(T(ctx, q), T(ctx, kn), T(ctx, vn), kcd, vcd,
+                            T(ctx, [pos], np.int64), nH, D, T_).numpy()
+    kc[:, pos] = kn.reshape(nH, D)
+    vc[:, pos] = vn.reshape(nH, D)
+    t = pos + 1
+    s = np.einsum("hd,htd->ht", q.reshape(nH, D).astype(np.float64), kc[:, :t]) / 8.0
+    ref = np.einsum("ht,htd->hd", ref64.softmax(s), vc[:, :t]).ravel()
+    assert np.isfinite(out).all()
+    close(out, ref)
+    np.testing.assert_array_equal(kcd.numpy()[:, pos], kn.reshape(nH, D))
+    np.testing.assert_array_equal(vcd.numpy()[:, pos], vn.reshape(nH, D))
