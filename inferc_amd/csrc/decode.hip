@@ -121,8 +121,37 @@ __global__ __launch_bounds__(kBlock) void kv_append_attend_kernel(KvP p) {
 // (indices past the last key are clamped to it and weighted by 0), so a
 // chunk costs one memory round trip. Per chunk: s_j = (q . k_j) / sqrt(64)
 // (the with-past graph's MatMul -> Div), m = max s_j, e_j = exp(s_j - m),
-// l = sum e_j, O = sum e_j v_j; chunks are merged online within a wave and
-// the eight waves through LDS in wave order; out = O / L.
+// l = sum e_j, O = sum e_j v_j (e_j shared across the wave through LDS);
+// chunks are merged online within a wave and the eight waves through LDS in
+// wave order; out = O / L.
+// Wave64 reductions without LDS: DPP rotations within each 16-lane row
+// (every lane then holds its row's result), then the four rows' values read
+// as scalars. The attention's lane pairs swap through a DPP quad permutation.
+template <int R>
+__device__ __forceinline__ float dpp_row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + R, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_pair_swap(float v) {  // quad_perm [1,0,3,2]
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_lane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_row_ror<8>(v));
+  v = fmaxf(v, dpp_row_ror<4>(v));
+  v = fmaxf(v, dpp_row_ror<2>(v));
+  v = fmaxf(v, dpp_row_ror<1>(v));
+  return fmaxf(fmaxf(row_lane(v, 0), row_lane(v, 16)), fmaxf(row_lane(v, 32), row_lane(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_row_ror<8>(v);
+  v += dpp_row_ror<4>(v);
+  v += dpp_row_ror<2>(v);
+  v += dpp_row_ror<1>(v);
+  return (row_lane(v, 0) + row_lane(v, 16)) + (row_lane(v, 32) + row_lane(v, 48));
+}
+
 struct AttnDecP {
   int64_t T;
   const int64_t* pos;
@@ -140,6 +169,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode_d64(AttnDecP p) {
   constexpr int D = 64;
   __shared__ float sm[kDecWaves], sl[kDecWaves];
   __shared__ float so[kDecWaves][D];
+  __shared__ __align__(16) float se[kDecWaves][kDecChunk];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t h = blockIdx.x;
   const int64_t pos = *p.pos;
@@ -178,14 +208,24 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode_d64(AttnDecP p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       dot += qv[i].x * kv[i].x + qv[i].y * kv[i].y + qv[i].z * kv[i].z + qv[i].w * kv[i].w;
-    dot += __shfl_xor(dot, 1, 64);
+    dot += dpp_pair_swap(dot);
     const float s = (jl < t) ? dot / rs : -INFINITY;
-    const float m = wave_max(s);
+    const float m = wave_max_dpp(s);
     const float e = (jl < t) ? expf(s - m) : 0.0f;
-    const float l = wave_sum((lane & 1) ? 0.0f : e);
+    const float l = wave_sum_dpp((lane & 1) ? 0.0f : e);
+    // e_k of the chunk's 32 keys through the wave's own LDS slot: one write,
+    // then eight broadcast reads (LDS ops of one wave run in order, so no
+    // barrier; an indexed shuffle per key would be 32 dependent LDS trips)
+    if (!(lane & 1)) se[wave][lane >> 1] = e;
     float o = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kDecChunk; ++k) o += __shfl(e, 2 * k, 64) * vv[k];
+    for (int k4 = 0; k4 < kDecChunk / 4; ++k4) {
+      const float4 e4 = *reinterpret_cast<const float4*>(&se[wave][4 * k4]);
+      o += e4.x * vv[4 * k4];
+      o += e4.y * vv[4 * k4 + 1];
+      o += e4.z * vv[4 * k4 + 2];
+      o += e4.w * vv[4 * k4 + 3];
+    }
     const float Mn = fmaxf(M, m);
     const float a = expf(M - Mn), b = expf(m - Mn);
     L = L * a + l * b;
