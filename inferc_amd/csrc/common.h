@@ -124,6 +124,35 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Wave64 reductions without LDS: DPP rotations within each 16-lane row
+// (every lane then holds its row's result), then the four rows' values read
+// as scalars; all 64 lanes must be active. dpp_pair_swap exchanges lanes
+// 2i and 2i+1 through a DPP quad permutation.
+template <int R>
+__device__ __forceinline__ float dpp_row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + R, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_pair_swap(float v) {  // quad_perm [1,0,3,2]
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_lane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_row_ror<8>(v));
+  v = fmaxf(v, dpp_row_ror<4>(v));
+  v = fmaxf(v, dpp_row_ror<2>(v));
+  v = fmaxf(v, dpp_row_ror<1>(v));
+  return fmaxf(fmaxf(row_lane(v, 0), row_lane(v, 16)), fmaxf(row_lane(v, 32), row_lane(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_row_ror<8>(v);
+  v += dpp_row_ror<4>(v);
+  v += dpp_row_ror<2>(v);
+  v += dpp_row_ror<1>(v);
+  return (row_lane(v, 0) + row_lane(v, 16)) + (row_lane(v, 32) + row_lane(v, 48));
+}
+
 // LayerNorm of one row by one wave64: the reference's two passes (mean, then
 // the centred second moment; activation.cc:103-150), with y = (d * inv) *
 // gamma + beta. x (+ res when given) is read once when the row fits 64*VPL

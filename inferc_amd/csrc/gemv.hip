@@ -152,14 +152,14 @@ __device__ __forceinline__ void gemv2_x(const Gemv2P& p, int lane, float4 (&xv)[
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < KV; ++j) s += (xv[j].x + xv[j].y) + (xv[j].z + xv[j].w);
-    const float mean = wave_sum(s) / float(K);
+    const float mean = wave_sum_dpp(s) / float(K);
     float q = 0.0f;
 #pragma unroll
     for (int j = 0; j < KV; ++j) {
       xv[j].x -= mean; xv[j].y -= mean; xv[j].z -= mean; xv[j].w -= mean;
       q += (xv[j].x * xv[j].x + xv[j].y * xv[j].y) + (xv[j].z * xv[j].z + xv[j].w * xv[j].w);
     }
-    const float var = wave_sum(q) / float(K);
+    const float var = wave_sum_dpp(q) / float(K);
     const float inv = 1.0f / sqrtf(var + p.ln_eps);
 #pragma unroll
     for (int j = 0; j < KV; ++j) {
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(kBlock) void gemv2_kernel(Gemv2P p) {
 #pragma unroll
     for (int j = 0; j < KV; ++j)
       a += w[i][j].x * xv[j].x + w[i][j].y * xv[j].y + w[i][j].z * xv[j].z + w[i][j].w * xv[j].w;
-    acc[i] = wave_sum(a);
+    acc[i] = wave_sum_dpp(a);
   }
   float bv = -INFINITY;
   int64_t bi = INT64_MAX;
