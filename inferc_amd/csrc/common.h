@@ -178,7 +178,7 @@ __device__ __forceinline__ void ln_row(int lane, const float* __restrict__ xr,
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) s += v[i];
-    const float mean = wave_sum(s) * inv_n;
+    const float mean = wave_sum_dpp(s) * inv_n;
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -187,7 +187,7 @@ __device__ __forceinline__ void ln_row(int lane, const float* __restrict__ xr,
       v[i] = d;
       q += d * d;
     }
-    const float var = wave_sum(q) * inv_n;
+    const float var = wave_sum_dpp(q) * inv_n;
     const float inv = 1.0f / sqrtf(var + eps);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -198,13 +198,13 @@ __device__ __forceinline__ void ln_row(int lane, const float* __restrict__ xr,
   }
   float s = 0.0f;
   for (int64_t c = lane; c < feat; c += 64) s += rr ? xr[c] + rr[c] : xr[c];
-  const float mean = wave_sum(s) * inv_n;
+  const float mean = wave_sum_dpp(s) * inv_n;
   float q = 0.0f;
   for (int64_t c = lane; c < feat; c += 64) {
     const float d = (rr ? xr[c] + rr[c] : xr[c]) - mean;
     q += d * d;
   }
-  const float inv = 1.0f / sqrtf(wave_sum(q) * inv_n + eps);
+  const float inv = 1.0f / sqrtf(wave_sum_dpp(q) * inv_n + eps);
   for (int64_t c = lane; c < feat; c += 64) {
     const float d = (rr ? xr[c] + rr[c] : xr[c]) - mean;
     yr[c] = (d * inv) * g[c] + b[c];
