@@ -751,14 +751,14 @@ __global__ __launch_bounds__(kI4DecBlock) void int4_gemv_dec_kernel(Int4DecP p, 
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < PL; ++i) sum += xs[i];
-    const float mean = wave_sum(sum) / float(K);
+    const float mean = wave_sum_dpp(sum) / float(K);
     float q2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < PL; ++i) {
       const float dd = xs[i] - mean;
       q2 += dd * dd;
     }
-    const float inv = 1.0f / sqrtf(wave_sum(q2) / float(K) + p.ln_eps);
+    const float inv = 1.0f / sqrtf(wave_sum_dpp(q2) / float(K) + p.ln_eps);
     const float4* gp = reinterpret_cast<const float4*>(p.ln_g + 8 * DW * s);
     const float4* bp = reinterpret_cast<const float4*>(p.ln_b + 8 * DW * s);
 #pragma unroll
