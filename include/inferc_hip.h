@@ -78,7 +78,9 @@ int inferc_hip_device_count(int* count);
 int inferc_hip_create(int device, inferc_hip_ctx** out);
 int inferc_hip_destroy(inferc_hip_ctx* ctx);
 /* Reserve at least `bytes` of context workspace (split-K partials, argmax
- * partials, descriptor tables). Ops grow it on demand outside graph capture. */
+ * partials, int4 x preparation). Ops grow it on demand outside graph capture.
+ * The context also keeps up to 32 grouped-GEMV descriptor tables on the
+ * device, keyed by their bytes, and frees them all when a launch needs room. */
 int inferc_hip_reserve_workspace(inferc_hip_ctx* ctx, size_t bytes);
 
 int inferc_hip_malloc(inferc_hip_ctx* ctx, size_t bytes, void** dptr);
@@ -97,8 +99,8 @@ int inferc_hip_timer_stop(inferc_hip_ctx* ctx, float* ms);
  * its graph per call; a replay issues the whole sequence at once). Entry
  * points that would allocate or upload during capture fail with
  * INFERC_ERR_STATE, so run the sequence once before capturing it. A replay
- * fails with INFERC_ERR_STATE if the context workspace was reallocated after
- * the capture. */
+ * fails with INFERC_ERR_STATE if the context workspace was reallocated, or
+ * its cached descriptor tables freed, after the capture. */
 typedef struct inferc_hip_capture inferc_hip_capture;
 int inferc_hip_capture_begin(inferc_hip_ctx* ctx);
 int inferc_hip_capture_end(inferc_hip_ctx* ctx, inferc_hip_capture** out);
@@ -353,7 +355,12 @@ int inferc_executor_set_input(inferc_executor* ex, const char* name, int dtype,
 int inferc_executor_set_input_device(inferc_executor* ex, const char* name,
                                      int dtype, int rank, const int64_t* shape,
                                      const void* dev_data);
-/* Enqueue one forward pass on the context stream. */
+/* Enqueue one forward pass on the context stream. A Gather whose indices
+ * are on the device (e.g. input_ids) cannot check them before the pass runs:
+ * an out-of-range index sets a flag that the next call waiting for the
+ * stream (get_output, output_argmax, output_device, run_profiled) reports as
+ * INFERC_ERR_ARG "Gather: index out of range" (src/kernels/embedding.cc:63),
+ * clearing it. */
 int inferc_executor_run(inferc_executor* ex);
 /* Shape and dtype of a graph output after run(); shape has room for 8 dims. */
 int inferc_executor_output_info(inferc_executor* ex, const char* name,

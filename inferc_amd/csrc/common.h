@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "../../include/inferc_hip.h"
 
@@ -81,13 +82,32 @@ struct inferc_hip_ctx {
   hipEvent_t ev_start = nullptr, ev_stop = nullptr;
   void* workspace = nullptr;
   size_t workspace_bytes = 0;
-  // Bumped whenever the workspace is reallocated: a captured HIP graph that
-  // baked in the old address must be re-captured.
+  // Bumped whenever device memory that a captured HIP graph may have baked in
+  // is freed (the workspace on regrowth, the descriptor tables on eviction):
+  // such a graph must be captured again.
   uint64_t ws_generation = 0;
   bool capturing = false;  // set while a HIP graph is being recorded
 
+  // Device copies of small launch descriptor tables, keyed by their bytes,
+  // so repeated launches over the same operands skip the upload.
+  struct Table {
+    std::string key;
+    void* dev = nullptr;
+  };
+  static constexpr size_t kMaxTables = 32;
+  std::vector<Table> tables;
+
   // Returns a workspace of at least `bytes`; grows it outside capture only.
   void* ws(size_t bytes);
+  // Makes room for `n` tables not yet cached, so that every table one launch
+  // uploads is still alive when it runs: when the cache cannot take them all,
+  // it waits for the stream and frees every cached table first (outside
+  // capture only). Call it before the first table() of a launch.
+  void reserve_tables(size_t n);
+  // The device copy of `bytes` (len bytes), uploaded on a miss. A miss needs
+  // a slot reserved by reserve_tables() and is refused during capture.
+  const void* table(const void* bytes, size_t len);
+  void free_tables();
   void make_current() const;
 };
 

@@ -38,6 +38,40 @@ void* inferc_hip_ctx::ws(size_t bytes) {
   return workspace;
 }
 
+void inferc_hip_ctx::free_tables() {
+  if (tables.empty()) return;
+  IH_HIP(hipStreamSynchronize(stream));
+  for (Table& t : tables) (void)hipFree(t.dev);
+  tables.clear();
+  ++ws_generation;
+}
+
+void inferc_hip_ctx::reserve_tables(size_t n) {
+  IH_REQUIRE(n <= kMaxTables, INFERC_ERR_SHAPE, "launch needs too many descriptor tables");
+  if (tables.size() + n <= kMaxTables || capturing) return;
+  free_tables();
+}
+
+const void* inferc_hip_ctx::table(const void* bytes, size_t len) {
+  for (const Table& t : tables)
+    if (t.key.size() == len && std::memcmp(t.key.data(), bytes, len) == 0) return t.dev;
+  IH_REQUIRE(!capturing, INFERC_ERR_STATE,
+             "descriptor table must be uploaded before graph capture");
+  IH_REQUIRE(tables.size() < kMaxTables, INFERC_ERR_STATE,
+             "descriptor table cache full (reserve_tables was not called)");
+  Table t;
+  t.key.assign(static_cast<const char*>(bytes), len);
+  IH_HIP(hipMalloc(&t.dev, len));
+  try {
+    IH_HIP(hipMemcpy(t.dev, bytes, len, hipMemcpyHostToDevice));
+  } catch (...) {
+    (void)hipFree(t.dev);
+    throw;
+  }
+  tables.push_back(std::move(t));
+  return tables.back().dev;
+}
+
 extern "C" {
 
 const char* inferc_hip_last_error(void) { return ih::g_last_error.c_str(); }
@@ -88,6 +122,8 @@ int inferc_hip_destroy(inferc_hip_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    for (auto& t : ctx->tables) (void)hipFree(t.dev);
+    ctx->tables.clear();
     if (ctx->workspace) (void)hipFree(ctx->workspace);
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);

@@ -186,9 +186,15 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode_d64(AttnDecP p) {
     const float e = (jl < t) ? expf(s - m) : 0.0f;
     const float l = wave_sum_dpp((lane & 1) ? 0.0f : e);
     // e_k of the chunk's 32 keys through the wave's own LDS slot: one write,
-    // then eight broadcast reads (LDS ops of one wave run in order, so no
-    // barrier; an indexed shuffle per key would be 32 dependent LDS trips)
+    // then eight broadcast reads (an indexed shuffle per key would be 32
+    // dependent LDS trips). The slot is private to the wave, whose LDS
+    // operations execute in program order; the wave-scope fences keep the
+    // compiler from moving the reads above the write, or the next chunk's
+    // write above these reads.
     if (!(lane & 1)) se[wave][lane >> 1] = e;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     float o = 0.0f;
 #pragma unroll
     for (int k4 = 0; k4 < kDecChunk / 4; ++k4) {
@@ -198,6 +204,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode_d64(AttnDecP p) {
       o += e4.z * vv[4 * k4 + 2];
       o += e4.w * vv[4 * k4 + 3];
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const float Mn = fmaxf(M, m);
     const float a = expf(M - Mn), b = expf(m - Mn);
     L = L * a + l * b;

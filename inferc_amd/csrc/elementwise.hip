@@ -259,14 +259,20 @@ __global__ __launch_bounds__(kEwBlock) void gather_t_kernel(int64_t outer, int64
                                                             int64_t inner,
                                                             const T* __restrict__ x,
                                                             const int64_t* __restrict__ idx,
-                                                            int64_t n_idx, T* __restrict__ y) {
+                                                            int64_t n_idx, T* __restrict__ y,
+                                                            int32_t* err) {
   const int64_t total = outer * n_idx * inner;
   for (int64_t e = int64_t(blockIdx.x) * kEwBlock + threadIdx.x; e < total;
        e += int64_t(gridDim.x) * kEwBlock) {
     const int64_t c = e % inner, k = (e / inner) % n_idx, o = e / (inner * n_idx);
     int64_t i = idx[k];
     if (i < 0) i += rows;
-    y[e] = (i < 0 || i >= rows) ? T(0) : x[(o * rows + i) * inner + c];
+    if (i < 0 || i >= rows) {
+      y[e] = T(0);
+      if (err) *err = 1;
+    } else {
+      y[e] = x[(o * rows + i) * inner + c];
+    }
   }
 }
 
@@ -485,7 +491,7 @@ void ew_reduce_mean(inferc_hip_ctx* ctx, const std::vector<int64_t>& in,
 }
 
 void ew_gather(inferc_hip_ctx* ctx, int dtype, int64_t outer, int64_t rows, int64_t inner,
-               const void* x, const int64_t* idx, int64_t n_idx, void* y) {
+               const void* x, const int64_t* idx, int64_t n_idx, void* y, int32_t* err) {
   const int64_t total = outer * n_idx * inner;
   if (total == 0) return;
   by_dtype(dtype, [&](auto tag) {
@@ -502,7 +508,7 @@ void ew_gather(inferc_hip_ctx* ctx, int dtype, int64_t outer, int64_t rows, int6
       }
     } else {
       hipLaunchKernelGGL(gather_t_kernel<T>, dim3(ew_grid(total)), dim3(kEwBlock), 0, ctx->stream,
-                         outer, rows, inner, xp, idx, n_idx, yp);
+                         outer, rows, inner, xp, idx, n_idx, yp, err);
       check_launch("gather");
     }
   });

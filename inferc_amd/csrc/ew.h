@@ -45,10 +45,11 @@ void ew_slice(inferc_hip_ctx* ctx, int dtype, const std::vector<int64_t>& in,
 void ew_reduce_mean(inferc_hip_ctx* ctx, const std::vector<int64_t>& in,
                     const std::vector<bool>& reduce, const float* x, float* y);
 // Gather along one axis of x viewed as [outer, rows, inner]. The device form
-// writes 0 for an out-of-range index (callers validate host-known indices);
-// the host form fails.
+// writes 0 for an out-of-range index and sets *err (when err is not null) to
+// 1; the host form fails.
 void ew_gather(inferc_hip_ctx* ctx, int dtype, int64_t outer, int64_t rows, int64_t inner,
-               const void* x, const int64_t* idx, int64_t n_idx, void* y);
+               const void* x, const int64_t* idx, int64_t n_idx, void* y,
+               int32_t* err = nullptr);
 
 std::string shape_str(const std::vector<int64_t>& s);
 

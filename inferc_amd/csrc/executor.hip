@@ -21,6 +21,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <set>
 #include <sstream>
 #include <string>
 #include <unordered_map>
@@ -149,6 +150,16 @@ struct inferc_executor {
   std::unordered_map<std::string, LnRead> ln_reads;  // by h
   std::unordered_map<std::string, bool> ln_on;       // this run, by h
   uint64_t graph_ws_gen = 0;
+  // Sticky device flag of the gathers whose indices live on the device: set
+  // by the kernel on an out-of-range index, read (and cleared) by the calls
+  // that wait for the stream, which then fail as Gather does on the host
+  // (embedding.cc:63). dev_gather: the last walk launched such a gather.
+  int32_t* gather_err = nullptr;
+  bool dev_gather = false;
+  // Gather outputs (this walk) whose Gather applied the LayerNorm the
+  // peephole had moved into their Gemm reader (a feature-axis gather).
+  std::set<std::string> ln_gemm_off;
+  void check_gather_err();
   std::vector<hipEvent_t> prof_ev;  // one per node boundary of a profiled pass
   // Device KV caches of FusedAttentionPast nodes (bind_kv_cache): per node,
   // K and V as [B, nH, kv_max_t, dh] and the number of positions held.
@@ -183,6 +194,7 @@ struct inferc_executor {
     for (auto& kv : inputs)
       if (kv.second.from_host && kv.second.v.dev) (void)hipFree(kv.second.v.dev);
     for (void* p : init_allocs) (void)hipFree(p);
+    if (gather_err) (void)hipFree(gather_err);
   }
 
   void drop_graph() {
@@ -494,9 +506,13 @@ void inferc_executor::peephole() {
       inferc_graph::Node& c = nodes[j];
       if (dead[j] || c.in.empty() || c.in[0] != gt.out[0]) continue;
       if (c.op == "Gemm" && ih::attr_int(c, "transB", 0) == 1 && ih::attr_int(c, "transA", 0) == 0) {
-        c.attrs["__ln_g"] = ln.in[1];
-        c.attrs["__ln_b"] = ln.in[2];
-        c.attrs["__ln_eps"] = std::to_string(ih::attr_float(ln, "epsilon", 1e-5f));
+        // both carry the LayerNorm: the Gather applies it itself when it
+        // selects along the feature axis (where the two do not commute)
+        for (inferc_graph::Node* t : {&c, &gt}) {
+          t->attrs["__ln_g"] = ln.in[1];
+          t->attrs["__ln_b"] = ln.in[2];
+          t->attrs["__ln_eps"] = std::to_string(ih::attr_float(ln, "epsilon", 1e-5f));
+        }
         gt.in[0] = ln.in[0];
         dead[size_t(li)] = true;
       }
@@ -912,7 +928,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, {g.M, g.N}).dev);
     g.ldy = g.N;
     auto ln = n.attrs.find("__ln_g");
-    if (ln != n.attrs.end()) {
+    if (ln != n.attrs.end() && !ln_gemm_off.count(n.in[0])) {
       // A's rows through the LayerNorm that preceded the Gather (peephole)
       const float* lg = static_cast<const float*>(dev_of(ln->second));
       const float* lb = static_cast<const float*>(dev_of(n.attrs.at("__ln_b")));
@@ -1070,6 +1086,31 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     const int64_t r = int64_t(data.shape.size());
     if (axis < 0) axis += r;
     IH_REQUIRE(axis >= 0 && axis < r, INFERC_ERR_ARG, "Gather: axis out of range");
+    auto lnf = n.attrs.find("__ln_g");
+    if (lnf != n.attrs.end() && axis == r - 1) {
+      // The peephole moved the LayerNorm of the data into the Gemm reading
+      // this result, but a gather along the feature axis does not commute
+      // with it: normalize the data here, gather from that, and let the
+      // Gemm read plain rows.
+      require_f32(data, "data");
+      const int64_t feat = data.shape.back();
+      IH_REQUIRE(inits.at(lnf->second).numel() == feat, INFERC_ERR_SHAPE,
+                 "LayerNorm: scale/bias size mismatch with feature dim");
+      inferc_graph::Node m = n;
+      m.attrs.erase("__ln_g");
+      m.in[0] = "__lnfull:" + n.out[0];
+      float* t = static_cast<float*>(make_dev(m.in[0], INFERC_DT_F32, data.shape).dev);
+      if (!dry && feat > 0) {
+        layernorm_res_period(ctx, data.numel() / feat, feat,
+                             static_cast<const float*>(dev_of(n.in[0])), nullptr, 1,
+                             static_cast<const float*>(dev_of(lnf->second)),
+                             static_cast<const float*>(dev_of(n.attrs.at("__ln_b"))),
+                             std::stof(n.attrs.at("__ln_eps")), t);
+      }
+      ln_gemm_off.insert(n.out[0]);
+      exec_node(m);
+      return;
+    }
     std::vector<int64_t> os(data.shape.begin(), data.shape.begin() + axis);
     for (int64_t d : idx.shape) os.push_back(d);
     for (int64_t i = axis + 1; i < r; ++i) os.push_back(data.shape[size_t(i)]);
@@ -1111,7 +1152,11 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       const void* xp = dev_of(n.in[0]);
       const int64_t* ip = static_cast<const int64_t*>(dev_of(n.in[1]));
       void* y = make_dev(n.out[0], data.dtype, os).dev;
-      if (!dry) ew_gather(ctx, data.dtype, outer, ad, inner, xp, ip, idx.numel(), y);
+      if (!dry) {
+        ew_gather(ctx, data.dtype, outer, ad, inner, xp, ip, idx.numel(), y,
+                  idx.host ? nullptr : gather_err);
+        dev_gather = dev_gather || !idx.host;
+      }
       return;
     }
     require_f32(data, "data");
@@ -1142,7 +1187,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     }
     float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
     // one device gather for any axis; host-known indices are validated here
-    // and uploaded once (device indices are checked by the kernel's flag)
+    // and uploaded once, device indices set the executor's sticky flag
     if (idx.host) {
       for (int64_t i : host_i64(idx, "Gather"))
         IH_REQUIRE(i >= -ad && i < ad, INFERC_ERR_ARG, "Gather: index out of range");
@@ -1153,7 +1198,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     IH_REQUIRE(idx.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED, "Gather: int64 indices only");
     const int64_t* ip = static_cast<const int64_t*>(dev_of(n.in[1]));
     if (!dry) {
-      gather_axis(ctx, outer, ad, inner, dp, ip, idx.numel(), y, nullptr);
+      gather_axis(ctx, outer, ad, inner, dp, ip, idx.numel(), y, idx.host ? nullptr : gather_err);
+      dev_gather = dev_gather || !idx.host;
     }
     return;
   }
@@ -1716,6 +1762,8 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
 
 void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
   vals = inits;
+  dev_gather = false;
+  ln_gemm_off.clear();
   cache_views.clear();
   for (auto& kv : inputs) vals[kv.first] = kv.second.v;
   const bool events = act != nullptr && !dry;
@@ -1795,6 +1843,19 @@ void inferc_executor::run() {
   IH_HIP(hipGraphLaunch(exec, ctx->stream));
 }
 
+// Waits for the stream, then fails if a device-index gather of the passes
+// enqueued so far met an out-of-range index; the flag is cleared first, so
+// the next pass starts clean.
+void inferc_executor::check_gather_err() {
+  if (dry || !dev_gather || !gather_err) return;
+  int32_t flag = 0;
+  IH_HIP(hipStreamSynchronize(ctx->stream));
+  IH_HIP(hipMemcpy(&flag, gather_err, sizeof(flag), hipMemcpyDeviceToHost));
+  if (flag == 0) return;
+  IH_HIP(hipMemset(gather_err, 0, sizeof(int32_t)));
+  ih::fail(INFERC_ERR_ARG, "Gather: index out of range");
+}
+
 // One eager pass recorded as a profiler iteration (executor.cc:121-125,
 // 145-160, 349-354): each node's time is the device time between HIP events
 // recorded on the stream before and after it (host-only shape nodes read
@@ -1829,6 +1890,7 @@ void inferc_executor::run_profiled(inferc_profiler* p) {
   p->begin_iteration();
   walk(&act, p->track_activation_bytes);
   IH_HIP(hipEventSynchronize(prof_ev[nodes.size()]));
+  check_gather_err();
   for (size_t i = 0; i < nodes.size(); ++i) {
     float ms = 0.0f;
     IH_HIP(hipEventElapsedTime(&ms, prof_ev[i], prof_ev[i + 1]));
@@ -2063,6 +2125,8 @@ int inferc_executor_create(inferc_hip_ctx* ctx, const inferc_graph* g, inferc_ex
       }
       ex->inits[in.name] = v;
     }
+    IH_HIP(hipMalloc(&ex->gather_err, sizeof(int32_t)));
+    IH_HIP(hipMemset(ex->gather_err, 0, sizeof(int32_t)));
     ex->peephole();
     ex->fold_ln_weights();
     *out = ex.release();
@@ -2196,6 +2260,7 @@ int inferc_executor_get_output(inferc_executor* ex, const char* name, void* host
       return;
     }
     IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+    ex->check_gather_err();
     auto cv = ex->cache_views.find(name);
     if (!v.dev && !v.host && cv != ex->cache_views.end()) {
       const auto& w = cv->second;
@@ -2261,6 +2326,7 @@ int inferc_executor_output_device(inferc_executor* ex, const char* name, const v
     const ih::Value& v = ex->get(name);
     IH_REQUIRE(v.dev != nullptr, INFERC_ERR_STATE,
                std::string("output '") + name + "' has no contiguous device buffer");
+    ex->check_gather_err();
     *ptr = v.dev;
   });
 }
@@ -2279,6 +2345,7 @@ int inferc_executor_output_argmax(inferc_executor* ex, const char* name, int64_t
     ih::argmax(ex->ctx, n, last, d, nullptr);
     IH_HIP(hipMemcpyAsync(index, d, sizeof(int64_t), hipMemcpyDeviceToHost, ex->ctx->stream));
     IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+    ex->check_gather_err();
   });
 }
 

@@ -1490,46 +1490,11 @@ void gemv(inferc_hip_ctx* ctx, int64_t N, int64_t K, const float* W, const float
 
 namespace {
 
-// Device copies of recently used grouped-GEMV descriptor tables, keyed by
-// their bytes, so repeated calls with the same matrices skip the upload.
-template <class T>
-struct TableCache {
-  struct Entry {
-    std::vector<T> key;
-    T* dev = nullptr;
-  };
-  std::vector<Entry> entries;
-};
-
-template <class T>
-TableCache<T>& table_cache(inferc_hip_ctx* ctx) {
-  static thread_local std::vector<std::pair<inferc_hip_ctx*, TableCache<T>>> caches;
-  for (auto& c : caches)
-    if (c.first == ctx) return c.second;
-  caches.emplace_back(ctx, TableCache<T>{});
-  return caches.back().second;
-}
-
+// The context's device copy of a launch's descriptor table. The launch calls
+// ctx->reserve_tables() with its table count before the first upload.
 template <class T>
 const T* upload_table(inferc_hip_ctx* ctx, const std::vector<T>& mats) {
-  TableCache<T>& tc = table_cache<T>(ctx);
-  for (auto& e : tc.entries)
-    if (e.key.size() == mats.size() &&
-        std::memcmp(e.key.data(), mats.data(), mats.size() * sizeof(T)) == 0)
-      return e.dev;
-  IH_REQUIRE(!ctx->capturing, INFERC_ERR_STATE,
-             "int4 grouped GEMV: descriptor table must be uploaded before graph capture");
-  if (tc.entries.size() >= 32) {
-    IH_HIP(hipStreamSynchronize(ctx->stream));
-    for (auto& e : tc.entries) (void)hipFree(e.dev);
-    tc.entries.clear();
-  }
-  typename TableCache<T>::Entry e;
-  e.key = mats;
-  IH_HIP(hipMalloc(&e.dev, mats.size() * sizeof(T)));
-  IH_HIP(hipMemcpy(e.dev, mats.data(), mats.size() * sizeof(T), hipMemcpyHostToDevice));
-  tc.entries.push_back(std::move(e));
-  return tc.entries.back().dev;
+  return static_cast<const T*>(ctx->table(mats.data(), mats.size() * sizeof(T)));
 }
 
 struct Int4MfMat {
@@ -1565,6 +1530,7 @@ void launch_int4_mfma_k(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats,
     }
     IH_REQUIRE(blocks < (int64_t(1) << 31) && tab.size() < (size_t(1) << 20), INFERC_ERR_SHAPE,
                "int4 gemv: launch too large");
+    ctx->reserve_tables(1);
     const Int4MfDesc* dev = upload_table(ctx, tab);
     hipLaunchKernelGGL(int4_gemv_mfma_kernel<STEPS>, dim3(unsigned(blocks)), dim3(kBlock), 0,
                        ctx->stream, dev, int(tab.size()), nb);
@@ -1614,6 +1580,7 @@ void launch_int4_stream_g(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mat
   }
   IH_REQUIRE(blocks < (int64_t(1) << 31) && mats.size() <= 65535, INFERC_ERR_SHAPE,
              "int4 gemv: launch too large");
+  ctx->reserve_tables(2);
   const I4PrepDesc* pdev = upload_table(ctx, ptab);
   const I4StreamDesc* sdev = upload_table(ctx, stab);
   int64_t smax = 1;
@@ -1683,6 +1650,7 @@ void launch_int4_valu_pair(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& a,
   }
   IH_REQUIRE(ceil_div(waves, kBlock / 64) < (int64_t(1) << 31), INFERC_ERR_SHAPE,
              "int4 gemv: launch too large");
+  ctx->reserve_tables(1);
   const Int4VaDesc* dev = upload_table(ctx, tab);
   hipLaunchKernelGGL((int4_gemv_valu_kernel<DA, LA, DB, LB>),
                      dim3(unsigned(ceil_div(waves, kBlock / 64))), dim3(kBlock), 0, ctx->stream,
@@ -1775,6 +1743,7 @@ void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const 
   launch_int4_mfma(ctx, mf, batch);
   if (mats.empty()) return;
   IH_REQUIRE(blocks < (int64_t(1) << 31), INFERC_ERR_SHAPE, "int4 gemv: launch too large");
+  ctx->reserve_tables(1);
   const Int4Mat* dev = upload_table(ctx, mats);
   hipLaunchKernelGGL(int4_gemv_kernel, dim3(unsigned(blocks)), dim3(kBlock), 0, ctx->stream, dev,
                      int(mats.size()), int(batch));

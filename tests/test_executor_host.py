@@ -134,3 +134,35 @@ def test_peephole_folds_add_into_layernorm_with_broadcast():
     ex.run_async()
     assert ex.output_shape("y") == ((3, 5, 8), np.dtype(np.float32))
     assert Executor.dry(graph(True)).node_count() == 2
+
+
+# (data shape, Gather axis, constant indices): the Gather feeds the Gemm
+# directly with a 2-D result. Rows: the encoder head's CLS select; a scalar
+# select on the feature axis (K = S != H); a feature-axis permutation whose
+# count equals H (the case a blind fold would get silently wrong); a row select.
+LN_GATHER_CASES = [((2, 5, 8), 1, 0), ((2, 5, 8), -1, 3), ((6, 8), 1, [3, 1, 2, 7, 0, 4, 6, 5]),
+                   ((6, 8), 0, [4, 0, 2])]
+
+
+@pytest.mark.parametrize("shape,axis,idx", LN_GATHER_CASES)
+def test_layernorm_gather_gemm_peephole_respects_axis(shape, axis, idx):
+    """LayerNorm -> Gather(constant) -> Gemm(transB): the executor moves the
+    LayerNorm into the Gemm only where the two commute (a Gather that keeps
+    whole feature rows); a feature-axis Gather applies it itself, so planning
+    a K != H product does not fail on the LayerNorm's scale size."""
+    H = shape[-1]
+    sel = np.take(np.zeros(shape), np.asarray(idx), axis=axis)
+    g = Graph()
+    g.add_initializer("g", np.ones(H, np.float32))
+    g.add_initializer("b", np.zeros(H, np.float32))
+    g.add_initializer("ix", np.asarray(idx, np.int64))
+    g.add_initializer("W", np.zeros((3, sel.shape[1]), np.float32))
+    g.add_node("FusedLayerNorm", ["x", "g", "b"], ["xn"], epsilon=1e-5)
+    g.add_node("Gather", ["xn", "ix"], ["sel"], axis=axis)
+    g.add_node("Gemm", ["sel", "W"], ["y"], transB=1)
+    g.add_output("y")
+    ex = Executor.dry(g)
+    assert ex.node_count() == 2  # the LayerNorm moved (the Gather may take it back)
+    ex.set_input("x", np.zeros(shape, np.float32))
+    ex.run_async()
+    assert ex.output_shape("y") == ((sel.shape[0], 3), np.dtype(np.float32))
