@@ -121,6 +121,21 @@ int inferc_hip_gemm_f32(inferc_hip_ctx* ctx, int trans_a, int trans_b,
                         int64_t ldb, float beta, const float* C, int c_kind,
                         int64_t ldc, const float* R, int64_t ldr, int act,
                         float* Y, int64_t ldy);
+/* inferc_hip_gemm_f32 that allocates nothing: no counterpart in the
+ * reference. It is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc). The
+ * split-K partial sums that inferc_hip_gemm_f32 keeps in the context
+ * workspace (growing it when needed) live here in a fixed 16 MiB static
+ * device array, one per device, held until the process ends. A product whose
+ * partial sums need more fails with INFERC_ERR_SHAPE before launching. Every
+ * call on one device shares that array: calls that overlap on one device
+ * (other streams, other threads) race. */
+int inferc_hip_gemm_f32_noalloc(inferc_hip_ctx* ctx, int trans_a, int trans_b,
+                                int64_t M, int64_t N, int64_t K, float alpha,
+                                const float* A, int64_t lda, const float* B,
+                                int64_t ldb, float beta, const float* C,
+                                int c_kind, int64_t ldc, const float* R,
+                                int64_t ldr, int act, float* Y, int64_t ldy);
 
 /* numpy MatMul over a flattened batch: Y[b] = A[b*stride_a] * B[b*stride_b],
  * a stride of 0 broadcasts. Replaces rt::MatMul, src/kernels/matmul.cc:63-159. */

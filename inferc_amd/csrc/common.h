@@ -287,7 +287,17 @@ struct GemmArgs {
   const float* gemv_ln_g = nullptr;
   const float* gemv_ln_b = nullptr;
   float gemv_ln_eps = 1e-5f;
+  // Split-K partial sums go to this caller-given device buffer of
+  // partial_bytes instead of the context workspace (a product that needs
+  // more fails); null: the workspace.
+  void* partial_buf = nullptr;
+  size_t partial_bytes = 0;
 };
+
+// Looks up, once per device, the device address of the allocation-free
+// GEMM's static scratch array; `device` must be current. Called when a
+// context is created.
+void init_gemm_scratch(int device);
 
 // Whether gemm() sends `a` to the batch-1 GEMV (one row of A times a [N,K]
 // B^T), the route that can apply a LayerNorm to the A row (gemv_ln_*).

@@ -108,6 +108,7 @@ int inferc_hip_create(int device, inferc_hip_ctx** out) {
       IH_HIP(hipEventCreate(&c->ev_start));
       IH_HIP(hipEventCreate(&c->ev_stop));
       c->ws(size_t(16) << 20);
+      ih::init_gemm_scratch(device);
     } catch (...) {
       if (c->stream) (void)hipStreamDestroy(c->stream);
       delete c;

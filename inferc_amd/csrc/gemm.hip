@@ -23,6 +23,10 @@
 // shapes run the 64x64 kernel with K split over blocks; partial sums land in
 // the context workspace, and a second kernel reduces them in fixed order
 // (deterministic) and applies the epilogue.
+#include <mutex>
+#include <string>
+#include <vector>
+
 #include "common.h"
 
 namespace ih {
@@ -725,8 +729,10 @@ void launch_tile(const GemmParams& p, int64_t slices, bool ta, bool tb, bool vec
 }
 
 // Chooses the tile and the K split, then launches the product (and the
-// split-K reduction when K was split).
-void run(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool ta, bool tb, bool vec) {
+// split-K reduction when K was split). The split-K partials go to
+// partial_buf (partial_bytes) when given, else to the context workspace.
+void run(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool ta, bool tb, bool vec,
+         void* partial_buf = nullptr, size_t partial_bytes = 0) {
   struct Cfg { int bm, bn, bk; };
   const int64_t cus = ctx->num_cus;
   const Cfg big{128, 128, 16}, wide{128, 64, 16}, small{64, 64, 32};
@@ -752,7 +758,15 @@ void run(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool ta, bool tb, bo
   p.k_per_split = splits > 1 ? ceil_div(ceil_div(p.K, splits), c.bk) * c.bk : (p.K > 0 ? p.K : 1);
   if (splits > 1) {
     const size_t need = size_t(slices) * size_t(splits) * size_t(p.M) * size_t(p.N) * sizeof(float);
-    p.partial = static_cast<float*>(ctx->ws(need));
+    if (partial_buf) {
+      IH_REQUIRE(need <= partial_bytes, INFERC_ERR_SHAPE,
+                 "gemm: split-K partial sums need " + std::to_string(need) +
+                     " bytes, more than the " + std::to_string(partial_bytes) +
+                     "-byte scratch of the allocation-free entry point");
+      p.partial = static_cast<float*>(partial_buf);
+    } else {
+      p.partial = static_cast<float*>(ctx->ws(need));
+    }
   }
   if (c.bn == big.bn) launch_tile<128, 128, 16>(p, slices, ta, tb, vec, ctx->stream);
   else if (c.bm == wide.bm) launch_tile<128, 64, 16>(p, slices, ta, tb, vec, ctx->stream);
@@ -871,7 +885,7 @@ void gemm(inferc_hip_ctx* ctx, const GemmArgs& a) {
                    a.stride_a % 4 == 0 && a.stride_b % 4 == 0 &&
                    (a.trans_a ? a.M % 4 == 0 : a.K % 4 == 0) &&
                    (a.trans_b ? a.K % 4 == 0 : a.N % 4 == 0);
-  run(ctx, p, a.batch, a.trans_a != 0, a.trans_b != 0, vec);
+  run(ctx, p, a.batch, a.trans_a != 0, a.trans_b != 0, vec, a.partial_buf, a.partial_bytes);
 }
 
 void gemm_qkv(inferc_hip_ctx* ctx, int64_t M, int64_t K, int64_t N, const float* X,
@@ -900,6 +914,37 @@ void gemm_qkv(inferc_hip_ctx* ctx, int64_t M, int64_t K, int64_t N, const float*
   run(ctx, p, 3, false, false, vec);
 }
 
+// ---- scratch of the allocation-free entry point ----
+// Split-K partial sums of inferc_hip_gemm_f32_noalloc: a file-scope device
+// array, one copy per device, held until the process ends. In host code
+// `scratch` names a host-side stand-in, never the device memory; kernels get
+// the address looked up by init_gemm_scratch.
+constexpr size_t kGemmScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kGemmScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // device address of `scratch`, by device
+}  // namespace
+
+void init_gemm_scratch(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  IH_REQUIRE(device >= 0, INFERC_ERR_ARG, "gemm scratch: bad device");
+  if (g_scratch_ptr.size() <= size_t(device)) g_scratch_ptr.resize(size_t(device) + 1, nullptr);
+  if (g_scratch_ptr[size_t(device)]) return;
+  void* ptr = nullptr;
+  IH_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  IH_REQUIRE(ptr != nullptr, INFERC_ERR_HIP, "gemm scratch: no device address");
+  g_scratch_ptr[size_t(device)] = ptr;
+}
+
+void* gemm_scratch(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  IH_REQUIRE(size_t(device) < g_scratch_ptr.size() && g_scratch_ptr[size_t(device)],
+             INFERC_ERR_STATE, "gemm scratch: not set up for this device");
+  return g_scratch_ptr[size_t(device)];
+}
+
 }  // namespace ih
 
 extern "C" {
@@ -916,6 +961,25 @@ int inferc_hip_gemm_f32(inferc_hip_ctx* ctx, int trans_a, int trans_b, int64_t M
     a.A = A; a.lda = lda; a.B = B; a.ldb = ldb;
     a.C = C; a.c_kind = c_kind; a.ldc = ldc;
     a.R = R; a.ldr = ldr; a.act = act; a.Y = Y; a.ldy = ldy;
+    ih::gemm(ctx, a);
+  });
+}
+
+int inferc_hip_gemm_f32_noalloc(inferc_hip_ctx* ctx, int trans_a, int trans_b, int64_t M,
+                                int64_t N, int64_t K, float alpha, const float* A, int64_t lda,
+                                const float* B, int64_t ldb, float beta, const float* C,
+                                int c_kind, int64_t ldc, const float* R, int64_t ldr, int act,
+                                float* Y, int64_t ldy) {
+  return ih::guard([&] {
+    ih::check_ctx(ctx)->make_current();
+    ih::GemmArgs a;
+    a.trans_a = trans_a; a.trans_b = trans_b;
+    a.M = M; a.N = N; a.K = K; a.alpha = alpha; a.beta = beta;
+    a.A = A; a.lda = lda; a.B = B; a.ldb = ldb;
+    a.C = C; a.c_kind = c_kind; a.ldc = ldc;
+    a.R = R; a.ldr = ldr; a.act = act; a.Y = Y; a.ldy = ldy;
+    a.partial_buf = ih::gemm_scratch(ctx->device);
+    a.partial_bytes = ih::kGemmScratchBytes;
     ih::gemm(ctx, a);
   });
 }

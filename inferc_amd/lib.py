@@ -68,6 +68,8 @@ _SIGS = {
     "inferc_hip_capture_destroy": [vp],
     "inferc_hip_gemm_f32": [vp, i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i32,
                             i64, vp, i64, i32, vp, i64],
+    "inferc_hip_gemm_f32_noalloc": [vp, i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp,
+                                    i32, i64, vp, i64, i32, vp, i64],
     "inferc_hip_matmul_f32": [vp, i64, i64, i64, i64, vp, i64, vp, i64, vp],
     "inferc_hip_fused_matmul_add_gelu_f32": [vp, i64, i64, i64, vp, vp, vp, vp],
     "inferc_hip_fused_qkv_f32": [vp, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
