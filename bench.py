@@ -221,86 +221,277 @@ def bench_int4(ctx, batch: int, copies: int = 5, reps: int = 240):
             "copies_rotated": copies}
 
 
-def roofline_ffn_up_gemm(ctx, reps: int = 200):
-    """Dominant kernel of the primary workload: the FFN-up GEMM with the fused
-    bias + erf-GELU epilogue at the b=1, s=128 shape (M=128, N=3072, K=768),
-    launched through the C-ABI exactly as the executor launches it, timed
-    with HIP events over `reps` back-to-back launches."""
+# The kernel with the most time per encoder forward at b=1: the residual
+# GEMMs (out-proj and FFN-down, 12 launches per forward) run one template,
+# gemm_f32_ksplit<16,32,8,2>; its largest launch is the FFN-down,
+# Y = X[128,3072] W[3072,768] + b + residual.
+ROOF_M, ROOF_N, ROOF_K = 128, 768, 3072
+ROOF_KERNEL = "gemm_f32_ksplit<16,32,8,2>"
+
+
+def _roofline_operands(ctx):
     from inferc_amd import graphs, rt
 
-    M, N, K = 128, 3072, 768
+    M, N, K = ROOF_M, ROOF_N, ROOF_K
     x = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rx", (M, K), 1.0))
     w = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rw", (K, N)))
     b = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rb", (N,)))
+    r = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rr", (M, N), 1.0))
     y = rt.Tensor.empty(ctx, (M, N))
     lib = ctx._lib
 
     def launch():
-        rc = lib.inferc_hip_fused_matmul_add_gelu_f32(ctx.handle, M, N, K, x.ptr, w.ptr, b.ptr,
-                                                       y.ptr)
-        if rc:
-            from inferc_amd.lib import check
-            check(rc)
+        from inferc_amd import lib as L
 
+        L.check(lib.inferc_hip_gemm_f32(ctx.handle, 0, 0, M, N, K, C.c_float(1.0), x.ptr, K,
+                                        w.ptr, N, C.c_float(1.0), b.ptr, L.C_ROW, 0, r.ptr, N,
+                                        L.ACT_NONE, y.ptr, N))
+
+    return launch, (x, w, b, r, y)
+
+
+def roofline_kernel(ctx, reps: int = 400):
+    """Roofline of the dominant kernel of the primary workload: the residual
+    GEMM template at the encoder's FFN-down shape (M=128, N=768, K=3072,
+    bias row + residual epilogue), launched through the C-ABI, timed with
+    HIP events on the context stream over back-to-back replays of a captured
+    sequence of 20 launches (the stream the kernel runs on)."""
+    M, N, K = ROOF_M, ROOF_N, ROOF_K
+    launch, keep = _roofline_operands(ctx)
     launch()
     per_graph = 20
     cap = ctx.capture(lambda: [launch() for _ in range(per_graph)])
     ms = time_replays(ctx, cap, per_graph, reps)
+    del keep
     flops = 2.0 * M * N * K
     achieved = flops / (ms * 1e-3) / 1e12
     traffic = None
     tf = ROOT / "profiles" / "traffic.json"
     if tf.exists():
-        traffic = json.loads(tf.read_text()).get("gemm_ffn_up_b1")
+        traffic = json.loads(tf.read_text()).get("gemm_residual_ffn_down_b1")
     return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-            "traffic": traffic, "kernel": "gemm_f32_ksplit<32,48,8,2> (FusedMatMulAddGELU)",
+            "traffic": traffic,
+            "kernel": f"{ROOF_KERNEL} (residual GEMM: the encoder's out-proj and FFN-down)",
             "shape": [M, N, K], "algorithmic_flops_per_launch": flops,
+            "algorithmic_bytes_per_launch": 4 * (M * K + K * N + N + 2 * M * N),
             "avg_launch_us": round(ms * 1e3, 3)}
 
 
-def roofline_only(ctx, launches: int = 50) -> dict:
-    """For counter runs (rocprofv3 --pmc): `launches` eager launches of the
-    roofline kernel, then one 64 MiB device-to-device copy whose FETCH_SIZE /
-    WRITE_SIZE calibrate the counters (the copy moves exactly 64 MiB each way)."""
-    from inferc_amd import graphs, rt
+COUNTER_PARTS = ("encoder", "roofline", "int4", "decode")
 
-    M, N, K = 128, 3072, 768
-    x = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rx", (M, K), 1.0))
-    w = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rw", (K, N)))
-    b = rt.Tensor.from_numpy(ctx, graphs.normal(9, "rb", (N,)))
-    y = rt.Tensor.empty(ctx, (M, N))
-    for _ in range(launches):
-        rc = ctx._lib.inferc_hip_fused_matmul_add_gelu_f32(ctx.handle, M, N, K, x.ptr, w.ptr,
-                                                            b.ptr, y.ptr)
-        if rc:
-            from inferc_amd.lib import check
-            check(rc)
+
+def counters_workload(ctx, parts=COUNTER_PARTS) -> dict:
+    """For rocprofv3 --pmc runs: eager dispatches of the kernels the counter
+    summaries cover, then one 64 MiB device copy whose FETCH_SIZE /
+    WRITE_SIZE calibrate the counters (the copy moves 64 MiB each way).
+    - encoder: 3 forwards at b=1 and 1 at b=32 (graph mode off);
+    - roofline: 10 launches of the roofline kernel;
+    - int4: 3 launches of the 49-matrix int4 GEMV at B=1 and at B=8 on each
+      of 5 weight copies (316 MB per rotation, so weights stream from HBM);
+    - decode: 8-token greedy decodes, fp32 and int4 (steps replayed from the
+      step graph)."""
+    from inferc_amd import graphs, rt
+    from inferc_amd.lib import check
+
+    if "encoder" in parts:
+        cfg = graphs.DISTILBERT
+        w = graphs.encoder_weights(cfg, 1)
+        for B, n in ((1, 3), (32, 1)):
+            ex = rt.Executor(ctx, graphs.encoder_graph(cfg, w))
+            ex.set_graph_mode(False)
+            ids, mask = graphs.encoder_inputs(cfg, B, 128)
+            keep = device_inputs(ctx, ex, {"input_ids": ids, "attention_mask": mask})
+            for _ in range(n):
+                ex.run_async()
+            ctx.sync()
+            del keep
+            ex.close()
+    if "roofline" in parts:
+        launch, keep = _roofline_operands(ctx)
+        for _ in range(10):
+            launch()
+        ctx.sync()
+        del keep
+    shapes = graphs.int4_matrices()
+    for B in ((1, 8) if "int4" in parts else ()):
+        sets = []
+        for c in range(5):
+            mats = []
+            for i, (N, K) in enumerate(shapes):
+                W, s = graphs.int4_weights(N, K, 100 + c, f"b{i}")
+                mats.append((rt.Tensor.from_numpy(ctx, W), rt.Tensor.from_numpy(ctx, s),
+                             rt.Tensor.from_numpy(ctx, graphs.normal(200 + c, f"x{i}_{B}",
+                                                                     (B, K), std=1.0)),
+                             rt.Tensor.empty(ctx, (B, N)), K))
+            sets.append(mats)
+        for _ in range(3):
+            for mats in sets:
+                rt.int4_gemv_grouped(ctx, mats, B)
+        ctx.sync()
+        del sets
+    if "decode" in parts:
+        gcfg = graphs.GPT2_SMALL
+        dec = rt.Gpt2Decoder(ctx, gcfg, graphs.gpt2_weights(gcfg, 2), max_t=64)
+        prompt = graphs.gpt2_prompt(gcfg, 32)
+        dec.generate(prompt, 8)
+        dec.use_int4()
+        dec.generate(prompt, 8)
+        dec.close()
     nbytes = 64 << 20
     src, dst = rt.Tensor.empty(ctx, (nbytes // 4,)), rt.Tensor.empty(ctx, (nbytes // 4,))
     ctx.sync()
-    from inferc_amd.lib import check
     check(ctx._lib.inferc_hip_d2d(ctx.handle, dst.ptr, src.ptr, nbytes))
     ctx.sync()
-    return {"roofline_kernel_launches": launches, "copy_bytes": nbytes,
-            "algorithmic_bytes_per_launch": 4 * (M * K + K * N + N + M * N)}
+    return {"copy_bytes": nbytes, "parts": list(parts),
+            "roofline_shape": [ROOF_M, ROOF_N, ROOF_K]}
 
 
-def cpu_baseline_encoder(weights, budget_s: float = 12.0):
+def cpu_info() -> dict:
+    """CPU model name, physical cores (distinct (package, core) pairs in
+    /proc/cpuinfo), logical CPUs and the CPUs this process may run on."""
+    model, cores = "unknown", set()
+    try:
+        for block in Path("/proc/cpuinfo").read_text().split("\n\n"):
+            kv = {}
+            for line in block.splitlines():
+                if ":" in line:
+                    k, v = line.split(":", 1)
+                    kv[k.strip()] = v.strip()
+            if "model name" in kv:
+                model = kv["model name"]
+            if "core id" in kv:
+                cores.add((kv.get("physical id", "0"), kv["core id"]))
+    except OSError:
+        pass
+    return {"model": model, "physical_cores": len(cores) or None,
+            "logical_cpus": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0))}
+
+
+def _time_cpu(fn, budget_s: float, max_n: int = 1000,
+              min_n: int = 1) -> tuple[float, float, int]:
+    """(min, mean) seconds of fn over as many calls as fit in budget_s (at
+    least min_n, at most max_n, after one untimed call)."""
+    fn()
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < min_n or (time.perf_counter() < t_end and len(ts) < max_n):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return min(ts), sum(ts) / len(ts), len(ts)
+
+
+def cpu_decode_ms_per_token(cfg, w, prompt, steps: int) -> float:
+    """Mean ms of the oracle GPT-2's greedy decode steps after `prompt`, each
+    step timed by the oracle itself around its forward and LM head
+    (main.cpp:863-872); the prefill is not timed."""
+    import oracle as O
+
+    return float(np.mean(O.gpt2_decode_step_ms(cfg, w, prompt, 1 + steps)))
+
+
+def cpu_baseline(enc_w, gpt2_w, full: bool) -> dict:
+    """The C oracle (this repo's restatement of inferc's CPU kernels) timed on
+    the host's cores, all cores (OpenMP default) and 1 thread, on bounded
+    samples of every config: encoder b1 (the `value` workload) and b32,
+    FFN+LN M=128, QKV+MHA S=128, GPT-2 decode steps at cache lengths 32-47
+    and 144-159 (config 4 spans 32-159), and the 49-matrix int4 GEMV at B=1
+    and B=8 with GB/s as streamed int4 bytes / best time
+    (bench/amx/int4_gemv_amx.cc:556-567)."""
     import oracle as O
     from inferc_amd import graphs
 
+    info = cpu_info()
+    all_t = O.num_threads()
     cfg = graphs.DISTILBERT
-    ids, mask = graphs.encoder_inputs(cfg, 1, 128)
-    O.encoder_forward(cfg, weights, ids, mask)  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        O.encoder_forward(cfg, weights, ids, mask)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 200:
-            break
-    return el / n * 1e3, n, O.num_threads()
+    ids1, mask1 = graphs.encoder_inputs(cfg, 1, 128)
+    res = {"threads_all": all_t, "cpu": info, "configs": {}}
+    c = res["configs"]
+
+    def timed(name, fn, budget_all, budget_1, unit_ms=True):
+        row = {}
+        for th, budget in ((all_t, budget_all), (1, budget_1)):
+            if budget is None:
+                continue
+            O.set_num_threads(th)
+            try:
+                best, mean, n = _time_cpu(fn, budget)
+            finally:
+                O.set_num_threads(all_t)
+            key = "all" if th == all_t else "1t"
+            row[key] = {"ms": round(mean * 1e3, 3), "ms_min": round(best * 1e3, 3), "n": n}
+        c[name] = row
+        return row
+
+    log("  cpu: encoder b1 s128")
+    timed("encoder_b1_s128", lambda: O.encoder_forward(cfg, enc_w, ids1, mask1), 6.0, 2.0)
+    if full:
+        ids32, mask32 = graphs.encoder_inputs(cfg, 32, 128)
+        log("  cpu: encoder b32 s128")
+        timed("encoder_b32_s128", lambda: O.encoder_forward(cfg, enc_w, ids32, mask32), 2.0, None)
+        g, x = ffn_ln_graph(128)
+        w1, b1, w2, b2 = (g.initializer(n) for n in ("w1", "b1", "w2", "b2"))
+        ones, zeros = np.ones(768, np.float32), np.zeros(768, np.float32)
+
+        def ffn():
+            f = O.fused_matmul_add_gelu(x, w1, b1)
+            return O.layernorm(O.add_bcast(O.matmul(f, w2), b2), ones, zeros, 1e-12)
+
+        log("  cpu: ffn+ln M=128")
+        timed("ffn_ln_m128", ffn, 2.0, 1.0)
+        g, xq, mask, _ = qkv_mha_graph(128)
+        qw = [g.initializer(n) for n in ("wq", "bq", "wk", "bk", "wv", "bv")]
+        x2 = xq.reshape(-1, 768)
+
+        def qkv_mha():
+            q, k, v = O.fused_qkv(x2, *qw)
+            return O.fused_attention(q.reshape(32, 128, 768), k.reshape(32, 128, 768),
+                                     v.reshape(32, 128, 768), mask, 64, graphs.FILL_MIN)
+
+        log("  cpu: qkv+mha S=128")
+        timed("qkv_mha_b32_s128", qkv_mha, 2.0, None)
+        gcfg = graphs.GPT2_SMALL
+        dec = {}
+        for lo, steps_all, steps_1 in ((32, 15, 6), (144, 15, 6)):
+            prompt = graphs.gpt2_prompt(gcfg, lo, seed=11)
+            log(f"  cpu: gpt2 decode, cache {lo}..{lo + steps_all}")
+            row = {}
+            for th, steps in ((all_t, steps_all), (1, steps_1)):
+                O.set_num_threads(th)
+                try:
+                    ms = cpu_decode_ms_per_token(gcfg, gpt2_w, prompt, steps)
+                finally:
+                    O.set_num_threads(all_t)
+                row["all" if th == all_t else "1t"] = {"ms_per_token": round(ms, 3),
+                                                       "steps": steps}
+            dec[f"cache_{lo}_{lo + steps_all}"] = row
+        c["gpt2_decode"] = dec
+        shapes = graphs.int4_matrices()
+        mats = [graphs.int4_weights(N, K, 100, f"b{i}") for i, (N, K) in enumerate(shapes)]
+        int4_bytes = sum(N * K for N, K in shapes) // 2
+        for B in (1, 8):
+            xs = [graphs.normal(200, f"x{i}_{B}", (B, K), std=1.0)
+                  for i, (_, K) in enumerate(shapes)]
+
+            def sweep():
+                for (W, sc), xb, (_, K) in zip(mats, xs, shapes):
+                    O.int4_gemv_f32acc(W, sc, xb, K)
+
+            log(f"  cpu: int4 GEMV sweep B={B}")
+            row = {}
+            for th in (all_t, 1):
+                reps = 6 if th == all_t else 2  # best of 6, as int4_gemv_amx.cc:558-566
+                O.set_num_threads(th)
+                try:
+                    best, mean, n = _time_cpu(sweep, 0.0, reps, reps)
+                finally:
+                    O.set_num_threads(all_t)
+                row["all" if th == all_t else "1t"] = {
+                    "ms_min": round(best * 1e3, 3), "n": n,
+                    "gbps_int4": round(int4_bytes / best / 1e9, 2)}
+            c[f"int4_gemv_b{B}"] = row
+    return res
 
 
 def cpu_profile_encoder(weights, B: int = 1, S: int = 128, iters: int = 3):
@@ -405,20 +596,6 @@ def write_profiles(ctx, out_dir: str, enc_w) -> None:
     dec.close()
 
 
-def cpu_baseline_decode(weights, prompt, tokens: int = 6):
-    import oracle as O
-    from inferc_amd import graphs
-
-    cfg = graphs.GPT2_SMALL
-    t0 = time.perf_counter()
-    O.gpt2_generate(cfg, weights, prompt[:8], 1)
-    prefill = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    O.gpt2_generate(cfg, weights, prompt[:8], tokens + 1)
-    total = time.perf_counter() - t0
-    return (total - prefill) / tokens * 1e3
-
-
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -426,8 +603,13 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="primary workload and roofline only")
+    ap.add_argument("--counters", nargs="*", choices=COUNTER_PARTS, default=None,
+                    help="eager dispatches of the profiled kernels (all parts, or the "
+                         "ones named) + a calibration copy (for rocprofv3 --pmc runs)")
     ap.add_argument("--roofline-only", action="store_true",
-                    help="roofline kernel + calibration copy only (for rocprofv3 --pmc runs)")
+                    help="the roofline kernel's timed replays only, printed as JSON")
+    ap.add_argument("--encoder-only", type=int, nargs="?", const=1, default=None,
+                    metavar="B", help="the encoder forward at batch B only, as text")
     ap.add_argument("--decode-only", nargs="?", const="both", choices=["fp32", "int4", "both"],
                     help="GPT-2 decode only (fp32 weights, int4 weights or both), one "
                          "generate each, printed as text (for rocprofv3 --kernel-trace runs)")
@@ -445,8 +627,18 @@ def main(argv=None) -> int:
     from inferc_amd import graphs, rt
 
     ctx = rt.Context(0)
+    if args.counters is not None:
+        print(json.dumps(counters_workload(ctx, tuple(args.counters) or COUNTER_PARTS)),
+              flush=True)
+        ctx.close()
+        return 0
     if args.roofline_only:
-        print(json.dumps(roofline_only(ctx)), flush=True)
+        print(json.dumps(roofline_kernel(ctx)), flush=True)
+        ctx.close()
+        return 0
+    if args.encoder_only is not None:
+        ms, _, _ = bench_encoder(ctx, args.encoder_only, args.steps, args.warmup)
+        print(f"encoder b{args.encoder_only} s128: {ms:.4f} ms/forward", flush=True)
         ctx.close()
         return 0
     if args.decode_only:
@@ -465,7 +657,7 @@ def main(argv=None) -> int:
                                                         PEAK_FP32_TFLOPS, 4)}
     log(f"  {ms_b1:.4f} ms/forward")
     log("roofline kernel")
-    roof = roofline_ffn_up_gemm(ctx)
+    roof = roofline_kernel(ctx)
     log(f"  {roof['avg_launch_us']} us, {roof['achieved']} TFLOP/s")
 
     dec = None
@@ -523,15 +715,18 @@ def main(argv=None) -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        log("cpu baseline (oracle) encoder b1 s128")
-        cms, n, thr = cpu_baseline_encoder(enc_w)
-        cpu = {"value": round(cms, 3), "unit": "ms", "cores": thr, "kind": "port",
-               "sample": f"{n} encoder forwards at b1 s128 (C oracle, OpenMP {thr} threads)"}
-        if dec is not None:
-            cdec = cpu_baseline_decode(gw, prompt)
-            cpu["gpt2_decode_ms_per_token"] = round(cdec, 3)
-            cpu["sample"] += "; GPT-2 decode 6 tokens after an 8-token prompt"
-        log(f"  {cms:.2f} ms/forward on {thr} threads")
+        log("cpu baseline (oracle)")
+        gpt2_w = None if args.quick else gw
+        cb = cpu_baseline(enc_w, gpt2_w, full=not args.quick)
+        b1 = cb["configs"]["encoder_b1_s128"]
+        thr = cb["threads_all"]
+        cpu = {"value": b1["all"]["ms"], "unit": "ms", "cores": thr, "kind": "port",
+               "sample": (f"{b1['all']['n']} encoder forwards at b1 s128 on {thr} OpenMP "
+                          f"threads ({b1['1t']['n']} on 1 thread) of the C oracle; other "
+                          "configs in `configs`, each on a bounded sample (see its n / "
+                          "steps)"),
+               "value_1_thread": b1["1t"]["ms"], "cpu": cb["cpu"], "configs": cb["configs"]}
+        log(f"  {cpu['value']:.2f} ms/forward on {thr} threads, {cpu['value_1_thread']:.2f} on 1")
 
     if args.profile_dir:
         log(f"per-op profiles -> {args.profile_dir}")

@@ -39,6 +39,7 @@ def load():
     sig = {
         "orc_num_threads": ([], C.c_int),
         "orc_set_num_threads": ([C.c_int], None),
+        "orc_parallel_blocks": ([i64, i64, i64, I64, I64], i64),
         "orc_sgemm": ([C.c_int, C.c_int, i64, i64, i64, f32, F, i64, F, i64, f32, F, i64], None),
         "orc_matmul": ([i64, i64, i64, i64, F, i64, F, i64, F], None),
         "orc_gemm": ([C.c_int, C.c_int, i64, i64, i64, f32, F, F, f32, F, C.c_int, F], None),
@@ -63,6 +64,8 @@ def load():
         "orc_sgemv_rows": ([i64, i64, F, F, F], None),
         "orc_encoder_forward": ([C.c_void_p, C.POINTER(F), i64, i64, I64, I64, F], C.c_int),
         "orc_gpt2_generate": ([C.c_void_p, C.POINTER(F), I64, i64, i64, I64, F, F], C.c_int),
+        "orc_gpt2_generate_timed": ([C.c_void_p, C.POINTER(F), I64, i64, i64, I64, F, F,
+                                     C.POINTER(C.c_double)], C.c_int),
         "orc_gpt2_forward": ([C.c_void_p, C.POINTER(F), I64, i64, F], C.c_int),
     }
     for name, (args, res) in sig.items():
@@ -87,6 +90,16 @@ def num_threads() -> int:
 
 def set_num_threads(n: int) -> None:
     load().orc_set_num_threads(n)
+
+
+def parallel_blocks(n: int, grain: int, max_threads: int) -> list[tuple[int, int]]:
+    """par::ParallelFor's [begin, end) blocks (src/util/parallel.cc:49-72)."""
+    cap = max(1, max_threads)
+    b = np.zeros(cap, np.int64)
+    e = np.zeros(cap, np.int64)
+    k = load().orc_parallel_blocks(n, grain, max_threads, b.ctypes.data_as(I64),
+                                   e.ctypes.data_as(I64))
+    return list(zip(b[:k].tolist(), e[:k].tolist()))
 
 
 def sgemm(a, b, trans_a=False, trans_b=False, alpha=1.0, beta=0.0, c=None):
@@ -355,6 +368,23 @@ def gpt2_generate(cfg: dict, weights, prompt, max_tokens):
     if rc != 0:
         raise RuntimeError("gpt2_generate: bad token id or sequence too long")
     return toks, logits, margins
+
+
+def gpt2_decode_step_ms(cfg: dict, weights, prompt, max_tokens) -> np.ndarray:
+    """Wall time in ms of each of the max_tokens - 1 decode steps after the
+    prompt (the step's forward and LM head; main.cpp:863-872)."""
+    p = np.ascontiguousarray(prompt, dtype=np.int64)
+    ws, ptrs = _wptrs(weights)
+    c = _Gpt2Cfg(cfg["layers"], cfg["hidden"], cfg["heads"], cfg["ffn"], cfg["vocab"],
+                 cfg["max_pos"], cfg["eps"])
+    toks = np.empty(max_tokens, np.int64)
+    ms = np.zeros(max(1, max_tokens - 1), np.float64)
+    rc = load().orc_gpt2_generate_timed(C.byref(c), ptrs, p.ctypes.data_as(I64), p.size,
+                                        max_tokens, toks.ctypes.data_as(I64), None, None,
+                                        ms.ctypes.data_as(C.POINTER(C.c_double)))
+    if rc != 0:
+        raise RuntimeError("gpt2_generate: bad token id or sequence too long")
+    return ms[: max_tokens - 1]
 
 
 def gpt2_forward(cfg: dict, weights, ids):

@@ -16,6 +16,7 @@
 #ifdef _OPENMP
 #include <omp.h>
 #endif
+#include <time.h>
 
 int orc_num_threads(void) {
 #ifdef _OPENMP
@@ -31,6 +32,26 @@ void orc_set_num_threads(int n) {
 #else
   (void)n;
 #endif
+}
+
+int64_t orc_parallel_blocks(int64_t n, int64_t grain, int64_t max_threads,
+                            int64_t* begin, int64_t* end) {
+  if (n <= 0) return 0;
+  const int64_t max_blocks = max_threads > 1 ? max_threads : 1;
+  const int64_t by_grain = grain > 0 ? (n + grain - 1) / grain : max_blocks;
+  int64_t blocks = by_grain > 1 ? by_grain : 1;
+  if (blocks > max_blocks) blocks = max_blocks;
+  const int64_t chunk = (n + blocks - 1) / blocks;
+  int64_t out = 0;
+  for (int64_t b = 0; b < blocks; ++b) {
+    const int64_t lo = b * chunk, hi = lo + chunk < n ? lo + chunk : n;
+    if (lo < hi) {
+      begin[out] = lo;
+      end[out] = hi;
+      ++out;
+    }
+  }
+  return out;
 }
 
 /* numpy MatMul over a flattened batch (src/kernels/matmul.cc:63-159): one
@@ -513,12 +534,24 @@ static int gpt2_block_run(gpt2_state* st, const int64_t* ids, int64_t n,
   return rc;
 }
 
-/* logits[n,V] = hrows[n,H] * wte^T: the LM head reads wte rows directly, which
- * is the same product as the reference's MatMul against the folded wte^T. */
-static void gpt2_lm_head(const orc_gpt2_cfg* cfg, const float* wte,
+/* wte^T [H,V], materialized once per model run as FoldConstantTranspose does
+ * when it folds the LM head's Transpose into a new initializer
+ * (constant_fold.cc:12-54); NULL if the allocation fails. */
+static float* gpt2_fold_wte_t(const orc_gpt2_cfg* cfg, const float* wte) {
+  const int64_t H = cfg->hidden, V = cfg->vocab;
+  float* t = (float*)malloc(sizeof(float) * (size_t)(H * V));
+  if (!t) return NULL;
+#pragma omp parallel for schedule(static)
+  for (int64_t c = 0; c < H; ++c)
+    for (int64_t v = 0; v < V; ++v) t[c * V + v] = wte[v * H + c];
+  return t;
+}
+
+/* logits[n,V] = hrows[n,H] * wte^T, the MatMul against the folded wte^T. */
+static void gpt2_lm_head(const orc_gpt2_cfg* cfg, const float* wte_t,
                          const float* hrows, int64_t n, float* logits) {
-  orc_sgemm(0, 1, n, cfg->vocab, cfg->hidden, 1.0f, hrows, cfg->hidden, wte,
-            cfg->hidden, 0.0f, logits, cfg->vocab);
+  orc_sgemm(0, 0, n, cfg->vocab, cfg->hidden, 1.0f, hrows, cfg->hidden, wte_t,
+            cfg->vocab, 0.0f, logits, cfg->vocab);
 }
 
 int orc_gpt2_forward(const orc_gpt2_cfg* cfg, const float* const* w,
@@ -529,9 +562,10 @@ int orc_gpt2_forward(const orc_gpt2_cfg* cfg, const float* const* w,
   st.kc = (float*)malloc(sizeof(float) * (size_t)(cfg->layers * nH * n * hd));
   st.vc = (float*)malloc(sizeof(float) * (size_t)(cfg->layers * nH * n * hd));
   float* hrows = (float*)malloc(sizeof(float) * (size_t)(n * cfg->hidden));
-  int rc = gpt2_block_run(&st, ids, n, 0, hrows);
-  if (rc == 0) gpt2_lm_head(cfg, w[0], hrows, n, logits);
-  free(st.kc); free(st.vc); free(hrows);
+  float* wte_t = gpt2_fold_wte_t(cfg, w[0]);
+  int rc = wte_t ? gpt2_block_run(&st, ids, n, 0, hrows) : -1;
+  if (rc == 0) gpt2_lm_head(cfg, wte_t, hrows, n, logits);
+  free(st.kc); free(st.vc); free(hrows); free(wte_t);
   return rc;
 }
 
@@ -542,10 +576,24 @@ static float top2_margin(int64_t n, const float* x, int64_t best) {
   return x[best] - second;
 }
 
+static double now_ms(void) {
+  struct timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return (double)ts.tv_sec * 1e3 + (double)ts.tv_nsec * 1e-6;
+}
+
 int orc_gpt2_generate(const orc_gpt2_cfg* cfg, const float* const* w,
                       const int64_t* prompt, int64_t n_prompt,
                       int64_t max_tokens, int64_t* tokens_out,
                       float* last_logits, float* margins) {
+  return orc_gpt2_generate_timed(cfg, w, prompt, n_prompt, max_tokens, tokens_out,
+                                 last_logits, margins, NULL);
+}
+
+int orc_gpt2_generate_timed(const orc_gpt2_cfg* cfg, const float* const* w,
+                            const int64_t* prompt, int64_t n_prompt,
+                            int64_t max_tokens, int64_t* tokens_out,
+                            float* last_logits, float* margins, double* step_ms) {
   if (n_prompt <= 0 || max_tokens <= 0) return -1;
   gpt2_state st;
   st.cfg = cfg; st.w = w; st.tmax = n_prompt + max_tokens;
@@ -554,18 +602,22 @@ int orc_gpt2_generate(const orc_gpt2_cfg* cfg, const float* const* w,
   st.vc = (float*)calloc((size_t)(cfg->layers * nH * st.tmax * hd), sizeof(float));
   float* hrows = (float*)malloc(sizeof(float) * (size_t)(n_prompt * cfg->hidden));
   float* logits = (float*)malloc(sizeof(float) * (size_t)V);
+  float* wte_t = gpt2_fold_wte_t(cfg, w[0]);
   /* prefill; only the last position's logits are read (main.cpp:820-828) */
-  int rc = gpt2_block_run(&st, prompt, n_prompt, 0, hrows);
+  int rc = wte_t ? gpt2_block_run(&st, prompt, n_prompt, 0, hrows) : -1;
   if (rc == 0) {
-    gpt2_lm_head(cfg, w[0], hrows + (n_prompt - 1) * cfg->hidden, 1, logits);
+    gpt2_lm_head(cfg, wte_t, hrows + (n_prompt - 1) * cfg->hidden, 1, logits);
     int64_t next = orc_argmax(V, logits);
     tokens_out[0] = next;
     if (margins) margins[0] = top2_margin(V, logits, next);
     int64_t pos = n_prompt;
     for (int64_t step = 1; step < max_tokens && rc == 0; ++step) {
+      /* the step's forward only, as main.cpp:863-872 times it */
+      const double t0 = step_ms ? now_ms() : 0.0;
       rc = gpt2_block_run(&st, &next, 1, pos, hrows);
       if (rc != 0) break;
-      gpt2_lm_head(cfg, w[0], hrows, 1, logits);
+      gpt2_lm_head(cfg, wte_t, hrows, 1, logits);
+      if (step_ms) step_ms[step - 1] = now_ms() - t0;
       next = orc_argmax(V, logits);
       tokens_out[step] = next;
       if (margins) margins[step] = top2_margin(V, logits, next);
@@ -573,6 +625,6 @@ int orc_gpt2_generate(const orc_gpt2_cfg* cfg, const float* const* w,
     }
     if (rc == 0 && last_logits) memcpy(last_logits, logits, sizeof(float) * (size_t)V);
   }
-  free(st.kc); free(st.vc); free(hrows); free(logits);
+  free(st.kc); free(st.vc); free(hrows); free(logits); free(wte_t);
   return rc;
 }

@@ -34,6 +34,13 @@ enum { ORC_C_NONE = 0, ORC_C_ROW = 1, ORC_C_FULL = 2, ORC_C_SCALAR = 3 };
 
 int orc_num_threads(void);
 void orc_set_num_threads(int n);
+/* par::ParallelFor's partition of [0, n) (src/util/parallel.cc:49-72):
+ * blocks = min(max_threads, max(1, ceil(n / grain))) (grain <= 0: max_threads
+ * blocks), chunk = ceil(n / blocks), block b = [b*chunk, min(n, b*chunk +
+ * chunk)), empty blocks skipped. Writes the non-empty blocks' bounds (room
+ * for max(1, max_threads) entries) and returns their count; n <= 0 gives 0. */
+int64_t orc_parallel_blocks(int64_t n, int64_t grain, int64_t max_threads,
+                            int64_t* begin, int64_t* end);
 
 /* C[M,N] = alpha*op(A)*op(B) + beta*C (row-major, leading dims in elements). */
 void orc_sgemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
@@ -141,6 +148,14 @@ int orc_gpt2_generate(const orc_gpt2_cfg* cfg, const float* const* w,
                       const int64_t* prompt, int64_t n_prompt,
                       int64_t max_tokens, int64_t* tokens_out,
                       float* last_logits, float* margins);
+/* orc_gpt2_generate that also writes each decode step's wall time in ms
+ * (step_ms[max_tokens-1], nullable): the step's forward and LM head, not
+ * the argmax or the prefill, as the reference's step timer
+ * (src/cli/main.cpp:863-872). */
+int orc_gpt2_generate_timed(const orc_gpt2_cfg* cfg, const float* const* w,
+                            const int64_t* prompt, int64_t n_prompt,
+                            int64_t max_tokens, int64_t* tokens_out,
+                            float* last_logits, float* margins, double* step_ms);
 
 /* full-sequence GPT-2 forward logits for every position: logits [n, vocab]. */
 int orc_gpt2_forward(const orc_gpt2_cfg* cfg, const float* const* w,
