@@ -5,7 +5,14 @@ only, then linked into one shared library that exports the C-ABI declared in
 ``include/inferc_hip.h``. Packed-fp32 VALU instructions are disabled
 (``-target-feature -packed-fp32-ops``) for all device code.
 
-Usage: ``python -m inferc_amd.build [--jobs N]``.
+Usage: ``python -m inferc_amd.build [--jobs N] [--sanitize]``.
+
+``--sanitize`` builds ``libinferc_hip_san.so`` instead (objects under
+``_build_san/``): the host code compiled with AddressSanitizer and
+UndefinedBehaviorSanitizer (each ``-fsanitize=`` applies to the host pass
+only, through ``-Xarch_host``; device code is unchanged). It is for the CPU
+tests (``tests/run_sanitized.sh``), which load it through ``INFERC_HIP_LIB``
+with the clang ASan runtime preloaded.
 """
 from __future__ import annotations
 
@@ -21,6 +28,12 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libinferc_hip.so"
+BUILD_SAN = PKG / "_build_san"
+LIB_SAN = PKG / "libinferc_hip_san.so"
+# host-pass-only sanitizer flags (compile and link)
+SAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+             "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer",
+             "-Xarch_host", "-g"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -36,40 +49,45 @@ CXXFLAGS = [
 ]
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *CXXFLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, out_dir: Path = BUILD, extra: tuple = ()) -> Path:
+    obj = out_dir / (src.stem + ".o")
+    cmd = [HIPCC, *CXXFLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
+def build(jobs: int | None = None, verbose: bool = False, sanitize: bool = False) -> Path:
     """Compiles all HIP sources and links the library; returns its path."""
-    BUILD.mkdir(exist_ok=True)
+    out_dir, lib = (BUILD_SAN, LIB_SAN) if sanitize else (BUILD, LIB)
+    extra = tuple(SAN_FLAGS) if sanitize else ()
+    out_dir.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     jobs = jobs or min(len(sources), os.cpu_count() or 4, 8)
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(_compile, sources))
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)]
+        objs = list(pool.map(lambda src: _compile(src, out_dir, extra), sources))
+    tmp = lib.with_suffix(".so.tmp")
+    cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *extra, *map(str, objs), "-o",
+           str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB} from {len(sources)} sources")
-    return LIB
+        print(f"built {lib} from {len(sources)} sources")
+    return lib
 
 
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--sanitize", action="store_true",
+                    help="host ASan + UBSan build (libinferc_hip_san.so) for the CPU tests")
     args = ap.parse_args(argv)
-    build(args.jobs, verbose=True)
+    build(args.jobs, verbose=True, sanitize=args.sanitize)
     return 0
 
 

@@ -8,13 +8,16 @@ numpy wrappers of the C restatement in ``oracle.c`` / ``oracle_blas.c``. Only
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
+
 _DIR = Path(__file__).resolve().parent
-_LIB = _DIR / "build" / "liboracle.so"
+# ORACLE_LIB selects another build of the same sources (the sanitized one)
+_LIB = Path(os.environ.get("ORACLE_LIB", _DIR / "build" / "liboracle.so"))
 _lib = None
 
 F = C.POINTER(C.c_float)

@@ -6,6 +6,7 @@
  * Compiled with -ffp-contract=off so products such as the int4 dequant
  * scale*(nib-8) round exactly once, as the reference writes them.
  */
+#define _POSIX_C_SOURCE 199309L /* clock_gettime for the decode step timer */
 #include "oracle.h"
 
 #include <float.h>
