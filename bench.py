@@ -173,6 +173,32 @@ def bench_decode(ctx, max_tokens: int = 128, prompt_len: int = 32, int4: bool = 
     return float(np.mean(steps)), float(np.median(steps)), float(np.min(steps)), toks, w, prompt
 
 
+GPT2_SMALL_PAST_ONNX = ROOT / "tests" / "golden" / "gpt2_small_past_noparams.onnx"
+
+
+def bench_onnx_decode(ctx, weights, prompt, max_tokens: int = 128):
+    """`inferc decode` over the exported with-past graph of GPT-2-small (the
+    reference's own caller, main.cpp:700-936): the structure-only export with
+    the config-4 weights bound, the pass pipeline, the device KV cache, and
+    each step run eagerly through the executor (its input shapes grow by one
+    position per step). ms/token is the host wall time of each post-prompt
+    step, as main.cpp:863-872 times Run."""
+    from inferc_amd import graphs, rt
+
+    g = rt.Graph.from_onnx(str(GPT2_SMALL_PAST_ONNX))
+    graphs.gpt2_bind_weights(g, graphs.GPT2_SMALL, weights)
+    dec = rt.OnnxDecoder(ctx, g, max_t=len(prompt) + max_tokens)
+    ms: list = []
+    dec.generate(prompt, 8)  # warm: plans and allocates the executor's buffers
+    toks = dec.generate(prompt, max_tokens, step_ms=ms)
+    nodes = dec.ex.node_count()
+    counts = dec.counts
+    dec.close()
+    return {"ms_per_token": round(float(np.mean(ms)), 4), "p50": round(float(np.median(ms)), 4),
+            "min": round(float(np.min(ms)), 4), "timed_steps": len(ms),
+            "nodes_after_fusion": nodes, "fusions": counts}, toks
+
+
 def gpt2_bytes_per_token(cfg: dict, mean_ctx: float, int4: bool = False) -> float:
     H, F, V, L = cfg["hidden"], cfg["ffn"], cfg["vocab"], cfg["layers"]
     weights = L * (3 * H * H + H * H + 2 * H * F) + V * H
@@ -697,6 +723,11 @@ def main(argv=None) -> int:
                "hbm_gbps": round(bpt / (d_mean * 1e-3) / 1e9, 1),
                "hbm_frac": round(bpt / (d_mean * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
         log(f"  {d_mean:.4f} ms/token")
+        log("gpt2 decode over the exported with-past graph")
+        od, otoks = bench_onnx_decode(ctx, gw, prompt)
+        od["tokens_match_native"] = bool(np.array_equal(otoks, toks))
+        extra["gpt2_decode_onnx_with_past"] = od
+        log(f"  {od['ms_per_token']:.4f} ms/token, tokens match: {od['tokens_match_native']}")
         log("gpt2 decode, int4 weight-only")
         i_mean, i_p50, i_min, _, _, _ = bench_decode(ctx, int4=True)
         ibpt = gpt2_bytes_per_token(graphs.GPT2_SMALL, 32 + 64, int4=True)

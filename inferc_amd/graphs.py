@@ -172,6 +172,42 @@ def gpt2_int4_dequantized(cfg: dict, w: list[np.ndarray]) -> list[np.ndarray]:
     return out
 
 
+def gpt2_bind_weights(graph, cfg: dict, weights: list[np.ndarray]) -> None:
+    """Binds `weights` (the order of gpt2_weights) to a GPT-2 graph exported
+    without parameters: each parameter input (inner.transformer.wte.weight,
+    .h.{l}.ln_1.weight, ..., .ln_f.bias) becomes an initializer of that name,
+    and the one [hidden, vocab] input, the LM head's folded transpose of the
+    tied wte, becomes wte^T (the initializer FoldConstantTranspose makes,
+    constant_fold.cc:12-54). Fails on any parameter input it cannot place."""
+    H, V, L = cfg["hidden"], cfg["vocab"], cfg["layers"]
+    p = "inner.transformer."
+    names = {p + "wte.weight": weights[0], p + "wpe.weight": weights[1],
+             p + "ln_f.weight": weights[2 + 12 * L], p + "ln_f.bias": weights[3 + 12 * L]}
+    parts = ["ln_1.weight", "ln_1.bias", "attn.c_attn.weight", "attn.c_attn.bias",
+             "attn.c_proj.weight", "attn.c_proj.bias", "ln_2.weight", "ln_2.bias",
+             "mlp.c_fc.weight", "mlp.c_fc.bias", "mlp.c_proj.weight", "mlp.c_proj.bias"]
+    for l in range(L):
+        for k, part in enumerate(parts):
+            names[f"{p}h.{l}.{part}"] = weights[2 + 12 * l + k]
+    bound = 0
+    for i in graph.to_dict()["inputs"]:
+        nm, shape = i["name"], list(i["shape"])
+        if nm in names:
+            arr = names[nm]
+        elif shape == [H, V]:
+            arr = np.ascontiguousarray(weights[0].T)
+        else:
+            if nm.startswith(p) or nm.startswith("onnx::"):
+                raise ValueError(f"gpt2_bind_weights: no weight for input {nm} {shape}")
+            continue
+        if list(arr.shape) != shape:
+            raise ValueError(f"gpt2_bind_weights: {nm} is {shape}, weight is {list(arr.shape)}")
+        graph.add_initializer(nm, np.ascontiguousarray(arr, np.float32))
+        bound += 1
+    if bound != len(names) + 1:
+        raise ValueError(f"gpt2_bind_weights: bound {bound} of {len(names) + 1} parameters")
+
+
 def gpt2_prompt(cfg: dict, n: int, seed: int = 3) -> np.ndarray:
     return rng_for(seed, f"prompt_{n}").integers(0, cfg["vocab"], size=n, dtype=np.int64)
 

@@ -12,6 +12,7 @@ returns a new tensor, as the reference's functions return a new
 from __future__ import annotations
 
 import ctypes as C
+import time
 from typing import Sequence
 
 import numpy as np
@@ -892,12 +893,15 @@ class OnnxDecoder:
             self.ex.run_async()
         return self.ex.output_argmax("logits")
 
-    def generate(self, prompt: np.ndarray, max_tokens: int, profiler=None) -> np.ndarray:
+    def generate(self, prompt: np.ndarray, max_tokens: int, profiler=None,
+                 step_ms: list | None = None) -> np.ndarray:
         """Greedy tokens. With a prefill graph the prompt runs there
         (main.cpp:786-828) and its present.* seed the cache on the first
         step, device to device; without one the prompt is the with-past
         graph's first step. `profiler` records each post-prompt step as one
-        iteration (main.cpp:846-872)."""
+        iteration (main.cpp:846-872). `step_ms`, when given, receives each
+        post-prompt step's host wall time in ms, from setting its inputs to
+        its token (the step timer of main.cpp:863-872 around Run)."""
         p = np.asarray(prompt, np.int64).reshape(1, -1)
         n = p.shape[1]
         if n + max_tokens - 1 > self.max_t:
@@ -914,13 +918,23 @@ class OnnxDecoder:
         else:
             toks = [self._step(p, n)]
         for k in range(1, max_tokens):
+            t0 = time.perf_counter()
             toks.append(self._step(np.array([[toks[-1]]], np.int64), n + k, seed=seed,
                                    profiler=profiler))
+            if step_ms is not None:
+                step_ms.append((time.perf_counter() - t0) * 1e3)
             seed = None
         return np.array(toks, np.int64)
 
     def logits(self) -> np.ndarray:
         return self.ex.output("logits")
+
+    def close(self) -> None:
+        """Frees the executors (weights, arena, KV caches)."""
+        for ex in (self.ex, self.prefill_ex):
+            if ex is not None:
+                ex.close()
+        self.prefill_ex = None
 
 
 class Gpt2Config(C.Structure):

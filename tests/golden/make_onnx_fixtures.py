@@ -23,6 +23,13 @@ tests:
       The same GPT-2 as the reference's prefill decoder model: inputs
       input_ids and attention_mask, outputs logits and present.{i}.key/value
       (the first graph of `inferc decode --model`).
+  gpt2_small_past_noparams.onnx
+      GPT-2-small (12 layers, dim 768, 12 heads, vocab 50257, 1024 positions)
+      as the same with-past decoder, exported with export_params=False: the
+      graph's structure only, every parameter a named graph input
+      (inner.transformer.*), plus the LM head's folded transpose of the tied
+      wte as one [768, 50257] input. No weights are stored (450 KB); the
+      bench binds seeded weights to these inputs (graphs.gpt2_bind_weights).
 
 Every parameter is drawn at random (biases and LayerNorm weights included),
 so the exporter's deduplication of equal initializers does not fire.
@@ -42,14 +49,15 @@ import torch
 OUT = Path(__file__).resolve().parent
 
 
-def _export(model, args, input_names, output_names, dynamic_axes) -> bytes:
+def _export(model, args, input_names, output_names, dynamic_axes,
+            export_params: bool = True) -> bytes:
     from torch.onnx._internal.torchscript_exporter import onnx_proto_utils as opu
 
     opu._add_onnxscript_fn = lambda model_bytes, custom_opsets: model_bytes
     f = io.BytesIO()
     torch.onnx.export(model, args, f, input_names=input_names, output_names=output_names,
                       dynamic_axes=dynamic_axes, opset_version=13, dynamo=False,
-                      do_constant_folding=True)
+                      do_constant_folding=True, export_params=export_params)
     return f.getvalue()
 
 
@@ -129,10 +137,8 @@ def gpt2() -> None:
     gpt2_past(m, cfg)
 
 
-def gpt2_past(m, cfg) -> None:
+def _past_wrapper(m, L):
     from transformers.cache_utils import DynamicCache
-
-    L = cfg.n_layer
 
     class Past(torch.nn.Module):
         def __init__(self, inner):
@@ -150,8 +156,10 @@ def gpt2_past(m, cfg) -> None:
                 pres += [out.past_key_values.layers[i].keys, out.past_key_values.layers[i].values]
             return (out.logits, *pres)
 
-    w = Past(m).eval()
-    nh, dh = cfg.n_head, cfg.n_embd // cfg.n_head
+    return Past(m).eval()
+
+
+def _past_io(L):
     names_in = ["input_ids", "attention_mask"] + [
         f"past_key_values.{i}.{kv}" for i in range(L) for kv in ("key", "value")]
     names_out = ["logits"] + [f"present.{i}.{kv}" for i in range(L) for kv in ("key", "value")]
@@ -161,6 +169,31 @@ def gpt2_past(m, cfg) -> None:
         dyn[nm] = {0: "batch", 2: "past_sequence"}
     for nm in names_out[1:]:
         dyn[nm] = {0: "batch", 2: "total_sequence"}
+    return names_in, names_out, dyn
+
+
+def gpt2_small_structure() -> None:
+    """GPT-2-small with-past decoder, structure only (export_params=False)."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+
+    cfg = GPT2Config(vocab_size=50257, n_positions=1024, n_embd=768, n_layer=12, n_head=12,
+                     use_cache=True)
+    cfg._attn_implementation = "eager"
+    m = GPT2LMHeadModel(cfg).eval()
+    _randomize(m, 13)  # distinct values: no parameter is merged with another
+    L, nh, dh = cfg.n_layer, cfg.n_head, cfg.n_embd // cfg.n_head
+    names_in, names_out, dyn = _past_io(L)
+    ex = (torch.tensor([[5]], dtype=torch.int64), torch.ones(1, 4, dtype=torch.int64),
+          *[torch.zeros(1, nh, 3, dh) for _ in range(2 * L)])
+    data = _export(_past_wrapper(m, L), ex, names_in, names_out, dyn, export_params=False)
+    (OUT / "gpt2_small_past_noparams.onnx").write_bytes(data)
+
+
+def gpt2_past(m, cfg) -> None:
+    L = cfg.n_layer
+    w = _past_wrapper(m, L)
+    nh, dh = cfg.n_head, cfg.n_embd // cfg.n_head
+    names_in, names_out, dyn = _past_io(L)
     ex_ids = torch.tensor([[5]], dtype=torch.int64)
     ex_mask = torch.ones(1, 4, dtype=torch.int64)
     ex_past = [torch.zeros(1, nh, 3, dh) for _ in range(2 * L)]
@@ -224,5 +257,6 @@ if __name__ == "__main__":
     torch.manual_seed(0)
     distilbert()
     gpt2()
+    gpt2_small_structure()
     for p in sorted(OUT.glob("*_tiny*")):
         print(p.name, p.stat().st_size)

@@ -103,3 +103,28 @@ def test_onnx_decoder_greedy_tokens_match_torch(ctx):
         ex.set_input_shape(i["name"], np.float32, [1, 4, 29, 16])
     with pytest.raises(RuntimeError, match="KV cache holds"):
         ex.run_async()
+
+
+def test_gpt2_small_with_past_graph_decode_config4(ctx):
+    """`inferc decode` over the exported with-past graph at GPT-2-small shape
+    (prompt 32, 128 greedy tokens): the structure-only
+    export with the config's seeded weights bound (graphs.gpt2_bind_weights),
+    the pass pipeline, the device KV cache. Tokens bit-exact against the CPU
+    oracle on the same weights (main.cpp:700-936; argmax rule :875-879)."""
+    import oracle as O
+    from inferc_amd import graphs
+
+    cfg = graphs.GPT2_SMALL
+    w = graphs.gpt2_weights(cfg, 2)
+    g = rt.Graph.from_onnx(GOLDEN / "gpt2_small_past_noparams.onnx")
+    graphs.gpt2_bind_weights(g, cfg, w)
+    prompt = graphs.gpt2_prompt(cfg, 32)
+    dec = rt.OnnxDecoder(ctx, g, max_t=160)
+    assert dec.counts["recognize_attention_additive"] == 12
+    ms: list = []
+    toks = dec.generate(prompt, 128, step_ms=ms)
+    ref, _, margins = O.gpt2_generate(cfg, w, prompt, 128)
+    print(f"with-past graph: {np.mean(ms):.3f} ms/token; min top-2 margin {margins.min():.3e}")
+    np.testing.assert_array_equal(toks, ref)
+    assert len(ms) == 127
+    dec.close()

@@ -471,3 +471,31 @@ def test_pipeline_on_exported_gpt2_with_past():
         assert n["attrs"]["head_dim"] == "16"
     assert "Concat" not in [n["op"] for n in g.to_dict()["nodes"]
                             if any(o.startswith("present.") for o in n["outputs"])]
+
+
+def test_pipeline_on_gpt2_small_structure_export():
+    """The GPT-2-small with-past export (structure only, parameters as graph
+    inputs) with seeded weights bound: every parameter input is placed, the
+    pipeline folds one attention-with-past per layer, 2 LayerNorms per layer
+    plus the final one, one tanh-GELU per layer, and the planned step writes
+    logits [1, 1, vocab] and presents of the grown cache."""
+    from inferc_amd import graphs
+    from inferc_amd.rt import Executor
+
+    cfg = graphs.GPT2_SMALL
+    g = Graph.from_onnx(Path(__file__).resolve().parent / "golden" /
+                        "gpt2_small_past_noparams.onnx")
+    graphs.gpt2_bind_weights(g, cfg, graphs.gpt2_weights(cfg, 2))
+    c = g.optimize()
+    assert c["recognize_attention_additive"] == 12
+    assert c["recognize_layernorm"] == 25
+    assert c["recognize_gelu_tanh"] == 12
+    ex = Executor.dry(g)
+    ex.set_input("input_ids", np.array([[5]], np.int64))
+    ex.set_input("attention_mask", np.ones((1, 33), np.int64))
+    for l in range(12):
+        for kv in ("key", "value"):
+            ex.set_input(f"past_key_values.{l}.{kv}", np.zeros((1, 12, 32, 64), np.float32))
+    ex.run_async()
+    assert ex.output_shape("logits") == ((1, 1, 50257), np.dtype(np.float32))
+    assert ex.output_shape("present.11.value") == ((1, 12, 33, 64), np.dtype(np.float32))
