@@ -254,10 +254,6 @@ __device__ __forceinline__ float4 gload_f4(const float4* p) {
       reinterpret_cast<uintptr_t>(p));
   return make_float4(v.x, v.y, v.z, v.w);
 }
-__device__ __forceinline__ uint32_t gload_u32(const uint32_t* p) {
-  return *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(
-      reinterpret_cast<uintptr_t>(p));
-}
 __device__ __forceinline__ int64_t gload_i64(const int64_t* p) {
   return *reinterpret_cast<const __attribute__((address_space(1))) int64_t*>(
       reinterpret_cast<uintptr_t>(p));
@@ -1051,252 +1047,231 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_mfma_kernel(const Int4MfDesc
     }
 }
 
-// Streaming int4 GEMV on the int8 matrix cores, for K = 768 * S (S = 1, 2
-// or 4) and up to 8 batches. Same exact arithmetic as above (fixed-point x
-// split into 4 int8 limbs, integer MFMA sums, -8 fold); the work is split
-// differently so that the weights stream at full rate:
-//
-// 1. int4_xprep_kernel, one block per (matrix, 768-k slab q, column group
-//    gr of 4 batches), writes the slab's B operands to the workspace: record
-//    (t, eo, lane) of 16 bytes, byte j = limb c%4 of
-//    x[4gr + c/4][768q + 128t + 32g + 2j + eo] for lane = (c = lane%16,
-//    g = lane/16), plus the slab's fold (each column's sum of limbs) and
-//    F / finiteness per batch, F from max|x| over the slab (so a slab's
-//    limbs use its own fixed-point scale).
-// 2. int4_gemv_stream_kernel: each wave owns one slab for its lifetime, so
-//    its B operands load once into registers; it then streams T tiles of 16
-//    rows (16 x 768 k = 6 KB each), the loads of tile i+2 issued before tile
-//    i+1 is computed, fully unrolled so the waits count exactly. With S > 1
-//    the S waves of a tile group take the S slabs of the same tiles and add
-//    their scaled partial sums through LDS. Both column groups (batches 0-3,
-//    4-7) reuse each unpacked weight operand, so weights are read once for
-//    all 8 batches.
-constexpr int kI4SlabK = 768;
-constexpr int kI4SlabSteps = kI4SlabK / 128;  // 128 k (64 bytes of a row) per step
+constexpr int kI4SlabK = 768;                 // k per slab: one fixed-point scale
+constexpr int kI4SlabSteps = kI4SlabK / 128;  // 128 k (64 bytes of a row) per MFMA step
 
-struct I4Prep {  // one (matrix, slab, column group)
-  uint32_t bop[kI4SlabSteps * 2 * 64 * 4];  // [t][even/odd][lane][4 dwords]
-  int32_t fold[16];                         // per column: sum of its limbs over the slab
-  int32_t F[4];                             // per batch: x scaled by 2^F before rounding
-  int32_t finite[4];                        // per batch: 0 if x holds a NaN or inf
-};
-
-struct I4PrepDesc {
-  const float* x;  // [batch][K]
-  int64_t K;
-  int64_t slab_begin;  // first slab of this matrix in the launch
-  I4Prep* out;         // [group][slab]
-};
-
-__global__ __launch_bounds__(kBlock) void int4_xprep_kernel(const I4PrepDesc* __restrict__ tab,
-                                                            int batch) {
-  __shared__ float smax[kBlock / 64][4];
-  __shared__ int sfold[16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int q = blockIdx.x, gr = blockIdx.z;  // slab, column group
-  const I4PrepDesc d = tab[blockIdx.y];       // matrix
-  const int64_t K = d.K;
-  const int S = int(K / kI4SlabK);
-  if (q >= S) return;  // grid.x covers the longest row
-  const int b0 = 4 * gr, nbg = min(4, batch - b0);
-  I4Prep* o = d.out + gr * S + q;
-  const float* xs = d.x + int64_t(b0) * K + kI4SlabK * q;  // this slab of batch b0
-  if (tid < 16) sfold[tid] = 0;
-
-  // Thread (t, eo, g, b) owns x[b][128t + 32g + 2j + eo], j < 16: it loads
-  // the 32 values x[b][128t + 32g + i] (its even/odd partner loads the same
-  // line), which together cover the slab for the maximum.
-  constexpr int kThreads = kI4SlabSteps * 2 * 4 * 4;  // 192
-  const bool active = tid < kThreads;
-  const int b = tid & 3, g = (tid >> 2) & 3, eo = (tid >> 4) & 1, t = tid >> 5;
-  float own[16];  // x[b][128t + 32g + 2j + eo]
-  float m = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) own[j] = 0.0f;
-  if (active && b < nbg) {
-    const float4* xr = reinterpret_cast<const float4*>(xs + int64_t(b) * K + 128 * t + 32 * g);
-    bool bad = false;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 v = gload_f4(xr + i);
-      const float a0 = fabsf(v.x), a1 = fabsf(v.y), a2 = fabsf(v.z), a3 = fabsf(v.w);
-      m = fmaxf(m, fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
-      bad |= !(a0 <= 3.4028235e38f && a1 <= 3.4028235e38f && a2 <= 3.4028235e38f &&
-               a3 <= 3.4028235e38f);
-      const float e0 = v.x, o0 = v.y, e1 = v.z, o1 = v.w;
-      own[2 * i] = eo ? o0 : e0;
-      own[2 * i + 1] = eo ? o1 : e1;
-    }
-    // fmaxf would drop a NaN, so a non-finite |x| enters the maximum as inf
-    m = bad ? INFINITY : m;
-  }
-#pragma unroll
-  for (int bb = 0; bb < 4; ++bb) {
-    const float w = wave_max(bb == b ? m : 0.0f);
-    if (lane == 0) smax[wave][bb] = w;
-  }
-  __syncthreads();
-  int F[4], fin[4];
-#pragma unroll
-  for (int bb = 0; bb < 4; ++bb) {
-    float mm = 0.0f;
-#pragma unroll
-    for (int w2 = 0; w2 < kBlock / 64; ++w2) mm = fmaxf(mm, smax[w2][bb]);
-    fin[bb] = mm <= 3.4028235e38f;
-    if (!fin[bb]) mm = 0.0f;
-    int e = 0;
-    (void)frexpf(mm, &e);  // mm < 2^e, so |x * 2^(30-e)| < 2^30
-    F[bb] = mm > 0.0f ? 30 - e : 0;
-  }
-
-  if (active) {
-    int Fb = 0, ok = 0;
-#pragma unroll
-    for (int bb = 0; bb < 4; ++bb) {
-      Fb = bb == b ? F[bb] : Fb;
-      ok = bb == b ? fin[bb] : ok;
-    }
-    // Balanced base-256 digits of X (three in [-128, 127], the top one in
-    // [-64, 64]): with Y = X + 0x808080 the low three are Y's bytes minus
-    // 128 and the top one is Y >> 24, so the digits' bytes are exactly the
-    // bytes of Z = Y ^ 0x808080 (byte - 128 = byte ^ 0x80 modulo 256).
-    uint32_t Z[16];
-    const bool use = b < nbg && ok;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int X = use ? int(rintf(ldexpf(own[j], Fb))) : 0;
-      Z[j] = uint32_t(X + 0x808080) ^ 0x808080u;
-    }
-    // Record of limb cl: byte j = byte cl of Z[j]. A 4x4 byte transpose per
-    // group of four values (v_perm_b32), and the limb's sum of signed bytes
-    // by a dot product with ones.
-    const int rec0 = (2 * t + eo) * 64 + 16 * g + 4 * b;
-    u32x4_t out[4];
-    int fsum[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t z0 = Z[4 * k], z1 = Z[4 * k + 1], z2 = Z[4 * k + 2], z3 = Z[4 * k + 3];
-      // lo01 = [z0.b0, z1.b0, z0.b1, z1.b1], hi01 = [z0.b2, z1.b2, z0.b3, z1.b3]
-      const uint32_t lo01 = __builtin_amdgcn_perm(z1, z0, 0x05010400u);
-      const uint32_t hi01 = __builtin_amdgcn_perm(z1, z0, 0x07030602u);
-      const uint32_t lo23 = __builtin_amdgcn_perm(z3, z2, 0x05010400u);
-      const uint32_t hi23 = __builtin_amdgcn_perm(z3, z2, 0x07030602u);
-      // limb c: [z0.bc, z1.bc, z2.bc, z3.bc]
-      const uint32_t l0 = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
-      const uint32_t l1 = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
-      const uint32_t l2 = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
-      const uint32_t l3 = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
-      out[0][k] = l0;
-      out[1][k] = l1;
-      out[2][k] = l2;
-      out[3][k] = l3;
-      fsum[0] = __builtin_amdgcn_sdot4(int(l0), 0x01010101, fsum[0], false);
-      fsum[1] = __builtin_amdgcn_sdot4(int(l1), 0x01010101, fsum[1], false);
-      fsum[2] = __builtin_amdgcn_sdot4(int(l2), 0x01010101, fsum[2], false);
-      fsum[3] = __builtin_amdgcn_sdot4(int(l3), 0x01010101, fsum[3], false);
-    }
-#pragma unroll
-    for (int cl = 0; cl < 4; ++cl) {
-      *reinterpret_cast<__attribute__((address_space(1))) u32x4_t*>(
-          reinterpret_cast<uintptr_t>(o->bop + 4 * (rec0 + cl))) = out[cl];
-      atomicAdd(&sfold[4 * b + cl], fsum[cl]);  // integer: exact in any order
-    }
-  }
-  __syncthreads();
-  if (tid < 16) o->fold[tid] = sfold[tid];
-  if (tid < 4) {
-    o->F[tid] = F[tid];
-    o->finite[tid] = tid < nbg ? fin[tid] : 1;
-  }
-}
-
-struct I4StreamDesc {
+// int4 GEMV for batches 2-8 with K = 768 * S (S = 1, 2 or 4): the exact
+// integer arithmetic of int4_gemv_mfma_kernel (x to fixed point per 768-k
+// slab, 4 balanced int8 limbs, v_mfma_i32_16x16x64_i8, the -8 offset through
+// each column's limb sum), one launch for every matrix of the call, one
+// long-lived block per CU:
+// - A block owns T tiles of 16 rows per wave group of one matrix. Its NW
+//   waves split into NW / S groups of S waves; wave w streams slab w % S of
+//   its group's tiles, so every wave reads 384-byte row pieces whatever K.
+// - At its start the block turns x into the B operands of every (slab,
+//   column group) in LDS (S x G x 12 KB), wave by (batch, slab): three
+//   coalesced 1 KB loads, the slab's largest |x| and the columns' limb sums
+//   by DPP within the wave, the digit records written as 16-bit pieces. The
+//   first R tiles' weights are already in flight meanwhile.
+// - Each wave then runs its T tiles through a ring of R in flight: a tile's
+//   MFMAs, the next load into its slot, its epilogue. A slab's limb terms
+//   acc - 8 fold (below 2^24, exact in fp32) are scaled by 2^(8 limb - F);
+//   with S > 1 the group's S waves meet in LDS and add their terms in slab
+//   order, then a batch's 4 limbs (a lane quad) add and the row's scale
+//   applies.
+// Each block reads its own descriptor (one scalar load): at a launch's start
+// every dependent load is a full memory round trip.
+struct I4B8Block {
   const uint8_t* W;
   const float* s;
-  float* y;  // [batch][N]
-  int64_t N, K;
-  int64_t block_begin;  // first block of this matrix in the launch
-  const I4Prep* prep;   // [group][slab]
+  const float* x;  // [batch][K]
+  float* y;        // [batch][N]
+  int32_t N;
+  int32_t S;     // slabs per row
+  int32_t rblk;  // this block's row block of the matrix
+  int32_t unused;
 };
 
-__device__ __forceinline__ i32x4_t gload_i32x4(const uint32_t* p) {
-  const u32x4_t v = *reinterpret_cast<const __attribute__((address_space(1))) u32x4_t*>(
-      reinterpret_cast<uintptr_t>(p));
-  return i32x4_t{int(v.x), int(v.y), int(v.z), int(v.w)};
+// Wave-wide reductions through DPP within rows of 16 lanes, then the four
+// rows' lanes 0, 16, 32 and 48 (every lane must be active).
+__device__ __forceinline__ int wave_max_bits(int v) {
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0x124, 0xF, 0xF, false));  // row_ror:4
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false));  // row_ror:8
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+__device__ __forceinline__ int wave_sum_int(int v) {
+  v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x124, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);
+  return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 
-template <int G, int T, int R>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(G == 1 && R <= 2 ? 3 : 2)))
-void int4_gemv_stream_kernel(
-    const I4StreamDesc* __restrict__ tab, int n, int batch) {
-  constexpr int NW = kBlock / 64;
-  __shared__ f32x4_t part[2][NW][G][64];  // S > 1: per-slab partial terms, by tile parity
+// Workgroup barrier for LDS data only: unlike __syncthreads it does not make
+// the wave wait for its global loads still in flight.
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int G, int T, int R, int RE, int NW>
+__global__ __launch_bounds__(64 * NW) void int4_gemv_b8_kernel(const I4B8Block* __restrict__ tab,
+                                                               int batch) {
+  constexpr int ST = kI4SlabSteps;  // 6 MFMA steps of 128 k per slab
+  constexpr int NB = 4 * G;         // batch columns
+  constexpr int SMAX = 4;
+  constexpr int TASKS = (NB * SMAX + NW - 1) / NW;  // (batch, slab) preparations per wave
+  static_assert(NW % SMAX == 0, "waves split into slab groups");
+  // B operands: [slab][step][parity][group][lane][16 bytes]
+  __shared__ __attribute__((aligned(16))) uint32_t bop[SMAX * ST * 2 * G * 64 * 4];
+  __shared__ int sfold[SMAX][G][16];
+  __shared__ int sF[SMAX][NB];
+  __shared__ int sfin[SMAX][NB];
+  __shared__ f32x4_t part[2][NW][G][64];  // S > 1: slab terms, by tile parity
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t bid = blockIdx.x;
-  int cnt = 0;  // this block's matrix (block_begin ascends)
-  for (int base = 0; base < n; base += 64) {
-    const int j = base + lane;
-    const int c = __popcll(__ballot(j < n && gload_i64(&tab[j].block_begin) <= bid));
-    cnt += c;
-    if (c < 64) break;
-  }
-  const I4StreamDesc d = tab[__builtin_amdgcn_readfirstlane(cnt - 1)];
-  const int64_t N = d.N, rb = d.K / 2;
-  const int S = int(d.K / kI4SlabK);
-  const int q = wave % S, tg = wave / S, tgs = NW / S;
-  const int64_t tile0 = ((bid - d.block_begin) * tgs + tg) * T;
+  const I4B8Block d = tab[blockIdx.x];
+  const int S = d.S, NG = NW / S;
+  const int64_t N = d.N, K = int64_t(kI4SlabK) * S, rb = K / 2;
+  const int q = wave % S, wg = wave / S;  // this wave's slab and group
+  const int64_t rblk = d.rblk;
   const int r = lane & 15, g = lane >> 4, col = lane & 15, cl = col & 3;
+  auto tile_of = [&](int i) { return (rblk * T + i) * NG + wg; };
 
-  // this wave's slab: B operands, fold, exponent and finiteness of its column
-  i32x4_t bo[kI4SlabSteps][2][G];
-  int fold[G], Fc[G], fin[G];
+  // 1. x loads of this wave's (batch, slab) tasks: lane l of piece j holds
+  //    positions 256 j + 4 l + e (e < 4) of the slab. Idle tasks load the
+  //    first piece of x and drop it: a load under a branch would make the
+  //    wave wait for it.
+  float4 xv[TASKS][3];
 #pragma unroll
-  for (int gr = 0; gr < G; ++gr) {
-    const I4Prep* pp = d.prep + gr * S + q;
+  for (int k = 0; k < TASKS; ++k) {
+    const int task = wave + NW * k, tb = task % NB, tq = task / NB;
+    const bool on = tq < S && tb < batch;
+    const float4* xs = reinterpret_cast<const float4*>(
+        d.x + (on ? int64_t(tb) * K + kI4SlabK * tq : 0));
 #pragma unroll
-    for (int t = 0; t < kI4SlabSteps; ++t)
-#pragma unroll
-      for (int eo = 0; eo < 2; ++eo) bo[t][eo][gr] = gload_i32x4(pp->bop + ((2 * t + eo) * 64 + lane) * 4);
-    fold[gr] = *reinterpret_cast<const __attribute__((address_space(1))) int32_t*>(
-        reinterpret_cast<uintptr_t>(pp->fold + col));
-    Fc[gr] = *reinterpret_cast<const __attribute__((address_space(1))) int32_t*>(
-        reinterpret_cast<uintptr_t>(pp->F + (col >> 2)));
-    fin[gr] = *reinterpret_cast<const __attribute__((address_space(1))) int32_t*>(
-        reinterpret_cast<uintptr_t>(pp->finite + (col >> 2)));
+    for (int j = 0; j < 3; ++j) xv[k][j] = gload_f4(xs + 64 * j + lane);
   }
   __builtin_amdgcn_sched_barrier(0);
-
-  // tile i: lane (r, g) holds row 16i + r, bytes [384q + 64t + 16g, +16) for
-  // t < 6, and the scales of rows 16i + 4g + v (rows past N are clamped)
-  uint4 wb[R][kI4SlabSteps];
+  // the ring: slot j holds a tile's 6 steps (lane (r, g): row 16 i + r, bytes
+  // [384 q + 64 t + 16 g, +16)) and the scales of rows 16 i + 4 g + v; rows
+  // past N are clamped and never stored
+  uint4 wb[R][ST];
   float sb[R][4];
   auto load_tile = [&](int slot, int64_t tile) {
     int64_t row = tile * 16 + r;
     row = row < N ? row : N - 1;
     const uint8_t* rp = d.W + row * rb + kI4SlabK / 2 * q + 16 * g;
 #pragma unroll
-    for (int t = 0; t < kI4SlabSteps; ++t)
-      wb[slot][t] = gload_u4_nt(reinterpret_cast<const uint4*>(rp + 64 * t));
+    for (int t = 0; t < ST; ++t) wb[slot][t] = gload_u4(reinterpret_cast<const uint4*>(rp + 64 * t));
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      int64_t rw = tile * 16 + 4 * g + v;
+      const int64_t rw = tile * 16 + 4 * g + v;
       sb[slot][v] = gload_f(d.s + (rw < N ? rw : N - 1));
     }
   };
+  // RE tiles go out before the preparation, the rest of the ring after it
+  constexpr int R0 = R < T ? R : T, E0 = RE < R0 ? RE : R0;
 #pragma unroll
-  for (int j = 0; j < (R < T ? R : T); ++j) load_tile(j, tile0 + j);
+  for (int j = 0; j < E0; ++j) load_tile(j, tile_of(j));
   __builtin_amdgcn_sched_barrier(0);
 
+  // 2. the B operands
+#pragma unroll
+  for (int k = 0; k < TASKS; ++k) {
+    const int task = wave + NW * k, b = task % NB, tq = task / NB;
+    if (tq >= S) break;  // wave-uniform
+    const bool on = b < batch;
+    const int gr = b / 4, bb = b % 4;
+    // the slab's largest |x| (a non-finite value enters as inf, since fmaxf
+    // would drop a NaN; non-negative floats order as their bits) and F
+    float m = 0.0f;
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const float a0 = fabsf(xv[k][j].x), a1 = fabsf(xv[k][j].y), a2 = fabsf(xv[k][j].z),
+                  a3 = fabsf(xv[k][j].w);
+      m = fmaxf(m, fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
+      bad |= !(a0 <= 3.4028235e38f && a1 <= 3.4028235e38f && a2 <= 3.4028235e38f &&
+               a3 <= 3.4028235e38f);
+    }
+    float mm = __int_as_float(wave_max_bits(on ? __float_as_int(bad ? INFINITY : m) : 0));
+    const bool fin = mm <= 3.4028235e38f;
+    if (!fin) mm = 0.0f;
+    int e = 0;
+    (void)frexpf(mm, &e);  // mm < 2^e, so |x * 2^(30-e)| < 2^30
+    const int F = mm > 0.0f ? 30 - e : 0;
+    const bool use = on && fin;
+    // Balanced base-256 digits of X = rint(x 2^F) (three in [-128, 127],
+    // the top one in [-64, 64]): with Y = X + 0x808080 the low three are
+    // Y's bytes minus 128 and the top one is Y >> 24, so the digits' bytes
+    // are exactly the bytes of Z = Y ^ 0x808080 (byte - 128 = byte ^ 0x80
+    // modulo 256). Record (t, eo, gr, lane' = 4 bb + c + 16 kg) of the slab
+    // holds in byte
+    // jj limb c of x[b][128 t + 32 kg + 2 jj + eo]; lane l of piece j has
+    // t = 2 j + l / 32, kg = (l % 32) / 8 and bytes jj = 2 (l % 8) + {0, 1}.
+    int fsum[4] = {0, 0, 0, 0};
+    uint8_t* recs = reinterpret_cast<uint8_t*>(bop) + tq * (ST * 2 * G * 64 * 16);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const float vals[4] = {xv[k][j].x, xv[k][j].y, xv[k][j].z, xv[k][j].w};
+      uint32_t Z[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int X = int(rintf(ldexpf(vals[u], F)));
+        Z[u] = uint32_t((use ? X : 0) + 0x808080) ^ 0x808080u;
+      }
+      // limb c of the 4 values: [Z0.c, Z1.c, Z2.c, Z3.c]
+      const uint32_t lo01 = __builtin_amdgcn_perm(Z[1], Z[0], 0x05010400u);
+      const uint32_t hi01 = __builtin_amdgcn_perm(Z[1], Z[0], 0x07030602u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(Z[3], Z[2], 0x05010400u);
+      const uint32_t hi23 = __builtin_amdgcn_perm(Z[3], Z[2], 0x07030602u);
+      const uint32_t lc[4] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u),
+                              __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                              __builtin_amdgcn_perm(hi23, hi01, 0x05040100u),
+                              __builtin_amdgcn_perm(hi23, hi01, 0x07060302u)};
+      const int t = 2 * j + lane / 32, kg = (lane % 32) / 8;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        fsum[c] = __builtin_amdgcn_sdot4(int(lc[c]), 0x01010101, fsum[c], false);
+#pragma unroll
+        for (int eo = 0; eo < 2; ++eo) {
+          // bytes eo and eo + 2 of lc[c]: the values e = eo, eo + 2
+          const uint32_t h = __builtin_amdgcn_perm(lc[c], lc[c], eo ? 0x0c0c0301u : 0x0c0c0200u);
+          const int rec = ((t * 2 + eo) * G + gr) * 64 + 4 * bb + c + 16 * kg;
+          *reinterpret_cast<uint16_t*>(recs + rec * 16 + 2 * (lane % 8)) = uint16_t(h);
+        }
+      }
+    }
+    // the columns' limb sums over the slab: exact integers
+#pragma unroll
+    for (int c = 0; c < 4; ++c) fsum[c] = wave_sum_int(fsum[c]);
+    if (lane == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sfold[tq][gr][4 * bb + c] = fsum[c];
+      sF[tq][b] = F;
+      sfin[tq][b] = on ? int(fin) : 1;
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = E0; j < R0; ++j) load_tile(j, tile_of(j));
+  __builtin_amdgcn_sched_barrier(0);
+  lds_sync();
+
+  // this wave's slab: fold, exponent and finiteness of its column
+  int fold[G], ex[G], fin[G];
+#pragma unroll
+  for (int gr = 0; gr < G; ++gr) {
+    const int b = 4 * gr + (col >> 2);
+    fold[gr] = sfold[q][gr][col];
+    ex[gr] = 8 * cl - sF[q][b];
+    fin[gr] = sfin[q][b];
+  }
+  const uint32_t* bq = bop + q * (ST * 2 * G * 64 * 4);
+
+  // 3. the tiles through the ring
 #pragma unroll
   for (int i = 0; i < T; ++i) {
     const int slot = i % R;
-    __builtin_amdgcn_sched_barrier(0);
     i32x4_t acc[G];
 #pragma unroll
     for (int gr = 0; gr < G; ++gr) acc[gr] = i32x4_t{0, 0, 0, 0};
 #pragma unroll
-    for (int t = 0; t < kI4SlabSteps; ++t) {
+    for (int t = 0; t < ST; ++t) {
       const uint4 w = wb[slot][t];
       const i32x4_t ev = {int(low_nibbles(w.x)), int(low_nibbles(w.y)), int(low_nibbles(w.z)),
                           int(low_nibbles(w.w))};
@@ -1304,33 +1279,36 @@ void int4_gemv_stream_kernel(
                           int(low_nibbles(w.z >> 4)), int(low_nibbles(w.w >> 4))};
 #pragma unroll
       for (int gr = 0; gr < G; ++gr) {
-        acc[gr] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ev, bo[t][0][gr], acc[gr], 0, 0, 0);
-        acc[gr] = __builtin_amdgcn_mfma_i32_16x16x64_i8(od, bo[t][1][gr], acc[gr], 0, 0, 0);
+        const u32x4_t e4 = *reinterpret_cast<const u32x4_t*>(bq + (((t * 2 + 0) * G + gr) * 64 + lane) * 4);
+        const u32x4_t o4 = *reinterpret_cast<const u32x4_t*>(bq + (((t * 2 + 1) * G + gr) * 64 + lane) * 4);
+        acc[gr] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+            ev, i32x4_t{int(e4.x), int(e4.y), int(e4.z), int(e4.w)}, acc[gr], 0, 0, 0);
+        acc[gr] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+            od, i32x4_t{int(o4.x), int(o4.y), int(o4.z), int(o4.w)}, acc[gr], 0, 0, 0);
       }
     }
     float sc[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) sc[v] = sb[slot][v];
     __builtin_amdgcn_sched_barrier(0);
-    if (i + R < T) load_tile(slot, tile0 + i + R);
+    if (i + R < T) load_tile(slot, tile_of(i + R));
     __builtin_amdgcn_sched_barrier(0);
-    // acc[gr][v]: row 16i + 4g + v, column (batch 4gr + col/4, limb cl). Each
-    // limb term acc - 8*fold is below 2^24, so it and its power-of-two
-    // scaling are exact in fp32; a slab whose x is not finite gives NaN, so
-    // the whole output is non-finite, as in the reference.
+    // acc[gr][v]: row 16 i + 4 g + v, column (batch 4 gr + col / 4, limb
+    // cl); a slab whose x is not finite gives NaN, so the whole output row
+    // is non-finite, as in the reference
     f32x4_t tv[G];
 #pragma unroll
     for (int gr = 0; gr < G; ++gr)
 #pragma unroll
       for (int v = 0; v < 4; ++v)
-        tv[gr][v] = fin[gr] ? ldexpf(float(acc[gr][v] - 8 * fold[gr]), 8 * cl - Fc[gr])
+        tv[gr][v] = fin[gr] ? ldexpf(float(acc[gr][v] - 8 * fold[gr]), ex[gr])
                             : __int_as_float(0x7fc00000);
     bool report = true;
     if (S > 1) {
-      // the S slabs' terms meet in LDS and add in slab order; slab 0 reports
+      // the group's S slab terms meet in LDS and add in slab order
 #pragma unroll
       for (int gr = 0; gr < G; ++gr) part[i & 1][wave][gr][lane] = tv[gr];
-      __syncthreads();
+      lds_sync();
       report = q == 0;
       if (report) {
         for (int s2 = 1; s2 < S; ++s2)
@@ -1340,7 +1318,7 @@ void int4_gemv_stream_kernel(
     }
     if (report) {
       // a batch's 4 limb terms (a lane quad) add in fp32
-      const int64_t tile = tile0 + i;
+      const int64_t tile = tile_of(i);
 #pragma unroll
       for (int gr = 0; gr < G; ++gr) {
         const int b = 4 * gr + (col >> 2);
@@ -1558,48 +1536,37 @@ bool int4_stream_ok(int64_t K, const uint8_t* W) {
   return K > 0 && K % kI4SlabK == 0 && (S == 1 || S == 2 || S == 4) && aligned16(W);
 }
 
-constexpr int kI4StreamTiles = 6;  // 16-row tiles per wave
-constexpr int kI4StreamRing = 2;   // tiles in flight per wave
+constexpr int kI4B8Tiles = 6;  // 16-row tiles per wave group
+constexpr int kI4B8Ring = 2;   // tiles in flight per wave
+constexpr int kI4B8Early = 1;  // of which issued before the x preparation
+constexpr int kI4B8Waves = 8;  // waves per block
 
+// One int4_gemv_b8_kernel launch over every matrix; a block covers
+// 16 x kI4B8Tiles x (kI4B8Waves / S) rows of one matrix.
 template <int G>
-void launch_int4_stream_g(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats, int batch) {
-  int64_t slabs = 0, blocks = 0;
-  for (const Int4MfMat& m : mats) slabs += m.K / kI4SlabK;
-  I4Prep* ws = static_cast<I4Prep*>(ctx->ws(size_t(slabs) * G * sizeof(I4Prep)));
-  std::vector<I4PrepDesc> ptab;
-  std::vector<I4StreamDesc> stab;
-  int64_t sb = 0;
+void launch_int4_b8(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats, int batch) {
+  std::vector<I4B8Block> tab;
   for (const Int4MfMat& m : mats) {
     const int64_t S = m.K / kI4SlabK;
-    I4Prep* out = ws + sb * G;  // this matrix's [group][slab] records
-    ptab.push_back(I4PrepDesc{m.x, m.K, sb, out});
-    stab.push_back(I4StreamDesc{m.W, m.s, m.y, m.N, m.K, blocks, out});
-    sb += S;
-    const int64_t tiles = ceil_div(m.N, 16);
-    blocks += ceil_div(tiles, (kBlock / 64 / S) * kI4StreamTiles);
+    IH_REQUIRE(m.N < (int64_t(1) << 31), INFERC_ERR_SHAPE, "int4 gemv: too many rows");
+    const int64_t rblocks = ceil_div(m.N, 16 * kI4B8Tiles * (kI4B8Waves / S));
+    for (int64_t rbk = 0; rbk < rblocks; ++rbk)
+      tab.push_back(I4B8Block{m.W, m.s, m.x, m.y, int32_t(m.N), int32_t(S), int32_t(rbk), 0});
   }
-  IH_REQUIRE(blocks < (int64_t(1) << 31) && mats.size() <= 65535, INFERC_ERR_SHAPE,
-             "int4 gemv: launch too large");
-  ctx->reserve_tables(2);
-  const I4PrepDesc* pdev = upload_table(ctx, ptab);
-  const I4StreamDesc* sdev = upload_table(ctx, stab);
-  int64_t smax = 1;
-  for (const Int4MfMat& m : mats) smax = std::max<int64_t>(smax, m.K / kI4SlabK);
-  hipLaunchKernelGGL(int4_xprep_kernel, dim3(unsigned(smax), unsigned(ptab.size()), unsigned(G)),
-                     dim3(kBlock), 0, ctx->stream, pdev, batch);
-  check_launch("int4_xprep");
-  hipLaunchKernelGGL((int4_gemv_stream_kernel<G, kI4StreamTiles, kI4StreamRing>),
-                     dim3(unsigned(blocks)),
-                     dim3(kBlock), 0, ctx->stream, sdev, int(stab.size()), batch);
-  check_launch("int4_gemv_stream");
+  IH_REQUIRE(tab.size() < (size_t(1) << 31), INFERC_ERR_SHAPE, "int4 gemv: launch too large");
+  ctx->reserve_tables(1);
+  const I4B8Block* dev = upload_table(ctx, tab);
+  hipLaunchKernelGGL((int4_gemv_b8_kernel<G, kI4B8Tiles, kI4B8Ring, kI4B8Early, kI4B8Waves>),
+                     dim3(unsigned(tab.size())), dim3(64 * kI4B8Waves), 0, ctx->stream, dev, batch);
+  check_launch("int4_gemv_b8");
 }
 
 void launch_int4_stream(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats, int64_t batch) {
   if (mats.empty()) return;
   if (batch <= 4)
-    launch_int4_stream_g<1>(ctx, mats, int(batch));
+    launch_int4_b8<1>(ctx, mats, int(batch));
   else
-    launch_int4_stream_g<2>(ctx, mats, int(batch));
+    launch_int4_b8<2>(ctx, mats, int(batch));
 }
 
 // Dwords per lane for the VALU kernel: L = (K/8)/DW lanes per row must be a
