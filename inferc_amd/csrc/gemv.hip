@@ -303,7 +303,10 @@ __device__ __forceinline__ float ubyte(uint32_t v) {
 // v & 0x0F0F0F0F with the result's known bits hidden from the optimiser: if
 // it sees that the high nibble of every byte is zero, it rewrites each
 // ubyte<N> of the result as a 4-bit field extract plus ubyte<0> (two
-// instructions where v_cvt_f32_ubyteN alone suffices).
+// instructions where v_cvt_f32_ubyteN alone suffices). For VALU consumers
+// only: the compiler does not insert the wait states between a VALU write
+// and a matrix-core read of the same register around inline assembly, and
+// an MFMA fed by this value read stale operands in some schedules.
 __device__ __forceinline__ uint32_t low_nibbles(uint32_t v) {
   uint32_t r;
   asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(v));
@@ -1107,29 +1110,47 @@ __device__ __forceinline__ void lds_sync() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <int G, int T, int R, int RE, int NW>
-__global__ __launch_bounds__(64 * NW) void int4_gemv_b8_kernel(const I4B8Block* __restrict__ tab,
-                                                               int batch) {
+template <int G, int NW>
+struct I4B8Smem {
+  // B operands: [slab][step][parity][group][lane][16 bytes]
+  __attribute__((aligned(16))) uint32_t bop[4 * kI4SlabSteps * 2 * G * 64 * 4];
+  int sfold[4][G][16];  // per slab and column: the sum of its limbs
+  int sF[4][4 * G];     // per slab and batch: x scaled by 2^F before rounding
+  int sfin[4][4 * G];   // per slab and batch: 0 if x holds a NaN or inf
+  __attribute__((aligned(16))) float ystage[NW][4 * G][16];  // a tile's outputs, per wave
+};
+
+// One block of int4_gemv_b8_kernel for rows of S slabs: each wave runs U
+// units (16-row tile, slab), the slabs of a tile in order, through a ring of
+// R; RE of them go out before the x preparation.
+//
+// Every vector memory instruction in the loop is issued unconditionally. On
+// this GPU loads and stores return in issue order under one counter, and the
+// compiler cannot count an instruction behind a branch: the wait for the next
+// unit would then also wait for as many later loads as such stores issued,
+// draining the ring. So S is a template parameter (no branch around a tile's
+// epilogue), and the outputs go out as buffer stores whose lanes that must
+// not write get an offset past the buffer's end, which the hardware drops.
+template <int G, int S, int U, int R, int RE, int NW>
+__device__ __forceinline__ void int4_b8_block(I4B8Smem<G, NW>& sm, const I4B8Block& d, int batch) {
   constexpr int ST = kI4SlabSteps;  // 6 MFMA steps of 128 k per slab
   constexpr int NB = 4 * G;         // batch columns
   constexpr int SMAX = 4;
   constexpr int TASKS = (NB * SMAX + NW - 1) / NW;  // (batch, slab) preparations per wave
-  static_assert(NW % SMAX == 0, "waves split into slab groups");
-  // B operands: [slab][step][parity][group][lane][16 bytes]
-  __shared__ __attribute__((aligned(16))) uint32_t bop[SMAX * ST * 2 * G * 64 * 4];
-  __shared__ int sfold[SMAX][G][16];
-  __shared__ int sF[SMAX][NB];
-  __shared__ int sfin[SMAX][NB];
-  __shared__ f32x4_t part[2][NW][G][64];  // S > 1: slab terms, by tile parity
+  constexpr int SLAB = ST * 2 * G * 64 * 4;         // dwords of one slab's B operands
+  auto& bop = sm.bop;
+  auto& sfold = sm.sfold;
+  auto& sF = sm.sF;
+  auto& sfin = sm.sfin;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const I4B8Block d = tab[blockIdx.x];
-  const int S = d.S, NG = NW / S;
+  constexpr int ls = S == 4 ? 2 : S == 2 ? 1 : 0;  // log2 of the slabs per row
+  static_assert(U % S == 0, "whole tiles per wave");
   const int64_t N = d.N, K = int64_t(kI4SlabK) * S, rb = K / 2;
-  const int q = wave % S, wg = wave / S;  // this wave's slab and group
-  const int64_t rblk = d.rblk;
+  const int64_t tile0 = d.rblk * (U >> ls);  // this block's first tile per wave
   const int r = lane & 15, g = lane >> 4, col = lane & 15, cl = col & 3;
-  auto tile_of = [&](int i) { return (rblk * T + i) * NG + wg; };
+  // unit u: tile (tile0 + u / S) * NW + wave, slab u % S
+  auto tile_of = [&](int u) { return (tile0 + (u >> ls)) * NW + wave; };
 
   // 1. x loads of this wave's (batch, slab) tasks: lane l of piece j holds
   //    positions 256 j + 4 l + e (e < 4) of the slab. Idle tasks load the
@@ -1146,27 +1167,23 @@ __global__ __launch_bounds__(64 * NW) void int4_gemv_b8_kernel(const I4B8Block* 
     for (int j = 0; j < 3; ++j) xv[k][j] = gload_f4(xs + 64 * j + lane);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // the ring: slot j holds a tile's 6 steps (lane (r, g): row 16 i + r, bytes
-  // [384 q + 64 t + 16 g, +16)) and the scales of rows 16 i + 4 g + v; rows
-  // past N are clamped and never stored
+  // the ring: slot j holds a unit's 6 steps (lane (r, g): row 16 i + r,
+  // bytes [384 q + 64 t + 16 g, +16)) and, with the slab-0 unit of a tile,
+  // the scale of row 16 i + r; rows past N are clamped and never stored
   uint4 wb[R][ST];
-  float sb[R][4];
-  auto load_tile = [&](int slot, int64_t tile) {
-    int64_t row = tile * 16 + r;
+  float sb[R];
+  auto load_unit = [&](int slot, int u) {
+    int64_t row = tile_of(u) * 16 + r;
     row = row < N ? row : N - 1;
+    const int q = u & (S - 1);
     const uint8_t* rp = d.W + row * rb + kI4SlabK / 2 * q + 16 * g;
 #pragma unroll
     for (int t = 0; t < ST; ++t) wb[slot][t] = gload_u4(reinterpret_cast<const uint4*>(rp + 64 * t));
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int64_t rw = tile * 16 + 4 * g + v;
-      sb[slot][v] = gload_f(d.s + (rw < N ? rw : N - 1));
-    }
+    if (q == 0) sb[slot] = gload_f(d.s + row);
   };
-  // RE tiles go out before the preparation, the rest of the ring after it
-  constexpr int R0 = R < T ? R : T, E0 = RE < R0 ? RE : R0;
+  constexpr int R0 = R < U ? R : U, E0 = RE < R0 ? RE : R0;
 #pragma unroll
-  for (int j = 0; j < E0; ++j) load_tile(j, tile_of(j));
+  for (int j = 0; j < E0; ++j) load_unit(j, j);
   __builtin_amdgcn_sched_barrier(0);
 
   // 2. the B operands
@@ -1176,33 +1193,33 @@ __global__ __launch_bounds__(64 * NW) void int4_gemv_b8_kernel(const I4B8Block* 
     if (tq >= S) break;  // wave-uniform
     const bool on = b < batch;
     const int gr = b / 4, bb = b % 4;
-    // the slab's largest |x| (a non-finite value enters as inf, since fmaxf
-    // would drop a NaN; non-negative floats order as their bits) and F
-    float m = 0.0f;
-    bool bad = false;
+    // the slab's largest |x| as the largest bits of |x| (non-negative floats
+    // order as their bits; NaN and inf lie above every finite value), and F
+    int mb = 0;
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
-      const float a0 = fabsf(xv[k][j].x), a1 = fabsf(xv[k][j].y), a2 = fabsf(xv[k][j].z),
-                  a3 = fabsf(xv[k][j].w);
-      m = fmaxf(m, fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)));
-      bad |= !(a0 <= 3.4028235e38f && a1 <= 3.4028235e38f && a2 <= 3.4028235e38f &&
-               a3 <= 3.4028235e38f);
+      mb = max(mb, __float_as_int(xv[k][j].x) & 0x7fffffff);
+      mb = max(mb, __float_as_int(xv[k][j].y) & 0x7fffffff);
+      mb = max(mb, __float_as_int(xv[k][j].z) & 0x7fffffff);
+      mb = max(mb, __float_as_int(xv[k][j].w) & 0x7fffffff);
     }
-    float mm = __int_as_float(wave_max_bits(on ? __float_as_int(bad ? INFINITY : m) : 0));
-    const bool fin = mm <= 3.4028235e38f;
-    if (!fin) mm = 0.0f;
+    mb = on ? wave_max_bits(mb) : 0;
+    const bool fin = mb < 0x7f800000;
+    const float mm = fin ? __int_as_float(mb) : 0.0f;
     int e = 0;
     (void)frexpf(mm, &e);  // mm < 2^e, so |x * 2^(30-e)| < 2^30
     const int F = mm > 0.0f ? 30 - e : 0;
-    const bool use = on && fin;
     // Balanced base-256 digits of X = rint(x 2^F) (three in [-128, 127],
     // the top one in [-64, 64]): with Y = X + 0x808080 the low three are
     // Y's bytes minus 128 and the top one is Y >> 24, so the digits' bytes
     // are exactly the bytes of Z = Y ^ 0x808080 (byte - 128 = byte ^ 0x80
-    // modulo 256). Record (t, eo, gr, lane' = 4 bb + c + 16 kg) of the slab
-    // holds in byte
-    // jj limb c of x[b][128 t + 32 kg + 2 jj + eo]; lane l of piece j has
-    // t = 2 j + l / 32, kg = (l % 32) / 8 and bytes jj = 2 (l % 8) + {0, 1}.
+    // modulo 256). A batch past the call's or with a non-finite x gets
+    // digits that no output uses.
+    // Record (t, eo, gr, lane' = 4 bb + c + 16 kg) of the slab holds in byte
+    // jj limb c of x[b][128 t + 32 kg + 2 jj + eo]. Lane l of piece j holds
+    // e = 0..3 at t = 2 j + l / 32, kg = (l % 32) / 8, jj = 2 (l % 8) +
+    // e / 2, eo = e % 2: per parity, the 16-bit piece at byte 2 (l % 8) of
+    // limb c's record is [limb c of e = eo, limb c of e = eo + 2].
     int fsum[4] = {0, 0, 0, 0};
     uint8_t* recs = reinterpret_cast<uint8_t*>(bop) + tq * (ST * 2 * G * 64 * 16);
 #pragma unroll
@@ -1210,30 +1227,23 @@ __global__ __launch_bounds__(64 * NW) void int4_gemv_b8_kernel(const I4B8Block* 
       const float vals[4] = {xv[k][j].x, xv[k][j].y, xv[k][j].z, xv[k][j].w};
       uint32_t Z[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int X = int(rintf(ldexpf(vals[u], F)));
-        Z[u] = uint32_t((use ? X : 0) + 0x808080) ^ 0x808080u;
-      }
-      // limb c of the 4 values: [Z0.c, Z1.c, Z2.c, Z3.c]
-      const uint32_t lo01 = __builtin_amdgcn_perm(Z[1], Z[0], 0x05010400u);
-      const uint32_t hi01 = __builtin_amdgcn_perm(Z[1], Z[0], 0x07030602u);
-      const uint32_t lo23 = __builtin_amdgcn_perm(Z[3], Z[2], 0x05010400u);
-      const uint32_t hi23 = __builtin_amdgcn_perm(Z[3], Z[2], 0x07030602u);
-      const uint32_t lc[4] = {__builtin_amdgcn_perm(lo23, lo01, 0x05040100u),
-                              __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
-                              __builtin_amdgcn_perm(hi23, hi01, 0x05040100u),
-                              __builtin_amdgcn_perm(hi23, hi01, 0x07060302u)};
+      for (int u = 0; u < 4; ++u)
+        Z[u] = uint32_t(int(rintf(ldexpf(vals[u], F))) + 0x808080) ^ 0x808080u;
       const int t = 2 * j + lane / 32, kg = (lane % 32) / 8;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        fsum[c] = __builtin_amdgcn_sdot4(int(lc[c]), 0x01010101, fsum[c], false);
-#pragma unroll
-        for (int eo = 0; eo < 2; ++eo) {
-          // bytes eo and eo + 2 of lc[c]: the values e = eo, eo + 2
-          const uint32_t h = __builtin_amdgcn_perm(lc[c], lc[c], eo ? 0x0c0c0301u : 0x0c0c0200u);
-          const int rec = ((t * 2 + eo) * G + gr) * 64 + 4 * bb + c + 16 * kg;
-          *reinterpret_cast<uint16_t*>(recs + rec * 16 + 2 * (lane % 8)) = uint16_t(h);
-        }
+      for (int eo = 0; eo < 2; ++eo) {
+        // [Z_eo.b0, Z_eo+2.b0, Z_eo.b1, Z_eo+2.b1] and the same for bytes 2, 3
+        const uint32_t p01 = __builtin_amdgcn_perm(Z[eo + 2], Z[eo], 0x05010400u);
+        const uint32_t p23 = __builtin_amdgcn_perm(Z[eo + 2], Z[eo], 0x07030602u);
+        fsum[0] = __builtin_amdgcn_sdot4(int(p01), 0x00000101, fsum[0], false);
+        fsum[1] = __builtin_amdgcn_sdot4(int(p01), 0x01010000, fsum[1], false);
+        fsum[2] = __builtin_amdgcn_sdot4(int(p23), 0x00000101, fsum[2], false);
+        fsum[3] = __builtin_amdgcn_sdot4(int(p23), 0x01010000, fsum[3], false);
+        uint8_t* rec = recs + (((t * 2 + eo) * G + gr) * 64 + 4 * bb + 16 * kg) * 16 + 2 * (lane % 8);
+        *reinterpret_cast<uint16_t*>(rec + 0 * 16) = uint16_t(p01);
+        *reinterpret_cast<uint16_t*>(rec + 1 * 16) = uint16_t(p01 >> 16);
+        *reinterpret_cast<uint16_t*>(rec + 2 * 16) = uint16_t(p23);
+        *reinterpret_cast<uint16_t*>(rec + 3 * 16) = uint16_t(p23 >> 16);
       }
     }
     // the columns' limb sums over the slab: exact integers
@@ -1248,35 +1258,31 @@ __global__ __launch_bounds__(64 * NW) void int4_gemv_b8_kernel(const I4B8Block* 
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int j = E0; j < R0; ++j) load_tile(j, tile_of(j));
+  for (int j = E0; j < R0; ++j) load_unit(j, j);
   __builtin_amdgcn_sched_barrier(0);
   lds_sync();
 
-  // this wave's slab: fold, exponent and finiteness of its column
-  int fold[G], ex[G], fin[G];
+  // 3. the units through the ring; a tile's slab terms add in slab order in
+  //    registers, then its epilogue
+  const __amdgpu_buffer_rsrc_t ybuf =
+      __builtin_amdgcn_make_buffer_rsrc(d.y, 0, int(batch * N * int64_t(sizeof(float))), 0x00020000);
+  f32x4_t tv[G];
+  float scale = 0.0f;
 #pragma unroll
-  for (int gr = 0; gr < G; ++gr) {
-    const int b = 4 * gr + (col >> 2);
-    fold[gr] = sfold[q][gr][col];
-    ex[gr] = 8 * cl - sF[q][b];
-    fin[gr] = sfin[q][b];
-  }
-  const uint32_t* bq = bop + q * (ST * 2 * G * 64 * 4);
-
-  // 3. the tiles through the ring
-#pragma unroll
-  for (int i = 0; i < T; ++i) {
-    const int slot = i % R;
+  for (int u = 0; u < U; ++u) {
+    const int slot = u % R, q = u & (S - 1);
+    const uint32_t* bq = bop + q * SLAB;
     i32x4_t acc[G];
 #pragma unroll
     for (int gr = 0; gr < G; ++gr) acc[gr] = i32x4_t{0, 0, 0, 0};
 #pragma unroll
     for (int t = 0; t < ST; ++t) {
       const uint4 w = wb[slot][t];
-      const i32x4_t ev = {int(low_nibbles(w.x)), int(low_nibbles(w.y)), int(low_nibbles(w.z)),
-                          int(low_nibbles(w.w))};
-      const i32x4_t od = {int(low_nibbles(w.x >> 4)), int(low_nibbles(w.y >> 4)),
-                          int(low_nibbles(w.z >> 4)), int(low_nibbles(w.w >> 4))};
+      // plain masks, not low_nibbles: these feed the matrix cores
+      const i32x4_t ev = {int(w.x & 0x0F0F0F0Fu), int(w.y & 0x0F0F0F0Fu), int(w.z & 0x0F0F0F0Fu),
+                          int(w.w & 0x0F0F0F0Fu)};
+      const i32x4_t od = {int((w.x >> 4) & 0x0F0F0F0Fu), int((w.y >> 4) & 0x0F0F0F0Fu),
+                          int((w.z >> 4) & 0x0F0F0F0Fu), int((w.w >> 4) & 0x0F0F0F0Fu)};
 #pragma unroll
       for (int gr = 0; gr < G; ++gr) {
         const u32x4_t e4 = *reinterpret_cast<const u32x4_t*>(bq + (((t * 2 + 0) * G + gr) * 64 + lane) * 4);
@@ -1287,52 +1293,73 @@ __global__ __launch_bounds__(64 * NW) void int4_gemv_b8_kernel(const I4B8Block* 
             od, i32x4_t{int(o4.x), int(o4.y), int(o4.z), int(o4.w)}, acc[gr], 0, 0, 0);
       }
     }
-    float sc[4];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) sc[v] = sb[slot][v];
+    if (q == 0) scale = sb[slot];
     __builtin_amdgcn_sched_barrier(0);
-    if (i + R < T) load_tile(slot, tile_of(i + R));
+    if (u + R < U) load_unit(slot, u + R);
     __builtin_amdgcn_sched_barrier(0);
     // acc[gr][v]: row 16 i + 4 g + v, column (batch 4 gr + col / 4, limb
-    // cl); a slab whose x is not finite gives NaN, so the whole output row
-    // is non-finite, as in the reference
-    f32x4_t tv[G];
+    // cl). A limb term acc - 8 fold is below 2^24, so it and its power-of-two
+    // scaling are exact in fp32; a slab whose x is not finite gives NaN, so
+    // the whole output row is non-finite, as in the reference.
 #pragma unroll
-    for (int gr = 0; gr < G; ++gr)
+    for (int gr = 0; gr < G; ++gr) {
+      const int b = 4 * gr + (col >> 2);
+      const int fold = sfold[q][gr][col], ex = 8 * cl - sF[q][b];
+      const bool fin = sfin[q][b] != 0;
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        tv[gr][v] = fin[gr] ? ldexpf(float(acc[gr][v] - 8 * fold[gr]), ex[gr])
-                            : __int_as_float(0x7fc00000);
-    bool report = true;
-    if (S > 1) {
-      // the group's S slab terms meet in LDS and add in slab order
-#pragma unroll
-      for (int gr = 0; gr < G; ++gr) part[i & 1][wave][gr][lane] = tv[gr];
-      lds_sync();
-      report = q == 0;
-      if (report) {
-        for (int s2 = 1; s2 < S; ++s2)
-#pragma unroll
-          for (int gr = 0; gr < G; ++gr) tv[gr] += part[i & 1][wave + s2][gr][lane];
+      for (int v = 0; v < 4; ++v) {
+        const float term = fin ? ldexpf(float(acc[gr][v] - 8 * fold), ex) : __int_as_float(0x7fc00000);
+        tv[gr][v] = q == 0 ? term : tv[gr][v] + term;
       }
     }
-    if (report) {
-      // a batch's 4 limb terms (a lane quad) add in fp32
-      const int64_t tile = tile_of(i);
+    if (q == S - 1) {
+      // a batch's 4 limb terms (a lane quad) add in fp32, times the rows'
+      // scales (from lanes 4 g + v); lane (4 bb, g) then holds rows 4 g ..
+      // 4 g + 3 of batch 4 gr + bb, staged in LDS so that each store writes
+      // 16 consecutive rows of a batch per 16 lanes
+      const int64_t row_base = tile_of(u) * 16;
+      float sc[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sc[v] = __shfl(scale, 4 * g + v, 64);
 #pragma unroll
       for (int gr = 0; gr < G; ++gr) {
         const int b = 4 * gr + (col >> 2);
+        f32x4_t o;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           float t2 = tv[gr][v];
           t2 += quad_xor_f<1>(t2);
           t2 += quad_xor_f<2>(t2);
-          const int64_t row = tile * 16 + 4 * g + v;
-          if (cl == 0 && b < batch && row < N) gstore_f(d.y + int64_t(b) * N + row, sc[v] * t2);
+          o[v] = sc[v] * t2;
         }
+        if (cl == 0) *reinterpret_cast<f32x4_t*>(&sm.ystage[wave][b][4 * g]) = o;
+      }
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        const int b = 4 * k + lane / 16, rr = lane % 16;
+        const int64_t row = row_base + rr;
+        const float v = sm.ystage[wave][b][rr];
+        const int off = b < batch && row < N ? int((int64_t(b) * N + row) * int64_t(sizeof(float)))
+                                             : int(0x80000000u);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ybuf, off, 0, 0);
       }
     }
   }
+}
+
+// U1 units per wave for K = 768 and 1536, U4 for K = 3072 (whose blocks
+// prepare four slabs of x and so stream fewer units).
+template <int G, int U1, int U4, int R, int RE, int NW>
+__global__ __launch_bounds__(64 * NW) void int4_gemv_b8_kernel(const I4B8Block* __restrict__ tab,
+                                                               int batch) {
+  __shared__ I4B8Smem<G, NW> sm;
+  const I4B8Block d = tab[blockIdx.x];
+  if (d.S == 4)
+    int4_b8_block<G, 4, U4, R, RE, NW>(sm, d, batch);
+  else if (d.S == 2)
+    int4_b8_block<G, 2, U1, R, RE, NW>(sm, d, batch);
+  else
+    int4_b8_block<G, 1, U1, R, RE, NW>(sm, d, batch);
 }
 
 // Fallback for K not a multiple of 32: one thread per (b, row), exact formula.
@@ -1536,27 +1563,33 @@ bool int4_stream_ok(int64_t K, const uint8_t* W) {
   return K > 0 && K % kI4SlabK == 0 && (S == 1 || S == 2 || S == 4) && aligned16(W);
 }
 
-constexpr int kI4B8Tiles = 6;  // 16-row tiles per wave group
-constexpr int kI4B8Ring = 2;   // tiles in flight per wave
-constexpr int kI4B8Early = 1;  // of which issued before the x preparation
-constexpr int kI4B8Waves = 8;  // waves per block
+constexpr int kI4B8Units = 6;   // (tile, slab) units per wave, K = 768 and 1536
+constexpr int kI4B8Units4 = 4;  // and K = 3072
+constexpr int kI4B8Ring = 2;    // units in flight per wave
+constexpr int kI4B8Early = 1;   // of which issued before the x preparation
+constexpr int kI4B8Waves = 8;   // waves per block
+static_assert(kI4B8Units % 2 == 0 && kI4B8Units4 % 4 == 0, "whole tiles per wave");
 
 // One int4_gemv_b8_kernel launch over every matrix; a block covers
-// 16 x kI4B8Tiles x (kI4B8Waves / S) rows of one matrix.
+// 16 x (units / S) x kI4B8Waves rows of one matrix.
 template <int G>
 void launch_int4_b8(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats, int batch) {
   std::vector<I4B8Block> tab;
   for (const Int4MfMat& m : mats) {
     const int64_t S = m.K / kI4SlabK;
-    IH_REQUIRE(m.N < (int64_t(1) << 31), INFERC_ERR_SHAPE, "int4 gemv: too many rows");
-    const int64_t rblocks = ceil_div(m.N, 16 * kI4B8Tiles * (kI4B8Waves / S));
+    // buffer-store offsets of the output are 31-bit byte counts
+    IH_REQUIRE(m.N * batch * int64_t(sizeof(float)) < (int64_t(1) << 31), INFERC_ERR_SHAPE,
+               "int4 gemv: output too large for one launch");
+    const int64_t tiles = (S == 4 ? kI4B8Units4 : kI4B8Units) / S;
+    const int64_t rblocks = ceil_div(m.N, 16 * tiles * kI4B8Waves);
     for (int64_t rbk = 0; rbk < rblocks; ++rbk)
       tab.push_back(I4B8Block{m.W, m.s, m.x, m.y, int32_t(m.N), int32_t(S), int32_t(rbk), 0});
   }
   IH_REQUIRE(tab.size() < (size_t(1) << 31), INFERC_ERR_SHAPE, "int4 gemv: launch too large");
   ctx->reserve_tables(1);
   const I4B8Block* dev = upload_table(ctx, tab);
-  hipLaunchKernelGGL((int4_gemv_b8_kernel<G, kI4B8Tiles, kI4B8Ring, kI4B8Early, kI4B8Waves>),
+  hipLaunchKernelGGL((int4_gemv_b8_kernel<G, kI4B8Units, kI4B8Units4, kI4B8Ring, kI4B8Early,
+                                          kI4B8Waves>),
                      dim3(unsigned(tab.size())), dim3(64 * kI4B8Waves), 0, ctx->stream, dev, batch);
   check_launch("int4_gemv_b8");
 }
