@@ -1577,9 +1577,10 @@ void launch_int4_b8(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats, int
   std::vector<I4B8Block> tab;
   for (const Int4MfMat& m : mats) {
     const int64_t S = m.K / kI4SlabK;
-    // buffer-store offsets of the output are 31-bit byte counts
+    // buffer-store offsets of the output are 31-bit byte counts (int4_grouped
+    // sends larger outputs to the int8-MFMA kernel)
     IH_REQUIRE(m.N * batch * int64_t(sizeof(float)) < (int64_t(1) << 31), INFERC_ERR_SHAPE,
-               "int4 gemv: output too large for one launch");
+               "int4 gemv: output too large for the batched kernel");
     const int64_t tiles = (S == 4 ? kI4B8Units4 : kI4B8Units) / S;
     const int64_t rblocks = ceil_div(m.N, 16 * tiles * kI4B8Waves);
     for (int64_t rbk = 0; rbk < rblocks; ++rbk)
@@ -1713,7 +1714,9 @@ void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const 
       va.push_back(Int4MfMat{W[i], scales[i], x[i], y[i], N, K});
       continue;
     }
-    if (int4_stream_ok(K, W[i]) && aligned16(x[i])) {
+    // (its output is addressed with 31-bit buffer offsets)
+    if (int4_stream_ok(K, W[i]) && aligned16(x[i]) &&
+        N * batch * int64_t(sizeof(float)) < (int64_t(1) << 31)) {
       st.push_back(Int4MfMat{W[i], scales[i], x[i], y[i], N, K});
       continue;
     }

@@ -72,7 +72,7 @@ def _gpt2_int4_set(ctx, seed, batch):
 
 def test_int4_grouped_gpt2_volume_batch8_two_copies(ctx):
     """BASELINE config 5 at B=8: all 49 GPT-2-small matrices in one grouped
-    call (x preparation + streaming int8-MFMA launch), every row of every
+    call (one launch of the batched int8-MFMA kernel), every row of every
     matrix checked. Two weight copies are launched in rotation, as the bench
     does, and the first copy again, so the cached descriptor tables are
     looked up and reused."""
@@ -87,10 +87,32 @@ def test_int4_grouped_gpt2_volume_batch8_two_copies(ctx):
             _check_rows(y.numpy(), W, s, x, K)
 
 
+@pytest.mark.parametrize("B", [2, 5, 8])
+def test_int4_grouped_mixed_row_lengths_and_odd_rows(ctx, B):
+    """One grouped call of the batched kernel over K = 768, 1536 and 3072
+    (one, two and four slabs per row), with row counts that end mid-tile and
+    mid-block, odd ones whose output rows of later batches start unaligned,
+    and single-row matrices: every row of every matrix against the oracle,
+    outputs pre-filled with NaN so a row left unwritten fails."""
+    shapes = [(1, 768), (4099, 768), (17, 1536), (385, 1536), (1, 3072), (769, 3072),
+              (33, 3072), (2304, 768)]
+    mats, host = [], []
+    for i, (N, K) in enumerate(shapes):
+        W, s = graphs.int4_weights(N, K, 320 + i, f"mix{i}")
+        x = rnd((B, K), 7000 + 10 * B + i)
+        y = Tensor.empty(ctx, (B, N))
+        _fill(y, np.nan)
+        mats.append((T(ctx, W, np.uint8), T(ctx, s), T(ctx, x), y, K))
+        host.append((W, s, x, K))
+    rt.int4_gemv_grouped(ctx, mats, B)
+    for (_, _, _, y, _), (W, s, x, K) in zip(mats, host):
+        _check_rows(y.numpy(), W, s, x, K)
+
+
 def test_int4_grouped_table_cache_eviction(ctx):
     """A fresh context fills its descriptor-table cache to one slot short of
     full with single-table batch-1 launches; a batch-8 grouped launch then
-    needs two tables. Both must be alive when its kernels run."""
+    needs one more table, which must be alive when its kernel runs."""
     with rt.Context(0) as c2:
         N, K = 64, 768
         W, s = graphs.int4_weights(N, K, 310, "evict")
