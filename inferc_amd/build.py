@@ -43,6 +43,9 @@ CXXFLAGS = [
     "-fPIC",
     f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # leading scalar kernel arguments arrive in SGPRs at wave launch, so a
+    # kernel's first loads need no scalar load of its argument block
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-result",
     f"-I{ROOT / 'include'}",

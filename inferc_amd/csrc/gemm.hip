@@ -455,8 +455,16 @@ struct KsFrag {
 
 // P is the register ring depth: k-groups in flight per wave.
 template <int WM, int WN, int W, int P, bool TB, bool LNA, bool LNR>
-__global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t tiles_m,
-                                                          int64_t tiles_n) {
+__global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(const float* __restrict__ A0,
+                                                          const float* __restrict__ B0,
+                                                          int lda_, int ldb_, int M_, int N_, int K_,
+                                                          int kps_, int tiles_m_, int tiles_n_,
+                                                          GemmParams p) {
+  // The first ring needs only the leading scalar arguments, which the
+  // hardware preloads into SGPRs at wave launch; the rest of p (epilogue,
+  // LayerNorm terms, other slices) is read while those loads are in flight.
+  const int64_t lda = lda_, ldb = ldb_, M = M_, N = N_, K = K_, kps = kps_;
+  const int64_t tiles_m = tiles_m_, tiles_n = tiles_n_;
   constexpr int RA = WM / 16, CB = WN / 16;
   static_assert(W * WM * WN * 4 <= 65536, "partial tiles must fit the LDS of one block");
   __shared__ __attribute__((aligned(16))) float red[W * WM * WN];
@@ -475,15 +483,19 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
   const int64_t m0 = (t % tiles_m) * WM, n0 = (t / tiles_m) * WN;
 
   const int slice = blockIdx.y;
-  const float* A = p.A + slice * p.sa;
-  const float* B = p.use_table ? p.Bt[slice] : p.B + slice * p.sb;
+  const float* A = A0;  // slice 0's operands
+  const float* B = B0;
+  if (slice != 0) {
+    A = p.A + slice * p.sa;
+    B = p.use_table ? p.Bt[slice] : p.B + slice * p.sb;
+  }
 
   // Wave w owns K range [kb, ke); it runs `rings` rounds of P 16-deep
   // k-groups (the host sizes k_per_split so that rounds are mostly full;
   // groups past ke load zeros).
-  const int64_t kb = int64_t(wave) * p.k_per_split;
-  const int64_t ke = kb + p.k_per_split < p.K ? kb + p.k_per_split : p.K;
-  const int64_t rings = (p.k_per_split + 16 * P - 1) / (16 * P);
+  const int64_t kb = int64_t(wave) * kps;
+  const int64_t ke = kb + kps < K ? kb + kps : K;
+  const int64_t rings = (kps + 16 * P - 1) / (16 * P);
 
   floatx4 acc[RA][CB];
 #pragma unroll
@@ -498,17 +510,17 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
   // the loads below, whose waits are then counted exactly).
 #pragma unroll
   for (int q = 0; q < P; ++q)
-    f[q].load(A, p.lda, B, p.ldb, p.M, p.N, p.K, m0, n0, kb + 16 * q, ke, r, g);
+    f[q].load(A, lda, B, ldb, M, N, K, m0, n0, kb + 16 * q, ke, r, g);
   __builtin_amdgcn_sched_barrier(0);
   // LayerNorm statistics of the tile's rows (row 4 * wave + lane / 16 per
   // lane group), needed only by the epilogue: loaded behind the first ring
   // and merged after the K loop.
   static_assert(WM <= 4 * W, "a lane group per row of the tile");
   const int si = 4 * wave + (lane >> 4);
-  const int64_t srow = m0 + si < p.M ? m0 + si : p.M - 1;
+  const int64_t srow = m0 + si < M ? m0 + si : M - 1;
   RowStatLoads sla, slr;
-  if (LNA) row_stats_load(sla, p.na_stats, srow, p.K / 16, lane);
-  if (LNR) row_stats_load(slr, p.nr_stats, srow, p.N / 16, lane);
+  if (LNA) row_stats_load(sla, p.na_stats, srow, K / 16, lane);
+  if (LNR) row_stats_load(slr, p.nr_stats, srow, N / 16, lane);
   // This thread's epilogue operands (elements e = tid + 64 W k of the tile),
   // fetched now so the epilogue after the K loop waits on no memory: C, R,
   // the column sums (LNA) and R's gamma and beta (LNR). The loads are
@@ -522,8 +534,8 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
 #pragma unroll
   for (int k = 0; k < EPT; ++k) {
     const int e = tid + 64 * W * k < WM * WN ? tid + 64 * W * k : 0;
-    const int64_t row = m0 + e / WN < p.M ? m0 + e / WN : p.M - 1;
-    const int64_t col = n0 + e % WN < p.N ? n0 + e % WN : p.N - 1;
+    const int64_t row = m0 + e / WN < M ? m0 + e / WN : M - 1;
+    const int64_t col = n0 + e % WN < N ? n0 + e % WN : N - 1;
     const int64_t ci = p.c_kind == INFERC_C_ROW ? col
                        : p.c_kind == INFERC_C_FULL ? row * p.ldc + col
                                                    : 0;
@@ -544,7 +556,7 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
         // out as soon as slot q has been consumed.
         __builtin_amdgcn_sched_barrier(0);
         f[q].mma(acc);
-        f[q].load(A, p.lda, B, p.ldb, p.M, p.N, p.K, m0, n0, k_next + 16 * q, ke, r, g);
+        f[q].load(A, lda, B, ldb, M, N, K, m0, n0, k_next + 16 * q, ke, r, g);
       }
     }
 #pragma unroll
@@ -557,11 +569,11 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
   // The rows' statistics, merged after the K loop, behind the barrier that
   // publishes the partial tiles.
   if constexpr (LNA) {
-    const float2 v = row_stats_merge(sla, p.K / 16, p.na_eps, lane);
+    const float2 v = row_stats_merge(sla, K / 16, p.na_eps, lane);
     if ((lane & 15) == 0 && si < WM) nstat[0][si] = v;
   }
   if constexpr (LNR) {
-    const float2 v = row_stats_merge(slr, p.N / 16, p.nr_eps, lane);
+    const float2 v = row_stats_merge(slr, N / 16, p.nr_eps, lane);
     if ((lane & 15) == 0 && si < WM) nstat[1][si] = v;
   }
   // Partial tiles to LDS in [row][col] order of the block's output tile.
@@ -585,7 +597,7 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
 #pragma unroll
     for (int w = 1; w < W; ++w) s += red[w * (WM * WN) + e];
     const int64_t row = m0 + e / WN, col = n0 + e % WN;
-    if (row < p.M && col < p.N) {
+    if (row < M && col < N) {
       if constexpr (LNA) {
         // A read through its LayerNorm with gamma folded into B:
         // rstd * (sum_k a_k B'_kn - mean * colsum_n); beta's share is in C
@@ -617,7 +629,7 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
     for (int idx = tid; idx < WM * NCH; idx += 64 * W) {
       const int i = idx / NCH, c = idx % NCH;
       const int64_t row = m0 + i, col0 = n0 + 16 * c;
-      if (row >= p.M || col0 >= p.N) continue;
+      if (row >= M || col0 >= N) continue;
       const float* v = red + i * WN + 16 * c;
       float mean = 0.0f;
 #pragma unroll
@@ -629,7 +641,7 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
         const float d = v[k] - mean;
         m2 += d * d;
       }
-      float* o = p.st_out + (int64_t(slice) * p.M * (p.N / 16) + row * (p.N / 16) + col0 / 16) * 2;
+      float* o = p.st_out + (int64_t(slice) * M * (N / 16) + row * (N / 16) + col0 / 16) * 2;
       o[0] = mean;
       o[1] = m2;
     }
@@ -637,6 +649,13 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(GemmParams p, int64_t 
 }
 
 struct KsCfg { int wm, wn, w, p; };
+
+// The small-M kernel takes its extents and leading dimensions as 32-bit
+// kernel arguments.
+inline bool ks_fits_i32(const GemmParams& p) {
+  const int64_t lim = int64_t(1) << 31;
+  return p.M < lim && p.N < lim && p.K < lim && p.lda < lim && p.ldb < lim;
+}
 
 // K per wave: whole rings of P k-groups, split as evenly as that allows.
 inline int64_t ks_k_per_wave(int64_t K, int w, int depth) {
@@ -652,10 +671,13 @@ void launch_ksplit(GemmParams p, int64_t slices, bool tb, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(slices));
   const dim3 block(64 * W);
   const bool lna = p.na_stats != nullptr, lnr = p.nr_stats != nullptr;
+  const float* B0 = p.use_table ? p.Bt[0] : p.B;  // slice 0's B
+  IH_REQUIRE(ks_fits_i32(p), INFERC_ERR_SHAPE, "gemm: small-M shape beyond 32-bit extents");
 #define IH_KS(TB_, LNA_, LNR_)                                                           \
   if (tb == TB_ && lna == LNA_ && lnr == LNR_) {                                         \
     hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, TB_, LNA_, LNR_>), grid, block, 0, s, \
-                       p, tm, tn);                                                        \
+                       p.A, B0, int(p.lda), int(p.ldb), int(p.M), int(p.N), int(p.K),   \
+                       int(p.k_per_split), int(tm), int(tn), p);                        \
     return;                                                                               \
   }
   IH_KS(false, false, false)
@@ -693,7 +715,8 @@ bool ksplit_supported(const GemmParams& p, int64_t slices, bool ta, bool vec, in
                       int64_t big_tiles) {
   // Operands need float4 rows (vec), A row-major; the shape must be one the
   // LDS-tiled kernel would have split over K (too few 128x128 tiles).
-  return !ta && vec && big_tiles < cus && p.M <= 512 && p.K > 0 && slices < 65536;
+  return !ta && vec && big_tiles < cus && p.M <= 512 && p.K > 0 && slices < 65536 &&
+         ks_fits_i32(p);
 }
 
 void run_ksplit(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool tb) {

@@ -143,11 +143,27 @@ struct Gemv2P {
   ValIdxPart* amax;      // [gridDim.x]
 };
 
+// x (and LayerNorm's gamma and beta) for the lane's columns; the loads go
+// out before any of them is used.
 template <int KV, int XSRC>
-__device__ __forceinline__ void gemv2_x(const Gemv2P& p, int lane, float4 (&xv)[KV]) {
-  constexpr int K = 256 * KV;
+__device__ __forceinline__ void gemv2_x_load(const Gemv2P& p, const float* x, int lane,
+                                             float4 (&xv)[KV], float4 (&lg)[KV], float4 (&lb)[KV]) {
 #pragma unroll
-  for (int j = 0; j < KV; ++j) xv[j] = *reinterpret_cast<const float4*>(p.x + 4 * lane + 256 * j);
+  for (int j = 0; j < KV; ++j) xv[j] = *reinterpret_cast<const float4*>(x + 4 * lane + 256 * j);
+  if (XSRC == XSRC_LN) {
+#pragma unroll
+    for (int j = 0; j < KV; ++j) {
+      lg[j] = *reinterpret_cast<const float4*>(p.ln_g + 4 * lane + 256 * j);
+      lb[j] = *reinterpret_cast<const float4*>(p.ln_b + 4 * lane + 256 * j);
+    }
+  }
+}
+
+// x through the optional LayerNorm prologue
+template <int KV, int XSRC>
+__device__ __forceinline__ void gemv2_x(const Gemv2P& p, int lane, float4 (&xv)[KV],
+                                        const float4 (&lg)[KV], const float4 (&lb)[KV]) {
+  constexpr int K = 256 * KV;
   if (XSRC == XSRC_LN) {
     float s = 0.0f;
 #pragma unroll
@@ -163,8 +179,7 @@ __device__ __forceinline__ void gemv2_x(const Gemv2P& p, int lane, float4 (&xv)[
     const float inv = 1.0f / sqrtf(var + p.ln_eps);
 #pragma unroll
     for (int j = 0; j < KV; ++j) {
-      const float4 g = *reinterpret_cast<const float4*>(p.ln_g + 4 * lane + 256 * j);
-      const float4 b = *reinterpret_cast<const float4*>(p.ln_b + 4 * lane + 256 * j);
+      const float4 g = lg[j], b = lb[j];
       xv[j].x = (xv[j].x * inv) * g.x + b.x;
       xv[j].y = (xv[j].y * inv) * g.y + b.y;
       xv[j].z = (xv[j].z * inv) * g.z + b.z;
@@ -174,20 +189,35 @@ __device__ __forceinline__ void gemv2_x(const Gemv2P& p, int lane, float4 (&xv)[
 }
 
 template <int R, int KV, int XSRC, bool ARGMAX>
-__global__ __launch_bounds__(kBlock) void gemv2_kernel(Gemv2P p) {
+// W, x and N lead the arguments, so the first loads wait on no scalar load of
+// the argument block (leading arguments arrive in SGPRs); every other operand
+// (LayerNorm terms, bias, residual) is fetched right behind them.
+__global__ __launch_bounds__(kBlock) void gemv2_kernel(const float* __restrict__ W,
+                                                      const float* __restrict__ x, int64_t N,
+                                                      Gemv2P p) {
   constexpr int K = 256 * KV;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t r0 = (int64_t(blockIdx.x) * kWaves + wave) * R;
   float4 w[R][KV];
 #pragma unroll
-  for (int i = 0; i < R; ++i)
+  for (int i = 0; i < R; ++i) {
+    const int64_t rc = r0 + i < N ? r0 + i : N - 1;  // rows past N: clamped, never stored
 #pragma unroll
     for (int j = 0; j < KV; ++j)
-      w[i][j] = (r0 + i < p.N)
-                    ? *reinterpret_cast<const float4*>(p.W + (r0 + i) * K + 4 * lane + 256 * j)
-                    : make_float4(0.f, 0.f, 0.f, 0.f);
-  float4 xv[KV];
-  gemv2_x<KV, XSRC>(p, lane, xv);
+      w[i][j] = *reinterpret_cast<const float4*>(W + rc * K + 4 * lane + 256 * j);
+  }
+  float4 xv[KV], lg[KV], lb[KV];
+  gemv2_x_load<KV, XSRC>(p, x, lane, xv, lg, lb);
+  // the epilogue's bias and residual of the wave's rows (an absent operand
+  // reads W instead)
+  float bb[R], rr[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int64_t rc = r0 + i < N ? r0 + i : N - 1;
+    bb[i] = (p.bias ? p.bias : W)[p.bias ? rc : 0];
+    rr[i] = (p.res ? p.res : W)[p.res ? rc : 0];
+  }
+  gemv2_x<KV, XSRC>(p, lane, xv, lg, lb);
   float acc[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
@@ -202,10 +232,10 @@ __global__ __launch_bounds__(kBlock) void gemv2_kernel(Gemv2P p) {
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int64_t r = r0 + i;
-    if (r < p.N) {
+    if (r < N) {
       float v = acc[i];
-      if (p.bias) v = v + p.bias[r0 + i];
-      if (p.res) v = v + p.res[r0 + i];
+      if (p.bias) v = v + bb[i];
+      if (p.res) v = v + rr[i];
       v = apply_act(v, p.act);
       if (lane == i) p.y[r] = v;
       if (ARGMAX && v > bv) {  // rows ascend: strict '>' keeps the first max
@@ -1414,12 +1444,16 @@ template <int R, int KV>
 void gemv2_launch_r(const Gemv2P& p, unsigned blocks, int xsrc, bool argmax, hipStream_t s) {
   const dim3 g(blocks), b(kBlock);
   if (argmax) {
-    if (xsrc == XSRC_LN) hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_LN, true>), g, b, 0, s, p);
-    else hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_PLAIN, true>), g, b, 0, s, p);
+    if (xsrc == XSRC_LN)
+      hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_LN, true>), g, b, 0, s, p.W, p.x, p.N, p);
+    else
+      hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_PLAIN, true>), g, b, 0, s, p.W, p.x, p.N, p);
     return;
   }
-  if (xsrc == XSRC_LN) hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_LN, false>), g, b, 0, s, p);
-  else hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_PLAIN, false>), g, b, 0, s, p);
+  if (xsrc == XSRC_LN)
+    hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_LN, false>), g, b, 0, s, p.W, p.x, p.N, p);
+  else
+    hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_PLAIN, false>), g, b, 0, s, p.W, p.x, p.N, p);
 }
 
 }  // namespace
