@@ -236,8 +236,9 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode_d64(AttnDecP p) {
 // blocks' (max logit, first index) partials (the strict '>' rule of
 // main.cpp:875-879), records tokens[pos+1], advances state = {pos+1, tok,
 // tok}, and writes the next step's input h = wte[tok] + wpe[pos+1]. Each
-// thread loads all of its partials before merging them (one memory round
-// trip instead of one per partial).
+// thread loads all of its partials, pos and its first wpe value before
+// merging them (one memory round trip instead of one per partial; only the
+// wte row waits for the merged token).
 constexpr int kFinishThreads = 1024;
 constexpr int kFinishPerThread = 8;  // up to 8192 partials
 
@@ -247,13 +248,18 @@ __global__ __launch_bounds__(kFinishThreads) void decode_finish_kernel(
     float* __restrict__ h, int64_t H, int64_t max_pos) {
   __shared__ float sv[kFinishThreads / 64];
   __shared__ int64_t si[kFinishThreads / 64];
-  __shared__ int64_t s_tok, s_pos;
+  __shared__ int64_t s_tok;
   ValIdxPart q[kFinishPerThread];
 #pragma unroll
   for (int k = 0; k < kFinishPerThread; ++k) {
     const int e = threadIdx.x + k * kFinishThreads;
     q[k] = e < n ? parts[e] : ValIdxPart{-INFINITY, INT64_MAX};
   }
+  // state[0] is read by every thread here, before thread 0 rewrites it
+  // behind the first barrier
+  const int64_t pos0 = state[0];
+  const bool emb = pos0 + 1 < max_pos;
+  const float wp0 = emb && threadIdx.x < H ? wpe[(pos0 + 1) * H + threadIdx.x] : 0.0f;
   float v = -INFINITY;
   int64_t i = INT64_MAX;
 #pragma unroll
@@ -284,18 +290,19 @@ __global__ __launch_bounds__(kFinishThreads) void decode_finish_kernel(
         i = si[w];
       }
     const int64_t tok = (i == INT64_MAX) ? 0 : i;
-    const int64_t pos = state[0];
-    tokens[pos + 1] = tok;
+    tokens[pos0 + 1] = tok;
     state[2] = tok;
     state[1] = tok;
-    state[0] = pos + 1;
+    state[0] = pos0 + 1;
     s_tok = tok;
-    s_pos = pos + 1;
   }
   __syncthreads();
-  if (s_pos < max_pos)
-    for (int64_t c = threadIdx.x; c < H; c += kFinishThreads)
-      h[c] = wte[s_tok * H + c] + wpe[s_pos * H + c];
+  if (emb) {
+    const int64_t tok = s_tok, p1 = pos0 + 1;
+    if (threadIdx.x < H) h[threadIdx.x] = wte[tok * H + threadIdx.x] + wp0;
+    for (int64_t c = threadIdx.x + kFinishThreads; c < H; c += kFinishThreads)
+      h[c] = wte[tok * H + c] + wpe[p1 * H + c];
+  }
 }
 
 // h[c] = wte[tok][c] + wpe[pos][c] with (pos, tok) = (state[0], state[1]).

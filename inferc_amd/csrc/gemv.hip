@@ -724,15 +724,13 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_valu_kernel(const Int4VaDesc
 //   - amax set (the LM head): each wave also stores the first maximum
 //     (value, row) of its rows, for the step's finishing kernel (y may be
 //     null then).
+// The pointers and sizes the first loads need lead the kernel's arguments,
+// which then arrive in SGPRs; the rest come in Int4DecP.
 struct Int4DecP {
-  Int4VaDesc d;
-  const float* ln_g;
-  const float* ln_b;
-  float ln_eps;
-  const float* bias;
-  const float* res;
-  int act;
+  float* y;
   ValIdxPart* amax;
+  float ln_eps;
+  int act;
 };
 
 // One wave per block: a decode-step matrix (1.7 to 2.4 MB of int4) is a few
@@ -740,13 +738,15 @@ struct Int4DecP {
 constexpr int kI4DecBlock = 64;
 
 template <int DW, int LT, int NC>
-__global__ __launch_bounds__(kI4DecBlock) void int4_gemv_dec_kernel(Int4DecP p, int64_t n_waves) {
+__global__ __launch_bounds__(kI4DecBlock) void int4_gemv_dec_kernel(
+    const uint8_t* __restrict__ W, const float* __restrict__ sc, const float* __restrict__ x,
+    const float* __restrict__ ln_g, const float* __restrict__ ln_b,
+    const float* __restrict__ bias, const float* resid, int32_t N, int32_t chunks, Int4DecP p) {
   static_assert(LT >= 4 && NC <= LT / 4, "a lane keeps one chunk's row");
   constexpr int K = 8 * DW * LT, rpp = 64 / LT;
   const int lane = threadIdx.x & 63;
-  const int64_t wid = blockIdx.x;
-  if (wid >= n_waves) return;
-  const Int4VaDesc& d = p.d;
+  const int64_t wid = blockIdx.x;  // the grid is exactly the matrix's waves
+  const Int4VaDesc d{W, sc, x, p.y, N, K, 0, DW, chunks, NC};
   const int s = lane & (LT - 1), rg = lane / LT;
   const int64_t c0 = wid * NC;
   const int n = int(d.chunks - c0 < NC ? d.chunks - c0 : NC);
@@ -758,7 +758,7 @@ __global__ __launch_bounds__(kI4DecBlock) void int4_gemv_dec_kernel(Int4DecP p, 
   for (int q = 0; q < 2 * DW; ++q) xv[q] = gload_f4(xp + q);
   constexpr int PL = K / 64;  // x values per lane for the row statistics
   float xs[PL];
-  if (p.ln_g) {
+  if (ln_g) {
 #pragma unroll
     for (int i = 0; i < PL; ++i) xs[i] = gload_f(d.x + lane + 64 * i);
   }
@@ -773,10 +773,10 @@ __global__ __launch_bounds__(kI4DecBlock) void int4_gemv_dec_kernel(Int4DecP p, 
   const int jr = s % (LT / 4), pr = s / (LT / 4);
   const int64_t r = ((c0 + jr) * kI4Passes + pr) * rpp + rg;
   const int64_t rc = r < d.N ? r : d.N - 1;
-  const float bpre = gload_f((p.bias ? p.bias : d.s) + (p.bias ? rc : 0));
-  const float rpre = gload_f((p.res ? p.res : d.s) + (p.res ? rc : 0));
+  const float bpre = gload_f((bias ? bias : d.s) + (bias ? rc : 0));
+  const float rpre = gload_f((resid ? resid : d.s) + (resid ? rc : 0));
   __builtin_amdgcn_sched_barrier(0);
-  if (p.ln_g) {
+  if (ln_g) {
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < PL; ++i) sum += xs[i];
@@ -788,8 +788,8 @@ __global__ __launch_bounds__(kI4DecBlock) void int4_gemv_dec_kernel(Int4DecP p, 
       q2 += dd * dd;
     }
     const float inv = 1.0f / sqrtf(wave_sum_dpp(q2) / float(K) + p.ln_eps);
-    const float4* gp = reinterpret_cast<const float4*>(p.ln_g + 8 * DW * s);
-    const float4* bp = reinterpret_cast<const float4*>(p.ln_b + 8 * DW * s);
+    const float4* gp = reinterpret_cast<const float4*>(ln_g + 8 * DW * s);
+    const float4* bp = reinterpret_cast<const float4*>(ln_b + 8 * DW * s);
 #pragma unroll
     for (int q = 0; q < 2 * DW; ++q) {
       const float4 g = gload_f4(gp + q), b = gload_f4(bp + q);
@@ -820,8 +820,8 @@ __global__ __launch_bounds__(kI4DecBlock) void int4_gemv_dec_kernel(Int4DecP p, 
   const bool valid = jr < n && r < d.N;
   float v = res;
   if (valid) {
-    if (p.bias) v += bpre;
-    if (p.res) v += rpre;
+    if (bias) v += bpre;
+    if (resid) v += rpre;
     v = apply_act(v, p.act);
   }
   if (valid && d.y) gstore_f(d.y + r, v);
@@ -1840,21 +1840,21 @@ void int4_gemv_dec(inferc_hip_ctx* ctx, int64_t N, int64_t K, const uint8_t* W,
   const int dw = K == 768 ? 3 : 6, nc = int4_dec_chunks(N, K);
   const int64_t L = K / 8 / dw, chunks = ceil_div(N, int64_t(kI4Passes) * (64 / L));
   const int64_t waves = int4_dec_waves(N, K);
-  Int4DecP p{};
-  p.d = Int4VaDesc{W, scales, x, y, N, K, 0, dw, chunks, nc};
-  p.ln_g = ln_g; p.ln_b = ln_b; p.ln_eps = ln_eps;
-  p.bias = bias; p.res = res; p.act = act; p.amax = amax;
+  const Int4DecP p{y, amax, ln_eps, act};
+  const int32_t n32 = int32_t(N), c32 = int32_t(chunks);
   const dim3 grid{unsigned(waves)}, block{unsigned(kI4DecBlock)};
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, block, 0, ctx->stream, W, scales, x, ln_g, ln_b, bias, res, n32,
+                       c32, p);
+  };
   if (dw == 3 && nc == 1)
-    hipLaunchKernelGGL((int4_gemv_dec_kernel<3, 32, 1>), grid, block, 0, ctx->stream, p, waves);
+    go(int4_gemv_dec_kernel<3, 32, 1>);
   else if (dw == 3)
-    hipLaunchKernelGGL((int4_gemv_dec_kernel<3, 32, kI4RunKB / 3>), grid, block, 0, ctx->stream,
-                       p, waves);
+    go(int4_gemv_dec_kernel<3, 32, kI4RunKB / 3>);
   else if (nc == 1)
-    hipLaunchKernelGGL((int4_gemv_dec_kernel<6, 64, 1>), grid, block, 0, ctx->stream, p, waves);
+    go(int4_gemv_dec_kernel<6, 64, 1>);
   else
-    hipLaunchKernelGGL((int4_gemv_dec_kernel<6, 64, kI4RunKB / 6>), grid, block, 0, ctx->stream,
-                       p, waves);
+    go(int4_gemv_dec_kernel<6, 64, kI4RunKB / 6>);
   check_launch("int4_gemv_dec");
 }
 
