@@ -9,12 +9,12 @@
 // is (acc + b) + residual for MatMul->Add(b)->Add(res) and GELU(acc + b) for
 // the fused FFN, as the reference computes them.
 //
-// Design: 256-thread blocks (4 wave64s in a 2x2 grid). Each wave owns a
-// (BM/2)x(BN/2) sub-tile made of 32x32 MFMA tiles. K advances in BK-deep
-// panels staged through LDS, double-buffered: the global loads of panel t+1
-// are in flight while panel t feeds the matrix cores. Both operands sit in
-// LDS k-major ([BK][outer]) so every MFMA operand read is 32 consecutive
-// floats per half-wave.
+// Design: 256-thread blocks (4 wave64s in a 2x2 or 4x1 grid). Each wave owns
+// a sub-tile made of 32x32 MFMA tiles. K advances in BK-deep panels staged
+// through LDS, double-buffered, with the global loads two panels ahead: those
+// of panel t+2 are in flight while panel t feeds the matrix cores. Both
+// operands sit in LDS k-major ([BK][outer]) so every MFMA operand read is 32
+// consecutive floats per half-wave.
 //
 // Shapes with too few 128x128 tiles to fill the 256 CUs go to one of two
 // other paths. Small M with float4-aligned row-major A (the b=1 encoder, GPT-2
@@ -33,6 +33,7 @@ namespace ih {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kMaxSlices = 3;
@@ -172,43 +173,80 @@ __device__ __forceinline__ float epilogue(const GemmParams& p, const float* C,
 // from global memory into registers, then into LDS laid out [BK][STRIDE].
 // KCONTIG: element (o,k) lives at P[o*ld + k] (K contiguous); otherwise at
 // P[k*ld + o] (the output dimension contiguous).
-template <int OUTER, int BK, int STRIDE, bool KCONTIG, bool VEC>
-struct PanelLoader {
+//
+// PanelAddr holds a thread's element offsets, computed once (32-bit: the
+// host keeps each operand below 2^31 elements); PanelRegs loads one panel
+// at depth k0 from them. Every load is issued, from coordinates clamped
+// into the matrix: a load under a branch would make the compiler wait for
+// all loads in flight at the join, not just for the panel being written.
+// Rows and columns past M and N only reach outputs that are never written;
+// k past the panel's valid depth is zeroed in LDS (zero_tail).
+template <int OUTER, int BK, bool KCONTIG, bool VEC>
+struct PanelAddr {
   static_assert((OUTER * BK) % (4 * kThreads) == 0, "panel must split into float4 per thread");
   static constexpr int NV = OUTER * BK / (4 * kThreads);
-  float4 r[NV];
+  int off[NV];  // the thread's float4 i at k0 = 0 (o clamped into the matrix)
+  int lim[NV];  // largest k0 whose load stays inside the matrix
+  int d[NV][4];  // !KCONTIG && !VEC: column j's offset, clamped
+  int ld;
 
-  __device__ __forceinline__ void load(const float* __restrict__ P, int64_t ld,
-                                       int64_t o0, int64_t o_lim, int64_t k0,
-                                       int64_t k_lim, int tid) {
+  // k_end: the matrix's K (the loads' bound; a split's own end is kn's)
+  __device__ __forceinline__ void init(int64_t ld_, int64_t o0, int64_t o_lim, int64_t k_end,
+                                       int tid) {
+    ld = int(ld_);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int idx = tid + kThreads * i;
-      int64_t o, k;
       if (KCONTIG) {
-        o = o0 + idx / (BK / 4);
-        k = k0 + (idx % (BK / 4)) * 4;
+        const int64_t o = o0 + idx / (BK / 4);
+        const int kq = (idx % (BK / 4)) * 4;
+        const int oc = int(o < o_lim ? o : o_lim - 1);
+        off[i] = oc * ld + kq;
+        // VEC: the float4 at k0 + kq must end by k_end (k_end % 4 == 0)
+        lim[i] = int(k_end - (VEC ? 4 : 1) - kq);
       } else {
-        k = k0 + idx / (OUTER / 4);
-        o = o0 + (idx % (OUTER / 4)) * 4;
-      }
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (VEC) {
-        // The contiguous extent is a multiple of 4, so an in-range first
-        // element implies the whole float4 is in range.
-        if (o < o_lim && k < k_lim)
-          v = *reinterpret_cast<const float4*>(KCONTIG ? P + o * ld + k : P + k * ld + o);
-      } else {
-        float e[4];
+        const int kl = idx / (OUTER / 4);
+        const int64_t o = o0 + (idx % (OUTER / 4)) * 4;
+        // VEC: o_lim % 4 == 0, so a float4 starting in range stays in range
+        const int oc = int(VEC ? (o < o_lim ? o : o_lim - 4) : o);
+        off[i] = kl * ld + oc;
+        lim[i] = int(k_end - 1 - kl);
+        if (!VEC) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t oj = KCONTIG ? o : o + j;
-          const int64_t kj = KCONTIG ? k + j : k;
-          e[j] = (oj < o_lim && kj < k_lim) ? P[KCONTIG ? oj * ld + kj : kj * ld + oj] : 0.0f;
+          for (int j = 0; j < 4; ++j) d[i][j] = int((o + j < o_lim ? o + j : o_lim - 1) - o);
         }
-        v = make_float4(e[0], e[1], e[2], e[3]);
       }
-      r[i] = v;
+    }
+  }
+};
+
+template <int OUTER, int BK, int STRIDE, bool KCONTIG, bool VEC>
+struct PanelRegs {
+  using Addr = PanelAddr<OUTER, BK, KCONTIG, VEC>;
+  static constexpr int NV = Addr::NV;
+  floatx4 r[NV];  // a native vector: whole-value copies stay in registers
+
+  __device__ __forceinline__ void load(const float* __restrict__ P, const Addr& a, int k0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if (KCONTIG) {
+        if (VEC) {
+          r[i] = *reinterpret_cast<const floatx4*>(P + (a.off[i] + (k0 < a.lim[i] ? k0 : a.lim[i])));
+        } else {
+          float e[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) e[j] = P[a.off[i] + (k0 + j < a.lim[i] ? k0 + j : a.lim[i])];
+          r[i] = floatx4{e[0], e[1], e[2], e[3]};
+        }
+      } else {
+        const int row = a.off[i] + (k0 < a.lim[i] ? k0 : a.lim[i]) * a.ld;
+        if (VEC) {
+          r[i] = *reinterpret_cast<const floatx4*>(P + row);
+        } else {
+          r[i] = floatx4{P[row + a.d[i][0]], P[row + a.d[i][1]], P[row + a.d[i][2]],
+                         P[row + a.d[i][3]]};
+        }
+      }
     }
   }
 
@@ -218,31 +256,60 @@ struct PanelLoader {
       const int idx = tid + kThreads * i;
       if (KCONTIG) {
         const int ol = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;
-        S[(kq + 0) * STRIDE + ol] = r[i].x;
-        S[(kq + 1) * STRIDE + ol] = r[i].y;
-        S[(kq + 2) * STRIDE + ol] = r[i].z;
-        S[(kq + 3) * STRIDE + ol] = r[i].w;
+        S[(kq + 0) * STRIDE + ol] = r[i][0];
+        S[(kq + 1) * STRIDE + ol] = r[i][1];
+        S[(kq + 2) * STRIDE + ol] = r[i][2];
+        S[(kq + 3) * STRIDE + ol] = r[i][3];
       } else {
         const int kl = idx / (OUTER / 4), oq = (idx % (OUTER / 4)) * 4;
-        *reinterpret_cast<float4*>(S + kl * STRIDE + oq) = r[i];
+        *reinterpret_cast<floatx4*>(S + kl * STRIDE + oq) = r[i];
+      }
+    }
+  }
+
+  // Zeroes the k rows at or past kn of what this thread stored (a last,
+  // partial panel); the writes carry constants only, so no load of the
+  // panel is made conditional on kn.
+  __device__ __forceinline__ void zero_tail(float* __restrict__ S, int tid, int kn) const {
+    if (kn >= BK) return;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int idx = tid + kThreads * i;
+      if (KCONTIG) {
+        const int ol = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (kq + j >= kn) S[(kq + j) * STRIDE + ol] = 0.0f;
+      } else {
+        const int kl = idx / (OUTER / 4), oq = (idx % (OUTER / 4)) * 4;
+        if (kl >= kn) *reinterpret_cast<floatx4*>(S + kl * STRIDE + oq) = floatx4{0, 0, 0, 0};
       }
     }
   }
 };
 
-template <int BM, int BN, int BK, bool TA, bool TB, bool VEC>
+// Four waves in a WGM x WGN grid, each owning a (BM/WGM) x (BN/WGN) sub-tile of
+// 32x32 MFMA tiles. Two register sets stage the panels, so the loads of panel
+// t+2 are issued before panel t's MFMAs and panel t+1, loaded during panel
+// t-1, is written to LDS after them: a panel's global latency is hidden
+// behind two panels of MFMAs instead of one. Every load is unconditional (a
+// panel index past the end repeats the last panel, whose copy is never
+// read), so the wait before each LDS write counts exactly the loads it needs.
+template <int BM, int BN, int BK, int WGM, int WGN, bool TA, bool TB, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmParams p) {
+  static_assert(WGM * WGN * 64 == kThreads, "four waves");
   // LDS row padding: 2 floats where rows are written element-wise (breaks
   // bank aliasing of the transposing stores), 4 where they are written as
   // float4 (keeps 16-byte alignment).
   constexpr int SA = BM + (TA ? 4 : 2);
   constexpr int SB = BN + (TB ? 2 : 4);
-  constexpr int TM = BM / 64, TN = BN / 64;
+  constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM * 32 == WTM && TN * 32 == WTN, "wave tiles of whole 32x32 MFMA tiles");
   __shared__ __attribute__((aligned(16))) float As[2][BK * SA];
   __shared__ __attribute__((aligned(16))) float Bs[2][BK * SB];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+  const int wm = (wave / WGN) * WTM, wn = (wave % WGN) * WTN;
   const int half = lane >> 5, l32 = lane & 31;
 
   const int64_t m0 = int64_t(blockIdx.y) * BM, n0 = int64_t(blockIdx.x) * BN;
@@ -263,42 +330,69 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  PanelLoader<BM, BK, SA, !TA, VEC> la;
-  PanelLoader<BN, BK, SB, TB, VEC> lb;
+  auto compute = [&](const float* as, const float* bs) {
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 2) {
+      float a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = as[(kk + half) * SA + wm + i * 32 + l32];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = bs[(kk + half) * SB + wn + j * 32 + l32];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
 
   if (nt > 0) {
-    la.load(A, p.lda, m0, p.M, kb, ke, tid);
-    lb.load(B, p.ldb, n0, p.N, kb, ke, tid);
-    la.store(As[0], tid);
-    lb.store(Bs[0], tid);
-    __syncthreads();
-    for (int64_t t = 0; t < nt; ++t) {
-      const int cur = int(t & 1);
-      if (t + 1 < nt) {
-        la.load(A, p.lda, m0, p.M, kb + (t + 1) * BK, ke, tid);
-        lb.load(B, p.ldb, n0, p.N, kb + (t + 1) * BK, ke, tid);
-      }
-      const float* as = As[cur];
-      const float* bs = Bs[cur];
-#pragma unroll
-      for (int kk = 0; kk < BK; kk += 2) {
-        float a[TM], b[TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i) a[i] = as[(kk + half) * SA + wm + i * 32 + l32];
-#pragma unroll
-        for (int j = 0; j < TN; ++j) b[j] = bs[(kk + half) * SB + wn + j * 32 + l32];
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
-      }
-      if (t + 1 < nt) {
-        la.store(As[cur ^ 1], tid);
-        lb.store(Bs[cur ^ 1], tid);
-      }
-      __syncthreads();
+    PanelAddr<BM, BK, !TA, VEC> aa;
+    PanelAddr<BN, BK, TB, VEC> ab;
+    aa.init(p.lda, m0, p.M, p.K, tid);
+    ab.init(p.ldb, n0, p.N, p.K, tid);
+    PanelRegs<BM, BK, SA, !TA, VEC> la0, la1;
+    PanelRegs<BN, BK, SB, TB, VEC> lb0, lb1;
+    // depth of panel t (the last panel repeats for t past the end), and
+    // its valid depth (BK but for a last, partial panel)
+    const int kb32 = int(kb), ntm1 = int(nt - 1), ke32 = int(ke);
+#define IH_K_OF(t) (kb32 + ((t) < ntm1 ? (t) : ntm1) * BK)
+#define IH_KN_OF(t) (ke32 - IH_K_OF(t) < BK ? ke32 - IH_K_OF(t) : BK)
+    la0.load(A, aa, IH_K_OF(0));
+    lb0.load(B, ab, IH_K_OF(0));
+    la1.load(A, aa, IH_K_OF(1));
+    lb1.load(B, ab, IH_K_OF(1));
+    la0.store(As[0], tid);
+    lb0.store(Bs[0], tid);
+    la0.zero_tail(As[0], tid, IH_KN_OF(0));
+    lb0.zero_tail(Bs[0], tid, IH_KN_OF(0));
+    lds_barrier();
+    // panels in pairs; both halves unconditional, so the two register sets
+    // stay two sets of registers
+    int t = 0;
+    for (; t + 1 <= ntm1; t += 2) {
+      la0.load(A, aa, IH_K_OF(t + 2));
+      lb0.load(B, ab, IH_K_OF(t + 2));
+      __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
+      compute(As[0], Bs[0]);
+      la1.store(As[1], tid);
+      lb1.store(Bs[1], tid);
+      la1.zero_tail(As[1], tid, IH_KN_OF(t + 1));
+      lb1.zero_tail(Bs[1], tid, IH_KN_OF(t + 1));
+      lds_barrier();
+      la1.load(A, aa, IH_K_OF(t + 3));
+      lb1.load(B, ab, IH_K_OF(t + 3));
+      __builtin_amdgcn_sched_barrier(0);
+      compute(As[1], Bs[1]);
+      la0.store(As[0], tid);
+      lb0.store(Bs[0], tid);
+      la0.zero_tail(As[0], tid, IH_KN_OF(t + 2));
+      lb0.zero_tail(Bs[0], tid, IH_KN_OF(t + 2));
+      lds_barrier();
     }
+    if (t == ntm1) compute(As[0], Bs[0]);  // an odd panel count's last panel
+#undef IH_K_OF
+#undef IH_KN_OF
   }
 
   // Accumulator layout of a 32x32 MFMA tile: register v of lane l holds
@@ -320,6 +414,54 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmParams p) {
   const float* C = p.use_table ? p.Ct[slice] : p.C;
   const float* R = p.R ? p.R + slice * p.sr : nullptr;
   float* Y = p.use_table ? p.Yt[slice] : p.Y + slice * p.sy;
+  if (m0 + BM <= p.M && n0 + BN <= p.N) {
+    // A whole tile: every operand load first, then the arithmetic and the
+    // stores (epilogue()'s order). Loads under a per-element bounds branch
+    // would cost one memory round trip per element.
+    const bool has_c = C != nullptr && p.beta != 0.0f;
+    const int kind = has_c ? p.c_kind : INFERC_C_NONE;
+    float cr[TN], cx[TM][TN][16], rx[TM][TN][16];
+    const float c0 = kind == INFERC_C_SCALAR ? C[0] : 0.0f;
+    if (kind == INFERC_C_ROW) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) cr[j] = C[n0 + wn + j * 32 + l32];
+    }
+    // (the uniform tests sit outside the loops, so each loop is one block of
+    // loads)
+    auto gather = [&](const float* X, int64_t ld, float (&dst)[TM][TN][16]) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int64_t row = m0 + wm + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            const int64_t col = n0 + wn + j * 32 + l32;
+            dst[i][j][v] = X[row * ld + col];
+          }
+    };
+    if (kind == INFERC_C_FULL) gather(C, p.ldc, cx);
+    if (R != nullptr) gather(R, p.ldr, rx);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t row = m0 + wm + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+          const int64_t col = n0 + wn + j * 32 + l32;
+          float x = p.alpha * acc[i][j][v];
+          if (has_c) {
+            const float c = kind == INFERC_C_ROW    ? cr[j]
+                            : kind == INFERC_C_FULL ? cx[i][j][v]
+                                                    : c0;  // 0 for an unknown kind
+            x = x + p.beta * c;
+          }
+          if (R != nullptr) x = x + rx[i][j][v];
+          Y[row * p.ldy + col] = apply_act(x, p.act);
+        }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -369,7 +511,6 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(GemmParams p) {
 // 16x16 block.
 // ---------------------------------------------------------------------------
 
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 
 template <int WM, int WN, bool TB>
@@ -728,18 +869,20 @@ void run_ksplit(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool tb) {
   check_launch("gemm_f32_ksplit");
 }
 
-template <int BM, int BN, int BK, bool TA, bool TB, bool VEC>
+template <int BM, int BN, int BK, int WGM, int WGN, bool TA, bool TB, bool VEC>
 void launch_cfg(const GemmParams& p, int64_t slices, hipStream_t s) {
   dim3 grid(unsigned(ceil_div(p.N, BN)), unsigned(ceil_div(p.M, BM)),
             unsigned(slices * p.splits));
-  hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, TA, TB, VEC>), grid, dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, TA, TB, VEC>), grid, dim3(kThreads), 0,
+                     s, p);
 }
 
-template <int BM, int BN, int BK>
+template <int BM, int BN, int BK, int WGM, int WGN>
 void launch_tile(const GemmParams& p, int64_t slices, bool ta, bool tb, bool vec,
                  hipStream_t s) {
-#define IH_GEMM_CASE(TA_, TB_, V_) \
-  if (ta == TA_ && tb == TB_ && vec == V_) return launch_cfg<BM, BN, BK, TA_, TB_, V_>(p, slices, s);
+#define IH_GEMM_CASE(TA_, TB_, V_)                                                      \
+  if (ta == TA_ && tb == TB_ && vec == V_)                                             \
+    return launch_cfg<BM, BN, BK, WGM, WGN, TA_, TB_, V_>(p, slices, s);
   IH_GEMM_CASE(false, false, true)
   IH_GEMM_CASE(false, true, true)
   IH_GEMM_CASE(true, false, true)
@@ -758,16 +901,32 @@ void run(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool ta, bool tb, bo
          void* partial_buf = nullptr, size_t partial_bytes = 0) {
   struct Cfg { int bm, bn, bk; };
   const int64_t cus = ctx->num_cus;
-  const Cfg big{128, 128, 16}, wide{128, 64, 16}, small{64, 64, 32};
+  const Cfg big{128, 128, 16}, mid{128, 96, 32}, wide{128, 64, 16}, small{64, 64, 32};
   auto tiles = [&](const Cfg& c) { return ceil_div(p.M, c.bm) * ceil_div(p.N, c.bn) * slices; };
   if (ksplit_supported(p, slices, ta, vec, cus, tiles(big))) return run_ksplit(ctx, p, slices, tb);
   IH_REQUIRE(p.na_stats == nullptr && p.nr_stats == nullptr && p.st_out == nullptr,
              INFERC_ERR_UNSUPPORTED,
              "gemm: LayerNorm-on-read operands and row statistics need the small-M path");
+  // the kernels address each operand with 32-bit element offsets
+  auto extent = [](int64_t rows, int64_t ld, int64_t cols) {
+    return rows > 0 && cols > 0 ? (rows - 1) * ld + cols : int64_t(0);
+  };
+  const int64_t ea = ta ? extent(p.K, p.lda, p.M) : extent(p.M, p.lda, p.K);
+  const int64_t eb = tb ? extent(p.N, p.ldb, p.K) : extent(p.K, p.ldb, p.N);
+  const int64_t lim32 = (int64_t(1) << 31) - 64;
+  IH_REQUIRE(ea < lim32 && eb < lim32 && p.lda < lim32 && p.ldb < lim32 && p.K < lim32,
+             INFERC_ERR_UNSUPPORTED, "gemm: an operand spans 2^31 elements or more");
   // 128x128 tiles hold 3 blocks per CU (164 VGPRs). Between one and three
   // tiles per CU a round leaves CUs idle, and 128x64 tiles balance better
   // (the b=32 fused QKV, M=4096 N=3x768 K=768: 175 us against 196 us).
-  Cfg c = tiles(big) >= 3 * cus ? big : tiles(big) >= cus ? wide : small;
+  // 128x96 tiles, waves stacked 4x1 (32x96 each), for N a multiple of 96:
+  // the encoder's N = 768 (256 tiles at M = 4096, one per CU), 3x768 and
+  // 3072 (at b=32: out-proj 51 us, FFN-down 173-188 us, QKV 140 us, FFN-up
+  // 182 us, against 61, 205, 153 and 194 us with the tiles below).
+  Cfg c = (p.N % 96 == 0 && tiles(mid) >= cus) ? mid
+          : tiles(big) >= 3 * cus             ? big
+          : tiles(big) >= cus                 ? wide
+                                              : small;
   int64_t splits = 1;
   if (c.bm == small.bm) {
     const int64_t t = tiles(small);
@@ -791,9 +950,10 @@ void run(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool ta, bool tb, bo
       p.partial = static_cast<float*>(ctx->ws(need));
     }
   }
-  if (c.bn == big.bn) launch_tile<128, 128, 16>(p, slices, ta, tb, vec, ctx->stream);
-  else if (c.bm == wide.bm) launch_tile<128, 64, 16>(p, slices, ta, tb, vec, ctx->stream);
-  else launch_tile<64, 64, 32>(p, slices, ta, tb, vec, ctx->stream);
+  if (c.bn == big.bn) launch_tile<128, 128, 16, 2, 2>(p, slices, ta, tb, vec, ctx->stream);
+  else if (c.bn == mid.bn) launch_tile<128, 96, 32, 4, 1>(p, slices, ta, tb, vec, ctx->stream);
+  else if (c.bm == wide.bm) launch_tile<128, 64, 16, 2, 2>(p, slices, ta, tb, vec, ctx->stream);
+  else launch_tile<64, 64, 32, 2, 2>(p, slices, ta, tb, vec, ctx->stream);
   check_launch("gemm_f32_mfma");
   if (splits > 1) {
     const int64_t blocks = ceil_div(p.M * p.N, kThreads);
