@@ -24,6 +24,7 @@
 // the context workspace, and a second kernel reduces them in fixed order
 // (deterministic) and applies the epilogue.
 #include <mutex>
+#include <type_traits>
 #include <string>
 #include <vector>
 
@@ -180,7 +181,7 @@ __device__ __forceinline__ float epilogue(const GemmParams& p, const float* C,
 // into the matrix: a load under a branch would make the compiler wait for
 // all loads in flight at the join, not just for the panel being written.
 // Rows and columns past M and N only reach outputs that are never written;
-// k past the panel's valid depth is zeroed in LDS (zero_tail).
+// k past the last panel's valid depth is masked when that panel is read.
 template <int OUTER, int BK, bool KCONTIG, bool VEC>
 struct PanelAddr {
   static_assert((OUTER * BK) % (4 * kThreads) == 0, "panel must split into float4 per thread");
@@ -266,26 +267,6 @@ struct PanelRegs {
       }
     }
   }
-
-  // Zeroes the k rows at or past kn of what this thread stored (a last,
-  // partial panel); the writes carry constants only, so no load of the
-  // panel is made conditional on kn.
-  __device__ __forceinline__ void zero_tail(float* __restrict__ S, int tid, int kn) const {
-    if (kn >= BK) return;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int idx = tid + kThreads * i;
-      if (KCONTIG) {
-        const int ol = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (kq + j >= kn) S[(kq + j) * STRIDE + ol] = 0.0f;
-      } else {
-        const int kl = idx / (OUTER / 4), oq = (idx % (OUTER / 4)) * 4;
-        if (kl >= kn) *reinterpret_cast<floatx4*>(S + kl * STRIDE + oq) = floatx4{0, 0, 0, 0};
-      }
-    }
-  }
 };
 
 // Four waves in a WGM x WGN grid, each owning a (BM/WGM) x (BN/WGN) sub-tile of
@@ -298,10 +279,13 @@ struct PanelRegs {
 template <int BM, int BN, int BK, int WGM, int WGN, bool TA, bool TB, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmParams p) {
   static_assert(WGM * WGN * 64 == kThreads, "four waves");
-  // LDS row padding: 2 floats where rows are written element-wise (breaks
-  // bank aliasing of the transposing stores), 4 where they are written as
-  // float4 (keeps 16-byte alignment).
-  constexpr int SA = BM + (TA ? 4 : 2);
+  // LDS row padding: 4 floats where rows are written as float4 (keeps
+  // 16-byte alignment); where rows are written element-wise (the
+  // transposing stores of a row-major A) the padding makes a half-wave's 32
+  // stores hit 32 banks: lanes (a, b) = (lane % (BK/4), lane / (BK/4)) write
+  // bank 4*SA*a + b (mod 32), distinct when SA = 2 (mod 8) for BK = 16 and
+  // SA = 1 (mod 8) for BK = 32.
+  constexpr int SA = BM + (TA ? 4 : BK == 32 ? 1 : 2);
   constexpr int SB = BN + (TB ? 2 : 4);
   constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
   static_assert(TM * 32 == WTM && TN * 32 == WTN, "wave tiles of whole 32x32 MFMA tiles");
@@ -345,6 +329,25 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmParams p) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
     }
   };
+  // the last panel, of valid depth kn <= BK: LDS rows at or past kn hold
+  // stale or clamped values, so both operands of those k are taken as 0
+  auto compute_last = [&](const float* as, const float* bs, int kn) {
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 2) {
+      if (kk >= kn) break;
+      const bool in = kk + half < kn;
+      float a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = in ? as[(kk + half) * SA + wm + i * 32 + l32] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = in ? bs[(kk + half) * SB + wn + j * 32 + l32] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  };
 
   if (nt > 0) {
     PanelAddr<BM, BK, !TA, VEC> aa;
@@ -353,46 +356,48 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmParams p) {
     ab.init(p.ldb, n0, p.N, p.K, tid);
     PanelRegs<BM, BK, SA, !TA, VEC> la0, la1;
     PanelRegs<BN, BK, SB, TB, VEC> lb0, lb1;
-    // depth of panel t (the last panel repeats for t past the end), and
-    // its valid depth (BK but for a last, partial panel)
-    const int kb32 = int(kb), ntm1 = int(nt - 1), ke32 = int(ke);
-#define IH_K_OF(t) (kb32 + ((t) < ntm1 ? (t) : ntm1) * BK)
-#define IH_KN_OF(t) (ke32 - IH_K_OF(t) < BK ? ke32 - IH_K_OF(t) : BK)
+    // depth of panel t, and the last panel's valid depth (BK but for a
+    // partial last panel)
+    const int kb32 = int(kb), ntm1 = int(nt - 1);
+    const int kn_last = int(ke - (kb + int64_t(ntm1) * BK));
+#define IH_K_OF(t) (kb32 + (t) * BK)
     la0.load(A, aa, IH_K_OF(0));
     lb0.load(B, ab, IH_K_OF(0));
-    la1.load(A, aa, IH_K_OF(1));
-    lb1.load(B, ab, IH_K_OF(1));
+    la1.load(A, aa, IH_K_OF(ntm1 > 0 ? 1 : 0));
+    lb1.load(B, ab, IH_K_OF(ntm1 > 0 ? 1 : 0));
     la0.store(As[0], tid);
     lb0.store(Bs[0], tid);
-    la0.zero_tail(As[0], tid, IH_KN_OF(0));
-    lb0.zero_tail(Bs[0], tid, IH_KN_OF(0));
     lds_barrier();
-    // panels in pairs; both halves unconditional, so the two register sets
-    // stay two sets of registers
+    // Panels in pairs while two more follow the pair (both halves
+    // unconditional, so the two register sets stay two sets of registers);
+    // then the last one or two, without further loads.
     int t = 0;
-    for (; t + 1 <= ntm1; t += 2) {
+    for (; t + 2 <= ntm1; t += 2) {
       la0.load(A, aa, IH_K_OF(t + 2));
       lb0.load(B, ab, IH_K_OF(t + 2));
       __builtin_amdgcn_sched_barrier(0);  // the loads go out before the MFMAs
       compute(As[0], Bs[0]);
       la1.store(As[1], tid);
       lb1.store(Bs[1], tid);
-      la1.zero_tail(As[1], tid, IH_KN_OF(t + 1));
-      lb1.zero_tail(Bs[1], tid, IH_KN_OF(t + 1));
       lds_barrier();
-      la1.load(A, aa, IH_K_OF(t + 3));
-      lb1.load(B, ab, IH_K_OF(t + 3));
+      la1.load(A, aa, IH_K_OF(t + 3 <= ntm1 ? t + 3 : ntm1));
+      lb1.load(B, ab, IH_K_OF(t + 3 <= ntm1 ? t + 3 : ntm1));
       __builtin_amdgcn_sched_barrier(0);
       compute(As[1], Bs[1]);
       la0.store(As[0], tid);
       lb0.store(Bs[0], tid);
-      la0.zero_tail(As[0], tid, IH_KN_OF(t + 2));
-      lb0.zero_tail(Bs[0], tid, IH_KN_OF(t + 2));
       lds_barrier();
     }
-    if (t == ntm1) compute(As[0], Bs[0]);  // an odd panel count's last panel
+    if (t + 1 == ntm1) {  // panels t (in LDS) and t + 1 (in la1/lb1) remain
+      compute(As[0], Bs[0]);
+      la1.store(As[1], tid);
+      lb1.store(Bs[1], tid);
+      lds_barrier();
+      compute_last(As[1], Bs[1], kn_last);
+    } else {  // panel t is the last
+      compute_last(As[0], Bs[0], kn_last);
+    }
 #undef IH_K_OF
-#undef IH_KN_OF
   }
 
   // Accumulator layout of a 32x32 MFMA tile: register v of lane l holds
@@ -415,51 +420,61 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmParams p) {
   const float* R = p.R ? p.R + slice * p.sr : nullptr;
   float* Y = p.use_table ? p.Yt[slice] : p.Y + slice * p.sy;
   if (m0 + BM <= p.M && n0 + BN <= p.N) {
-    // A whole tile: every operand load first, then the arithmetic and the
-    // stores (epilogue()'s order). Loads under a per-element bounds branch
-    // would cost one memory round trip per element.
+    // A whole tile, one row of 32x32 MFMA tiles at a time: every operand
+    // load of the row first, then the arithmetic and the stores
+    // (epilogue()'s order). Loads under a per-element bounds branch would
+    // cost one memory round trip per element. The activation is a template
+    // argument of the store loop (one straight run of stores per activation
+    // instead of a switch per element), and the uniform tests sit outside the
+    // load loops, so each loop is one block of loads.
     const bool has_c = C != nullptr && p.beta != 0.0f;
     const int kind = has_c ? p.c_kind : INFERC_C_NONE;
-    float cr[TN], cx[TM][TN][16], rx[TM][TN][16];
+    float cr[TN];
     const float c0 = kind == INFERC_C_SCALAR ? C[0] : 0.0f;
     if (kind == INFERC_C_ROW) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) cr[j] = C[n0 + wn + j * 32 + l32];
     }
-    // (the uniform tests sit outside the loops, so each loop is one block of
-    // loads)
-    auto gather = [&](const float* X, int64_t ld, float (&dst)[TM][TN][16]) {
+    // element (v, j) of the lane sits at row r0 + 8*(v/4) + v%4, column c0 + 32j
+    const int64_t r0 = m0 + wm + 4 * half, cb = n0 + wn + l32;
+    auto finish = [&](auto act_tag) {
+      constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i) {
+        const int64_t ri = r0 + i * 32;
+        float cx[TN][16], rx[TN][16];
+        auto gather = [&](const float* X, int64_t ld, float (&dst)[TN][16]) {
+          const float* xb = X + ri * ld + cb;
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) dst[j][v] = xb[(8 * (v >> 2) + (v & 3)) * ld + 32 * j];
+        };
+        if (kind == INFERC_C_FULL) gather(C, p.ldc, cx);
+        if (R != nullptr) gather(R, p.ldr, rx);
+        float* yb = Y + ri * p.ldy + cb;
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
-            const int64_t row = m0 + wm + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-            const int64_t col = n0 + wn + j * 32 + l32;
-            dst[i][j][v] = X[row * ld + col];
+            float x = p.alpha * acc[i][j][v];
+            if (has_c) {
+              const float c = kind == INFERC_C_ROW    ? cr[j]
+                              : kind == INFERC_C_FULL ? cx[j][v]
+                                                      : c0;  // 0 for an unknown kind
+              x = x + p.beta * c;
+            }
+            if (R != nullptr) x = x + rx[j][v];
+            yb[(8 * (v >> 2) + (v & 3)) * p.ldy + 32 * j] = apply_act(x, ACT);
           }
+      }
     };
-    if (kind == INFERC_C_FULL) gather(C, p.ldc, cx);
-    if (R != nullptr) gather(R, p.ldr, rx);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t row = m0 + wm + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-          const int64_t col = n0 + wn + j * 32 + l32;
-          float x = p.alpha * acc[i][j][v];
-          if (has_c) {
-            const float c = kind == INFERC_C_ROW    ? cr[j]
-                            : kind == INFERC_C_FULL ? cx[i][j][v]
-                                                    : c0;  // 0 for an unknown kind
-            x = x + p.beta * c;
-          }
-          if (R != nullptr) x = x + rx[i][j][v];
-          Y[row * p.ldy + col] = apply_act(x, p.act);
-        }
+    switch (p.act) {
+      case INFERC_ACT_GELU_ERF: finish(std::integral_constant<int, INFERC_ACT_GELU_ERF>{}); break;
+      case INFERC_ACT_GELU_TANH: finish(std::integral_constant<int, INFERC_ACT_GELU_TANH>{}); break;
+      case INFERC_ACT_RELU: finish(std::integral_constant<int, INFERC_ACT_RELU>{}); break;
+      default: finish(std::integral_constant<int, INFERC_ACT_NONE>{}); break;
+    }
     return;
   }
 #pragma unroll
