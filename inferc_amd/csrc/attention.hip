@@ -53,12 +53,15 @@ __device__ __forceinline__ void wave_lds_barrier() {
 }
 
 // One 32-key tile for a wave's 32 queries: S^T = K Q^T on the matrix cores,
-// scale, mask, online-softmax update, then O^T += V^T P^T.
+// scale, mask, online-softmax update, then O^T += V^T P^T. BITS: the mask
+// comes as mbits (bit v: score register v's key is masked, loaded ahead by
+// the caller); otherwise it is read here from mbase.
+template <bool BITS = false>
 __device__ __forceinline__ void attn_tile(const AttnP& p, const float* __restrict__ ks,
                                           const float* __restrict__ vs, int64_t k0, int64_t qi,
                                           const uint8_t* mbase, const float (&qf)[kD / 2],
                                           floatx16 (&oacc)[2], float& m_run, float& l_run,
-                                          int half, int l32) {
+                                          int half, int l32, uint32_t mbits = 0) {
   const int64_t S = p.S;
   floatx16 sacc;
 #pragma unroll
@@ -79,6 +82,8 @@ __device__ __forceinline__ void attn_tile(const AttnP& p, const float* __restric
       s = -INFINITY;  // key does not exist
     } else if (p.causal) {
       if (j > qi) s = p.fill;
+    } else if (BITS) {
+      if ((mbits >> v) & 1u) s = p.fill;
     } else if (mbase && qi < S) {
       if (mbase[qi * p.ms2 + j * p.ms3]) s = p.fill;
     }
@@ -87,11 +92,13 @@ __device__ __forceinline__ void attn_tile(const AttnP& p, const float* __restric
   }
   tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
   const float m_new = fmaxf(m_run, tmax);
-  const float corr = __expf(m_run - m_new);
+  // A fill of -inf can leave a tile with no finite score; keep the state.
+  const bool none = m_new == -INFINITY;
+  const float corr = none ? 1.0f : __expf(m_run - m_new);
   float lsum = 0.0f;
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
-    sv[v] = __expf(sv[v] - m_new);
+    sv[v] = none ? 0.0f : __expf(sv[v] - m_new);
     lsum += sv[v];
   }
   lsum += __shfl_xor(lsum, 32, 64);
@@ -135,7 +142,14 @@ __device__ __forceinline__ void attn_store(const AttnP& p, int64_t b, int64_t h,
     }
 }
 
-template <int WAVES>
+// Large grids: WAVES waves of 32 queries share each K/V tile, staged through
+// LDS (double-buffered). The loads of tile t+1, the lane's 16 mask bytes
+// included, are issued before tile t's matrix-core work and are unconditional
+// (keys clamped into the sequence; a clamped key's score is -inf and its V
+// row weighs 0), so the waits before the LDS writes count them exactly.
+// VEC: 16-byte aligned rows (float4 loads). MASKED: a mask that is neither
+// absent nor replaced by the causal rule.
+template <int WAVES, bool VEC, bool MASKED>
 __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
   constexpr int NT = 64 * WAVES;
   __shared__ __attribute__((aligned(16))) float Ks[2][kKT * kKS];
@@ -149,6 +163,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
   const int64_t q0 = qb0 + 32 * wave;
   const int64_t qi = q0 + l32;  // this lane's query
   const int64_t S = p.S;
+  const int64_t qc = qi < S ? qi : S - 1;
 
   const float* qbase = p.q + b * S * p.ldq + h * kD;
   const float* kbase = p.k + b * S * p.ldk + h * kD;
@@ -160,7 +175,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
   if (p.causal) {
     const int64_t qlast = qb0 + 32 * WAVES;
     key_end = qlast < S ? qlast : S;
-  } else if (mbase && p.ms2 == 0) {
+  } else if (MASKED && p.ms2 == 0) {
     // Query-independent mask: stop after the last unmasked key. If every key
     // is masked, keep all of them (softmax over `fill` values, as the
     // reference computes it).
@@ -175,10 +190,12 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
   }
   const int64_t ntiles = (key_end + kKT - 1) / kKT;
 
-  // Q^T operand: step s covers dims 2s, 2s+1; lane supplies Q[qi][2s+half].
+  // Q^T operand: step s covers dims 2s, 2s+1; lane supplies Q[qi][2s+half]
+  // (a lane past the sequence reads the last query; its output is not
+  // written).
   float qf[kD / 2];
 #pragma unroll
-  for (int s = 0; s < kD / 2; ++s) qf[s] = (qi < S) ? qbase[qi * p.ldq + 2 * s + half] : 0.0f;
+  for (int s = 0; s < kD / 2; ++s) qf[s] = qbase[qc * p.ldq + 2 * s + half];
 
   floatx16 oacc[2];
 #pragma unroll
@@ -188,20 +205,32 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
   float m_run = -INFINITY, l_run = 0.0f;
 
   // Cooperative K/V tile staging: 32 keys x 64 dims = 512 float4 per tensor.
-  constexpr int NV = (kKT * kD / 4 + NT - 1) / NT;
+  static_assert((kKT * kD / 4) % NT == 0, "tile must split into float4 per thread");
+  constexpr int NV = kKT * kD / 4 / NT;
   float4 kr[NV], vr[NV];
+  uint8_t mk[16];
+  const uint8_t* mrow = MASKED ? mbase + qc * p.ms2 : nullptr;
   auto load_tile = [&](int64_t k0) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int idx = tid + NT * i;
       const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
-      kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      vr[i] = kr[i];
-      if (idx < kKT * kD / 4 && k0 + key < S) {
-        const float* kp = kbase + (k0 + key) * p.ldk + dq;
-        const float* vp = vbase + (k0 + key) * p.ldv + dq;
+      const int64_t kc = k0 + key < S ? k0 + key : S - 1;
+      const float* kp = kbase + kc * p.ldk + dq;
+      const float* vp = vbase + kc * p.ldv + dq;
+      if (VEC) {
+        kr[i] = *reinterpret_cast<const float4*>(kp);
+        vr[i] = *reinterpret_cast<const float4*>(vp);
+      } else {
         kr[i] = make_float4(kp[0], kp[1], kp[2], kp[3]);
         vr[i] = make_float4(vp[0], vp[1], vp[2], vp[3]);
+      }
+    }
+    if (MASKED) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t j = k0 + 8 * (v >> 2) + 4 * half + (v & 3);
+        mk[v] = mrow[(j < S ? j : S - 1) * p.ms3];
       }
     }
   };
@@ -209,32 +238,160 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int idx = tid + NT * i;
-      if (idx < kKT * kD / 4) {
-        const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
-        float* ks = &Ks[buf][key * kKS + dq];
-        ks[0] = kr[i].x; ks[1] = kr[i].y; ks[2] = kr[i].z; ks[3] = kr[i].w;
-        *reinterpret_cast<float4*>(&Vs[buf][key * kVS + dq]) = vr[i];
-      }
+      const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
+      float* ks = &Ks[buf][key * kKS + dq];
+      ks[0] = kr[i].x; ks[1] = kr[i].y; ks[2] = kr[i].z; ks[3] = kr[i].w;
+      *reinterpret_cast<float4*>(&Vs[buf][key * kVS + dq]) = vr[i];
     }
+  };
+  auto mask_bits = [&]() {
+    uint32_t m = 0;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) m |= uint32_t(mk[v] != 0) << v;
+    return m;
   };
 
   if (ntiles > 0) {
     load_tile(0);
     store_tile(0);
   }
+  uint32_t mbits = MASKED && ntiles > 0 ? mask_bits() : 0u;
   __syncthreads();
 
   for (int64_t t = 0; t < ntiles; ++t) {
     const int cur = int(t & 1);
     const int64_t k0 = t * kKT;
-    if (t + 1 < ntiles) load_tile(k0 + kKT);
+    // the next tile's loads (the last tile repeats itself past the end)
+    load_tile(t + 1 < ntiles ? k0 + kKT : k0);
 
     // A wave whose 32 queries all lie above this tile's keys skips it
     // (causal), as does a wave past the end of the sequence.
     const bool skip = (q0 >= S) || (p.causal && k0 > q0 + 31);
-    if (!skip) attn_tile(p, Ks[cur], Vs[cur], k0, qi, mbase, qf, oacc, m_run, l_run, half, l32);
-    if (t + 1 < ntiles) store_tile(cur ^ 1);
+    if (!skip)
+      attn_tile<MASKED>(p, Ks[cur], Vs[cur], k0, qi, nullptr, qf, oacc, m_run, l_run, half, l32,
+                        mbits);
+    store_tile(cur ^ 1);
+    if (MASKED) mbits = mask_bits();
     __syncthreads();
+  }
+  if (qi < S) attn_store(p, b, h, qi, oacc, 1.0f / l_run, half);
+}
+
+// Short sequences (S <= 32*MAXT keys) on large grids: the block stages the
+// whole K and V of its (batch, head), and the mask row of a query-independent
+// mask, in LDS at once, so every global load of the block goes out in one
+// round trip and the tile loop runs without further loads or barriers. (The
+// tiled kernel above waits for each tile's loads and a barrier per tile; at
+// S = 128 that latency, not the matrix cores, sets its time.) Mask handling
+// as the tiled kernel: keys past the last unmasked key are skipped, and if
+// every key is masked all are kept. WAVES waves of 32 queries per block;
+// VEC: 16-byte aligned rows. MASK_ROW: a query-independent mask (ms2 == 0).
+template <int WAVES, int MAXT, bool VEC, bool MASK_ROW>
+__global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64_full(AttnP p) {
+  constexpr int NT = 64 * WAVES;
+  __shared__ __attribute__((aligned(16))) float Ks[MAXT][kKT * kKS];
+  __shared__ __attribute__((aligned(16))) float Vs[MAXT][kKT * kVS];
+  __shared__ uint8_t s_mask[MAXT * kKT];
+  __shared__ int s_last_valid;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const int64_t qb0 = int64_t(blockIdx.x) * (32 * WAVES);
+  const int64_t q0 = qb0 + 32 * wave;
+  const int64_t qi = q0 + l32;
+  const int64_t S = p.S;  // 1 <= S <= MAXT * kKT (host-checked)
+  const int64_t qc = qi < S ? qi : S - 1;
+  const float* qbase = p.q + b * S * p.ldq + h * kD;
+  const float* kbase = p.k + b * S * p.ldk + h * kD;
+  const float* vbase = p.v + b * S * p.ldv + h * kD;
+  const uint8_t* mbase = MASK_ROW ? p.mask + b * p.ms0 + h * p.ms1 : nullptr;
+
+  // Every load first: Q, all K/V tiles, the mask row (keys clamped into the
+  // sequence; a clamped key's score is -inf, so its V row weighs 0).
+  float qf[kD / 2];
+#pragma unroll
+  for (int s = 0; s < kD / 2; ++s) qf[s] = qbase[qc * p.ldq + 2 * s + half];
+  static_assert((kKT * kD / 4) % NT == 0, "tile must split into float4 per thread");
+  constexpr int NV = kKT * kD / 4 / NT;
+  float4 kr[MAXT][NV], vr[MAXT][NV];
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t)
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int idx = tid + NT * i;
+      const int key = t * kKT + idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
+      const int64_t kc = key < S ? key : S - 1;
+      const float* kp = kbase + kc * p.ldk + dq;
+      const float* vp = vbase + kc * p.ldv + dq;
+      if (VEC) {
+        kr[t][i] = *reinterpret_cast<const float4*>(kp);
+        vr[t][i] = *reinterpret_cast<const float4*>(vp);
+      } else {
+        kr[t][i] = make_float4(kp[0], kp[1], kp[2], kp[3]);
+        vr[t][i] = make_float4(vp[0], vp[1], vp[2], vp[3]);
+      }
+    }
+  uint8_t mrow[(MAXT * kKT + NT - 1) / NT];
+  if (MASK_ROW) {
+#pragma unroll
+    for (int i = 0; i < (MAXT * kKT + NT - 1) / NT; ++i) {
+      const int j = tid + NT * i;
+      mrow[i] = mbase[(j < S ? j : S - 1) * p.ms3];
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t)
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int idx = tid + NT * i;
+      const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
+      float* ks = &Ks[t][key * kKS + dq];
+      ks[0] = kr[t][i].x; ks[1] = kr[t][i].y; ks[2] = kr[t][i].z; ks[3] = kr[t][i].w;
+      *reinterpret_cast<float4*>(&Vs[t][key * kVS + dq]) = vr[t][i];
+    }
+  int64_t key_end = S;
+  if (MASK_ROW) {
+    if (tid == 0) s_last_valid = -1;
+    int last = -1;
+#pragma unroll
+    for (int i = 0; i < (MAXT * kKT + NT - 1) / NT; ++i) {
+      const int j = tid + NT * i;
+      if (j < MAXT * kKT) s_mask[j] = mrow[i];
+      if (j < S && !mrow[i]) last = j;
+    }
+    __syncthreads();
+    if (last >= 0) atomicMax(&s_last_valid, last);
+    __syncthreads();
+    if (s_last_valid >= 0) key_end = s_last_valid + 1;
+  } else {
+    __syncthreads();
+    if (p.causal) {
+      const int64_t qlast = qb0 + 32 * WAVES;
+      key_end = qlast < S ? qlast : S;
+    }
+  }
+  const int ntiles = int((key_end + kKT - 1) / kKT);
+
+  floatx16 oacc[2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) oacc[d][v] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+  if (q0 < S) {
+    for (int t = 0; t < ntiles; ++t) {
+      const int64_t k0 = int64_t(t) * kKT;
+      if (p.causal && k0 > q0 + 31) break;  // later tiles are masked for all 32 queries
+      uint32_t mbits = 0;
+      if (MASK_ROW) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          mbits |= uint32_t(s_mask[k0 + 8 * (v >> 2) + 4 * half + (v & 3)] != 0) << v;
+      }
+      attn_tile<MASK_ROW>(p, Ks[t], Vs[t], k0, qi, nullptr, qf, oacc, m_run, l_run, half, l32,
+                          mbits);
+    }
   }
   if (qi < S) attn_store(p, b, h, qi, oacc, 1.0f / l_run, half);
 }
@@ -577,9 +734,30 @@ void attention(inferc_hip_ctx* ctx, const AttnArgs& a) {
       // few blocks: 16 queries per block, four waves splitting the key tiles
       dim3 grid(unsigned(ceil_div(a.S, 16)), unsigned(p.nH), unsigned(a.B));
       hipLaunchKernelGGL(attn_fwd_d64_q16<4>, grid, dim3(256), 0, ctx->stream, p);
-    } else if (blocks4 >= ctx->num_cus) {
+    } else if (blocks4 >= ctx->num_cus && a.S <= 4 * kKT &&
+               (p.mask == nullptr || p.causal || p.ms2 == 0)) {
+      // short sequences: the whole K/V of a (batch, head) staged at once
+      const bool mrow = p.mask != nullptr && !p.causal;
       dim3 grid(unsigned(ceil_div(a.S, 128)), unsigned(p.nH), unsigned(a.B));
-      hipLaunchKernelGGL(attn_fwd_d64<4>, grid, dim3(256), 0, ctx->stream, p);
+      auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, ctx->stream, p); };
+      if (vec) {
+        if (mrow) go(attn_fwd_d64_full<4, 4, true, true>);
+        else go(attn_fwd_d64_full<4, 4, true, false>);
+      } else {
+        if (mrow) go(attn_fwd_d64_full<4, 4, false, true>);
+        else go(attn_fwd_d64_full<4, 4, false, false>);
+      }
+    } else if (blocks4 >= ctx->num_cus) {
+      const bool masked = p.mask != nullptr && !p.causal;
+      dim3 grid(unsigned(ceil_div(a.S, 128)), unsigned(p.nH), unsigned(a.B));
+      auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, ctx->stream, p); };
+      if (vec) {
+        if (masked) go(attn_fwd_d64<4, true, true>);
+        else go(attn_fwd_d64<4, true, false>);
+      } else {
+        if (masked) go(attn_fwd_d64<4, false, true>);
+        else go(attn_fwd_d64<4, false, false>);
+      }
     } else {
       // few blocks: four waves per 32 queries, splitting the key tiles
       dim3 grid(unsigned(ceil_div(a.S, 32)), unsigned(p.nH), unsigned(a.B));

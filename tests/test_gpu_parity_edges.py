@@ -330,3 +330,77 @@ def test_layernorm_read_far_from_zero_mean_with_outliers(ctx, offset):
             print(f"offset {offset} {nm}: max|d| {err:.2e}")
             assert err <= 1e-4 * max(1.0, float(np.abs(ref).max())), nm
     ex.close()
+
+
+# --------------------------------------------------- attention, large grids
+
+def _attn_close(got, ref, tol=1e-4):
+    ref = np.asarray(ref, np.float64)
+    scale = max(1.0, float(np.abs(ref).max()))
+    np.testing.assert_allclose(np.asarray(got, np.float64), ref, rtol=0, atol=tol * scale)
+
+
+def _attn_raw(ctx, q, k, v, mask, hd, fill, shift):
+    """FusedAttention through the C-ABI with every float operand `shift`
+    floats past a 16-byte boundary (shift 1: the kernels' scalar loads and
+    stores)."""
+    B, S, H = q.shape
+    keep, ptrs = [], []
+    for a in (q, k, v):
+        t = T(ctx, np.concatenate([np.zeros(shift, np.float32), a.ravel()]))
+        keep.append(t)
+        ptrs.append(t.ptr + 4 * shift)
+    out = Tensor.empty(ctx, (B * S * H + shift,))
+    mptr = ms = None
+    if mask is not None:
+        mt = T(ctx, mask, np.uint8)
+        keep.append(mt)
+        mptr, ms = mt.ptr, rt._i64_array(rt.mask_strides(mask.shape))
+    rt.check(ctx._lib.inferc_hip_fused_attention_f32(ctx.handle, B, S, H, hd, *ptrs, mptr, ms,
+                                                     fill, out.ptr + 4 * shift))
+    return out.numpy()[shift:].reshape(B, S, H)
+
+
+def _row_mask(B, S, seed, lead=0):
+    """[B,1,1,S] padding masks of random valid lengths; batch 0 has every key
+    masked, batch 1 its first `lead` keys as well."""
+    lens = np.random.default_rng(seed).integers(1, S + 1, size=B)
+    m = (np.arange(S)[None, :] >= lens[:, None]).astype(np.uint8)
+    m[0, :] = 1
+    m[1, :lead] = 1
+    m[1, lead:] = 0
+    return m.reshape(B, 1, 1, S)
+
+
+# B=24 with 12 heads: at least one 128-query block per CU, the grids that the
+# encoder at b=32 and config 3 launch. S <= 128 stages a whole (batch, head)
+# in LDS at once; S > 128, or a per-query mask, takes the tiled kernel.
+@pytest.mark.parametrize("S,kind,shift", [
+    (100, "none", 0), (100, "row", 0), (100, "row", 1), (100, "query", 0),
+    (200, "none", 0), (200, "row", 0), (200, "row", 1), (200, "query", 1)])
+def test_attention_large_grid_paths(ctx, S, kind, shift):
+    B, H, hd = 24, 768, 64
+    q, k, v = rnd((B, S, H), 60 + S), rnd((B, S, H), 61 + S), rnd((B, S, H), 62 + S)
+    if kind == "none":
+        mask = None
+    elif kind == "row":
+        mask = _row_mask(B, S, 63 + S, lead=40)
+    else:
+        mask = (np.random.default_rng(64 + S).random((B, H // hd, S, S)) < 0.3).astype(np.uint8)
+    fill = graphs.FILL_MIN
+    got = _attn_raw(ctx, q, k, v, mask, hd, fill, shift)
+    _attn_close(got, O.fused_attention(q, k, v, mask, hd, fill))
+
+
+@pytest.mark.parametrize("S", [100, 200])
+def test_attention_large_grid_minus_inf_fill_with_masked_leading_tiles(ctx, S):
+    """fill = -inf with the first 64 keys masked: whole 32-key tiles have no
+    finite score, and the running state must stay (0, -inf) through them
+    rather than turn NaN."""
+    B, H, hd = 24, 768, 64
+    q, k, v = rnd((B, S, H), 70 + S), rnd((B, S, H), 71 + S), rnd((B, S, H), 72 + S)
+    mask = np.zeros((B, 1, 1, S), np.uint8)
+    mask[..., :64] = 1
+    got = _attn_raw(ctx, q, k, v, mask, hd, -np.inf, 0)
+    assert np.isfinite(got).all()
+    _attn_close(got, O.fused_attention(q, k, v, mask, hd, -np.inf))
