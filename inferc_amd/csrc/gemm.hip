@@ -277,7 +277,7 @@ struct PanelRegs {
 // panel index past the end repeats the last panel, whose copy is never
 // read), so the wait before each LDS write counts exactly the loads it needs.
 template <int BM, int BN, int BK, int WGM, int WGN, bool TA, bool TB, bool VEC>
-__global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmParams p) {
+__global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma(GemmParams p) {
   static_assert(WGM * WGN * 64 == kThreads, "four waves");
   // LDS row padding: 4 floats where rows are written as float4 (keeps
   // 16-byte alignment); where rows are written element-wise (the
@@ -419,74 +419,92 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmParams p) {
   const float* C = p.use_table ? p.Ct[slice] : p.C;
   const float* R = p.R ? p.R + slice * p.sr : nullptr;
   float* Y = p.use_table ? p.Yt[slice] : p.Y + slice * p.sy;
-  if (m0 + BM <= p.M && n0 + BN <= p.N) {
-    // A whole tile, one row of 32x32 MFMA tiles at a time: every operand
-    // load of the row first, then the arithmetic and the stores
-    // (epilogue()'s order). Loads under a per-element bounds branch would
-    // cost one memory round trip per element. The activation is a template
-    // argument of the store loop (one straight run of stores per activation
-    // instead of a switch per element), and the uniform tests sit outside the
-    // load loops, so each loop is one block of loads.
-    const bool has_c = C != nullptr && p.beta != 0.0f;
-    const int kind = has_c ? p.c_kind : INFERC_C_NONE;
-    float cr[TN];
-    const float c0 = kind == INFERC_C_SCALAR ? C[0] : 0.0f;
-    if (kind == INFERC_C_ROW) {
+  // One row of 32x32 MFMA tiles at a time: every operand load of the row
+  // first, then the arithmetic (epilogue()'s order) and the stores. Loads
+  // under a per-element bounds branch would cost one memory round trip per
+  // element, so a tile at the matrix's edge (EDGE) loads from rows and
+  // columns clamped into the matrix and bounds-checks only its stores. The
+  // activation is a template argument of the store loop (one straight run of
+  // stores per activation instead of a switch per element), and the uniform
+  // tests sit outside the load loops, so each loop is one block of loads.
+  const int64_t M = p.M, N = p.N;
+  const bool full = m0 + BM <= M && n0 + BN <= N;
+  const bool has_c = C != nullptr && p.beta != 0.0f;
+  const int kind = has_c ? p.c_kind : INFERC_C_NONE;
+  float cr[TN];
+  const float c0 = kind == INFERC_C_SCALAR ? C[0] : 0.0f;
+  if (kind == INFERC_C_ROW) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j) cr[j] = C[n0 + wn + j * 32 + l32];
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = n0 + wn + j * 32 + l32;
+      cr[j] = C[col < N ? col : N - 1];
     }
-    // element (v, j) of the lane sits at row r0 + 8*(v/4) + v%4, column c0 + 32j
-    const int64_t r0 = m0 + wm + 4 * half, cb = n0 + wn + l32;
-    auto finish = [&](auto act_tag) {
-      constexpr int ACT = decltype(act_tag)::value;
+  }
+  // element (v, j) of the lane sits at row r0 + 8*(v/4) + v%4, column cb + 32j
+  const int64_t r0 = m0 + wm + 4 * half, cb = n0 + wn + l32;
+  auto finish = [&](auto act_tag, auto edge_tag) {
+    constexpr int ACT = decltype(act_tag)::value;
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    // a whole row of tiles per batch of loads; an edge tile one 32-column
+    // block at a time (its clamped addresses cost registers)
+    constexpr int JB = EDGE ? 1 : TN;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int64_t ri = r0 + i * 32;
-        float cx[TN][16], rx[TN][16];
-        auto gather = [&](const float* X, int64_t ld, float (&dst)[TN][16]) {
+    for (int i = 0; i < TM; ++i) {
+      const int64_t ri = r0 + i * 32;
+#pragma unroll
+      for (int j0 = 0; j0 < TN; j0 += JB) {
+        float cx[JB][16], rx[JB][16];
+        auto gather = [&](const float* X, int64_t ld, float (&dst)[JB][16]) {
           const float* xb = X + ri * ld + cb;
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
+          for (int jj = 0; jj < JB; ++jj)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) dst[j][v] = xb[(8 * (v >> 2) + (v & 3)) * ld + 32 * j];
+            for (int v = 0; v < 16; ++v) {
+              if (EDGE) {
+                const int64_t row = ri + 8 * (v >> 2) + (v & 3), col = cb + 32 * (j0 + jj);
+                dst[jj][v] = X[(row < M ? row : M - 1) * ld + (col < N ? col : N - 1)];
+              } else {
+                dst[jj][v] = xb[(8 * (v >> 2) + (v & 3)) * ld + 32 * (j0 + jj)];
+              }
+            }
         };
         if (kind == INFERC_C_FULL) gather(C, p.ldc, cx);
         if (R != nullptr) gather(R, p.ldr, rx);
         float* yb = Y + ri * p.ldy + cb;
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int jj = 0; jj < JB; ++jj)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
+            const int j = j0 + jj;
             float x = p.alpha * acc[i][j][v];
             if (has_c) {
               const float c = kind == INFERC_C_ROW    ? cr[j]
-                              : kind == INFERC_C_FULL ? cx[j][v]
+                              : kind == INFERC_C_FULL ? cx[jj][v]
                                                       : c0;  // 0 for an unknown kind
               x = x + p.beta * c;
             }
-            if (R != nullptr) x = x + rx[j][v];
-            yb[(8 * (v >> 2) + (v & 3)) * p.ldy + 32 * j] = apply_act(x, ACT);
+            if (R != nullptr) x = x + rx[jj][v];
+            const float y = apply_act(x, ACT);
+            if (EDGE) {
+              const int64_t row = ri + 8 * (v >> 2) + (v & 3), col = cb + 32 * j;
+              if (row < M && col < N) Y[row * p.ldy + col] = y;
+            } else {
+              yb[(8 * (v >> 2) + (v & 3)) * p.ldy + 32 * j] = y;
+            }
           }
       }
-    };
-    switch (p.act) {
-      case INFERC_ACT_GELU_ERF: finish(std::integral_constant<int, INFERC_ACT_GELU_ERF>{}); break;
-      case INFERC_ACT_GELU_TANH: finish(std::integral_constant<int, INFERC_ACT_GELU_TANH>{}); break;
-      case INFERC_ACT_RELU: finish(std::integral_constant<int, INFERC_ACT_RELU>{}); break;
-      default: finish(std::integral_constant<int, INFERC_ACT_NONE>{}); break;
     }
-    return;
+  };
+  auto by_edge = [&](auto act_tag) {
+    if (full) finish(act_tag, std::false_type{});
+    else finish(act_tag, std::true_type{});
+  };
+  switch (p.act) {
+    case INFERC_ACT_GELU_ERF: by_edge(std::integral_constant<int, INFERC_ACT_GELU_ERF>{}); break;
+    case INFERC_ACT_GELU_TANH: by_edge(std::integral_constant<int, INFERC_ACT_GELU_TANH>{}); break;
+    case INFERC_ACT_RELU: by_edge(std::integral_constant<int, INFERC_ACT_RELU>{}); break;
+    default: by_edge(std::integral_constant<int, INFERC_ACT_NONE>{}); break;
   }
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t row = m0 + wm + i * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-        const int64_t col = n0 + wn + j * 32 + l32;
-        if (row < p.M && col < p.N) Y[row * p.ldy + col] = epilogue(p, C, R, acc[i][j][v], row, col);
-      }
 }
 
 // Sums the split-K partials in split order and applies the epilogue.

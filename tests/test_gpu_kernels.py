@@ -150,6 +150,30 @@ def test_gemm_single_row_transb_epilogues(ctx, N, K):
         close(got, ref)
 
 
+# Large-M products on the tiled kernel, with edge tiles (M, N not multiples
+# of the tile) and partial last K panels: 128x96 tiles (N % 96 == 0), 128x128
+# (N % 96 != 0, >= 3 tiles per CU), 128x64 (1-3 tiles per CU).
+@pytest.mark.parametrize("M,N,K", [(4000, 768, 768), (4000, 3072, 100), (4032, 768, 45),
+                                   (4000, 3136, 96), (2000, 2000, 130)])
+@pytest.mark.parametrize("act", [L.ACT_NONE, L.ACT_GELU_ERF])
+def test_gemm_large_m_edge_tiles(ctx, M, N, K, act):
+    A, B = rnd((M, K), M + K), rnd((K, N), N + K, 0.05)
+    bias, res = rnd(N, 3 + N), rnd((M, N), 4 + M)
+    got = rt.Gemm(T(ctx, A), T(ctx, B), T(ctx, bias), 1.0, 1.0, residual=T(ctx, res),
+                  act=act).numpy()
+    v = (A.astype(np.float64) @ B + bias) + res
+    close(got, ref64.gelu_erf(v) if act == L.ACT_GELU_ERF else v)
+
+
+@pytest.mark.parametrize("M,N,K", [(4000, 768, 70), (4096, 768, 64)])
+def test_gemm_large_m_c_kinds_alpha_beta(ctx, M, N, K):
+    A, B = rnd((M, K), 15), rnd((K, N), 16, 0.1)
+    for C in (rnd(N, 17), rnd((M, N), 18), np.array([1.5], np.float32)):
+        got = rt.Gemm(T(ctx, A), T(ctx, B), T(ctx, C), alpha=0.75, beta=-2.0).numpy()
+        close(got, 0.75 * (A.astype(np.float64) @ B) + -2.0 * np.broadcast_to(
+            C.astype(np.float64), (M, N)))
+
+
 def test_gemm_c_kinds_alpha_beta(ctx):
     A, B = rnd((37, 29), 5), rnd((29, 41), 6)
     for C in (rnd(41, 7), rnd((37, 41), 8), np.array([1.5], np.float32)):
