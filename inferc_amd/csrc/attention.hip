@@ -25,6 +25,7 @@ namespace ih {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 64;     // head_dim of the MFMA kernel
 constexpr int kKT = 32;    // keys per tile
@@ -150,7 +151,7 @@ __device__ __forceinline__ void attn_store(const AttnP& p, int64_t b, int64_t h,
 // VEC: 16-byte aligned rows (float4 loads). MASKED: a mask that is neither
 // absent nor replaced by the causal rule.
 template <int WAVES, bool VEC, bool MASKED>
-__global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
+__global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) {
   constexpr int NT = 64 * WAVES;
   __shared__ __attribute__((aligned(16))) float Ks[2][kKT * kKS];
   __shared__ __attribute__((aligned(16))) float Vs[2][kKT * kVS];
@@ -207,8 +208,10 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
   // Cooperative K/V tile staging: 32 keys x 64 dims = 512 float4 per tensor.
   static_assert((kKT * kD / 4) % NT == 0, "tile must split into float4 per thread");
   constexpr int NV = kKT * kD / 4 / NT;
-  float4 kr[NV], vr[NV];
-  uint8_t mk[16];
+  // native vectors: a whole-value copy of HIP's float4 struct becomes a
+  // private-memory copy
+  floatx4 kr[NV], vr[NV];
+  uint32_t mnext = 0;  // the next tile's mask bits (bit v: score register v)
   const uint8_t* mrow = MASKED ? mbase + qc * p.ms2 : nullptr;
   auto load_tile = [&](int64_t k0) {
 #pragma unroll
@@ -219,18 +222,19 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
       const float* kp = kbase + kc * p.ldk + dq;
       const float* vp = vbase + kc * p.ldv + dq;
       if (VEC) {
-        kr[i] = *reinterpret_cast<const float4*>(kp);
-        vr[i] = *reinterpret_cast<const float4*>(vp);
+        kr[i] = *reinterpret_cast<const floatx4*>(kp);
+        vr[i] = *reinterpret_cast<const floatx4*>(vp);
       } else {
-        kr[i] = make_float4(kp[0], kp[1], kp[2], kp[3]);
-        vr[i] = make_float4(vp[0], vp[1], vp[2], vp[3]);
+        kr[i] = floatx4{kp[0], kp[1], kp[2], kp[3]};
+        vr[i] = floatx4{vp[0], vp[1], vp[2], vp[3]};
       }
     }
     if (MASKED) {
+      mnext = 0;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int64_t j = k0 + 8 * (v >> 2) + 4 * half + (v & 3);
-        mk[v] = mrow[(j < S ? j : S - 1) * p.ms3];
+        mnext |= uint32_t(mrow[(j < S ? j : S - 1) * p.ms3] != 0) << v;
       }
     }
   };
@@ -240,22 +244,16 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
       const int idx = tid + NT * i;
       const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
       float* ks = &Ks[buf][key * kKS + dq];
-      ks[0] = kr[i].x; ks[1] = kr[i].y; ks[2] = kr[i].z; ks[3] = kr[i].w;
-      *reinterpret_cast<float4*>(&Vs[buf][key * kVS + dq]) = vr[i];
+      ks[0] = kr[i][0]; ks[1] = kr[i][1]; ks[2] = kr[i][2]; ks[3] = kr[i][3];
+      *reinterpret_cast<floatx4*>(&Vs[buf][key * kVS + dq]) = vr[i];
     }
-  };
-  auto mask_bits = [&]() {
-    uint32_t m = 0;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) m |= uint32_t(mk[v] != 0) << v;
-    return m;
   };
 
   if (ntiles > 0) {
     load_tile(0);
     store_tile(0);
   }
-  uint32_t mbits = MASKED && ntiles > 0 ? mask_bits() : 0u;
+  uint32_t mbits = mnext;
   __syncthreads();
 
   for (int64_t t = 0; t < ntiles; ++t) {
@@ -271,7 +269,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64(AttnP p) {
       attn_tile<MASKED>(p, Ks[cur], Vs[cur], k0, qi, nullptr, qf, oacc, m_run, l_run, half, l32,
                         mbits);
     store_tile(cur ^ 1);
-    if (MASKED) mbits = mask_bits();
+    mbits = mnext;
     __syncthreads();
   }
   if (qi < S) attn_store(p, b, h, qi, oacc, 1.0f / l_run, half);
@@ -314,7 +312,7 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64_full(AttnP p) {
   for (int s = 0; s < kD / 2; ++s) qf[s] = qbase[qc * p.ldq + 2 * s + half];
   static_assert((kKT * kD / 4) % NT == 0, "tile must split into float4 per thread");
   constexpr int NV = kKT * kD / 4 / NT;
-  float4 kr[MAXT][NV], vr[MAXT][NV];
+  floatx4 kr[MAXT][NV], vr[MAXT][NV];
 #pragma unroll
   for (int t = 0; t < MAXT; ++t)
 #pragma unroll
@@ -325,11 +323,11 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64_full(AttnP p) {
       const float* kp = kbase + kc * p.ldk + dq;
       const float* vp = vbase + kc * p.ldv + dq;
       if (VEC) {
-        kr[t][i] = *reinterpret_cast<const float4*>(kp);
-        vr[t][i] = *reinterpret_cast<const float4*>(vp);
+        kr[t][i] = *reinterpret_cast<const floatx4*>(kp);
+        vr[t][i] = *reinterpret_cast<const floatx4*>(vp);
       } else {
-        kr[t][i] = make_float4(kp[0], kp[1], kp[2], kp[3]);
-        vr[t][i] = make_float4(vp[0], vp[1], vp[2], vp[3]);
+        kr[t][i] = floatx4{kp[0], kp[1], kp[2], kp[3]};
+        vr[t][i] = floatx4{vp[0], vp[1], vp[2], vp[3]};
       }
     }
   uint8_t mrow[(MAXT * kKT + NT - 1) / NT];
@@ -347,8 +345,8 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64_full(AttnP p) {
       const int idx = tid + NT * i;
       const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
       float* ks = &Ks[t][key * kKS + dq];
-      ks[0] = kr[t][i].x; ks[1] = kr[t][i].y; ks[2] = kr[t][i].z; ks[3] = kr[t][i].w;
-      *reinterpret_cast<float4*>(&Vs[t][key * kVS + dq]) = vr[t][i];
+      ks[0] = kr[t][i][0]; ks[1] = kr[t][i][1]; ks[2] = kr[t][i][2]; ks[3] = kr[t][i][3];
+      *reinterpret_cast<floatx4*>(&Vs[t][key * kVS + dq]) = vr[t][i];
     }
   int64_t key_end = S;
   if (MASK_ROW) {
@@ -528,7 +526,6 @@ __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_ks(AttnP p) {
 //                 operand is V[that key][16db + r].
 // The KW partial states (m, l, O) are merged through LDS, wave w merging dim
 // block w for all 16 queries.
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 template <int KW>
 __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_q16(AttnP p) {
