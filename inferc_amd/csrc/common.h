@@ -335,6 +335,13 @@ void attention(inferc_hip_ctx* ctx, const AttnArgs& a);
 void layernorm(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
                const float* residual, const float* gamma, const float* beta, float eps,
                float* y);
+// As layernorm_res_period, with row r of x being row ids[r] of table
+// [vocab, feat] (an embedding Gather folded in; an out-of-range id sets
+// *err, which may be null).
+void layernorm_gather(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* table,
+                      int64_t vocab, const int64_t* ids, int32_t* err, const float* residual,
+                      int64_t res_rows, const float* gamma, const float* beta, float eps,
+                      float* y);
 // As layernorm, with row r adding residual row r % res_rows.
 void layernorm_res_period(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
                           const float* residual, int64_t res_rows, const float* gamma,

@@ -22,6 +22,7 @@
 #include <map>
 #include <memory>
 #include <set>
+#include <unordered_set>
 #include <sstream>
 #include <string>
 #include <unordered_map>
@@ -156,6 +157,18 @@ struct inferc_executor {
   // (embedding.cc:63). dev_gather: the last walk launched such a gather.
   int32_t* gather_err = nullptr;
   bool dev_gather = false;
+  // Gathers of embedding rows whose one reader is a LayerNorm (its rows or
+  // its residual): the LayerNorm kernel gathers the rows itself, so no
+  // [rows, feat] copy is written (decided when planning; the indices must
+  // turn out to live on the device, else the Gather runs).
+  std::unordered_set<std::string> gather_ln;
+  struct PendingGather {
+    const float* table;
+    const int64_t* ids;
+    int64_t vocab, feat, n;
+  };
+  std::unordered_map<std::string, PendingGather> pending_gather;  // this walk
+  void materialize_gather(const std::string& name);
   // Gather outputs (this walk) whose Gather applied the LayerNorm the
   // peephole had moved into their Gemm reader (a feature-axis gather).
   std::set<std::string> ln_gemm_off;
@@ -580,6 +593,24 @@ void inferc_executor::peephole() {
     }
     if (ok && !lr.readers.empty()) ln_reads[h] = std::move(lr);
   }
+  // Row gathers from an initializer table read by one FusedLayerNorm only
+  gather_ln.clear();
+  std::unordered_map<std::string, int> reads;
+  for (const auto& n : nodes)
+    for (const auto& t : n.in) ++reads[t];
+  for (const auto& g : nodes) {
+    if (g.op != "Gather" || g.in.size() != 2 || g.out.size() != 1 || !inits.count(g.in[0]) ||
+        inits.count(g.in[1]) || ih::attr_int(g, "axis", 0) != 0 || g.attrs.count("__ln_g") ||
+        reads[g.out[0]] != 1 ||
+        std::find(outputs.begin(), outputs.end(), g.out[0]) != outputs.end())
+      continue;
+    const ih::Value& t = inits.at(g.in[0]);
+    if (t.dtype != INFERC_DT_F32 || t.shape.size() != 2) continue;
+    for (const auto& n : nodes)
+      if (n.op == "FusedLayerNorm" && n.in.size() >= 3 &&
+          (n.in[0] == g.out[0] || (n.in.size() >= 4 && n.in[3] == g.out[0])))
+        gather_ln.insert(g.out[0]);
+  }
 }
 
 // Whether this run's readers of h apply its LayerNorm as they read (decided
@@ -969,6 +1000,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     // (y = LN(x + r), r repeated over leading dims as the Add broadcast it)
     size_t xi = 0, ri = 3;
     if (n.in.size() >= 4 && in(3).numel() > in(0).numel()) std::swap(xi, ri);
+    if (n.in.size() >= 4 && pending_gather.count(n.in[ri])) materialize_gather(n.in[ri]);
+    const auto pg = pending_gather.find(n.in[xi]);
     const Value x = in(xi);
     require_f32(x, "X");
     const int64_t feat = x.shape.back();
@@ -987,6 +1020,20 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       res_rows = rv.numel() / feat;
     }
     float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, x.shape).dev);
+    if (pg != pending_gather.end()) {
+      // x is a row gather from an embedding table: the kernel gathers
+      const PendingGather g = pg->second;
+      pending_gather.erase(pg);
+      IH_REQUIRE(g.feat == feat && g.n == x.numel() / feat, INFERC_ERR_SHAPE,
+                 "LayerNorm: gathered rows do not match the feature dim");
+      if (!dry) {
+        layernorm_gather(ctx, g.n, feat, g.table, g.vocab, g.ids, gather_err, res, res_rows,
+                         static_cast<const float*>(dev_of(n.in[1])),
+                         static_cast<const float*>(dev_of(n.in[2])), eps, y);
+        dev_gather = true;
+      }
+      return;
+    }
     if (!dry) {
       layernorm_res_period(ctx, x.numel() / feat, feat, static_cast<const float*>(dev_of(n.in[xi])),
                            res, res_rows, static_cast<const float*>(dev_of(n.in[1])),
@@ -1184,6 +1231,16 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
         vals[n.out[0]] = v;
         return;
       }
+    }
+    if (gather_ln.count(n.out[0]) && !idx.host && idx.dtype == INFERC_DT_I64 && outer == 1) {
+      // rows for the one LayerNorm reading this output, which gathers them
+      ih::Value v;
+      v.dtype = INFERC_DT_F32;
+      v.shape = os;
+      vals[n.out[0]] = v;
+      pending_gather[n.out[0]] = PendingGather{
+          dp, static_cast<const int64_t*>(dev_of(n.in[1])), ad, inner, idx.numel()};
+      return;
     }
     float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
     // one device gather for any axis; host-known indices are validated here
@@ -1764,6 +1821,7 @@ void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
   vals = inits;
   dev_gather = false;
   ln_gemm_off.clear();
+  pending_gather.clear();
   cache_views.clear();
   for (auto& kv : inputs) vals[kv.first] = kv.second.v;
   const bool events = act != nullptr && !dry;
@@ -1846,6 +1904,19 @@ void inferc_executor::run() {
 // Waits for the stream, then fails if a device-index gather of the passes
 // enqueued so far met an out-of-range index; the flag is cleared first, so
 // the next pass starts clean.
+// A row gather left pending for a LayerNorm that turned out to read it as
+// its residual: written out after all.
+void inferc_executor::materialize_gather(const std::string& name) {
+  const PendingGather g = pending_gather.at(name);
+  pending_gather.erase(name);
+  const std::vector<int64_t> shape = vals.at(name).shape;
+  float* y = static_cast<float*>(make_dev(name, INFERC_DT_F32, shape).dev);
+  if (!dry) {
+    ih::gather_axis(ctx, 1, g.vocab, g.feat, g.table, g.ids, g.n, y, gather_err);
+    dev_gather = true;
+  }
+}
+
 void inferc_executor::check_gather_err() {
   if (dry || !dev_gather || !gather_err) return;
   int32_t flag = 0;

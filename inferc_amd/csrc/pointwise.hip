@@ -20,6 +20,10 @@ constexpr int kBlock = 256;
 // reference's vDSP_meanv / vDSP_measqv sequence); wider rows are re-read.
 // Row r adds residual row r % res_rows (a residual repeated over leading
 // dims, as a suffix-broadcast Add would).
+//
+// ids set: row r of x is row ids[r] of a [vocab, feat] table (an embedding
+// Gather folded in, embedding.cc:9-72): negative ids wrap, and an id out of
+// range raises the error flag (the table's first row stands in).
 template <int VPL>
 __global__ __launch_bounds__(kBlock) void layernorm_kernel(int64_t rows, int64_t feat,
                                                            const float* __restrict__ x,
@@ -27,11 +31,22 @@ __global__ __launch_bounds__(kBlock) void layernorm_kernel(int64_t rows, int64_t
                                                            const float* __restrict__ g,
                                                            const float* __restrict__ b,
                                                            float eps, float* __restrict__ y,
-                                                           int64_t res_rows) {
+                                                           int64_t res_rows,
+                                                           const int64_t* __restrict__ ids,
+                                                           int64_t vocab, int32_t* err) {
   const int lane = threadIdx.x & 63;
   const int64_t row = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
   if (row >= rows) return;
-  ln_row<VPL>(lane, x + row * feat, res ? res + (row % res_rows) * feat : nullptr, g, b, feat,
+  int64_t xr = row;
+  if (ids) {
+    xr = ids[row];
+    if (xr < 0) xr += vocab;
+    if (xr < 0 || xr >= vocab) {
+      if (lane == 0 && err) *err = 1;
+      xr = 0;
+    }
+  }
+  ln_row<VPL>(lane, x + xr * feat, res ? res + (row % res_rows) * feat : nullptr, g, b, feat,
               eps, y + row * feat);
 }
 
@@ -190,22 +205,42 @@ void layernorm(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
   layernorm_res_period(ctx, rows, feat, x, residual, rows, gamma, beta, eps, y);
 }
 
-void layernorm_res_period(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
-                          const float* residual, int64_t res_rows, const float* gamma,
-                          const float* beta, float eps, float* y) {
+namespace {
+void launch_layernorm(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
+                      const float* residual, int64_t res_rows, const float* gamma,
+                      const float* beta, float eps, float* y, const int64_t* ids, int64_t vocab,
+                      int32_t* err) {
   IH_REQUIRE(rows >= 0 && feat > 0, INFERC_ERR_SHAPE, "layernorm: bad shape");
   IH_REQUIRE(residual == nullptr || (res_rows > 0 && rows % res_rows == 0), INFERC_ERR_SHAPE,
              "layernorm: residual rows must divide the rows");
   if (rows == 0) return;
   IH_REQUIRE(x && gamma && beta && y, INFERC_ERR_ARG, "layernorm: null pointer");
   const unsigned blocks = unsigned(ceil_div(rows, kBlock / 64));
+  const int64_t rr = residual ? res_rows : int64_t(1);
   if (feat <= 64 * 4)
     hipLaunchKernelGGL(layernorm_kernel<4>, dim3(blocks), dim3(kBlock), 0, ctx->stream, rows,
-                       feat, x, residual, gamma, beta, eps, y, residual ? res_rows : int64_t(1));
+                       feat, x, residual, gamma, beta, eps, y, rr, ids, vocab, err);
   else
     hipLaunchKernelGGL(layernorm_kernel<16>, dim3(blocks), dim3(kBlock), 0, ctx->stream, rows,
-                       feat, x, residual, gamma, beta, eps, y, residual ? res_rows : int64_t(1));
+                       feat, x, residual, gamma, beta, eps, y, rr, ids, vocab, err);
   check_launch("layernorm");
+}
+}  // namespace
+
+void layernorm_res_period(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
+                          const float* residual, int64_t res_rows, const float* gamma,
+                          const float* beta, float eps, float* y) {
+  launch_layernorm(ctx, rows, feat, x, residual, res_rows, gamma, beta, eps, y, nullptr, 0,
+                   nullptr);
+}
+
+void layernorm_gather(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* table,
+                      int64_t vocab, const int64_t* ids, int32_t* err, const float* residual,
+                      int64_t res_rows, const float* gamma, const float* beta, float eps,
+                      float* y) {
+  IH_REQUIRE(vocab > 0 && ids != nullptr, INFERC_ERR_ARG, "layernorm: gather without rows");
+  launch_layernorm(ctx, rows, feat, table, residual, res_rows, gamma, beta, eps, y, ids, vocab,
+                   err);
 }
 
 void activation(inferc_hip_ctx* ctx, int64_t n, const float* x, int act, float* y) {

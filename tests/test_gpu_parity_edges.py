@@ -404,3 +404,44 @@ def test_attention_large_grid_minus_inf_fill_with_masked_leading_tiles(ctx, S):
     got = _attn_raw(ctx, q, k, v, mask, hd, -np.inf, 0)
     assert np.isfinite(got).all()
     _attn_close(got, O.fused_attention(q, k, v, mask, hd, -np.inf))
+
+
+# ------------------------------------ embedding Gather folded into LayerNorm
+
+@pytest.mark.parametrize("as_residual", [False, True])
+def test_executor_gather_read_by_layernorm(ctx, as_residual):
+    """A row Gather from an initializer table whose one reader is a
+    FusedLayerNorm: the LayerNorm kernel gathers the rows itself when they
+    are its x (the encoder's word embeddings), and the Gather is written out
+    first when they turn out to be the residual. Against float64, and
+    out-of-range ids still raise (embedding.cc:63)."""
+    rng = np.random.default_rng(77)
+    V, F = 50, 96
+    table = rng.standard_normal((V, F)).astype(np.float32)
+    gam = (1.0 + 0.1 * rng.standard_normal(F)).astype(np.float32)
+    bet = (0.1 * rng.standard_normal(F)).astype(np.float32)
+    g = rt.Graph()
+    for nm, v in (("table", table), ("g", gam), ("b", bet)):
+        g.add_initializer(nm, v)
+    g.add_node("Gather", ["table", "ids"], ["e"], axis=0)
+    g.add_node("FusedLayerNorm", ["x", "g", "b", "e"] if as_residual else ["e", "g", "b", "x"],
+               ["y"], epsilon=1e-5)
+    g.add_output("y")
+    ex = rt.Executor(ctx, g)
+    ids = np.array([3, 49, -1, 0, 17, 8], np.int64)
+    if as_residual:   # x has more rows than the gathered residual
+        x = rng.standard_normal((4, 6, F)).astype(np.float32)
+        h = x.astype(np.float64) + table[ids].astype(np.float64)[None]
+    else:
+        x = rng.standard_normal((6, F)).astype(np.float32)
+        h = table[ids].astype(np.float64) + x
+    m = h.mean(-1, keepdims=True)
+    ref = (h - m) / np.sqrt(((h - m) ** 2).mean(-1, keepdims=True) + 1e-5) * gam + bet
+    for _ in range(3):  # eager, capture, replay
+        got = ex.run({"ids": ids, "x": x}, ["y"])["y"]
+        np.testing.assert_allclose(got, ref, rtol=0, atol=1e-5)
+    bad = ids.copy()
+    bad[2] = V
+    with pytest.raises(RuntimeError, match="Gather: index out of range"):
+        ex.run({"ids": bad, "x": x}, ["y"])
+    ex.close()
