@@ -53,6 +53,46 @@ __device__ __forceinline__ void wave_lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The head dim that S^T = K Q^T pairs with MFMA step s (of kD/2) in lane half
+// `half`: 8*(s/4) + 4*half + s%4. Any pairing gives the same dot product up to
+// summation order (the MFMA summation index is a dummy index); this one gives
+// each lane its 32 Q values as 8 runs of 4 consecutive dims, one float4 each.
+__device__ __forceinline__ int qk_dim(int s, int half) { return 8 * (s >> 2) + 4 * half + (s & 3); }
+
+constexpr int kQS = kD + 4;  // LDS row stride of the Q and O staging (float4 rows)
+
+// A wave's 32 query rows q0.. read whole: each load covers 4 rows of 256 bytes
+// (rows past S are clamped; their outputs are not written). Loading the
+// operand layout directly costs a load per 16 bytes of 32 rows instead.
+__device__ __forceinline__ void q_rows_load(const float* qbase, int64_t ldq, int64_t q0,
+                                            int64_t S, int lane, floatx4 (&qr)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int idx = lane + 64 * i;
+    const int64_t row = q0 + idx / 16;
+    const int64_t rc = row < S ? row : S - 1;
+    qr[i] = *reinterpret_cast<const floatx4*>(qbase + rc * ldq + (idx % 16) * 4);
+  }
+}
+
+// The rows of q_rows_load through the wave's LDS slice qs (32 rows of kQS)
+// into the B operand of S^T = K Q^T: qf[s] = Q[query l32][qk_dim(s, half)].
+__device__ __forceinline__ void q_rows_to_operand(float* qs, const floatx4 (&qr)[8], int lane,
+                                                  float (&qf)[kD / 2]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int idx = lane + 64 * i;
+    *reinterpret_cast<floatx4*>(qs + (idx / 16) * kQS + (idx % 16) * 4) = qr[i];
+  }
+  wave_lds_barrier();
+  const int half = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const floatx4 t = *reinterpret_cast<const floatx4*>(qs + l32 * kQS + 8 * j + 4 * half);
+    qf[4 * j] = t[0]; qf[4 * j + 1] = t[1]; qf[4 * j + 2] = t[2]; qf[4 * j + 3] = t[3];
+  }
+}
+
 // One 32-key tile for a wave's 32 queries: S^T = K Q^T on the matrix cores,
 // scale, mask, online-softmax update, then O^T += V^T P^T. BITS: the mask
 // comes as mbits (bit v: score register v's key is masked, loaded ahead by
@@ -69,7 +109,7 @@ __device__ __forceinline__ void attn_tile(const AttnP& p, const float* __restric
   for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
 #pragma unroll
   for (int s = 0; s < kD / 2; ++s) {
-    const float a = ks[l32 * kKS + 2 * s + half];
+    const float a = ks[l32 * kKS + qk_dim(s, half)];
     sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, qf[s], sacc, 0, 0, 0);
   }
   // sacc[v]: key k0 + 8*(v/4) + 4*half + v%4, query qi.
@@ -143,6 +183,34 @@ __device__ __forceinline__ void attn_store(const AttnP& p, int64_t b, int64_t h,
     }
 }
 
+// attn_store for 16-byte aligned rows: the wave's 32 output rows q0.. go
+// through its LDS slice os (32 rows of kQS) and out whole, 4 rows of 256
+// bytes per store. (Stored straight from the accumulator layout, each store
+// would write 32 bytes into each of 32 rows.)
+__device__ __forceinline__ void o_rows_store(const AttnP& p, int64_t b, int64_t h, int64_t q0,
+                                             float* os, const floatx16 (&oacc)[2], float inv,
+                                             int lane) {
+  const int half = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      floatx4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = oacc[d][4 * g + e] * inv;
+      *reinterpret_cast<floatx4*>(os + l32 * kQS + d * 32 + 8 * g + 4 * half) = o;
+    }
+  wave_lds_barrier();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int idx = lane + 64 * i;
+    const int64_t row = q0 + idx / 16;
+    const floatx4 o = *reinterpret_cast<const floatx4*>(os + (idx / 16) * kQS + (idx % 16) * 4);
+    if (row < p.S)
+      *reinterpret_cast<floatx4*>(p.out + (b * p.S + row) * p.ldo + h * kD + (idx % 16) * 4) = o;
+  }
+}
+
 // Large grids: WAVES waves of 32 queries share each K/V tile, staged through
 // LDS (double-buffered). The loads of tile t+1, the lane's 16 mask bytes
 // included, are issued before tile t's matrix-core work and are unconditional
@@ -153,8 +221,12 @@ __device__ __forceinline__ void attn_store(const AttnP& p, int64_t b, int64_t h,
 template <int WAVES, bool VEC, bool MASKED>
 __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) {
   constexpr int NT = 64 * WAVES;
-  __shared__ __attribute__((aligned(16))) float Ks[2][kKT * kKS];
-  __shared__ __attribute__((aligned(16))) float Vs[2][kKT * kVS];
+  // K and V tiles (double-buffered). With VEC the same LDS also holds each
+  // wave's Q rows before the first tile and its output rows after the last.
+  constexpr int kKVF = 2 * kKT * kKS + 2 * kKT * kVS, kQF = WAVES * 32 * kQS;
+  __shared__ __attribute__((aligned(16))) float lds[kKVF > kQF ? kKVF : kQF];
+  float(*Ks)[kKT * kKS] = reinterpret_cast<float(*)[kKT * kKS]>(lds);
+  float(*Vs)[kKT * kVS] = reinterpret_cast<float(*)[kKT * kVS]>(lds + 2 * kKT * kKS);
   __shared__ int s_last_valid;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -189,14 +261,19 @@ __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) 
     __syncthreads();
     if (s_last_valid >= 0) key_end = s_last_valid + 1;
   }
+  // key_end >= 1 (S >= 1; a masked row keeps at least key 0), so ntiles >= 1
   const int64_t ntiles = (key_end + kKT - 1) / kKT;
 
-  // Q^T operand: step s covers dims 2s, 2s+1; lane supplies Q[qi][2s+half]
-  // (a lane past the sequence reads the last query; its output is not
-  // written).
+  // Q^T operand: lane supplies Q[qi][qk_dim(s, half)] for step s (a lane
+  // past the sequence reads the last query; its output is not written).
   float qf[kD / 2];
+  floatx4 qr[8];
+  if constexpr (VEC) {
+    q_rows_load(qbase, p.ldq, q0, S, lane, qr);
+  } else {
 #pragma unroll
-  for (int s = 0; s < kD / 2; ++s) qf[s] = qbase[qc * p.ldq + 2 * s + half];
+    for (int s = 0; s < kD / 2; ++s) qf[s] = qbase[qc * p.ldq + qk_dim(s, half)];
+  }
 
   floatx16 oacc[2];
 #pragma unroll
@@ -249,10 +326,12 @@ __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) 
     }
   };
 
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
+  load_tile(0);
+  if constexpr (VEC) {
+    q_rows_to_operand(lds + wave * 32 * kQS, qr, lane, qf);
+    __syncthreads();  // every wave has its Q before tile 0 overwrites the slices
   }
+  store_tile(0);
   uint32_t mbits = mnext;
   __syncthreads();
 
@@ -272,7 +351,9 @@ __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) 
     mbits = mnext;
     __syncthreads();
   }
-  if (qi < S) attn_store(p, b, h, qi, oacc, 1.0f / l_run, half);
+  // (the loop's last barrier: no wave reads the K/V tiles any more)
+  if constexpr (VEC) o_rows_store(p, b, h, q0, lds + wave * 32 * kQS, oacc, 1.0f / l_run, lane);
+  else if (qi < S) attn_store(p, b, h, qi, oacc, 1.0f / l_run, half);
 }
 
 // Short sequences (S <= 32*MAXT keys) on large grids: the block stages the
@@ -285,7 +366,7 @@ __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) 
 // every key is masked all are kept. WAVES waves of 32 queries per block;
 // VEC: 16-byte aligned rows. MASK_ROW: a query-independent mask (ms2 == 0).
 template <int WAVES, int MAXT, bool VEC, bool MASK_ROW>
-__global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64_full(AttnP p) {
+__global__ __launch_bounds__(64 * WAVES, 2) void attn_fwd_d64_full(AttnP p) {
   constexpr int NT = 64 * WAVES;
   __shared__ __attribute__((aligned(16))) float Ks[MAXT][kKT * kKS];
   __shared__ __attribute__((aligned(16))) float Vs[MAXT][kKT * kVS];
@@ -306,10 +387,17 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64_full(AttnP p) {
   const uint8_t* mbase = MASK_ROW ? p.mask + b * p.ms0 + h * p.ms1 : nullptr;
 
   // Every load first: Q, all K/V tiles, the mask row (keys clamped into the
-  // sequence; a clamped key's score is -inf, so its V row weighs 0).
+  // sequence; a clamped key's score is -inf, so its V row weighs 0). With VEC
+  // the Q rows, and at the end the output rows, pass through Vs.
+  static_assert(WAVES * 32 * kQS <= MAXT * kKT * kVS, "Q/O staging must fit in Vs");
   float qf[kD / 2];
+  floatx4 qr[8];
+  if constexpr (VEC) {
+    q_rows_load(qbase, p.ldq, q0, S, lane, qr);
+  } else {
 #pragma unroll
-  for (int s = 0; s < kD / 2; ++s) qf[s] = qbase[qc * p.ldq + 2 * s + half];
+    for (int s = 0; s < kD / 2; ++s) qf[s] = qbase[qc * p.ldq + qk_dim(s, half)];
+  }
   static_assert((kKT * kD / 4) % NT == 0, "tile must split into float4 per thread");
   constexpr int NV = kKT * kD / 4 / NT;
   floatx4 kr[MAXT][NV], vr[MAXT][NV];
@@ -337,6 +425,10 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64_full(AttnP p) {
       const int j = tid + NT * i;
       mrow[i] = mbase[(j < S ? j : S - 1) * p.ms3];
     }
+  }
+  if constexpr (VEC) {
+    q_rows_to_operand(&Vs[0][0] + wave * 32 * kQS, qr, lane, qf);
+    __syncthreads();  // every wave has its Q before the tiles overwrite Vs
   }
 #pragma unroll
   for (int t = 0; t < MAXT; ++t)
@@ -391,7 +483,12 @@ __global__ __launch_bounds__(64 * WAVES) void attn_fwd_d64_full(AttnP p) {
                           mbits);
     }
   }
-  if (qi < S) attn_store(p, b, h, qi, oacc, 1.0f / l_run, half);
+  if constexpr (VEC) {
+    __syncthreads();  // every wave is done with the tiles in Vs
+    o_rows_store(p, b, h, q0, &Vs[0][0] + wave * 32 * kQS, oacc, 1.0f / l_run, lane);
+  } else if (qi < S) {
+    attn_store(p, b, h, qi, oacc, 1.0f / l_run, half);
+  }
 }
 
 // Small grids (b=1): the KW waves of a block share the same 32 queries and
@@ -436,7 +533,7 @@ __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_ks(AttnP p) {
 
   float qf[kD / 2];
 #pragma unroll
-  for (int s = 0; s < kD / 2; ++s) qf[s] = (qi < S) ? qbase[qi * p.ldq + 2 * s + half] : 0.0f;
+  for (int s = 0; s < kD / 2; ++s) qf[s] = (qi < S) ? qbase[qi * p.ldq + qk_dim(s, half)] : 0.0f;
   floatx16 oacc[2];
 #pragma unroll
   for (int d = 0; d < 2; ++d)
