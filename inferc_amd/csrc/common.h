@@ -335,17 +335,28 @@ void attention(inferc_hip_ctx* ctx, const AttnArgs& a);
 void layernorm(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
                const float* residual, const float* gamma, const float* beta, float eps,
                float* y);
+// An elementwise compare that rides along with a LayerNorm launch, on
+// operands independent of it: out[i] = (a[i] == b[i % b_n]) for i < n, with
+// n % b_n == 0 (an Equal on graph inputs, e.g. an encoder's padding mask).
+// n == 0: none.
+struct EqSide {
+  const int64_t* a = nullptr;
+  const int64_t* b = nullptr;
+  int64_t n = 0, b_n = 1;
+  uint8_t* out = nullptr;
+};
 // As layernorm_res_period, with row r of x being row ids[r] of table
 // [vocab, feat] (an embedding Gather folded in; an out-of-range id sets
 // *err, which may be null).
 void layernorm_gather(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* table,
                       int64_t vocab, const int64_t* ids, int32_t* err, const float* residual,
                       int64_t res_rows, const float* gamma, const float* beta, float eps,
-                      float* y);
+                      float* y, const EqSide& side = EqSide{});
 // As layernorm, with row r adding residual row r % res_rows.
 void layernorm_res_period(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
                           const float* residual, int64_t res_rows, const float* gamma,
-                          const float* beta, float eps, float* y);
+                          const float* beta, float eps, float* y,
+                          const EqSide& side = EqSide{});
 void activation(inferc_hip_ctx* ctx, int64_t n, const float* x, int act, float* y);
 void add_bcast(inferc_hip_ctx* ctx, int64_t n, const float* a, const float* b, int64_t b_n,
                float* y);

@@ -169,6 +169,11 @@ struct inferc_executor {
   };
   std::unordered_map<std::string, PendingGather> pending_gather;  // this walk
   void materialize_gather(const std::string& name);
+  // Equals on graph inputs and initializers, each computed by the launch of
+  // a LayerNorm before it (by that LayerNorm's output; decided when
+  // planning), and the ones done so in this walk.
+  std::unordered_map<std::string, size_t> eq_side;
+  std::unordered_set<std::string> eq_done;
   // Gather outputs (this walk) whose Gather applied the LayerNorm the
   // peephole had moved into their Gemm reader (a feature-axis gather).
   std::set<std::string> ln_gemm_off;
@@ -611,6 +616,24 @@ void inferc_executor::peephole() {
           (n.in[0] == g.out[0] || (n.in.size() >= 4 && n.in[3] == g.out[0])))
         gather_ln.insert(g.out[0]);
   }
+  // An Equal whose operands exist before any node runs (a graph input and an
+  // initializer) rides along with the launch of the nearest FusedLayerNorm
+  // before it: one launch fewer (an encoder's padding mask).
+  eq_side.clear();
+  std::unordered_set<std::string> produced;
+  for (const auto& n : nodes)
+    for (const auto& o : n.out) produced.insert(o);
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    const inferc_graph::Node& e = nodes[i];
+    if (e.op != "Equal" || e.in.size() != 2 || e.out.size() != 1 || inits.count(e.in[0]) ||
+        produced.count(e.in[0]) || !inits.count(e.in[1]))
+      continue;
+    for (size_t j = i; j-- > 0;)
+      if (nodes[j].op == "FusedLayerNorm" && nodes[j].out.size() == 1) {
+        if (!eq_side.count(nodes[j].out[0])) eq_side[nodes[j].out[0]] = i;
+        break;
+      }
+  }
 }
 
 // Whether this run's readers of h apply its LayerNorm as they read (decided
@@ -1020,6 +1043,25 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       res_rows = rv.numel() / feat;
     }
     float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, x.shape).dev);
+    ih::EqSide side;
+    const auto es = eq_side.find(n.out[0]);
+    if (es != eq_side.end()) {
+      // the Equal's own fast-path conditions (below), else it runs itself
+      const inferc_graph::Node& e = nodes[es->second];
+      const Value ea = get(e.in[0]);
+      const Value eb = get(e.in[1]);
+      if (ea.dtype == INFERC_DT_I64 && eb.dtype == INFERC_DT_I64 && !(ea.host && eb.host) &&
+          eb.numel() > 0 &&
+          (eb.numel() == ea.numel() || eb.numel() == 1 || suffix_broadcast(ea.shape, eb.shape)) &&
+          eb.numel() <= ea.numel()) {
+        side.a = static_cast<const int64_t*>(dev_of(e.in[0]));
+        side.b = static_cast<const int64_t*>(dev_of(e.in[1]));
+        side.n = ea.numel();
+        side.b_n = eb.numel();
+        side.out = static_cast<uint8_t*>(make_dev(e.out[0], INFERC_DT_BOOL, ea.shape).dev);
+        eq_done.insert(e.out[0]);
+      }
+    }
     if (pg != pending_gather.end()) {
       // x is a row gather from an embedding table: the kernel gathers
       const PendingGather g = pg->second;
@@ -1029,7 +1071,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       if (!dry) {
         layernorm_gather(ctx, g.n, feat, g.table, g.vocab, g.ids, gather_err, res, res_rows,
                          static_cast<const float*>(dev_of(n.in[1])),
-                         static_cast<const float*>(dev_of(n.in[2])), eps, y);
+                         static_cast<const float*>(dev_of(n.in[2])), eps, y, side);
         dev_gather = true;
       }
       return;
@@ -1037,7 +1079,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     if (!dry) {
       layernorm_res_period(ctx, x.numel() / feat, feat, static_cast<const float*>(dev_of(n.in[xi])),
                            res, res_rows, static_cast<const float*>(dev_of(n.in[1])),
-                           static_cast<const float*>(dev_of(n.in[2])), eps, y);
+                           static_cast<const float*>(dev_of(n.in[2])), eps, y, side);
     }
     return;
   }
@@ -1111,6 +1153,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "Equal") {
+    if (eq_done.count(n.out[0])) return;  // computed by a LayerNorm launch
     const Value a = in(0);
     const Value b = in(1);
     if (a.dtype != INFERC_DT_I64 || b.dtype != INFERC_DT_I64 || (a.host && b.host) ||
@@ -1822,6 +1865,7 @@ void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
   dev_gather = false;
   ln_gemm_off.clear();
   pending_gather.clear();
+  eq_done.clear();
   cache_views.clear();
   for (auto& kv : inputs) vals[kv.first] = kv.second.v;
   const bool events = act != nullptr && !dry;

@@ -33,9 +33,14 @@ __global__ __launch_bounds__(kBlock) void layernorm_kernel(int64_t rows, int64_t
                                                            float eps, float* __restrict__ y,
                                                            int64_t res_rows,
                                                            const int64_t* __restrict__ ids,
-                                                           int64_t vocab, int32_t* err) {
+                                                           int64_t vocab, int32_t* err,
+                                                           EqSide side) {
   const int lane = threadIdx.x & 63;
   const int64_t row = int64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  // the compare riding along (independent of the rows)
+  for (int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x; i < side.n;
+       i += int64_t(gridDim.x) * kBlock)
+    side.out[i] = side.a[i] == side.b[side.b_n == side.n ? i : i % side.b_n] ? 1 : 0;
   if (row >= rows) return;
   int64_t xr = row;
   if (ids) {
@@ -209,38 +214,45 @@ namespace {
 void launch_layernorm(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
                       const float* residual, int64_t res_rows, const float* gamma,
                       const float* beta, float eps, float* y, const int64_t* ids, int64_t vocab,
-                      int32_t* err) {
+                      int32_t* err, const EqSide& side) {
   IH_REQUIRE(rows >= 0 && feat > 0, INFERC_ERR_SHAPE, "layernorm: bad shape");
   IH_REQUIRE(residual == nullptr || (res_rows > 0 && rows % res_rows == 0), INFERC_ERR_SHAPE,
              "layernorm: residual rows must divide the rows");
-  if (rows == 0) return;
+  IH_REQUIRE(side.n >= 0 && side.b_n > 0 && (side.n == 0 || side.n % side.b_n == 0),
+             INFERC_ERR_SHAPE, "equal: broadcast size must divide the output size");
+  IH_REQUIRE(side.n == 0 || (side.a && side.b && side.out), INFERC_ERR_ARG,
+             "equal: null pointer");
+  if (rows == 0) {
+    if (side.n > 0) equal_i64(ctx, side.n, side.a, side.b, side.b_n, side.out);
+    return;
+  }
   IH_REQUIRE(x && gamma && beta && y, INFERC_ERR_ARG, "layernorm: null pointer");
   const unsigned blocks = unsigned(ceil_div(rows, kBlock / 64));
   const int64_t rr = residual ? res_rows : int64_t(1);
   if (feat <= 64 * 4)
     hipLaunchKernelGGL(layernorm_kernel<4>, dim3(blocks), dim3(kBlock), 0, ctx->stream, rows,
-                       feat, x, residual, gamma, beta, eps, y, rr, ids, vocab, err);
+                       feat, x, residual, gamma, beta, eps, y, rr, ids, vocab, err, side);
   else
     hipLaunchKernelGGL(layernorm_kernel<16>, dim3(blocks), dim3(kBlock), 0, ctx->stream, rows,
-                       feat, x, residual, gamma, beta, eps, y, rr, ids, vocab, err);
+                       feat, x, residual, gamma, beta, eps, y, rr, ids, vocab, err, side);
   check_launch("layernorm");
 }
 }  // namespace
 
 void layernorm_res_period(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* x,
                           const float* residual, int64_t res_rows, const float* gamma,
-                          const float* beta, float eps, float* y) {
+                          const float* beta, float eps, float* y, const EqSide& side) {
   launch_layernorm(ctx, rows, feat, x, residual, res_rows, gamma, beta, eps, y, nullptr, 0,
-                   nullptr);
+                   nullptr, side);
 }
 
 void layernorm_gather(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const float* table,
                       int64_t vocab, const int64_t* ids, int32_t* err, const float* residual,
                       int64_t res_rows, const float* gamma, const float* beta, float eps,
-                      float* y) {
+                      float* y, const EqSide& side) {
   IH_REQUIRE(vocab > 0 && ids != nullptr, INFERC_ERR_ARG, "layernorm: gather without rows");
   launch_layernorm(ctx, rows, feat, table, residual, res_rows, gamma, beta, eps, y, ids, vocab,
-                   err);
+                   err, side);
 }
 
 void activation(inferc_hip_ctx* ctx, int64_t n, const float* x, int act, float* y) {

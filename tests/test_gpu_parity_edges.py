@@ -445,3 +445,39 @@ def test_executor_gather_read_by_layernorm(ctx, as_residual):
     with pytest.raises(RuntimeError, match="Gather: index out of range"):
         ex.run({"ids": bad, "x": x}, ["y"])
     ex.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rhs", ["scalar", "row", "full"])
+def test_executor_equal_rides_with_layernorm(ctx, rhs):
+    """An Equal on a graph input and an initializer, after a FusedLayerNorm,
+    is computed by that LayerNorm's launch (the encoder's padding mask); the
+    mask and the LayerNorm both match numpy, for a scalar, a broadcast row and
+    a full right operand, over eager, captured and replayed runs."""
+    rng = np.random.default_rng(78)
+    F = 64
+    gam = (1.0 + 0.1 * rng.standard_normal(F)).astype(np.float32)
+    bet = (0.1 * rng.standard_normal(F)).astype(np.float32)
+    mask = rng.integers(0, 3, size=(5, 7)).astype(np.int64)
+    rhs_v = {"scalar": np.array(0, np.int64),
+             "row": rng.integers(0, 3, size=(7,)).astype(np.int64),
+             "full": rng.integers(0, 3, size=(5, 7)).astype(np.int64)}[rhs]
+    g = rt.Graph()
+    for nm, v in (("g", gam), ("b", bet), ("z", rhs_v)):
+        g.add_initializer(nm, v)
+    g.add_node("FusedLayerNorm", ["x", "g", "b"], ["y"], epsilon=1e-5)
+    g.add_node("Equal", ["mask", "z"], ["m"])
+    g.add_output("y")
+    g.add_output("m")
+    ex = rt.Executor(ctx, g)
+    x = rng.standard_normal((9, F)).astype(np.float32)
+    h = x.astype(np.float64)
+    mu = h.mean(-1, keepdims=True)
+    ref = (h - mu) / np.sqrt(((h - mu) ** 2).mean(-1, keepdims=True) + 1e-5) * gam + bet
+    for it in range(3):  # eager, capture, replay
+        mk = mask if it != 2 else (mask + 1) % 3  # the replay sees new mask values
+        out = ex.run({"x": x, "mask": mk}, ["y", "m"])
+        np.testing.assert_allclose(out["y"], ref, rtol=0, atol=1e-5)
+        assert out["m"].dtype == np.bool_ and out["m"].shape == mk.shape
+        np.testing.assert_array_equal(out["m"], mk == rhs_v)
+    ex.close()
