@@ -619,12 +619,17 @@ __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_ks(AttnP p) {
 //                 four float4 loads of dims [16g, 16g+16) each;
 //                 score register v of key block kb: key k0+16kb+4g+v, query r.
 //   O^T += V^T P^T: step (kb, v) pairs k-index g with key k0+16kb+4g+v, which
-//                 is exactly the probability the lane already holds; the V^T
-//                 operand is V[that key][16db + r].
+//                 is exactly the probability the lane already holds. Output
+//                 row i of dim block db is dim 4i + db, so the V^T operands
+//                 of the lane's four blocks are one float4, V[that key][4r..
+//                 4r+3], and accumulator register v of block db holds dim
+//                 16g + 4v + db of query r.
+// MROW: a query-independent mask (ms2 == 0, not causal): each wave loads the
+// tile's 32 mask bytes once, one per lane, and shares them by a ballot.
 // The KW partial states (m, l, O) are merged through LDS, wave w merging dim
 // block w for all 16 queries.
 
-template <int KW>
+template <int KW, bool MROW>
 __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_q16(AttnP p) {
   __shared__ __attribute__((aligned(16))) float obuf[KW][16][kD + 4];
   __shared__ float sm[KW][16], sl[KW][16];
@@ -656,7 +661,7 @@ __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_q16(AttnP p) {
     if (p.causal && k0 > q0 + 15) break;  // later tiles are masked for every query here
     // Operands of this tile, all loads issued before any use.
     float4 kv[2][4];
-    float vv[2][4][4];  // [kb][v][db]
+    floatx4 vv[2][4];  // [kb][v]: component db is the V^T operand of dim block db
     uint8_t mk[2][4];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -668,11 +673,15 @@ __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_q16(AttnP p) {
       for (int v = 0; v < 4; ++v) {
         const int64_t key = k0 + 16 * kb + 4 * g + v;
         const int64_t kc = key < S ? key : S - 1;
-        const float* vp = vbase + kc * p.ldv + r;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) vv[kb][v][db] = vp[16 * db];
-        mk[kb][v] = (mbase && !p.causal && qi < S) ? mbase[qi * p.ms2 + kc * p.ms3] : uint8_t(0);
+        vv[kb][v] = *reinterpret_cast<const floatx4*>(vbase + kc * p.ldv + 4 * r);
+        if (!MROW)
+          mk[kb][v] = (mbase && !p.causal && qi < S) ? mbase[qi * p.ms2 + kc * p.ms3] : uint8_t(0);
       }
+    }
+    uint8_t mown = 0;  // MROW: the mask byte of key k0 + lane % 32
+    if (MROW) {
+      const int64_t j = k0 + (lane & 31);
+      mown = mbase[(j < S ? j : S - 1) * p.ms3];
     }
     floatx4 sacc[2];
 #pragma unroll
@@ -689,14 +698,17 @@ __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_q16(AttnP p) {
     }
     float sv[2][4];
     float tmax = -INFINITY;
+    // bit o: key k0 + o is masked (lanes 32..63 repeat lanes 0..31)
+    const uint64_t mbits = MROW ? __ballot(mown != 0) : 0;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int64_t j = k0 + 16 * kb + 4 * g + v;
+        const bool masked = MROW ? ((mbits >> (16 * kb + 4 * g + v)) & 1u) != 0 : mk[kb][v] != 0;
         float s = p.scale * sacc[kb][v];
         if (j >= S) s = -INFINITY;  // key does not exist
-        else if (p.causal ? (j > qi) : (mk[kb][v] != 0)) s = p.fill;
+        else if (p.causal ? (j > qi) : masked) s = p.fill;
         sv[kb][v] = s;
         tmax = fmaxf(tmax, s);
       }
@@ -730,11 +742,11 @@ __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_q16(AttnP p) {
                                                           0, 0);
   }
 
-  // oacc[db] register v: dim 16db + 4g + v of query r.
+  // oacc[db] register v: dim 16g + 4v + db of query r.
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) obuf[wave][r][16 * db + 4 * g + v] = oacc[db][v];
+  for (int v = 0; v < 4; ++v)
+    *reinterpret_cast<floatx4*>(&obuf[wave][r][16 * g + 4 * v]) =
+        floatx4{oacc[0][v], oacc[1][v], oacc[2][v], oacc[3][v]};
   if (g == 0) {
     sm[wave][r] = m_run;
     sl[wave][r] = l_run;
@@ -827,7 +839,10 @@ void attention(inferc_hip_ctx* ctx, const AttnArgs& a) {
     if (blocks4 < ctx->num_cus && vec) {
       // few blocks: 16 queries per block, four waves splitting the key tiles
       dim3 grid(unsigned(ceil_div(a.S, 16)), unsigned(p.nH), unsigned(a.B));
-      hipLaunchKernelGGL(attn_fwd_d64_q16<4>, grid, dim3(256), 0, ctx->stream, p);
+      if (p.mask != nullptr && !p.causal && p.ms2 == 0)
+        hipLaunchKernelGGL((attn_fwd_d64_q16<4, true>), grid, dim3(256), 0, ctx->stream, p);
+      else
+        hipLaunchKernelGGL((attn_fwd_d64_q16<4, false>), grid, dim3(256), 0, ctx->stream, p);
     } else if (blocks4 >= ctx->num_cus && a.S <= 4 * kKT &&
                (p.mask == nullptr || p.causal || p.ms2 == 0)) {
       // short sequences: the whole K/V of a (batch, head) staged at once
