@@ -29,7 +29,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 64;     // head_dim of the MFMA kernel
 constexpr int kKT = 32;    // keys per tile
-constexpr int kKS = kD + 1;  // LDS row stride of K (odd: conflict-free column reads)
+constexpr int kKS = kD + 4;  // LDS row stride of K (float4 rows; 16 rows span all banks)
 constexpr int kVS = kD + 4;  // LDS row stride of V (float4-aligned rows)
 
 struct AttnP {
@@ -107,10 +107,14 @@ __device__ __forceinline__ void attn_tile(const AttnP& p, const float* __restric
   floatx16 sacc;
 #pragma unroll
   for (int v = 0; v < 16; ++v) sacc[v] = 0.0f;
+  // steps 4j..4j+3 take dims qk_dim(4j + e, half) = 8j + 4 half + e: one
+  // float4 of the lane's key row per four steps
 #pragma unroll
-  for (int s = 0; s < kD / 2; ++s) {
-    const float a = ks[l32 * kKS + qk_dim(s, half)];
-    sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, qf[s], sacc, 0, 0, 0);
+  for (int j = 0; j < kD / 8; ++j) {
+    const floatx4 a = *reinterpret_cast<const floatx4*>(ks + l32 * kKS + 8 * j + 4 * half);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qf[4 * j + e], sacc, 0, 0, 0);
   }
   // sacc[v]: key k0 + 8*(v/4) + 4*half + v%4, query qi.
   float sv[16];
@@ -320,8 +324,7 @@ __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) 
     for (int i = 0; i < NV; ++i) {
       const int idx = tid + NT * i;
       const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
-      float* ks = &Ks[buf][key * kKS + dq];
-      ks[0] = kr[i][0]; ks[1] = kr[i][1]; ks[2] = kr[i][2]; ks[3] = kr[i][3];
+      *reinterpret_cast<floatx4*>(&Ks[buf][key * kKS + dq]) = kr[i];
       *reinterpret_cast<floatx4*>(&Vs[buf][key * kVS + dq]) = vr[i];
     }
   };
@@ -436,8 +439,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attn_fwd_d64_full(AttnP p) {
     for (int i = 0; i < NV; ++i) {
       const int idx = tid + NT * i;
       const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
-      float* ks = &Ks[t][key * kKS + dq];
-      ks[0] = kr[t][i][0]; ks[1] = kr[t][i][1]; ks[2] = kr[t][i][2]; ks[3] = kr[t][i][3];
+      *reinterpret_cast<floatx4*>(&Ks[t][key * kKS + dq]) = kr[t][i];
       *reinterpret_cast<floatx4*>(&Vs[t][key * kVS + dq]) = vr[t][i];
     }
   int64_t key_end = S;
@@ -565,8 +567,7 @@ __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_ks(AttnP p) {
     for (int i = 0; i < 8; ++i) {
       const int idx = lane + 64 * i;
       const int key = idx / (kD / 4), dq = (idx % (kD / 4)) * 4;
-      float* kd = ks + key * kKS + dq;
-      kd[0] = kr[i].x; kd[1] = kr[i].y; kd[2] = kr[i].z; kd[3] = kr[i].w;
+      *reinterpret_cast<float4*>(ks + key * kKS + dq) = kr[i];
       *reinterpret_cast<float4*>(vs + key * kVS + dq) = vr[i];
     }
     wave_lds_barrier();  // this tile is visible to every lane of the wave
