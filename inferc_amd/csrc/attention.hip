@@ -96,8 +96,9 @@ __device__ __forceinline__ void q_rows_to_operand(float* qs, const floatx4 (&qr)
 // One 32-key tile for a wave's 32 queries: S^T = K Q^T on the matrix cores,
 // scale, mask, online-softmax update, then O^T += V^T P^T. BITS: the mask
 // comes as mbits (bit v: score register v's key is masked, loaded ahead by
-// the caller); otherwise it is read here from mbase.
-template <bool BITS = false>
+// the caller; KEYBITS: bit o: key k0 + o is masked); otherwise it is read
+// here from mbase.
+template <bool BITS = false, bool KEYBITS = false>
 __device__ __forceinline__ void attn_tile(const AttnP& p, const float* __restrict__ ks,
                                           const float* __restrict__ vs, int64_t k0, int64_t qi,
                                           const uint8_t* mbase, const float (&qf)[kD / 2],
@@ -128,7 +129,8 @@ __device__ __forceinline__ void attn_tile(const AttnP& p, const float* __restric
     } else if (p.causal) {
       if (j > qi) s = p.fill;
     } else if (BITS) {
-      if ((mbits >> v) & 1u) s = p.fill;
+      const int bit = KEYBITS ? 8 * (v >> 2) + 4 * half + (v & 3) : v;
+      if ((mbits >> bit) & 1u) s = p.fill;
     } else if (mbase && qi < S) {
       if (mbase[qi * p.ms2 + j * p.ms3]) s = p.fill;
     }
@@ -221,9 +223,12 @@ __device__ __forceinline__ void o_rows_store(const AttnP& p, int64_t b, int64_t 
 // (keys clamped into the sequence; a clamped key's score is -inf and its V
 // row weighs 0), so the waits before the LDS writes count them exactly.
 // VEC: 16-byte aligned rows (float4 loads). MASKED: a mask that is neither
-// absent nor replaced by the causal rule.
-template <int WAVES, bool VEC, bool MASKED>
+// absent nor replaced by the causal rule. MROW: a masked row that is the same
+// for every query (ms2 == 0): a tile's 32 mask bytes are one load per lane
+// (key k0 + lane % 32), shared by a ballot, instead of 16 per lane.
+template <int WAVES, bool VEC, bool MASKED, bool MROW = false>
 __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) {
+  static_assert(MASKED || !MROW, "MROW is a kind of mask");
   constexpr int NT = 64 * WAVES;
   // K and V tiles (double-buffered). With VEC the same LDS also holds each
   // wave's Q rows before the first tile and its output rows after the last.
@@ -293,6 +298,7 @@ __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) 
   // private-memory copy
   floatx4 kr[NV], vr[NV];
   uint32_t mnext = 0;  // the next tile's mask bits (bit v: score register v)
+  uint8_t mown = 0;    // MROW: the next tile's mask byte of key k0 + lane % 32
   const uint8_t* mrow = MASKED ? mbase + qc * p.ms2 : nullptr;
   auto load_tile = [&](int64_t k0) {
 #pragma unroll
@@ -310,7 +316,10 @@ __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) 
         vr[i] = floatx4{vp[0], vp[1], vp[2], vp[3]};
       }
     }
-    if (MASKED) {
+    if (MROW) {
+      const int64_t j = k0 + l32;
+      mown = mrow[(j < S ? j : S - 1) * p.ms3];
+    } else if (MASKED) {
       mnext = 0;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -318,6 +327,11 @@ __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) 
         mnext |= uint32_t(mrow[(j < S ? j : S - 1) * p.ms3] != 0) << v;
       }
     }
+  };
+  // the loaded tile's mask bits (MROW: bit o for key k0 + o, from lanes 0..31)
+  auto tile_bits = [&]() -> uint32_t {
+    if constexpr (MROW) return uint32_t(__ballot(mown != 0));
+    else return mnext;
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
@@ -335,7 +349,7 @@ __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) 
     __syncthreads();  // every wave has its Q before tile 0 overwrites the slices
   }
   store_tile(0);
-  uint32_t mbits = mnext;
+  uint32_t mbits = tile_bits();
   __syncthreads();
 
   for (int64_t t = 0; t < ntiles; ++t) {
@@ -348,10 +362,10 @@ __global__ __launch_bounds__(64 * WAVES, 12 / WAVES) void attn_fwd_d64(AttnP p) 
     // (causal), as does a wave past the end of the sequence.
     const bool skip = (q0 >= S) || (p.causal && k0 > q0 + 31);
     if (!skip)
-      attn_tile<MASKED>(p, Ks[cur], Vs[cur], k0, qi, nullptr, qf, oacc, m_run, l_run, half, l32,
-                        mbits);
+      attn_tile<MASKED, MROW>(p, Ks[cur], Vs[cur], k0, qi, nullptr, qf, oacc, m_run, l_run, half,
+                              l32, mbits);
     store_tile(cur ^ 1);
-    mbits = mnext;
+    mbits = tile_bits();
     __syncthreads();
   }
   // (the loop's last barrier: no wave reads the K/V tiles any more)
@@ -861,11 +875,14 @@ void attention(inferc_hip_ctx* ctx, const AttnArgs& a) {
       const bool masked = p.mask != nullptr && !p.causal;
       dim3 grid(unsigned(ceil_div(a.S, 128)), unsigned(p.nH), unsigned(a.B));
       auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, ctx->stream, p); };
+      const bool mrow = masked && p.ms2 == 0;
       if (vec) {
-        if (masked) go(attn_fwd_d64<4, true, true>);
+        if (mrow) go(attn_fwd_d64<4, true, true, true>);
+        else if (masked) go(attn_fwd_d64<4, true, true>);
         else go(attn_fwd_d64<4, true, false>);
       } else {
-        if (masked) go(attn_fwd_d64<4, false, true>);
+        if (mrow) go(attn_fwd_d64<4, false, true, true>);
+        else if (masked) go(attn_fwd_d64<4, false, true>);
         else go(attn_fwd_d64<4, false, false>);
       }
     } else {
