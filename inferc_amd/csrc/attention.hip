@@ -489,14 +489,10 @@ __global__ __launch_bounds__(64 * WAVES, 2) void attn_fwd_d64_full(AttnP p) {
     for (int t = 0; t < ntiles; ++t) {
       const int64_t k0 = int64_t(t) * kKT;
       if (p.causal && k0 > q0 + 31) break;  // later tiles are masked for all 32 queries
-      uint32_t mbits = 0;
-      if (MASK_ROW) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-          mbits |= uint32_t(s_mask[k0 + 8 * (v >> 2) + 4 * half + (v & 3)] != 0) << v;
-      }
-      attn_tile<MASK_ROW>(p, Ks[t], Vs[t], k0, qi, nullptr, qf, oacc, m_run, l_run, half, l32,
-                          mbits);
+      // bit o: key k0 + o is masked (one LDS byte per lane, shared by a ballot)
+      const uint32_t mbits = MASK_ROW ? uint32_t(__ballot(s_mask[k0 + l32] != 0)) : 0u;
+      attn_tile<MASK_ROW, true>(p, Ks[t], Vs[t], k0, qi, nullptr, qf, oacc, m_run, l_run, half,
+                                l32, mbits);
     }
   }
   if constexpr (VEC) {
