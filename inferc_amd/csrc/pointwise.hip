@@ -24,7 +24,63 @@ constexpr int kBlock = 256;
 // ids set: row r of x is row ids[r] of a [vocab, feat] table (an embedding
 // Gather folded in, embedding.cc:9-72): negative ids wrap, and an id out of
 // range raises the error flag (the table's first row stands in).
-template <int VPL>
+typedef float lnf4 __attribute__((ext_vector_type(4)));
+
+// ln_row with float4 access (feat % 4 == 0, feat <= 256 * V4, every row and
+// gamma/beta 16-byte aligned): lane holds features 4(lane + 64j) .. +3, so
+// each load moves 1 KB per wave instead of 256 bytes. Loads are unconditional
+// (a lane past the row reads chunk 0 and drops it).
+template <int V4>
+__device__ __forceinline__ void ln_row4(int lane, const float* __restrict__ xr,
+                                        const float* __restrict__ rr, const float* __restrict__ g,
+                                        const float* __restrict__ b, int64_t feat, float eps,
+                                        float* __restrict__ yr) {
+  const float inv_n = 1.0f / float(feat);
+  const int64_t n4 = feat / 4;
+  const lnf4* x4 = reinterpret_cast<const lnf4*>(xr);
+  const lnf4* r4 = reinterpret_cast<const lnf4*>(rr);
+  const lnf4* g4 = reinterpret_cast<const lnf4*>(g);
+  const lnf4* b4 = reinterpret_cast<const lnf4*>(b);
+  lnf4 v[V4], gv[V4], bv[V4], rv[V4];
+#pragma unroll
+  for (int j = 0; j < V4; ++j) {
+    const int64_t c = lane + 64 * j;
+    const int64_t cc = c < n4 ? c : 0;
+    v[j] = x4[cc];
+    rv[j] = rr ? r4[cc] : lnf4{0.f, 0.f, 0.f, 0.f};
+    gv[j] = g4[cc];
+    bv[j] = b4[cc];
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < V4; ++j) {
+    const bool in = lane + 64 * j < n4;
+    if (rr) v[j] = v[j] + rv[j];
+    v[j] = in ? v[j] : lnf4{0.f, 0.f, 0.f, 0.f};
+    s += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+  }
+  const float mean = wave_sum_dpp(s) * inv_n;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < V4; ++j) {
+    const bool in = lane + 64 * j < n4;
+    lnf4 d = v[j] - mean;
+    d = in ? d : lnf4{0.f, 0.f, 0.f, 0.f};
+    v[j] = d;
+    q += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
+  }
+  const float inv = 1.0f / sqrtf(wave_sum_dpp(q) * inv_n + eps);
+  lnf4* y4 = reinterpret_cast<lnf4*>(yr);
+#pragma unroll
+  for (int j = 0; j < V4; ++j) {
+    const int64_t c = lane + 64 * j;
+    if (c < n4) y4[c] = (v[j] * inv) * gv[j] + bv[j];
+  }
+}
+
+// VPL: values per lane of the scalar row routine; V4 > 0: the float4 routine
+// with V4 chunks per lane.
+template <int VPL, int V4>
 __global__ __launch_bounds__(kBlock) void layernorm_kernel(int64_t rows, int64_t feat,
                                                            const float* __restrict__ x,
                                                            const float* __restrict__ res,
@@ -51,8 +107,12 @@ __global__ __launch_bounds__(kBlock) void layernorm_kernel(int64_t rows, int64_t
       xr = 0;
     }
   }
-  ln_row<VPL>(lane, x + xr * feat, res ? res + (row % res_rows) * feat : nullptr, g, b, feat,
-              eps, y + row * feat);
+  if constexpr (V4 > 0)
+    ln_row4<V4>(lane, x + xr * feat, res ? res + (row % res_rows) * feat : nullptr, g, b, feat,
+                eps, y + row * feat);
+  else
+    ln_row<VPL>(lane, x + xr * feat, res ? res + (row % res_rows) * feat : nullptr, g, b, feat,
+                eps, y + row * feat);
 }
 
 __global__ __launch_bounds__(kBlock) void activation_kernel(int64_t n, const float* __restrict__ x,
@@ -229,12 +289,16 @@ void launch_layernorm(inferc_hip_ctx* ctx, int64_t rows, int64_t feat, const flo
   IH_REQUIRE(x && gamma && beta && y, INFERC_ERR_ARG, "layernorm: null pointer");
   const unsigned blocks = unsigned(ceil_div(rows, kBlock / 64));
   const int64_t rr = residual ? res_rows : int64_t(1);
-  if (feat <= 64 * 4)
-    hipLaunchKernelGGL(layernorm_kernel<4>, dim3(blocks), dim3(kBlock), 0, ctx->stream, rows,
-                       feat, x, residual, gamma, beta, eps, y, rr, ids, vocab, err, side);
-  else
-    hipLaunchKernelGGL(layernorm_kernel<16>, dim3(blocks), dim3(kBlock), 0, ctx->stream, rows,
-                       feat, x, residual, gamma, beta, eps, y, rr, ids, vocab, err, side);
+  const bool vec4 = feat % 4 == 0 && feat <= 256 * 4 && aligned16(x) && aligned16(gamma) &&
+                    aligned16(beta) && aligned16(y) && (residual == nullptr || aligned16(residual));
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kBlock), 0, ctx->stream, rows, feat, x, residual,
+                       gamma, beta, eps, y, rr, ids, vocab, err, side);
+  };
+  if (vec4 && feat <= 256 * 3) go(layernorm_kernel<16, 3>);
+  else if (vec4) go(layernorm_kernel<16, 4>);
+  else if (feat <= 64 * 4) go(layernorm_kernel<4, 0>);
+  else go(layernorm_kernel<16, 0>);
   check_launch("layernorm");
 }
 }  // namespace
