@@ -181,6 +181,23 @@ def test_gemm_c_kinds_alpha_beta(ctx):
         close(got, O.gemm(A, B, C, alpha=0.75, beta=-2.0))
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 768, 3072), (100, 768, 2048), (160, 768, 3072),
+                                   (256, 768, 4096), (128, 768, 2000)])
+@pytest.mark.parametrize("act", [L.ACT_NONE, L.ACT_GELU_ERF])
+def test_gemm_small_m_long_k(ctx, M, N, K, act):
+    """Small-M products with a long K (the b=1 FFN-down and its neighbours:
+    ragged M, K not a multiple of the waves' ring) with bias, residual and
+    activation, against float64, deterministic over repeats."""
+    A, B = rnd((M, K), 21 + M), rnd((K, N), 22 + K, 0.03)
+    bias, res = rnd(N, 23), rnd((M, N), 24)
+    a, b, c, r = T(ctx, A), T(ctx, B), T(ctx, bias), T(ctx, res)
+    got = rt.Gemm(a, b, c, 1.0, 1.0, residual=r, act=act).numpy()
+    v = (A.astype(np.float64) @ B + bias) + res
+    close(got, ref64.gelu_erf(v) if act == L.ACT_GELU_ERF else v)
+    for _ in range(2):
+        np.testing.assert_array_equal(rt.Gemm(a, b, c, 1.0, 1.0, residual=r, act=act).numpy(), got)
+
+
 def test_gemm_deterministic(ctx):
     A, B = rnd((128, 768), 9), rnd((768, 3072), 10, 0.02)
     a, b = T(ctx, A), T(ctx, B)
