@@ -218,7 +218,7 @@ __device__ __forceinline__ void o_rows_store(const AttnP& p, int64_t b, int64_t 
 }
 
 // Large grids: WAVES waves of 32 queries share each K/V tile, staged through
-// LDS (double-buffered). The loads of tile t+1, the lane's 16 mask bytes
+// LDS (double-buffered). The loads of tile t+1, the lane's mask bytes
 // included, are issued before tile t's matrix-core work and are unconditional
 // (keys clamped into the sequence; a clamped key's score is -inf and its V
 // row weighs 0), so the waits before the LDS writes count them exactly.
