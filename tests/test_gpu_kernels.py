@@ -258,6 +258,27 @@ def test_attention_general_mask_and_generic_head_dim(ctx):
         close(got, O.fused_attention(q, k, v, m4, hd, -1e30))
 
 
+@pytest.mark.parametrize("shape", [(1, 1, 70, 70), (2, 2, 70, 70), (2, 1, 1, 70)])
+def test_attention_small_grid_masks_head_dim_64(ctx, shape):
+    """Small grids (the 16-query kernel) at head_dim 64 with a per-query mask
+    ([B or 1, nH or 1, S, S]: one mask byte per score) and a key-only mask
+    ([B, 1, 1, S]: one byte per key, shared across the wave by a ballot),
+    S = 70 (a ragged last key tile and query block), a few rows fully
+    masked, against the oracle."""
+    B, S, H, hd = 2, 70, 128, 64
+    rng = np.random.default_rng(37)
+    q, k, v = rnd((B, S, H), 38), rnd((B, S, H), 39), rnd((B, S, H), 40)
+    m = (rng.random(shape) < 0.3).astype(np.uint8)
+    if shape[2] == S:
+        m[..., 5, :] = 1             # a fully masked query row
+    else:
+        m[..., 60:] = 1              # a masked tail of keys
+    fill = graphs.FILL_MIN
+    got = rt.FusedAttention(T(ctx, q), T(ctx, k), T(ctx, v), T(ctx, m, np.uint8), hd,
+                            fill).numpy()
+    close(got, O.fused_attention(q, k, v, m, hd, fill))
+
+
 @pytest.mark.parametrize("S", [128, 512])
 def test_config3_qkv_plus_mha(ctx, S):
     """fused QKV projection + MHA, B=32, valid length U[16,S]."""
