@@ -188,6 +188,15 @@ __device__ __forceinline__ void gemv2_x(const Gemv2P& p, int lane, float4 (&xv)[
   }
 }
 
+// A weight chunk, streamed once per call: a nontemporal load (the `nt`
+// cache policy) that does not displace reusable lines.
+__device__ __forceinline__ float4 w_load_nt(const float* p) {
+  typedef float v4 __attribute__((ext_vector_type(4)));
+  const v4 v = __builtin_nontemporal_load(
+      reinterpret_cast<const __attribute__((address_space(1))) v4*>(reinterpret_cast<uintptr_t>(p)));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
 template <int R, int KV, int XSRC, bool ARGMAX>
 // W, x and N lead the arguments, so the first loads wait on no scalar load of
 // the argument block (leading arguments arrive in SGPRs); every other operand
@@ -204,7 +213,7 @@ __global__ __launch_bounds__(kBlock) void gemv2_kernel(const float* __restrict__
     const int64_t rc = r0 + i < N ? r0 + i : N - 1;  // rows past N: clamped, never stored
 #pragma unroll
     for (int j = 0; j < KV; ++j)
-      w[i][j] = *reinterpret_cast<const float4*>(W + rc * K + 4 * lane + 256 * j);
+      w[i][j] = w_load_nt(W + rc * K + 4 * lane + 256 * j);
   }
   float4 xv[KV], lg[KV], lb[KV];
   gemv2_x_load<KV, XSRC>(p, x, lane, xv, lg, lb);
