@@ -304,6 +304,102 @@ def roofline_kernel(ctx, reps: int = 400):
             "avg_launch_us": round(ms * 1e3, 3)}
 
 
+def _chain_us(ctx, launches) -> float:
+    """Per-launch time of a captured chain of dependent launches (stream
+    order), from back-to-back replays timed with HIP events."""
+    for f in launches:
+        f()
+    ctx.sync()
+    cap = ctx.capture(lambda: [f() for f in launches])
+    for _ in range(3):
+        cap.replay()
+    ms = time_replays(ctx, cap, len(launches), 20 * len(launches))
+    cap.close()
+    return round(ms * 1e3, 3)
+
+
+def launch_floors(ctx) -> dict:
+    """What one dependent launch of the batch-1 decode step costs, by kind.
+
+    Each figure is the per-launch time of a captured chain of the same launch
+    (a graph replay, as the decode step runs):
+      - floor: a 4-row GEMV (one block), the cost of a dependent launch;
+      - the decode step's GEMV shapes through inferc_hip_gemv_f32 (plain: no
+        LayerNorm prologue, bias or residual), warm (one matrix, cache
+        resident) and cold (distinct matrices, together past the 256 MB
+        Infinity Cache, so every launch streams from HBM);
+      - decode attention (12 heads of 64, 12 layers' caches) at several key
+        counts t, through inferc_hip_kv_append_attend_f32.
+    `step_model_ms` sums one layer's cold launches (attention at the run's
+    mean t) over 12 layers plus the LM head and one floor launch for the
+    step's tail, to set beside the measured ms/token."""
+    lib = ctx._lib
+    rng = np.random.default_rng(7)
+    out = {}
+    x = rt_tensor(ctx, rng.standard_normal(3072, dtype=np.float32))
+    y = ctx.malloc(4 * 50304)
+
+    def gemv(N, K, w):
+        return lambda: check_rc(lib, lib.inferc_hip_gemv_f32(
+            ctx.handle, N, K, w, x.ptr, None, None, 0.0, None, None, 0, y))
+
+    src = rt_tensor(ctx, (rng.standard_normal((3072, 3072), dtype=np.float32) * 0.02))
+    out["floor_us"] = _chain_us(ctx, [gemv(4, 768, src.ptr)] * 60)
+    shapes = {"qkv": (2304, 768), "out_proj": (768, 768), "ffn_up": (3072, 768),
+              "ffn_down": (768, 3072), "lm_head": (50257, 768)}
+    for name, (N, K) in shapes.items():
+        nbytes = 4 * N * K
+        n_cold = max(4, -(-600_000_000 // nbytes))
+        mats = []
+        for _ in range(n_cold):
+            p = ctx.malloc(nbytes)
+            for off in range(0, nbytes, src.nbytes):
+                check_rc(lib, lib.inferc_hip_d2d(ctx.handle, p + off, src.ptr,
+                                                 min(src.nbytes, nbytes - off)))
+            mats.append(p)
+        warm = _chain_us(ctx, [gemv(N, K, mats[0])] * min(n_cold, 60))
+        cold = _chain_us(ctx, [gemv(N, K, p) for p in mats])
+        for p in mats:
+            ctx.free(p)
+        out[name] = {"warm_us": warm, "cold_us": cold, "mb": round(nbytes / 1e6, 2),
+                     "cold_hbm_gbps": round(nbytes / (cold * 1e-6) / 1e9, 1)}
+    nH, D, T = 12, 64, 160
+    caches = [(rt_tensor(ctx, rng.standard_normal((nH, T, D), dtype=np.float32)),
+               rt_tensor(ctx, rng.standard_normal((nH, T, D), dtype=np.float32)))
+              for _ in range(12)]
+    qkv = rt_tensor(ctx, rng.standard_normal(3 * nH * D, dtype=np.float32))
+    att = ctx.malloc(4 * nH * D)
+    out["attention_us"] = {}
+    for t in (1, 33, 96, 160):
+        pos = rt_tensor(ctx, np.array([t - 1], np.int64))
+
+        def attn(kc, vc, pos=pos):
+            return lambda: check_rc(lib, lib.inferc_hip_kv_append_attend_f32(
+                ctx.handle, nH, D, T, pos.ptr, qkv.ptr, qkv.ptr + 4 * nH * D,
+                qkv.ptr + 8 * nH * D, kc.ptr, vc.ptr, att))
+        out["attention_us"][str(t)] = _chain_us(ctx, [attn(kc, vc) for kc, vc in caches] * 5)
+    ctx.free(att)
+    ctx.free(y)
+    a = out["attention_us"]
+    attn_mean = (a["33"] + a["160"]) / 2.0  # the bench run's keys go 33 .. 160
+    layer = sum(out[k]["cold_us"] for k in ("qkv", "out_proj", "ffn_up", "ffn_down")) + attn_mean
+    out["step_model_ms"] = round((12 * layer + out["lm_head"]["cold_us"] + out["floor_us"]) / 1e3, 4)
+    out["step_launches"] = 62
+    out["launch_floor_ms"] = round(62 * out["floor_us"] / 1e3, 4)
+    return out
+
+
+def rt_tensor(ctx, arr):
+    from inferc_amd import rt
+    return rt.Tensor.from_numpy(ctx, arr)
+
+
+def check_rc(lib, rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(f"inferc_hip call failed ({rc}): "
+                           f"{lib.inferc_hip_last_error().decode(errors='replace')}")
+
+
 COUNTER_PARTS = ("encoder", "roofline", "int4", "decode")
 
 
@@ -639,6 +735,9 @@ def main(argv=None) -> int:
     ap.add_argument("--decode-only", nargs="?", const="both", choices=["fp32", "int4", "both"],
                     help="GPT-2 decode only (fp32 weights, int4 weights or both), one "
                          "generate each, printed as text (for rocprofv3 --kernel-trace runs)")
+    ap.add_argument("--floors", action="store_true",
+                    help="per-launch cost of dependent launch chains (launch floor, decode "
+                         "GEMV shapes warm and cold, decode attention by key count), as JSON")
     ap.add_argument("--profile-dir", default=None,
                     help="also write per-op profiles (reference JSON schema) to this folder")
     args = ap.parse_args(argv)
@@ -656,6 +755,10 @@ def main(argv=None) -> int:
     if args.counters is not None:
         print(json.dumps(counters_workload(ctx, tuple(args.counters) or COUNTER_PARTS)),
               flush=True)
+        ctx.close()
+        return 0
+    if args.floors:
+        print(json.dumps(launch_floors(ctx)), flush=True)
         ctx.close()
         return 0
     if args.roofline_only:
