@@ -15,6 +15,7 @@
 // exp(s - max) and accumulates sum_j e_j V[j] with lanes over dh (coalesced
 // rows of V), and the result is scaled by 1/sum at the end. Masked scores
 // take `fill` as in FusedAttention (src/kernels/attention.cc:77-91).
+// head_dim 64 (GPT-2) takes cache_attn_d64_kernel below.
 #include "common.h"
 #include "ew.h"
 
@@ -97,6 +98,107 @@ __global__ __launch_bounds__(64 * kCaWaves) void cache_attn_kernel(CacheAttnArgs
   }
 }
 
+// The same attention for head_dim 64: one block of 8 waves per (batch,
+// head, query row). Wave w takes key chunks w, w+8, ... of 32 keys; in a
+// chunk lane pair (2c, 2c+1) holds key c, each lane half of its 64 dims as
+// eight float4, so a key row is one coalesced 256-byte read and a chunk's
+// K and V loads (indices past the last key clamped to it, their weights
+// zero) all go out before any is used. Per chunk: the scores (a masked key
+// scores `fill`), their maximum m, e_j = exp(s_j - m), l = sum e_j and
+// O = sum e_j v_j over the wave's 64 dims, merged online within the wave and
+// across the eight waves through LDS in wave order; out = O / L.
+constexpr int kCa64Waves = 8;
+constexpr int kCa64Chunk = 32;
+
+__global__ __launch_bounds__(64 * kCa64Waves) void cache_attn_d64_kernel(CacheAttnArgs p,
+                                                                        float scale) {
+  constexpr int D = 64;
+  __shared__ float sm[kCa64Waves], sl[kCa64Waves];
+  __shared__ float so[kCa64Waves][D];
+  __shared__ __align__(16) float se[kCa64Waves][kCa64Chunk];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r = blockIdx.x;  // (b, h, i), i fastest
+  const int64_t i = r % p.S, h = (r / p.S) % p.nH, b = r / (p.S * p.nH);
+  const int64_t T = p.T;
+  const float* kbase = p.kc + (b * p.nH + h) * p.max_t * D;
+  const float* vbase = p.vc + (b * p.nH + h) * p.max_t * D;
+  const uint8_t* mrow = p.mask ? p.mask + b * p.ms[0] + h * p.ms[1] + i * p.ms[2] : nullptr;
+  const int dh = (lane & 1) * 32;
+  const float* qrow = p.q + (b * p.S + i) * p.ldq + h * D;
+  float4 qv[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) qv[k] = *reinterpret_cast<const float4*>(qrow + dh + 4 * k);
+  float M = -INFINITY, L = 0.0f, O = 0.0f;
+  for (int64_t j0 = int64_t(wave) * kCa64Chunk; j0 < T; j0 += kCa64Waves * kCa64Chunk) {
+    const int64_t jl = j0 + (lane >> 1);
+    const int64_t jc = jl < T ? jl : T - 1;
+    const float* kr = kbase + jc * D;
+    float4 kv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) kv[k] = *reinterpret_cast<const float4*>(kr + dh + 4 * k);
+    float vv[kCa64Chunk];
+#pragma unroll
+    for (int k = 0; k < kCa64Chunk; ++k) {
+      const int64_t jv = j0 + k < T ? j0 + k : T - 1;
+      vv[k] = vbase[jv * D + lane];
+    }
+    const bool masked = mrow != nullptr && mrow[jc * p.ms[3]] != 0;
+    float dot = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      dot += qv[k].x * kv[k].x + qv[k].y * kv[k].y + qv[k].z * kv[k].z + qv[k].w * kv[k].w;
+    dot += dpp_pair_swap(dot);
+    const float s = jl < T ? (masked ? p.fill : dot * scale) : -INFINITY;
+    const float m = wave_max_dpp(s);
+    const float e = jl < T ? expf(s - m) : 0.0f;
+    const float l = wave_sum_dpp((lane & 1) ? 0.0f : e);
+    // e_k of the chunk's keys through the wave's own LDS slot (one write,
+    // eight broadcast reads); the wave-scope fences order the slot's reuse
+    if (!(lane & 1)) se[wave][lane >> 1] = e;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float o = 0.0f;
+#pragma unroll
+    for (int k4 = 0; k4 < kCa64Chunk / 4; ++k4) {
+      const float4 e4 = *reinterpret_cast<const float4*>(&se[wave][4 * k4]);
+      o += e4.x * vv[4 * k4];
+      o += e4.y * vv[4 * k4 + 1];
+      o += e4.z * vv[4 * k4 + 2];
+      o += e4.w * vv[4 * k4 + 3];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // a chunk whose every score is -inf (fill = -inf) leaves the state as
+    // it was (its e are NaN, wave-uniformly)
+    if (m != -INFINITY) {
+      const float Mn = fmaxf(M, m);
+      const float a = expf(M - Mn), c = expf(m - Mn);
+      L = L * a + l * c;
+      O = O * a + o * c;
+      M = Mn;
+    }
+  }
+  if (lane == 0) {
+    sm[wave] = M;
+    sl[wave] = L;
+  }
+  so[wave][lane] = O;
+  __syncthreads();
+  if (wave == 0) {
+    float Mx = sm[0];
+    for (int w = 1; w < kCa64Waves; ++w) Mx = fmaxf(Mx, sm[w]);
+    float Lt = 0.0f, Ot = 0.0f;
+    for (int w = 0; w < kCa64Waves; ++w) {
+      const float c = expf(sm[w] - Mx);  // a wave without keys: sm = -inf, weight 0
+      Lt += c * sl[w];
+      Ot += c * so[w][lane];
+    }
+    p.out[(b * p.S + i) * p.ldo + h * D + lane] = Ot / Lt;
+  }
+}
+
 // cache[b, h, t0 + s, :] = src[b, s, h*dh : (h+1)*dh] (token-major rows).
 __global__ __launch_bounds__(256) void cache_write_tokens_kernel(int64_t B, int64_t S, int64_t nH,
                                                                  int64_t dh, int64_t max_t,
@@ -124,6 +226,14 @@ void cache_attention(inferc_hip_ctx* ctx, const CacheAttnArgs& a) {
   const int64_t rows = a.B * a.nH * a.S;
   if (rows == 0) return;
   const float scale = 1.0f / sqrtf(float(a.dh));
+  auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  if (a.dh == 64 && a.ldq % 4 == 0 && al16(a.q) && al16(a.kc) && al16(a.vc) &&
+      rows < (int64_t(1) << 31)) {
+    hipLaunchKernelGGL(cache_attn_d64_kernel, dim3(unsigned(rows)), dim3(64 * kCa64Waves), 0,
+                       ctx->stream, a, scale);
+    check_launch("cache attention");
+    return;
+  }
   hipLaunchKernelGGL(cache_attn_kernel, dim3(unsigned(ceil_div(rows, kCaWaves))),
                      dim3(64 * kCaWaves), 0, ctx->stream, a, scale);
   check_launch("cache attention");

@@ -118,9 +118,14 @@ struct inferc_executor {
     ih::Value v;
     bool from_host = false;
     std::vector<uint8_t> staged;  // host bytes awaiting upload
+    size_t cap = 0;               // bytes of the device buffer of a host input
   };
   std::unordered_map<std::string, Input> inputs;
   std::unordered_map<std::string, ih::Value> vals;  // the "tape" of the last run
+  // Outputs of Constant nodes, computed by the first unprofiled run and kept:
+  // later runs skip those nodes (const_done[i] for node i).
+  std::unordered_map<std::string, ih::Value> consts;
+  std::vector<char> const_done;
   struct Buf {
     void* p = nullptr;
     size_t bytes = 0;
@@ -239,20 +244,40 @@ struct inferc_executor {
       return b.p;
     }
     IH_REQUIRE(!ctx->capturing, INFERC_ERR_STATE, "executor: allocation during graph capture");
+    // A buffer that has to grow (a tensor whose shape grows run by run, as
+    // the with-past decode's do by one position per step) grows by half
+    // again at least, so it is reallocated, with the stream drained, a few
+    // times rather than on every run.
+    size_t want = bytes;
     if (b.p) {
       IH_HIP(hipStreamSynchronize(ctx->stream));
       IH_HIP(hipFree(b.p));
       b.p = nullptr;
+      const size_t grown = b.bytes + b.bytes / 2;
+      want = ((grown > bytes ? grown : bytes) + 255) & ~size_t(255);
     }
-    IH_HIP(hipMalloc(&b.p, bytes > 0 ? bytes : 4));
-    b.bytes = bytes;
+    IH_HIP(hipMalloc(&b.p, want > 0 ? want : 4));
+    b.bytes = want;
     return b.p;
   }
 
-  const ih::Value& get(const std::string& name) const {
+  // A value by name: this run's tape, then the Constant outputs folded by an
+  // earlier run, then the initializers (which the tape does not copy).
+  const ih::Value* find_val(const std::string& name) const {
     auto it = vals.find(name);
-    if (it == vals.end()) ih::fail(INFERC_ERR_STATE, "Executor: missing tensor '" + name + "'");
-    return it->second;
+    if (it != vals.end()) return &it->second;
+    auto ic = consts.find(name);
+    if (ic != consts.end()) return &ic->second;
+    auto ii = inits.find(name);
+    return ii != inits.end() ? &ii->second : nullptr;
+  }
+  ih::Value* find_val(const std::string& name) {
+    return const_cast<ih::Value*>(static_cast<const inferc_executor*>(this)->find_val(name));
+  }
+  const ih::Value& get(const std::string& name) const {
+    const ih::Value* v = find_val(name);
+    if (!v) ih::fail(INFERC_ERR_STATE, "Executor: missing tensor '" + name + "'");
+    return *v;
   }
 
   // Device pointer of a value. Host-only values (shape math consumed by a
@@ -264,7 +289,9 @@ struct inferc_executor {
   };
   std::unordered_map<std::string, Upload> uploads;
   void* dev_of(const std::string& name) {
-    ih::Value& v = vals.at(name);
+    ih::Value* vp = find_val(name);
+    if (!vp) ih::fail(INFERC_ERR_STATE, "Executor: missing tensor '" + name + "'");
+    ih::Value& v = *vp;
     if (v.dev) return v.dev;
     IH_REQUIRE(v.host != nullptr, INFERC_ERR_STATE, "tensor '" + name + "' has no data");
     Upload& up = uploads[name];
@@ -283,6 +310,45 @@ struct inferc_executor {
                           ctx->stream));
     v.dev = up.p;
     return up.p;
+  }
+
+  // [N, K] copies of [K, N] weight initializers, for products with one row
+  // of A: as transB operands they take the GEMV route of gemm() (the M == 1
+  // sgemv of src/kernels/matmul.cc:207-216), whose rows are coalesced reads
+  // of W, instead of a tiled GEMM with 1 of its 16..128 rows live. Made on
+  // first use, outside any capture, and kept with the initializers.
+  std::unordered_map<std::string, float*> wt_cache;
+  const float* transposed_init(const std::string& name) {
+    auto it = wt_cache.find(name);
+    if (it != wt_cache.end()) return it->second;
+    if (dry || ctx->capturing) return nullptr;
+    auto ii = inits.find(name);
+    if (ii == inits.end() || !ii->second.host || ii->second.dtype != INFERC_DT_F32 ||
+        ii->second.shape.size() != 2 || ii->second.host->size() != ii->second.bytes())
+      return nullptr;
+    const int64_t K = ii->second.shape[0], N = ii->second.shape[1];
+    const float* src = reinterpret_cast<const float*>(ii->second.host->data());
+    std::vector<float> t(size_t(N) * size_t(K));
+    for (int64_t k = 0; k < K; ++k)
+      for (int64_t c = 0; c < N; ++c) t[size_t(c) * size_t(K) + size_t(k)] = src[k * N + c];
+    void* d = nullptr;
+    IH_HIP(hipMalloc(&d, t.size() * sizeof(float)));
+    init_allocs.push_back(d);
+    IH_HIP(hipMemcpy(d, t.data(), t.size() * sizeof(float), hipMemcpyHostToDevice));
+    return wt_cache[name] = static_cast<float*>(d);
+  }
+  // Points g at the transposed copy of its B when the product has one row,
+  // B is a [K, N] initializer and the GEMV route takes the result.
+  void batch1_route(ih::GemmArgs& g, const std::string& b_name) {
+    if (dry || g.M != 1 || g.batch != 1 || g.trans_a || g.trans_b || g.ldb != g.N) return;
+    ih::GemmArgs t = g;
+    t.trans_b = 1;
+    t.ldb = g.K;
+    if (!ih::gemm_gemv_route(t)) return;
+    const float* wt = transposed_init(b_name);
+    if (!wt) return;
+    t.B = wt;
+    g = t;
   }
 
   ih::Value& make_dev(const std::string& name, int dtype, std::vector<int64_t> shape) {
@@ -322,12 +388,12 @@ struct inferc_executor {
     if (out_numel > (int64_t(1) << 16)) return false;
     for (const auto& i : n.in) {
       if (i.empty()) continue;
-      auto it = vals.find(i);
-      if (it == vals.end() || !it->second.host) return false;
+      const ih::Value* v = find_val(i);
+      if (!v || !v->host) return false;
     }
     return true;
   }
-  const void* host_of(const std::string& name) const { return vals.at(name).host->data(); }
+  const void* host_of(const std::string& name) const { return get(name).host->data(); }
 
   void alias(const std::string& out, const ih::Value& in, std::vector<int64_t> shape) {
     ih::Value v = in;
@@ -928,6 +994,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       if (lnr) g.norm_r = rnr;
     }
     g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
+    if (!lna) batch1_route(g, n.in[1]);
     if (op == "FusedGemmEpilogue" && ln_reads.count(n.out[0])) {
       // the producer of a LayerNorm read by its readers: decide for this
       // run, and write the row statistics they combine
@@ -981,6 +1048,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     g.act = int(attr_int(n, "__act", INFERC_ACT_NONE));
     g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, {g.M, g.N}).dev);
     g.ldy = g.N;
+    batch1_route(g, n.in[1]);
     auto ln = n.attrs.find("__ln_g");
     if (ln != n.attrs.end() && !ln_gemm_off.count(n.in[0])) {
       // A's rows through the LayerNorm that preceded the Gather (peephole)
@@ -1861,7 +1929,7 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
 }
 
 void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
-  vals = inits;
+  vals.clear();
   dev_gather = false;
   ln_gemm_off.clear();
   pending_gather.clear();
@@ -1869,11 +1937,24 @@ void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
   cache_views.clear();
   for (auto& kv : inputs) vals[kv.first] = kv.second.v;
   const bool events = act != nullptr && !dry;
+  // A profiled run executes every node, so the tape (and the activation
+  // bytes it reports) is the same as without the folded constants.
+  const bool fold = act == nullptr;
+  const_done.resize(nodes.size(), 0);
   for (size_t i = 0; i < nodes.size(); ++i) {
     const inferc_graph::Node& n = nodes[i];
+    if (fold && const_done[i]) continue;
     if (events) IH_HIP(hipEventRecord(prof_ev[i], ctx->stream));
     try {
       exec_node(n);
+      if (fold && n.op == "Constant" && n.out.size() == 1) {
+        auto it = vals.find(n.out[0]);
+        if (it != vals.end() && it->second.host) {
+          consts[n.out[0]] = std::move(it->second);
+          vals.erase(it);
+          const_done[i] = 1;
+        }
+      }
     } catch (ih::Error& e) {
       e.msg += " [node '" + n.name + "', op " + n.op + "]";
       throw;
@@ -1953,7 +2034,7 @@ void inferc_executor::run() {
 void inferc_executor::materialize_gather(const std::string& name) {
   const PendingGather g = pending_gather.at(name);
   pending_gather.erase(name);
-  const std::vector<int64_t> shape = vals.at(name).shape;
+  const std::vector<int64_t> shape = get(name).shape;
   float* y = static_cast<float*>(make_dev(name, INFERC_DT_F32, shape).dev);
   if (!dry) {
     ih::gather_axis(ctx, 1, g.vocab, g.feat, g.table, g.ids, g.n, y, gather_err);
@@ -2299,13 +2380,19 @@ int inferc_executor_set_input(inferc_executor* ex, const char* name, int dtype, 
     IH_REQUIRE(bytes == 0 || host_data != nullptr, INFERC_ERR_ARG, "null input data");
     if (ex->dry) {
       in.v.dev = ex->fake_ptr(bytes);
-    } else if (!in.from_host || in.v.bytes() != bytes) {
+    } else if (!in.from_host || bytes > in.cap) {
+      // an input that grows (the with-past decode's attention mask, one
+      // position per step) grows its buffer by half again at least
+      size_t want = bytes > 0 ? bytes : 8;
       if (in.from_host && in.v.dev) {
         IH_HIP(hipStreamSynchronize(ex->ctx->stream));
         IH_HIP(hipFree(in.v.dev));
+        const size_t grown = in.cap + in.cap / 2;
+        want = ((grown > want ? grown : want) + 255) & ~size_t(255);
       }
       in.v.dev = nullptr;
-      IH_HIP(hipMalloc(&in.v.dev, bytes > 0 ? bytes : 8));
+      IH_HIP(hipMalloc(&in.v.dev, want));
+      in.cap = want;
     }
     in.from_host = true;
     in.v.dtype = dtype;
