@@ -846,11 +846,11 @@ void inferc_executor::fold_ln_weights() {
 void inferc_executor::exec_node(const inferc_graph::Node& n) {
   using namespace ih;
   const std::string& op = n.op;
-  auto in = [&](size_t i) -> Value {
+  auto in = [&](size_t i) -> const Value& {
     IH_REQUIRE(i < n.in.size(), INFERC_ERR_ARG, op + ": missing input " + std::to_string(i));
     return get(n.in[i]);
   };
-  auto require_f32 = [&](const Value v, const char* what) {
+  auto require_f32 = [&](const Value& v, const char* what) {
     IH_REQUIRE(v.dtype == INFERC_DT_F32, INFERC_ERR_UNSUPPORTED,
                op + ": " + what + " must be float32");
   };
@@ -864,7 +864,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     const Value x = lna ? get(ha) : in(0);
     require_f32(x, "X");
     const int64_t K = x.shape.back(), M = x.numel() / K;
-    const Value wq = in(1);
+    const Value& wq = in(1);
     IH_REQUIRE(wq.shape.size() == 2 && wq.shape[0] == K, INFERC_ERR_SHAPE, "FusedQKV: W shape");
     const int64_t N = wq.shape[1];
     std::vector<int64_t> os = x.shape;
@@ -873,8 +873,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     const float* b[3];
     float* y[3];
     for (int i = 0; i < 3; ++i) {
-      const Value wi = in(size_t(1 + 2 * i));
-      const Value bi = in(size_t(2 + 2 * i));
+      const Value& wi = in(size_t(1 + 2 * i));
+      const Value& bi = in(size_t(2 + 2 * i));
       IH_REQUIRE(wi.shape == wq.shape && bi.numel() == N, INFERC_ERR_SHAPE,
                  "FusedQKV: projections must share shapes");
       w[i] = static_cast<const float*>(
@@ -891,7 +891,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "FusedAttention") {
-    const Value q = in(0);
+    const Value& q = in(0);
     require_f32(q, "Q");
     IH_REQUIRE(q.shape.size() == 3, INFERC_ERR_SHAPE, "FusedAttention: expect [B,S,H]");
     IH_REQUIRE(in(1).shape == q.shape && in(2).shape == q.shape, INFERC_ERR_SHAPE,
@@ -905,7 +905,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     a.v = static_cast<const float*>(dev_of(n.in[2]));
     a.ldq = a.ldk = a.ldv = a.ldo = a.H;
     if (n.in.size() >= 4 && !n.in[3].empty()) {
-      const Value m = in(3);
+      const Value& m = in(3);
       IH_REQUIRE(m.dtype == INFERC_DT_BOOL || m.dtype == INFERC_DT_U8, INFERC_ERR_UNSUPPORTED,
                  "FusedAttention: mask must be bool");
       IH_REQUIRE(m.shape.size() <= 4, INFERC_ERR_SHAPE, "FusedAttention: mask rank > 4");
@@ -929,7 +929,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     const bool lna = op != "MatMul" && ln_read_of(n, 'a', &ha, &rna, &rdr);
     const bool lnr = op == "FusedGemmEpilogue" && ln_read_of(n, 'r', &hr, &rnr);
     const Value x = lna ? get(ha) : in(0);
-    const Value w = in(1);
+    const Value& w = in(1);
     require_f32(x, "A");
     require_f32(w, "B");
     if (op == "MatMul" && (w.shape.size() != 2 || x.shape.size() < 2)) {
@@ -1011,8 +1011,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "Gemm") {
-    const Value a = in(0);
-    const Value b = in(1);
+    const Value& a = in(0);
+    const Value& b = in(1);
     require_f32(a, "A");
     require_f32(b, "B");
     IH_REQUIRE(a.shape.size() == 2 && b.shape.size() == 2, INFERC_ERR_SHAPE,
@@ -1032,7 +1032,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     g.B = static_cast<const float*>(dev_of(n.in[1]));
     g.ldb = b.shape[1];
     if (n.in.size() >= 3 && !n.in[2].empty() && g.beta != 0.0f) {
-      const Value c = in(2);
+      const Value& c = in(2);
       if (c.numel() == g.M * g.N) {
         g.c_kind = INFERC_C_FULL;
         g.ldc = g.N;
@@ -1093,7 +1093,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     if (n.in.size() >= 4 && in(3).numel() > in(0).numel()) std::swap(xi, ri);
     if (n.in.size() >= 4 && pending_gather.count(n.in[ri])) materialize_gather(n.in[ri]);
     const auto pg = pending_gather.find(n.in[xi]);
-    const Value x = in(xi);
+    const Value& x = in(xi);
     require_f32(x, "X");
     const int64_t feat = x.shape.back();
     IH_REQUIRE(in(1).numel() == feat && in(2).numel() == feat, INFERC_ERR_SHAPE,
@@ -1102,7 +1102,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     const float* res = nullptr;
     int64_t res_rows = 1;
     if (n.in.size() >= 4) {
-      const Value rv = in(ri);
+      const Value& rv = in(ri);
       require_f32(rv, "residual");
       IH_REQUIRE(rv.numel() > 0 && rv.numel() % feat == 0 && x.numel() % rv.numel() == 0 &&
                      (rv.shape.empty() || rv.shape.back() == feat),
@@ -1116,8 +1116,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     if (es != eq_side.end()) {
       // the Equal's own fast-path conditions (below), else it runs itself
       const inferc_graph::Node& e = nodes[es->second];
-      const Value ea = get(e.in[0]);
-      const Value eb = get(e.in[1]);
+      const Value& ea = get(e.in[0]);
+      const Value& eb = get(e.in[1]);
       if (ea.dtype == INFERC_DT_I64 && eb.dtype == INFERC_DT_I64 && !(ea.host && eb.host) &&
           eb.numel() > 0 &&
           (eb.numel() == ea.numel() || eb.numel() == 1 || suffix_broadcast(ea.shape, eb.shape)) &&
@@ -1152,7 +1152,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "Gelu" || op == "GeluTanh" || op == "Relu") {
-    const Value x = in(0);
+    const Value& x = in(0);
     require_f32(x, "X");
     const int act = op == "Gelu" ? INFERC_ACT_GELU_ERF
                     : op == "GeluTanh" ? INFERC_ACT_GELU_TANH
@@ -1164,7 +1164,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "Softmax") {
-    const Value x = in(0);
+    const Value& x = in(0);
     require_f32(x, "X");
     int64_t axis = attr_int(n, "axis", -1);
     const int64_t r = int64_t(x.shape.size());
@@ -1182,8 +1182,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "Add") {
-    const Value a0 = in(0);
-    const Value b0 = in(1);
+    const Value& a0 = in(0);
+    const Value& b0 = in(1);
     if (a0.host && b0.host && a0.dtype == INFERC_DT_I64 && b0.dtype == INFERC_DT_I64 &&
         b0.numel() == 1) {
       std::vector<int64_t> r = host_i64(a0, "Add");
@@ -1203,8 +1203,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     const bool swap = b0.numel() > a0.numel();
     const std::string& an = swap ? n.in[1] : n.in[0];
     const std::string& bn = swap ? n.in[0] : n.in[1];
-    const Value a = get(an);
-    const Value b = get(bn);
+    const Value& a = get(an);
+    const Value& b = get(bn);
     IH_REQUIRE(b.numel() == a.numel() || suffix_broadcast(a.shape, b.shape), INFERC_ERR_UNSUPPORTED,
                "Add: only suffix broadcasts are supported, got " + shape_str(a.shape) + " + " +
                    shape_str(b.shape));
@@ -1222,8 +1222,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
   }
   if (op == "Equal") {
     if (eq_done.count(n.out[0])) return;  // computed by a LayerNorm launch
-    const Value a = in(0);
-    const Value b = in(1);
+    const Value& a = in(0);
+    const Value& b = in(1);
     if (a.dtype != INFERC_DT_I64 || b.dtype != INFERC_DT_I64 || (a.host && b.host) ||
         !(b.numel() == a.numel() || b.numel() == 1 || suffix_broadcast(a.shape, b.shape)) ||
         b.numel() > a.numel()) {
@@ -1238,8 +1238,8 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "Gather") {
-    const Value data = in(0);
-    const Value idx = in(1);
+    const Value& data = in(0);
+    const Value& idx = in(1);
     int64_t axis = attr_int(n, "axis", 0);
     const int64_t r = int64_t(data.shape.size());
     if (axis < 0) axis += r;
@@ -1372,7 +1372,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "Shape") {
-    const Value x = in(0);
+    const Value& x = in(0);
     std::vector<int64_t> s = x.shape;
     make_host(n.out[0], INFERC_DT_I64, {int64_t(s.size())}, s.data());
     return;
@@ -1388,7 +1388,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
   }
   if (op == "Unsqueeze" || op == "Squeeze" || op == "Reshape" || op == "Identity" ||
       op == "Flatten") {
-    const Value x = in(0);
+    const Value& x = in(0);
     std::vector<int64_t> s = x.shape;
     if (op == "Unsqueeze" || op == "Squeeze") {
       std::vector<int64_t> axes =
@@ -1437,7 +1437,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "Split") {
-    const Value x = in(0);
+    const Value& x = in(0);
     require_f32(x, "X");
     int64_t axis = attr_int(n, "axis", 0);
     const int64_t r = int64_t(x.shape.size());
@@ -1469,13 +1469,13 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "Concat" && n.in.size() == 1) {
-    const Value x0 = in(0);
+    const Value& x0 = in(0);
     alias(n.out[0], x0, x0.shape);
     return;
   }
   if (op == "Concat") {
     int64_t axis = attr_int(n, "axis", 0);
-    const Value x0 = in(0);
+    const Value& x0 = in(0);
     const int64_t r = int64_t(x0.shape.size());
     if (axis < 0) axis += r;
     IH_REQUIRE(axis >= 0 && axis < r, INFERC_ERR_ARG, "Concat: axis out of range");
@@ -1483,7 +1483,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     os[size_t(axis)] = 0;
     std::vector<int64_t> sizes;
     for (size_t i = 0; i < n.in.size(); ++i) {
-      const Value p = in(i);
+      const Value& p = in(i);
       IH_REQUIRE(p.shape.size() == x0.shape.size() && p.dtype == x0.dtype, INFERC_ERR_SHAPE,
                  "Concat: rank/dtype mismatch");
       for (int64_t d = 0; d < r; ++d)
@@ -1588,7 +1588,7 @@ void inferc_executor::exec_attention_past(const inferc_graph::Node& n) {
   using namespace ih;
   IH_REQUIRE(n.in.size() >= 5 && n.out.size() == 3, INFERC_ERR_ARG,
              "FusedAttentionPast: needs q, k, v, past_k, past_v[, mask] and three outputs");
-  const Value q = get(n.in[0]);
+  const Value& q = get(n.in[0]);
   IH_REQUIRE(q.dtype == INFERC_DT_F32 && q.shape.size() == 3, INFERC_ERR_SHAPE,
              "FusedAttentionPast: q must be float32 [B,S,H]");
   IH_REQUIRE(get(n.in[1]).shape == q.shape && get(n.in[2]).shape == q.shape, INFERC_ERR_SHAPE,
@@ -1616,7 +1616,7 @@ void inferc_executor::exec_attention_past(const inferc_graph::Node& n) {
   a.q = static_cast<const float*>(dev_of(n.in[0]));
   a.ldq = a.ldo = H;
   if (n.in.size() >= 6 && !n.in[5].empty()) {
-    const Value m = get(n.in[5]);
+    const Value& m = get(n.in[5]);
     IH_REQUIRE(m.dtype == INFERC_DT_BOOL || m.dtype == INFERC_DT_U8, INFERC_ERR_UNSUPPORTED,
                "FusedAttentionPast: mask must be bool");
     IH_REQUIRE(m.shape.size() <= 4, INFERC_ERR_SHAPE, "FusedAttentionPast: mask rank > 4");
@@ -1724,7 +1724,7 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
   }
   auto ui = unary.find(op);
   if (ui != unary.end()) {
-    const Value x = get(n.in.at(0));
+    const Value& x = get(n.in.at(0));
     if (host_foldable(n, x.numel())) {
       void* y = make_host_buf(n.out[0], x.dtype, x.shape);
       ew_unary(nullptr, ui->second, x.dtype, x.numel(), x.host->data(), y);
@@ -1774,7 +1774,7 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
     return true;
   }
   if (op == "Cast") {
-    const Value x = get(n.in.at(0));
+    const Value& x = get(n.in.at(0));
     const int to = int(attr_int(n, "to", 0));
     (void)dtype_size(to);
     if (to == x.dtype) {
@@ -1792,7 +1792,7 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
     return true;
   }
   if (op == "Where") {
-    const Value c = get(n.in.at(0)), a = get(n.in.at(1)), b = get(n.in.at(2));
+    const Value& c = get(n.in.at(0)), a = get(n.in.at(1)), b = get(n.in.at(2));
     IH_REQUIRE(c.dtype == INFERC_DT_BOOL || c.dtype == INFERC_DT_U8, INFERC_ERR_UNSUPPORTED,
                "Where: condition must be bool");
     IH_REQUIRE(a.dtype == b.dtype, INFERC_ERR_UNSUPPORTED, "Where: branch types differ");
@@ -1811,7 +1811,7 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
     return true;
   }
   if (op == "Expand") {
-    const Value x = get(n.in.at(0));
+    const Value& x = get(n.in.at(0));
     const std::vector<int64_t> target = host_i64(get(n.in.at(1)), "Expand");
     const std::vector<int64_t> os = ew_broadcast_shape({x.shape, target});
     if (os == x.shape) {
@@ -1829,7 +1829,7 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
     return true;
   }
   if (op == "Transpose") {
-    const Value x = get(n.in.at(0));
+    const Value& x = get(n.in.at(0));
     std::vector<int64_t> perm = attr_ints(n, "perm");
     const int64_t r = int64_t(x.shape.size());
     if (perm.empty())
@@ -1854,7 +1854,7 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
     // opset 10+: data, starts, ends[, axes[, steps]]; clamping as ONNX
     // specifies (start to [0, d] / [0, d-1] for negative steps, end to
     // [0, d] / [-1, d-1])
-    const Value x = get(n.in.at(0));
+    const Value& x = get(n.in.at(0));
     const int64_t r = int64_t(x.shape.size());
     const std::vector<int64_t> starts = host_i64(get(n.in.at(1)), "Slice");
     const std::vector<int64_t> ends = host_i64(get(n.in.at(2)), "Slice");
@@ -1898,7 +1898,7 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
     return true;
   }
   if (op == "ReduceMean") {
-    const Value x = get(n.in.at(0));
+    const Value& x = get(n.in.at(0));
     IH_REQUIRE(x.dtype == INFERC_DT_F32, INFERC_ERR_UNSUPPORTED, "ReduceMean: float32 only");
     const int64_t r = int64_t(x.shape.size());
     std::vector<int64_t> axes = attr_ints(n, "axes");
