@@ -128,3 +128,48 @@ def test_gpt2_small_with_past_graph_decode_config4(ctx):
     np.testing.assert_array_equal(toks, ref)
     assert len(ms) == 127
     dec.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("P,S,fill", [(0, 40, -3.4028234663852886e38), (29, 1, -3.4028234663852886e38),
+                                      (300, 3, float("-inf")), (150, 2, -1e4)])
+def test_attention_past_head_dim_64_vs_float64(ctx, P, S, fill):
+    """FusedAttentionPast at head_dim 64 (the cache attention's 8-wave form):
+    keys past 256 (several chunks per wave), a per-row mask, a row whose
+    first 64 keys are all masked (with fill = -inf those chunks score -inf
+    throughout and must leave the running softmax alone), against float64
+    (attention.cc:59-98 with the cached keys first)."""
+    B, nH, dh = 2, 2, 64
+    H, T = nH * dh, P + S
+    rng = np.random.default_rng(P + S)
+    q, k, v = (rng.standard_normal((B, S, H)).astype(np.float32) for _ in range(3))
+    pk, pv = (rng.standard_normal((B, nH, P, dh)).astype(np.float32) for _ in range(2))
+    mask = rng.random((B, 1, S, T)) < 0.3
+    mask[:, :, :, -1] = False                      # every row keeps a key
+    mask[0, 0, 0, :min(64, T - 1)] = True          # whole leading chunks masked
+    g = rt.Graph()
+    for name, shape in (("q", q.shape), ("k", k.shape), ("v", v.shape)):
+        g.add_input(name, np.float32, shape)
+    if P:
+        g.add_input("pk", np.float32, pk.shape)
+        g.add_input("pv", np.float32, pv.shape)
+    g.add_input("mask", np.bool_, mask.shape)
+    g.add_node("FusedAttentionPast", ["q", "k", "v", "pk" if P else "", "pv" if P else "", "mask"],
+               ["ctx", "present_k", "present_v"], head_dim=dh, fill=fill)
+    g.add_output("ctx")
+    ex = rt.Executor(ctx, g)
+    feeds = {"q": q, "k": k, "v": v, "mask": mask}
+    if P:
+        feeds.update(pk=pk, pv=pv)
+    got = ex.run(feeds, ["ctx"])["ctx"]
+    ex.close()
+    heads = lambda x: x.reshape(B, S, nH, dh).transpose(0, 2, 1, 3).astype(np.float64)
+    K = np.concatenate([pk.astype(np.float64), heads(k)], axis=2)
+    V = np.concatenate([pv.astype(np.float64), heads(v)], axis=2)
+    s = heads(q) @ K.transpose(0, 1, 3, 2) / np.sqrt(dh)
+    s = np.where(mask, fill, s)
+    s = s - s.max(axis=-1, keepdims=True)
+    e = np.exp(s)
+    ref = (e / e.sum(axis=-1, keepdims=True)) @ V
+    ref = ref.transpose(0, 2, 1, 3).reshape(B, S, H)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-5)
