@@ -735,6 +735,8 @@ def main(argv=None) -> int:
     ap.add_argument("--decode-only", nargs="?", const="both", choices=["fp32", "int4", "both"],
                     help="GPT-2 decode only (fp32 weights, int4 weights or both), one "
                          "generate each, printed as text (for rocprofv3 --kernel-trace runs)")
+    ap.add_argument("--int4-only", action="store_true",
+                    help="the 49-matrix int4 GEMV at batch 1 and 8 only, printed as JSON")
     ap.add_argument("--floors", action="store_true",
                     help="per-launch cost of dependent launch chains (launch floor, decode "
                          "GEMV shapes warm and cold, decode attention by key count), as JSON")
@@ -759,6 +761,10 @@ def main(argv=None) -> int:
         return 0
     if args.floors:
         print(json.dumps(launch_floors(ctx)), flush=True)
+        ctx.close()
+        return 0
+    if args.int4_only:
+        print(json.dumps({f"int4_gemv_b{B}": bench_int4(ctx, B) for B in (1, 8)}), flush=True)
         ctx.close()
         return 0
     if args.roofline_only:

@@ -436,17 +436,33 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_kernel(const Int4Mat* __rest
   }
 }
 
+// Workgroup barrier for LDS data only: unlike __syncthreads it does not make
+// the wave wait for its global loads still in flight.
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Batch-1 int4 GEMV on the vector ALUs (the streaming form of the fp32
 // GEMV). Rows are contiguous in memory and L lanes share a row (L a power of
 // two, L * DW dwords = K/8): lane s owns dwords [DW*s, DW*s + DW) of every
 // row it visits, i.e. 8*DW consecutive weights, so one load instruction
 // covers 64/L whole consecutive rows. A chunk is kI4Passes passes of 64/L
-// rows. Each wave streams a run of consecutive chunks of one matrix (about
-// kI4RunKB of weights): it prepares its 8*DW x values once, then
-// software-pipelines the run, issuing the loads of chunk c+2 before it
-// computes chunk c+1 (a ring of two register buffers), so its memory
-// requests stay in flight while it computes. For the transformer row
-// lengths the run is fully unrolled; other shapes loop.
+// rows. Each wave streams a run of consecutive chunks of one matrix: it
+// prepares its 8*DW x values once, then software-pipelines the run, issuing
+// the loads of chunk c+2 before it computes chunk c+1 (a ring of two
+// register buffers), so its memory requests stay in flight while it
+// computes.
+//
+// The transformer row lengths (K = 768: DW 3, L 32; K = 3072: DW 6, L 64)
+// run fully unrolled in int4_gemv_b1_kernel. Its blocks each cover one
+// matrix, and their four waves stage that matrix's x in LDS once (a quarter
+// each) instead of each wave fetching its slice from L2. Run lengths per
+// wave are 18 KB at K = 3072, 15 KB for K = 768 matrices over kI4BigRows
+// rows and 12 KB for the other K = 768 matrices, longest runs first in the
+// launch: with 4 waves per SIMD (the register budget) the whole GPT-2 set
+// is ~4300 waves, about one residency round, and the short runs last fill
+// its tail. Other row lengths take int4_gemv_valu_kernel (run-time L,
+// looped runs of about kI4RunKB).
 //
 // Arithmetic per dword w (8 nibbles, low nibble = even k): with
 // e = w & 0x0F0F0F0F (even nibbles) and b_i = byte i of w = e_i + 16 o_i,
@@ -464,9 +480,9 @@ __global__ __launch_bounds__(kBlock) void int4_gemv_kernel(const Int4Mat* __rest
 // of its run, so every result is stored once, after the loop (a store
 // inside the pipelined loop would tie up registers the next loads need).
 // Other L reduce all 4 rows over all L lanes and lane s keeps chunk s.
-// One launch serves two (DW, L) forms (the wave's matrix picks one,
-// wave-uniformly), so matrices of two row lengths overlap instead of
-// running back to back; the descriptors live in a device table.
+// The descriptors live in a device table; one launch serves every matrix
+// of the unrolled forms (the wave's matrix picks the form, wave-uniformly),
+// so matrices of both row lengths overlap instead of running back to back.
 constexpr int kI4Passes = 4;
 constexpr int kI4RunKB = 12;  // weights per wave of the unrolled run
 constexpr int kI4Ring = 2;    // chunks in flight per wave
@@ -643,28 +659,45 @@ __device__ __forceinline__ void int4_valu_run(const Int4VaDesc& d, int64_t wid, 
 // The run with a compile-time lane count L (>= 4) and NC chunks per wave,
 // fully unrolled: straight-line code lets the compiler count every wait
 // exactly (in a loop, copies of registers whose loads are still in flight
-// make it wait for all of them). A matrix's last run may hold fewer than NC
-// chunks; the missing ones load the broadcast line and are not stored.
+// make it wait for all of them). A matrix's last runs may hold fewer than NC
+// chunks, or none (the waves that round a matrix up to whole blocks); the
+// missing ones load the broadcast line and are not stored. x comes through
+// xs: each of the block's kWaves waves loads a quarter of the matrix's x,
+// and one LDS barrier (which leaves the weight loads in flight) publishes it.
 template <int DW, int LT, int NC>
-__device__ __forceinline__ void int4_valu_fixed(const Int4VaDesc& d, int64_t wid, int lane) {
+__device__ __forceinline__ void int4_valu_fixed(const Int4VaDesc& d, int64_t wid, int lane,
+                                                float* xs) {
   static_assert(LT >= 4 && NC <= LT / 4, "a lane keeps one chunk's row");
-  constexpr int rpp = 64 / LT;
+  constexpr int rpp = 64 / LT, K = 8 * DW * LT;
+  constexpr int F4 = K / 4 / kWaves, PER = (F4 + 63) / 64;  // x float4s per wave, per lane
   const int s = lane & (LT - 1), rg = lane / LT;
+  const int wave = threadIdx.x >> 6;
   const int64_t c0 = (wid - d.task_begin) * NC;
-  const int n = int(d.chunks - c0 < NC ? d.chunks - c0 : NC);
+  const int n = int(d.chunks - c0 < NC ? d.chunks - c0 : NC);  // <= 0: a rounding wave
   auto keep = [&](int j) { return j < n ? ~0u : 0u; };
-  // x first: its preparation then waits for x alone, with both chunks'
-  // loads (issued after it) still in flight
-  float4 xv[2 * DW];
-  const float4* xp = reinterpret_cast<const float4*>(d.x + 8 * DW * s);
+  // x first: it is waited for (to be staged) while both chunks' loads,
+  // issued after it, stay in flight
+  float4 xl[PER];
 #pragma unroll
-  for (int q = 0; q < 2 * DW; ++q) xv[q] = gload_f4(xp + q);
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    xl[i] = gload_f4(reinterpret_cast<const float4*>(d.x) + wave * F4 + (e < F4 ? e : 0));
+  }
   __builtin_amdgcn_sched_barrier(0);
   constexpr int R = NC < kI4Ring ? NC : kI4Ring;
   I4Chunk<DW> buf[R];
 #pragma unroll
-  for (int j = 0; j < R; ++j) i4_load_chunk<DW, LT>(buf[j], d, c0 + j, j ? keep(j) : ~0u, rpp, rg, s);
+  for (int j = 0; j < R; ++j) i4_load_chunk<DW, LT>(buf[j], d, c0 + j, keep(j), rpp, rg, s);
   __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    if (e < F4) reinterpret_cast<float4*>(xs)[wave * F4 + e] = xl[i];
+  }
+  lds_sync();
+  float4 xv[2 * DW];
+#pragma unroll
+  for (int q = 0; q < 2 * DW; ++q) xv[q] = reinterpret_cast<const float4*>(xs + 8 * DW * s)[q];
   float xsum = 0.0f, xe[4 * DW], xo[4 * DW];
 #pragma unroll
   for (int q = 0; q < 2 * DW; ++q) {
@@ -688,38 +721,53 @@ __device__ __forceinline__ void int4_valu_fixed(const Int4VaDesc& d, int64_t wid
   if (j < n && r < d.N) gstore_f(d.y + r, res);
 }
 
-// Chunks per wave of the unrolled run: about 12 KB of weights.
-template <int DW>
-constexpr int i4_fixed_chunks() { return kI4RunKB / DW; }
+// Run lengths of int4_gemv_b1_kernel in chunks per wave (a sweep of run
+// lengths on the 49-matrix GPT-2 set, measured on the box).
+constexpr int kI4NcK3072 = 3;            // 18 KB
+constexpr int kI4NcK768 = 4;             // 12 KB
+constexpr int kI4NcK768Big = 5;          // 15 KB
+constexpr int64_t kI4BigRows = 8192;     // "big": more rows than this
+static_assert(kI4NcK768 != kI4NcK768Big, "the run length tells the K = 768 forms apart");
 
-// (DA, LA) and (DB, LB): the two forms of one launch; L = 0 means the lanes
-// per row come from K at run time.
-template <int DA, int LA, int DB, int LB>
-__global__ __launch_bounds__(kBlock) void int4_gemv_valu_kernel(const Int4VaDesc* __restrict__ tab,
-                                                               int n, int64_t n_waves) {
-  const int lane = threadIdx.x & 63;
-  const int64_t wid = int64_t(blockIdx.x) * (kBlock / 64) +
-                      __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
-  if (wid >= n_waves) return;
-  int cnt = 0;  // this wave's matrix (task_begin ascends), one ballot per 64 entries
+// Index of the descriptor whose waves hold wave `wid` (task_begin ascends):
+// one ballot per 64 entries.
+__device__ __forceinline__ int i4_find_desc(const Int4VaDesc* tab, int n, int64_t wid, int lane) {
+  int cnt = 0;
   for (int base = 0; base < n; base += 64) {
     const int j = base + lane;
     const int c = __popcll(__ballot(j < n && gload_i64(&tab[j].task_begin) <= wid));
     cnt += c;
     if (c < 64) break;
   }
-  const Int4VaDesc d = tab[__builtin_amdgcn_readfirstlane(cnt - 1)];
-  if ((DA == DB && LA == LB) || d.dw == DA) {
-    if constexpr (LA >= 4)
-      int4_valu_fixed<DA, LA, i4_fixed_chunks<DA>()>(d, wid, lane);
-    else
-      int4_valu_run<DA, 0>(d, wid, lane);
-  } else {
-    if constexpr (LB >= 4)
-      int4_valu_fixed<DB, LB, i4_fixed_chunks<DB>()>(d, wid, lane);
-    else
-      int4_valu_run<DB, 0>(d, wid, lane);
-  }
+  return __builtin_amdgcn_readfirstlane(cnt - 1);
+}
+
+// The unrolled forms (K = 768 and 3072) in one launch; each matrix's waves
+// are rounded up to whole blocks, so the grid is exactly the waves.
+__global__ __launch_bounds__(kBlock) void int4_gemv_b1_kernel(const Int4VaDesc* __restrict__ tab,
+                                                              int n) {
+  __shared__ __attribute__((aligned(16))) float xs[3072];
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = int64_t(blockIdx.x) * kWaves +
+                      __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const Int4VaDesc d = tab[i4_find_desc(tab, n, wid, lane)];
+  if (d.dw == 6)
+    int4_valu_fixed<6, 64, kI4NcK3072>(d, wid, lane, xs);
+  else if (d.per_wave == kI4NcK768Big)
+    int4_valu_fixed<3, 32, kI4NcK768Big>(d, wid, lane, xs);
+  else
+    int4_valu_fixed<3, 32, kI4NcK768>(d, wid, lane, xs);
+}
+
+// Other row lengths: DW dwords per lane, L from K at run time, looped runs.
+template <int DW>
+__global__ __launch_bounds__(kBlock) void int4_gemv_valu_kernel(const Int4VaDesc* __restrict__ tab,
+                                                               int n, int64_t n_waves) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = int64_t(blockIdx.x) * kWaves +
+                      __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  if (wid >= n_waves) return;
+  int4_valu_run<DW, 0>(tab[i4_find_desc(tab, n, wid, lane)], wid, lane);
 }
 
 // Batch-1 int4 GEMV of one matrix for the decode step: the unrolled run of
@@ -1141,12 +1189,6 @@ __device__ __forceinline__ int wave_sum_int(int v) {
   v += __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);
   return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
          (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
-}
-
-// Workgroup barrier for LDS data only: unlike __syncthreads it does not make
-// the wave wait for its global loads still in flight.
-__device__ __forceinline__ void lds_sync() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 template <int G, int NW>
@@ -1662,49 +1704,62 @@ int int4_valu_dw(int64_t K) {
 // Lanes per row of the VALU kernel for a given K and DW.
 int64_t int4_valu_lanes(int64_t K, int dw) { return (K / 8) / dw; }
 
-// One launch over matrices of two forms: a (DA, LA) and b (DB, LB); LA or
-// LB = 0 for a run-time lane count. Every wave streams about 12 KB of
-// weights; the larger chunks go first so the short ones fill the tail.
-template <int DA, int LA, int DB, int LB>
-void launch_int4_valu_pair(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& a,
-                           const std::vector<Int4MfMat>& b) {
-  if (a.empty() && b.empty()) return;
+// One int4_gemv_b1_kernel launch over the K = 768 and K = 3072 matrices,
+// longest runs first (K = 3072, then the big K = 768 matrices, then the
+// rest); each matrix's waves are rounded up to whole blocks.
+void launch_int4_b1(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& k3072,
+                    const std::vector<Int4MfMat>& k768) {
+  if (k3072.empty() && k768.empty()) return;
   std::vector<Int4VaDesc> tab;
   int64_t waves = 0;
-  auto add = [&](const std::vector<Int4MfMat>& mats, int dw, int lt) {
-    for (const Int4MfMat& m : mats) {
-      const int64_t L = int4_valu_lanes(m.K, dw);
-      const int64_t chunks = ceil_div(m.N, int64_t(kI4Passes) * (64 / L));
-      const int64_t chunk_bytes = int64_t(kI4Passes) * 64 * dw * 4;
-      // compile-time L: the unrolled run's fixed length; run-time L: about
-      // 12 KB, bounded by the lanes that keep a run's results
-      const int64_t per_wave =
-          lt >= 4 ? kI4RunKB / dw
-                  : std::min<int64_t>(L, std::max<int64_t>(1, kI4RunKB * 1024 / chunk_bytes));
-      tab.push_back(Int4VaDesc{m.W, m.s, m.x, m.y, m.N, m.K, waves, dw, chunks, per_wave});
-      waves += ceil_div(chunks, per_wave);
-    }
+  auto add = [&](const Int4MfMat& m, int dw, int nc) {
+    const int64_t L = int4_valu_lanes(m.K, dw);
+    const int64_t chunks = ceil_div(m.N, int64_t(kI4Passes) * (64 / L));
+    tab.push_back(Int4VaDesc{m.W, m.s, m.x, m.y, m.N, m.K, waves, dw, chunks, nc});
+    waves += ceil_div(ceil_div(chunks, nc), kWaves) * kWaves;
   };
-  if (DA >= DB) {
-    add(a, DA, LA);
-    if (DA != DB || LA != LB) add(b, DB, LB);
-  } else {
-    add(b, DB, LB);
-    add(a, DA, LA);
+  for (const Int4MfMat& m : k3072) add(m, 6, kI4NcK3072);
+  for (const Int4MfMat& m : k768)
+    if (m.N > kI4BigRows) add(m, 3, kI4NcK768Big);
+  for (const Int4MfMat& m : k768)
+    if (m.N <= kI4BigRows) add(m, 3, kI4NcK768);
+  IH_REQUIRE(waves / kWaves < (int64_t(1) << 31), INFERC_ERR_SHAPE, "int4 gemv: launch too large");
+  ctx->reserve_tables(1);
+  const Int4VaDesc* dev = upload_table(ctx, tab);
+  hipLaunchKernelGGL(int4_gemv_b1_kernel, dim3(unsigned(waves / kWaves)), dim3(kBlock), 0,
+                     ctx->stream, dev, int(tab.size()));
+  check_launch("int4_gemv_b1");
+}
+
+// One int4_gemv_valu_kernel<DW> launch (run-time lane count): every wave
+// streams about kI4RunKB of weights, bounded by the lanes that keep a run's
+// results.
+template <int DW>
+void launch_int4_valu_generic(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats) {
+  if (mats.empty()) return;
+  std::vector<Int4VaDesc> tab;
+  int64_t waves = 0;
+  for (const Int4MfMat& m : mats) {
+    const int64_t L = int4_valu_lanes(m.K, DW);
+    const int64_t chunks = ceil_div(m.N, int64_t(kI4Passes) * (64 / L));
+    const int64_t chunk_bytes = int64_t(kI4Passes) * 64 * DW * 4;
+    const int64_t per_wave =
+        std::min<int64_t>(L, std::max<int64_t>(1, kI4RunKB * 1024 / chunk_bytes));
+    tab.push_back(Int4VaDesc{m.W, m.s, m.x, m.y, m.N, m.K, waves, DW, chunks, per_wave});
+    waves += ceil_div(chunks, per_wave);
   }
-  IH_REQUIRE(ceil_div(waves, kBlock / 64) < (int64_t(1) << 31), INFERC_ERR_SHAPE,
+  IH_REQUIRE(ceil_div(waves, kWaves) < (int64_t(1) << 31), INFERC_ERR_SHAPE,
              "int4 gemv: launch too large");
   ctx->reserve_tables(1);
   const Int4VaDesc* dev = upload_table(ctx, tab);
-  hipLaunchKernelGGL((int4_gemv_valu_kernel<DA, LA, DB, LB>),
-                     dim3(unsigned(ceil_div(waves, kBlock / 64))), dim3(kBlock), 0, ctx->stream,
-                     dev, int(tab.size()), waves);
+  hipLaunchKernelGGL(int4_gemv_valu_kernel<DW>, dim3(unsigned(ceil_div(waves, kWaves))),
+                     dim3(kBlock), 0, ctx->stream, dev, int(tab.size()), waves);
   check_launch("int4_gemv_valu");
 }
 
 void launch_int4_valu(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats) {
-  // the transformer forms (K = 768: DW 3, L 32; K = 3072: DW 6, L 64) get
-  // compile-time lane counts and share one launch; the rest run per DW
+  // the transformer forms (K = 768: DW 3, L 32; K = 3072: DW 6, L 64) share
+  // one unrolled launch; the rest run per DW with a run-time lane count
   std::vector<Int4MfMat> k768, k3072, by_dw[7];
   for (const Int4MfMat& m : mats) {
     const int dw = int4_valu_dw(m.K);
@@ -1715,17 +1770,11 @@ void launch_int4_valu(inferc_hip_ctx* ctx, const std::vector<Int4MfMat>& mats) {
     else
       by_dw[dw].push_back(m);
   }
-  static const std::vector<Int4MfMat> none;
-  if (!k768.empty() && !k3072.empty())
-    launch_int4_valu_pair<6, 64, 3, 32>(ctx, k3072, k768);
-  else if (!k768.empty())
-    launch_int4_valu_pair<3, 32, 3, 32>(ctx, k768, none);
-  else if (!k3072.empty())
-    launch_int4_valu_pair<6, 64, 6, 64>(ctx, k3072, none);
-  launch_int4_valu_pair<2, 0, 2, 0>(ctx, by_dw[2], none);
-  launch_int4_valu_pair<3, 0, 3, 0>(ctx, by_dw[3], none);
-  launch_int4_valu_pair<4, 0, 4, 0>(ctx, by_dw[4], none);
-  launch_int4_valu_pair<6, 0, 6, 0>(ctx, by_dw[6], none);
+  launch_int4_b1(ctx, k3072, k768);
+  launch_int4_valu_generic<2>(ctx, by_dw[2]);
+  launch_int4_valu_generic<3>(ctx, by_dw[3]);
+  launch_int4_valu_generic<4>(ctx, by_dw[4]);
+  launch_int4_valu_generic<6>(ctx, by_dw[6]);
 }
 
 void int4_grouped(inferc_hip_ctx* ctx, int64_t n_mats, const int64_t* Ns, const int64_t* Ks,

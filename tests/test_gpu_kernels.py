@@ -442,11 +442,14 @@ def test_int4_reference_stand_in_shape(ctx):
 
 
 @pytest.mark.parametrize("N,K", [(1, 768), (7, 768), (65, 768), (97, 768), (1, 3072),
-                                 (5, 3072), (19, 3072), (40, 1536), (130, 512)])
+                                 (5, 3072), (19, 3072), (40, 1536), (130, 512), (8193, 768),
+                                 (8231, 768)])
 def test_int4_gemv_batch1_run_edges(ctx, N, K):
     """Batch 1, row counts that end a wave's run early (fewer rows than one
-    chunk, a partial last chunk, a partial last run) and the row lengths that
-    take the looped form (K = 1536, 512)."""
+    chunk, a partial last chunk, a partial last run, whole runs of waves that
+    only round a matrix up to a block), the 15 KB runs of K = 768 matrices
+    over 8192 rows, and the row lengths that take the looped form (K = 1536,
+    512)."""
     W, s = graphs.int4_weights(N, K, 102, "edges")
     x = rnd((1, K), 103)
     got = rt.Int4Gemv(T(ctx, W, np.uint8), T(ctx, s), T(ctx, x), K).numpy()
