@@ -82,6 +82,14 @@ int inferc_hip_destroy(inferc_hip_ctx* ctx);
  * The context also keeps up to 32 grouped-GEMV descriptor tables on the
  * device, keyed by their bytes, and frees them all when a launch needs room. */
 int inferc_hip_reserve_workspace(inferc_hip_ctx* ctx, size_t bytes);
+/* One-row products whose B is transposed ([N,K] rows) take the batch-1 GEMV
+ * route: on by default, off as the ablation baseline of `inferc decode
+ * --no-gemv`. Replaces rt::SetGemvDecodeEnabled / GemvDecodeEnabled
+ * (src/kernels/matmul.cc:56-61,207-216; main.cpp:718,727), per context
+ * instead of process-wide. Executors' captured graphs are recorded again
+ * after a change. */
+int inferc_hip_set_gemv_decode(inferc_hip_ctx* ctx, int enabled);
+int inferc_hip_gemv_decode_enabled(inferc_hip_ctx* ctx, int* enabled);
 
 int inferc_hip_malloc(inferc_hip_ctx* ctx, size_t bytes, void** dptr);
 int inferc_hip_free(inferc_hip_ctx* ctx, void* dptr);
@@ -412,6 +420,14 @@ int inferc_executor_output_device(inferc_executor* ex, const char* name,
  * (main.cpp:875-879). Synchronises the stream. */
 int inferc_executor_output_argmax(inferc_executor* ex, const char* name,
                                   int64_t* index);
+/* Device bytes the executor holds: the uploaded initializers, the
+ * transposed [N,K] copies of [K,N] weight initializers that one-row
+ * products read on the GEMV route (made on the first run of a signature
+ * that needs them, kept with the initializers), and the activation arena.
+ * No counterpart in the reference, whose tensors live on the host. Any
+ * pointer may be null. */
+int inferc_executor_device_bytes(inferc_executor* ex, int64_t* initializers,
+                                 int64_t* transposed_copies, int64_t* arena);
 
 /* ---------------- Profiler (src/profiler/profiler.h:40-89) ---------------- */
 

@@ -6,7 +6,8 @@ of the runtime hot path, with the reference's arguments and outputs.
       [--shape B,S] [--profile JSON] [-n N] [--warmup N] [--name LABEL]
       [--no-optimize]                       DoRun / CmdRun (main.cpp:324-465)
   decode --model M --past-model M --prompt-ids BIN --max-tokens N
-      --output BIN [--profile JSON] [--no-optimize]      CmdDecode (main.cpp:700-936)
+      --output BIN [--profile JSON] [--no-gemv] [--no-fold] [--no-optimize]
+      [--device N] [--native | --int4]      CmdDecode (main.cpp:700-936)
   compare <a.json> <b.json>                 CmdCompare (main.cpp:595-611)
 
 `run` reads int64 ids/mask files of shape B,S, loads the ONNX model with the
@@ -17,6 +18,15 @@ bytes. `decode` runs the prefill graph over the prompt and the with-past
 graph for each further token with the KV cache on the device, and writes the
 int64 tokens. Profiles are the reference's JSON schema with device per-op
 times.
+
+decode flags: --no-gemv (main.cpp:718,727) turns the one-row GEMV route of
+the graph executor off, --no-fold (main.cpp:719,756-775) leaves out the
+passes the reference's flag skips (FoldConstantTranspose, RecognizeLayerNorm,
+RecognizeGeluTanh); both are the reference's ablation baselines. Beyond the
+reference: --device N picks the GPU, --native runs the model the with-past
+graph describes (its weights read by parameter name) on the native decoder
+(one captured step per token), and --int4 does the same with int4
+weight-only projections (inferc_gpt2_use_int4).
 
 Usage: python -m inferc_amd <command> ...
 """
@@ -139,18 +149,26 @@ def cmd_run(args: list[str]) -> int:
 
 def cmd_decode(args: list[str]) -> int:
     try:
-        o, pos = _opts(args, {"--no-optimize"},
+        o, pos = _opts(args, {"--no-optimize", "--no-gemv", "--no-fold", "--native", "--int4"},
                        {"--model", "--past-model", "--prompt-ids", "--max-tokens", "--output",
-                        "--profile", "--max-t"})
+                        "--profile", "--max-t", "--device"})
     except ValueError as e:
         return _err(f"inferc decode: {e}")
     need = ("--model", "--past-model", "--prompt-ids", "--output")
     if pos or any(k not in o for k in need):
         return _err("usage: inferc decode --model <gpt2.onnx> --past-model <gpt2_with_past.onnx>\n"
                     "                     --prompt-ids <bin> --max-tokens N --output <bin>")
-    max_tokens = int(o.get("--max-tokens", 32))
+    try:
+        max_tokens = int(o.get("--max-tokens", 32))
+        device = int(o.get("--device", 0))
+    except ValueError:
+        return _err("inferc decode: --max-tokens and --device take integers")
     if max_tokens <= 0:
         return _err("inferc decode: missing required args")
+    native = "--native" in o or "--int4" in o
+    if native and ("--no-gemv" in o or "--no-fold" in o or "--no-optimize" in o):
+        return _err("inferc decode: --no-gemv, --no-fold and --no-optimize apply to the graph "
+                    "executor, not to --native/--int4")
     from . import rt
     from .profiler import Profiler
 
@@ -159,17 +177,26 @@ def cmd_decode(args: list[str]) -> int:
         print("inferc decode: empty prompt", file=sys.stderr)
         return 1
     max_t = int(o.get("--max-t", prompt.size + max_tokens))
-    ctx = rt.Context(0)
     try:
-        dec = rt.OnnxDecoder(ctx, o["--past-model"], max_t=max_t, prefill=o["--model"],
-                             optimize="--no-optimize" not in o)
+        ctx = rt.Context(device)
+    except RuntimeError as e:
+        print(f"inferc decode: device {device}: {e}", file=sys.stderr)
+        return 1
+    try:
         prof = Profiler() if "--profile" in o else None
         if prof is not None:
             prof.set_track_activation_bytes(False)
-        t0 = time.perf_counter()
-        toks = dec.generate(prompt, max_tokens, profiler=prof)
-        el = time.perf_counter() - t0
-    except RuntimeError as e:
+        if native:
+            toks, el = _decode_native(ctx, o, prompt, max_tokens, max_t, prof)
+        else:
+            ctx.set_gemv_decode("--no-gemv" not in o)
+            skip = rt.OnnxDecoder.FOLD_PASSES if "--no-fold" in o else ()
+            dec = rt.OnnxDecoder(ctx, o["--past-model"], max_t=max_t, prefill=o["--model"],
+                                 optimize="--no-optimize" not in o, skip_passes=skip)
+            t0 = time.perf_counter()
+            toks = dec.generate(prompt, max_tokens, profiler=prof)
+            el = time.perf_counter() - t0
+    except (RuntimeError, ValueError) as e:
         print(f"inferc decode: {e}", file=sys.stderr)
         return 1
     toks.astype(np.int64).tofile(o["--output"])
@@ -181,6 +208,25 @@ def cmd_decode(args: list[str]) -> int:
         Path(o["--profile"]).write_text(json.dumps(rep, indent=2, sort_keys=True))
         print(f"  decode profile -> {o['--profile']}")
     return 0
+
+
+def _decode_native(ctx, o: dict, prompt: np.ndarray, max_tokens: int, max_t: int, prof):
+    """--native / --int4: the GPT-2 the with-past graph holds, on the native
+    decoder; returns (tokens, seconds)."""
+    from . import rt
+
+    dec = rt.Gpt2Decoder.from_graph(ctx, o["--past-model"], max_t)
+    try:
+        if "--int4" in o:
+            dec.use_int4()
+        t0 = time.perf_counter()
+        if prof is not None:
+            toks = dec.generate_profiled(prompt, max_tokens, prof)
+        else:
+            toks, _, _ = dec.generate(prompt, max_tokens)
+        return toks, time.perf_counter() - t0
+    finally:
+        dec.close()
 
 
 def cmd_compare(args: list[str]) -> int:

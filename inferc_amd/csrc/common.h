@@ -87,6 +87,10 @@ struct inferc_hip_ctx {
   // such a graph must be captured again.
   uint64_t ws_generation = 0;
   bool capturing = false;  // set while a HIP graph is being recorded
+  // One-row products with a transposed B take the GEMV route (the
+  // reference's g_gemv_decode_enabled, src/kernels/matmul.cc:56-61,207-216).
+  bool gemv_decode = true;
+  uint64_t route_generation = 0;  // bumped when gemv_decode changes
 
   // Device copies of small launch descriptor tables, keyed by their bytes,
   // so repeated launches over the same operands skip the upload.
@@ -301,7 +305,7 @@ void init_gemm_scratch(int device);
 
 // Whether gemm() sends `a` to the batch-1 GEMV (one row of A times a [N,K]
 // B^T), the route that can apply a LayerNorm to the A row (gemv_ln_*).
-bool gemm_gemv_route(const GemmArgs& a);
+bool gemm_gemv_route(const inferc_hip_ctx* ctx, const GemmArgs& a);
 
 void gemm(inferc_hip_ctx* ctx, const GemmArgs& a);
 

@@ -140,6 +140,25 @@ int inferc_hip_reserve_workspace(inferc_hip_ctx* ctx, size_t bytes) {
   });
 }
 
+int inferc_hip_set_gemv_decode(inferc_hip_ctx* ctx, int enabled) {
+  return ih::guard([&] {
+    ih::check_ctx(ctx);
+    if (ctx->gemv_decode != (enabled != 0)) {
+      ctx->gemv_decode = enabled != 0;
+      // executors' captured graphs baked in the old route: they record again
+      ++ctx->route_generation;
+    }
+  });
+}
+
+int inferc_hip_gemv_decode_enabled(inferc_hip_ctx* ctx, int* enabled) {
+  return ih::guard([&] {
+    ih::check_ctx(ctx);
+    IH_REQUIRE(enabled != nullptr, INFERC_ERR_ARG, "null argument");
+    *enabled = ctx->gemv_decode ? 1 : 0;
+  });
+}
+
 int inferc_hip_malloc(inferc_hip_ctx* ctx, size_t bytes, void** dptr) {
   return ih::guard([&] {
     ih::check_ctx(ctx);

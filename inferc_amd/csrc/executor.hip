@@ -156,6 +156,7 @@ struct inferc_executor {
   std::unordered_map<std::string, LnRead> ln_reads;  // by h
   std::unordered_map<std::string, bool> ln_on;       // this run, by h
   uint64_t graph_ws_gen = 0;
+  uint64_t graph_route_gen = 0;
   // Sticky device flag of the gathers whose indices live on the device: set
   // by the kernel on an out-of-range index, read (and cleared) by the calls
   // that wait for the stream, which then fail as Gather does on the host
@@ -318,6 +319,7 @@ struct inferc_executor {
   // of W, instead of a tiled GEMM with 1 of its 16..128 rows live. Made on
   // first use, outside any capture, and kept with the initializers.
   std::unordered_map<std::string, float*> wt_cache;
+  size_t wt_cache_bytes = 0;  // device bytes of those copies
   const float* transposed_init(const std::string& name) {
     auto it = wt_cache.find(name);
     if (it != wt_cache.end()) return it->second;
@@ -335,16 +337,21 @@ struct inferc_executor {
     IH_HIP(hipMalloc(&d, t.size() * sizeof(float)));
     init_allocs.push_back(d);
     IH_HIP(hipMemcpy(d, t.data(), t.size() * sizeof(float), hipMemcpyHostToDevice));
+    wt_cache_bytes += t.size() * sizeof(float);
     return wt_cache[name] = static_cast<float*>(d);
   }
   // Points g at the transposed copy of its B when the product has one row,
-  // B is a [K, N] initializer and the GEMV route takes the result.
+  // B is a [K, N] initializer that no input, tape value or folded constant
+  // of the same name shadows, and the GEMV route (switched on in the
+  // context, as the reference's SetGemvDecodeEnabled) takes the result.
   void batch1_route(ih::GemmArgs& g, const std::string& b_name) {
     if (dry || g.M != 1 || g.batch != 1 || g.trans_a || g.trans_b || g.ldb != g.N) return;
+    auto ii = inits.find(b_name);
+    if (ii == inits.end() || find_val(b_name) != &ii->second) return;
     ih::GemmArgs t = g;
     t.trans_b = 1;
     t.ldb = g.K;
-    if (!ih::gemm_gemv_route(t)) return;
+    if (!ih::gemm_gemv_route(ctx, t)) return;
     const float* wt = transposed_init(b_name);
     if (!wt) return;
     t.B = wt;
@@ -994,7 +1001,6 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       if (lnr) g.norm_r = rnr;
     }
     g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
-    if (!lna) batch1_route(g, n.in[1]);
     if (op == "FusedGemmEpilogue" && ln_reads.count(n.out[0])) {
       // the producer of a LayerNorm read by its readers: decide for this
       // run, and write the row statistics they combine
@@ -1005,6 +1011,9 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
         g.stats_out = static_cast<float*>(
             buf("__lnstats:" + n.out[0], size_t(M) * size_t(N / 16) * 2 * sizeof(float)));
     }
+    // (after the row statistics are decided: a product that writes them
+    // stays off the GEMV route)
+    if (!lna) batch1_route(g, n.in[1]);
     if (!dry) {
       gemm(ctx, g);
     }
@@ -1057,7 +1066,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       const float eps = std::stof(n.attrs.at("__ln_eps"));
       IH_REQUIRE(!g.trans_a && inits.at(ln->second).numel() == g.K, INFERC_ERR_SHAPE,
                  "Gemm: LayerNorm of A: scale size must equal K");
-      if (gemm_gemv_route(g)) {
+      if (gemm_gemv_route(ctx, g)) {
         g.gemv_ln_g = lg;
         g.gemv_ln_b = lb;
         g.gemv_ln_eps = eps;
@@ -1993,20 +2002,24 @@ void inferc_executor::run() {
   ctx->make_current();
   stage_inputs();
   const std::string sig = signature();
-  if (graph_mode && exec && graph_sig == sig && graph_ws_gen == ctx->ws_generation) {
+  if (graph_mode && exec && graph_sig == sig && graph_ws_gen == ctx->ws_generation &&
+      graph_route_gen == ctx->route_generation) {
     IH_HIP(hipGraphLaunch(exec, ctx->stream));
     return;
   }
+  // a changed GEMV route is planned by an eager pass, as a new signature is
+  if (graph_route_gen != ctx->route_generation) last_sig.clear();
   if (!graph_mode || sig != last_sig) {
     // first run for this input signature: eager (allocates the arena)
     drop_graph();
     walk();
     last_sig = sig;
+    graph_route_gen = ctx->route_generation;
     return;
   }
   // second run with the same signature: record it, then replay
   drop_graph();
-  const uint64_t gen = ctx->ws_generation;
+  const uint64_t gen = ctx->ws_generation, route_gen = ctx->route_generation;
   IH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
   ctx->capturing = true;
   try {
@@ -2023,6 +2036,7 @@ void inferc_executor::run() {
   IH_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
   graph_sig = sig;
   graph_ws_gen = gen;
+  graph_route_gen = route_gen;
   IH_HIP(hipGraphLaunch(exec, ctx->stream));
 }
 
@@ -2079,7 +2093,11 @@ void inferc_executor::run_profiled(inferc_profiler* p) {
   stage_inputs();
   const std::string sig = signature();
   if (sig != last_sig) {
+    // a new input signature: one unrecorded eager pass first, so that the
+    // arena allocations and the one-row products' transposed weight copies
+    // (blocking allocations and uploads) fall outside the recorded pass
     drop_graph();  // buffers may be reallocated for the new shapes
+    walk();
     last_sig = sig;
   }
   IH_HIP(hipStreamSynchronize(ctx->stream));
@@ -2530,6 +2548,21 @@ int inferc_executor_output_device(inferc_executor* ex, const char* name, const v
                std::string("output '") + name + "' has no contiguous device buffer");
     ex->check_gather_err();
     *ptr = v.dev;
+  });
+}
+
+int inferc_executor_device_bytes(inferc_executor* ex, int64_t* initializers,
+                                 int64_t* transposed_copies, int64_t* arena) {
+  return ih::guard([&] {
+    IH_REQUIRE(ex != nullptr, INFERC_ERR_ARG, "null executor");
+    int64_t w = 0, a = 0;
+    for (const auto& kv : ex->inits)
+      if (kv.second.dev) w += int64_t(kv.second.bytes());
+    if (!ex->dry)
+      for (const auto& kv : ex->arena) a += int64_t(kv.second.bytes);
+    if (initializers) *initializers = w;
+    if (transposed_copies) *transposed_copies = int64_t(ex->wt_cache_bytes);
+    if (arena) *arena = a;
   });
 }
 

@@ -208,6 +208,46 @@ def gpt2_bind_weights(graph, cfg: dict, weights: list[np.ndarray]) -> None:
         raise ValueError(f"gpt2_bind_weights: bound {bound} of {len(names) + 1} parameters")
 
 
+def gpt2_weights_from_graph(graph) -> tuple[dict, list[np.ndarray]]:
+    """The config and weights (the order of gpt2_weights) of an exported HF
+    GPT-2 graph, read from its initializers by parameter name
+    (<prefix>transformer.wte.weight, .h.{l}.ln_1.weight, ..., .ln_f.bias):
+    what the native decoder (inferc_gpt2_create) needs to run the model the
+    graph describes. Heads come from the past_key_values.* inputs of a
+    with-past graph ([batch, heads, past, head_dim]); the LayerNorm epsilon
+    from the graph's fused LayerNorms (1e-5, GPT-2's, if none is fused)."""
+    d = graph.to_dict()
+    names = {i["name"] for i in d["initializers"]}
+    wte = [n for n in names if n.endswith("transformer.wte.weight")]
+    if len(wte) != 1:
+        raise ValueError("gpt2_weights_from_graph: no single transformer.wte.weight initializer")
+    p = wte[0][:-len("wte.weight")]
+    get = graph.initializer
+    L = 0
+    while f"{p}h.{L}.ln_1.weight" in names:
+        L += 1
+    if L == 0:
+        raise ValueError("gpt2_weights_from_graph: no transformer.h.0 parameters")
+    heads = [i["shape"][1] for i in d["inputs"] if i["name"].startswith("past_key_values.")
+             and len(i["shape"]) == 4]
+    if not heads or heads[0] <= 0:
+        raise ValueError("gpt2_weights_from_graph: head count needs the with-past graph's "
+                         "past_key_values.* inputs")
+    eps = [float(n["attrs"]["epsilon"]) for n in d["nodes"]
+           if n["op"] == "FusedLayerNorm" and "epsilon" in n.get("attrs", {})]
+    w = [get(p + "wte.weight"), get(p + "wpe.weight")]
+    parts = ["ln_1.weight", "ln_1.bias", "attn.c_attn.weight", "attn.c_attn.bias",
+             "attn.c_proj.weight", "attn.c_proj.bias", "ln_2.weight", "ln_2.bias",
+             "mlp.c_fc.weight", "mlp.c_fc.bias", "mlp.c_proj.weight", "mlp.c_proj.bias"]
+    for l in range(L):
+        w += [get(f"{p}h.{l}.{part}") for part in parts]
+    w += [get(p + "ln_f.weight"), get(p + "ln_f.bias")]
+    V, H = w[0].shape
+    cfg = dict(layers=L, hidden=int(H), heads=int(heads[0]), ffn=int(w[10].shape[1]),
+               vocab=int(V), max_pos=int(w[1].shape[0]), eps=eps[0] if eps else 1e-5)
+    return cfg, [np.ascontiguousarray(a, np.float32) for a in w]
+
+
 def gpt2_prompt(cfg: dict, n: int, seed: int = 3) -> np.ndarray:
     return rng_for(seed, f"prompt_{n}").integers(0, cfg["vocab"], size=n, dtype=np.int64)
 

@@ -54,6 +54,8 @@ _SIGS = {
     "inferc_hip_create": [i32, P(vp)],
     "inferc_hip_destroy": [vp],
     "inferc_hip_reserve_workspace": [vp, sz],
+    "inferc_hip_set_gemv_decode": [vp, C.c_int],
+    "inferc_hip_gemv_decode_enabled": [vp, P(C.c_int)],
     "inferc_hip_malloc": [vp, sz, P(vp)],
     "inferc_hip_free": [vp, vp],
     "inferc_hip_h2d": [vp, vp, vp, sz],
@@ -117,6 +119,7 @@ _SIGS = {
     "inferc_executor_bind_kv_cache": [vp, i64],
     "inferc_executor_set_input_shape": [vp, C.c_char_p, i32, i32, P(i64)],
     "inferc_executor_output_argmax": [vp, C.c_char_p, P(i64)],
+    "inferc_executor_device_bytes": [vp, P(i64), P(i64), P(i64)],
     "inferc_executor_output_device": [vp, C.c_char_p, P(vp)],
     "inferc_profiler_create": [P(vp)],
     "inferc_profiler_destroy": [vp],

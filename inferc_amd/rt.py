@@ -74,6 +74,16 @@ class Context:
     def reserve_workspace(self, nbytes: int) -> None:
         check(self._lib.inferc_hip_reserve_workspace(self.handle, nbytes))
 
+    def set_gemv_decode(self, enabled: bool) -> None:
+        """rt::SetGemvDecodeEnabled (src/kernels/matmul.cc:56-61) for this
+        context: one-row products with a transposed B take the GEMV route."""
+        check(self._lib.inferc_hip_set_gemv_decode(self.handle, int(bool(enabled))))
+
+    def gemv_decode_enabled(self) -> bool:
+        v = C.c_int()
+        check(self._lib.inferc_hip_gemv_decode_enabled(self.handle, C.byref(v)))
+        return bool(v.value)
+
     def malloc(self, nbytes: int) -> int:
         p = C.c_void_p()
         check(self._lib.inferc_hip_malloc(self.handle, nbytes, C.byref(p)))
@@ -806,6 +816,14 @@ class Executor:
                                                           C.byref(idx)))
         return idx.value
 
+    def device_bytes(self) -> dict[str, int]:
+        """Device bytes held: uploaded initializers, transposed copies of
+        [K, N] weights read by one-row products, activation arena."""
+        a, b, c = C.c_int64(), C.c_int64(), C.c_int64()
+        check(self.ctx._lib.inferc_executor_device_bytes(self.handle, C.byref(a), C.byref(b),
+                                                         C.byref(c)))
+        return {"initializers": a.value, "transposed_copies": b.value, "arena": c.value}
+
     def run_profiled(self, profiler) -> None:
         """Executor::Run(inputs, profiler) (src/runtime/executor.cc:98-125,
         349-354): one eager pass recorded as one profiler iteration, each
@@ -844,6 +862,17 @@ class Executor:
 
 # -------------------------------------------------------------------- GPT-2
 
+def _optimize(g: Graph, skip: Sequence[str] = ()) -> dict[str, int]:
+    """The pass pipeline in its order, leaving out the passes named in
+    `skip` (their count is 0)."""
+    bad = set(skip) - set(PASSES)
+    if bad:
+        raise HipError(L.ERR_ARG, f"unknown pass(es): {sorted(bad)}")
+    if not skip:
+        return g.optimize()
+    return {p: (0 if p in skip else g.run_pass(p)) for p in PASSES}
+
+
 class OnnxDecoder:
     """Greedy decode over an exported GPT-2 with-past graph (`inferc decode`,
     src/cli/main.cpp:700-936) with the KV cache on the device.
@@ -857,14 +886,18 @@ class OnnxDecoder:
     prompt is the first step (past length 0), then one token per step.
     Argmax (first maximum, main.cpp:875-879) runs on the device."""
 
-    def __init__(self, ctx: Context, with_past, max_t: int, prefill=None, optimize: bool = True):
+    # the passes `inferc decode --no-fold` leaves out (main.cpp:756-775)
+    FOLD_PASSES = ("fold_constant_transpose", "recognize_layernorm", "recognize_gelu_tanh")
+
+    def __init__(self, ctx: Context, with_past, max_t: int, prefill=None, optimize: bool = True,
+                 skip_passes: Sequence[str] = ()):
         self.graph = with_past if isinstance(with_past, Graph) else Graph.from_onnx(with_past)
-        self.counts = self.graph.optimize() if optimize else None
+        self.counts = _optimize(self.graph, skip_passes) if optimize else None
         self.prefill_ex = None
         if prefill is not None:
             pg = prefill if isinstance(prefill, Graph) else Graph.from_onnx(prefill)
             if optimize:
-                pg.optimize()
+                _optimize(pg, skip_passes)
             self.prefill_ex = Executor(ctx, pg)
         d = self.graph.to_dict()
         self.past = [i for i in d["inputs"] if i["name"].startswith("past_key_values.")]
@@ -985,6 +1018,24 @@ class Gpt2Decoder:
             self.handle, p.ctypes.data_as(C.POINTER(C.c_int64)), p.size, max_tokens,
             toks.ctypes.data_as(C.POINTER(C.c_int64)), profiler.handle))
         return toks
+
+    @classmethod
+    def from_graph(cls, ctx: Context, graph, max_t: int) -> "Gpt2Decoder":
+        """The GPT-2 an exported with-past graph (a Graph or an ONNX path)
+        describes, its weights read by parameter name
+        (graphs.gpt2_weights_from_graph), on the native decoder."""
+        from . import graphs
+
+        own = not isinstance(graph, Graph)
+        g = Graph.from_onnx(graph) if own else graph
+        try:
+            if not any(n["op"] == "FusedLayerNorm" for n in g.to_dict()["nodes"]):
+                g.run_pass("recognize_layernorm")  # the epsilon attribute, for the config
+            cfg, w = graphs.gpt2_weights_from_graph(g)
+        finally:
+            if own:
+                g.close()
+        return cls(ctx, cfg, w, max_t)
 
     def use_int4(self) -> None:
         """int4 weight-only decode (irreversible): see inferc_gpt2_use_int4."""

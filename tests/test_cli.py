@@ -41,6 +41,14 @@ def test_argument_errors(capsys, tmp_path):
     assert cli.main(["run", "m.onnx", "--bogus"]) == 2
     assert "unknown arg" in capsys.readouterr().err
     assert cli.main(["decode", "--model", "a.onnx"]) == 2
+    dec = ["decode", "--model", "a.onnx", "--past-model", "b.onnx", "--prompt-ids", "p.bin",
+           "--output", "o.bin"]
+    assert cli.main(dec + ["--device", "x"]) == 2
+    assert "integers" in capsys.readouterr().err
+    for flag in ("--no-gemv", "--no-fold", "--no-optimize"):
+        assert cli.main(dec + ["--int4", flag]) == 2
+        assert "graph executor" in capsys.readouterr().err
+    assert cli.main(dec + ["--no-such-flag"]) == 2
     assert cli.main(["compare", "only_one.json"]) == 2
     assert cli.main(["nope"]) == 1
 
@@ -89,3 +97,39 @@ def test_decode_two_graphs_matches_torch(ctx, tmp_path):
     np.testing.assert_array_equal(np.fromfile(out, np.int64), io["gen_tokens"])
     rep = json.loads(prof.read_text())
     assert rep["iterations"] == 11 and rep["op_counts"]["FusedAttentionPast"] == 2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("flags", [["--no-gemv"], ["--no-fold"], ["--no-gemv", "--no-fold"],
+                                   ["--device", "0"], ["--native"]])
+def test_decode_flags_keep_the_tokens(ctx, tmp_path, flags):
+    """The reference's ablation flags (--no-gemv: the one-row GEMV route off,
+    main.cpp:718,727; --no-fold: FoldConstantTranspose, RecognizeLayerNorm
+    and RecognizeGeluTanh left out, :719,756-775) change how the graphs run,
+    not the greedy tokens; --native runs the same weights on the native
+    decoder."""
+    io = np.load(GOLDEN / "gpt2_tiny_past_io.npz")
+    ids, out = tmp_path / "prompt.bin", tmp_path / "toks.bin"
+    io["prompt"].astype(np.int64).tofile(ids)
+    assert cli.main(["decode", "--model", str(GOLDEN / "gpt2_tiny_prefill.onnx"),
+                     "--past-model", str(GOLDEN / "gpt2_tiny_past.onnx"),
+                     "--prompt-ids", str(ids), "--max-tokens", "12", "--output", str(out)]
+                    + flags) == 0
+    np.testing.assert_array_equal(np.fromfile(out, np.int64), io["gen_tokens"])
+    assert ctx.gemv_decode_enabled()
+
+
+@pytest.mark.gpu
+def test_decode_int4_needs_the_gpt2_small_row_lengths(ctx, tmp_path, capsys):
+    """--int4 on a model whose projections the int4 decode GEMV does not
+    cover (hidden 64 here; it needs hidden 768, ffn 3072) fails cleanly with
+    exit code 1. The int4 route itself is checked at GPT-2-small shape in
+    test_gpu_onnx.py."""
+    io = np.load(GOLDEN / "gpt2_tiny_past_io.npz")
+    ids, out = tmp_path / "prompt.bin", tmp_path / "toks.bin"
+    io["prompt"].astype(np.int64).tofile(ids)
+    assert cli.main(["decode", "--model", str(GOLDEN / "gpt2_tiny_prefill.onnx"),
+                     "--past-model", str(GOLDEN / "gpt2_tiny_past.onnx"),
+                     "--prompt-ids", str(ids), "--max-tokens", "4", "--output", str(out),
+                     "--int4"]) == 1
+    assert "hidden 768, ffn 3072" in capsys.readouterr().err

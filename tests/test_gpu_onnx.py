@@ -130,6 +130,28 @@ def test_gpt2_small_with_past_graph_decode_config4(ctx):
     dec.close()
 
 
+def test_gpt2_small_graph_on_the_native_decoder_int4(ctx):
+    """`inferc decode --int4`'s route at GPT-2-small shape: the exported
+    with-past graph with config 4's weights bound, read back by parameter
+    name into the native decoder (Gpt2Decoder.from_graph), switched to int4
+    weight-only projections; tokens bit-exact against the CPU oracle on the
+    dequantised weights."""
+    import oracle as O
+    from inferc_amd import graphs
+
+    cfg = graphs.GPT2_SMALL
+    w = graphs.gpt2_weights(cfg, 2)
+    g = rt.Graph.from_onnx(GOLDEN / "gpt2_small_past_noparams.onnx")
+    graphs.gpt2_bind_weights(g, cfg, w)
+    prompt = graphs.gpt2_prompt(cfg, 16)
+    dec = rt.Gpt2Decoder.from_graph(ctx, g, max_t=48)
+    dec.use_int4()
+    toks, _, _ = dec.generate(prompt, 16)
+    ref, _, _ = O.gpt2_generate(cfg, graphs.gpt2_int4_dequantized(cfg, w), prompt, 16)
+    np.testing.assert_array_equal(toks, ref)
+    dec.close()
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("P,S,fill", [(0, 40, -3.4028234663852886e38), (29, 1, -3.4028234663852886e38),
                                       (300, 3, float("-inf")), (150, 2, -1e4)])

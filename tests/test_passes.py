@@ -499,3 +499,28 @@ def test_pipeline_on_gpt2_small_structure_export():
     ex.run_async()
     assert ex.output_shape("logits") == ((1, 1, 50257), np.dtype(np.float32))
     assert ex.output_shape("present.11.value") == ((1, 12, 33, 64), np.dtype(np.float32))
+
+
+def test_gpt2_weights_read_back_from_the_exported_graph():
+    """graphs.gpt2_weights_from_graph (the weights `inferc decode --native /
+    --int4` hands the native decoder) returns exactly the weights bound into
+    the GPT-2-small structure export, in gpt2_weights' order, and the config
+    of BASELINE config 4 (heads from the past inputs, eps from the fused
+    LayerNorms)."""
+    from inferc_amd import graphs
+
+    cfg = graphs.GPT2_SMALL
+    w = graphs.gpt2_weights(cfg, 2)
+    g = Graph.from_onnx(Path(__file__).resolve().parent / "golden" /
+                        "gpt2_small_past_noparams.onnx")
+    graphs.gpt2_bind_weights(g, cfg, w)
+    with pytest.raises(ValueError):
+        graphs.gpt2_weights_from_graph(Graph())
+    assert g.run_pass("recognize_layernorm") == 25
+    got_cfg, got = graphs.gpt2_weights_from_graph(g)
+    assert {k: v for k, v in got_cfg.items() if k != "eps"} == \
+        {k: v for k, v in cfg.items() if k != "eps"}
+    assert np.float32(got_cfg["eps"]) == np.float32(cfg["eps"])
+    assert len(got) == len(w)
+    for a, b in zip(got, w):
+        np.testing.assert_array_equal(a, b)
