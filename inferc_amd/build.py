@@ -52,8 +52,26 @@ CXXFLAGS = [
 ]
 
 
-def _compile(src: Path, out_dir: Path = BUILD, extra: tuple = ()) -> Path:
-    obj = out_dir / (src.stem + ".o")
+# Sources compiled more than once, each time with other defines (object
+# suffix, flags): gemm_tile.hip holds the LDS-tiled GEMM's launcher for one
+# tile form and A orientation per compile, so the forms build in parallel.
+VARIANTS = {
+    "gemm_tile": [(f"_f{f}_t{t}", (f"-DIH_TILE_FORM={f}", f"-DIH_TILE_TA={t}"))
+                  for f in range(4) for t in range(2)],
+}
+
+
+def _jobs(sources: list[Path]) -> list[tuple[Path, str, tuple]]:
+    """(source, object suffix, extra flags) for every compile."""
+    out = []
+    for src in sources:
+        for suffix, flags in VARIANTS.get(src.stem, [("", ())]):
+            out.append((src, suffix, flags))
+    return out
+
+
+def _compile(src: Path, out_dir: Path = BUILD, extra: tuple = (), suffix: str = "") -> Path:
+    obj = out_dir / (src.stem + suffix + ".o")
     cmd = [HIPCC, *CXXFLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -69,9 +87,14 @@ def build(jobs: int | None = None, verbose: bool = False, sanitize: bool = False
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    jobs = jobs or min(len(sources), os.cpu_count() or 4, 8)
+    work = _jobs(sources)
+    # the slowest compiles first, so they do not start last
+    work.sort(key=lambda w: w[0].stem != "gemm_tile")
+    jobs = jobs or min(len(work), os.cpu_count() or 4, 8)
+    for stale in out_dir.glob("*.o"):
+        stale.unlink()
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(lambda src: _compile(src, out_dir, extra), sources))
+        objs = list(pool.map(lambda w: _compile(w[0], out_dir, extra + w[2], w[1]), work))
     tmp = lib.with_suffix(".so.tmp")
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *extra, *map(str, objs), "-o",
            str(tmp)]
