@@ -405,6 +405,22 @@ int inferc_executor_set_graph_mode(inferc_executor* ex, int enabled);
  * replaces the reference's present -> past renaming through host tensors
  * (src/cli/main.cpp:831-836, 883-888). max_t = 0 unbinds. */
 int inferc_executor_bind_kv_cache(inferc_executor* ex, int64_t max_t);
+/* Decode mode for a with-past graph bound to a KV cache (no counterpart in
+ * the reference, which re-plans every step of main.cpp:854-889): the caches
+ * hold `len` positions (each FusedAttentionPast cache must hold at least
+ * that many), a count kept on the device. Each run is then one decode step:
+ * the caller gives the past inputs by shape with length 0 and the attention
+ * mask (mask_input, nullable) for the new positions alone, all ones (as
+ * `inferc decode` feeds, main.cpp:792-799); the attention nodes take the
+ * past length from the device and ignore the mask, the position-embedding
+ * gathers start at it, and the step advances it. Consecutive steps thus walk
+ * the same graph: the second records a HIP graph, the rest replay it. Fails
+ * with INFERC_ERR_UNSUPPORTED when a value derived from the past length
+ * reaches anything else. len < 0 leaves decode mode. */
+int inferc_executor_set_decode_position(inferc_executor* ex, int64_t len,
+                                        const char* mask_input);
+/* Positions the caches hold in decode mode (-1 outside it). */
+int inferc_executor_decode_position(inferc_executor* ex, int64_t* len);
 /* An input that carries only a shape (no data): a past the KV cache holds.
  * A node that needs its data fails with INFERC_ERR_STATE. */
 int inferc_executor_set_input_shape(inferc_executor* ex, const char* name,

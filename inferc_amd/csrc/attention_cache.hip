@@ -52,6 +52,7 @@ __global__ __launch_bounds__(64 * kCaWaves) void cache_attn_kernel(CacheAttnArgs
   const float* kbase = p.kc + (b * p.nH + h) * p.max_t * p.dh;
   const float* vbase = p.vc + (b * p.nH + h) * p.max_t * p.dh;
   const uint8_t* mrow = p.mask ? p.mask + b * p.ms[0] + h * p.ms[1] + i * p.ms[2] : nullptr;
+  const int64_t T = p.pos ? *p.pos + p.S : p.T;
   auto score = [&](int64_t j) {
     const float* kr = kbase + j * p.dh;
     float s = 0.0f;
@@ -61,20 +62,20 @@ __global__ __launch_bounds__(64 * kCaWaves) void cache_attn_kernel(CacheAttnArgs
     return s;
   };
   float mx = -INFINITY;
-  for (int64_t j0 = 0; j0 < p.T; j0 += 64) {
+  for (int64_t j0 = 0; j0 < T; j0 += 64) {
     const int64_t j = j0 + lane;
-    if (live && j < p.T) mx = fmaxf(mx, score(j));
+    if (live && j < T) mx = fmaxf(mx, score(j));
   }
   mx = wave_max(mx);
   float part = 0.0f;
   float acc[kCaMaxDh / 64] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int64_t j0 = 0; j0 < p.T; j0 += 64) {
+  for (int64_t j0 = 0; j0 < T; j0 += 64) {
     const int64_t j = j0 + lane;
-    const float e = (live && j < p.T) ? expf(score(j) - mx) : 0.0f;
+    const float e = (live && j < T) ? expf(score(j) - mx) : 0.0f;
     part += e;
     es[wave][lane] = e;
     __syncthreads();
-    const int n = int(p.T - j0 < 64 ? p.T - j0 : 64);
+    const int n = int(T - j0 < 64 ? T - j0 : 64);
     if (live) {
       for (int k = 0; k < n; ++k) {
         const float ek = es[wave][k];
@@ -107,6 +108,9 @@ __global__ __launch_bounds__(64 * kCaWaves) void cache_attn_kernel(CacheAttnArgs
 // scores `fill`), their maximum m, e_j = exp(s_j - m), l = sum e_j and
 // O = sum e_j v_j over the wave's 64 dims, merged online within the wave and
 // across the eight waves through LDS in wave order; out = O / L.
+// With kn/vn given, the new rows (keys P .. T-1) are read from there, and
+// wave 0 of the block of query row i appends row P + i of its head to the
+// cache (no read of the cache depends on that write).
 constexpr int kCa64Waves = 8;
 constexpr int kCa64Chunk = 32;
 
@@ -119,9 +123,18 @@ __global__ __launch_bounds__(64 * kCa64Waves) void cache_attn_d64_kernel(CacheAt
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t r = blockIdx.x;  // (b, h, i), i fastest
   const int64_t i = r % p.S, h = (r / p.S) % p.nH, b = r / (p.S * p.nH);
-  const int64_t T = p.T;
-  const float* kbase = p.kc + (b * p.nH + h) * p.max_t * D;
-  const float* vbase = p.vc + (b * p.nH + h) * p.max_t * D;
+  const int64_t P = p.pos ? *p.pos : p.T - p.S, T = P + p.S;
+  float* kcache = const_cast<float*>(p.kc) + (b * p.nH + h) * p.max_t * D;
+  float* vcache = const_cast<float*>(p.vc) + (b * p.nH + h) * p.max_t * D;
+  const float* kbase = kcache;
+  const float* vbase = vcache;
+  // new rows: key j >= P is row j - P of kn / vn (their head's 64 columns)
+  const float* knb = p.kn ? p.kn + b * p.S * p.ldn + h * D : nullptr;
+  const float* vnb = p.vn ? p.vn + b * p.S * p.ldn + h * D : nullptr;
+  if (p.kn && wave == 0) {
+    kcache[(P + i) * D + lane] = knb[i * p.ldn + lane];
+    vcache[(P + i) * D + lane] = vnb[i * p.ldn + lane];
+  }
   const uint8_t* mrow = p.mask ? p.mask + b * p.ms[0] + h * p.ms[1] + i * p.ms[2] : nullptr;
   const int dh = (lane & 1) * 32;
   const float* qrow = p.q + (b * p.S + i) * p.ldq + h * D;
@@ -132,7 +145,7 @@ __global__ __launch_bounds__(64 * kCa64Waves) void cache_attn_d64_kernel(CacheAt
   for (int64_t j0 = int64_t(wave) * kCa64Chunk; j0 < T; j0 += kCa64Waves * kCa64Chunk) {
     const int64_t jl = j0 + (lane >> 1);
     const int64_t jc = jl < T ? jl : T - 1;
-    const float* kr = kbase + jc * D;
+    const float* kr = knb && jc >= P ? knb + (jc - P) * p.ldn : kbase + jc * D;
     float4 kv[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) kv[k] = *reinterpret_cast<const float4*>(kr + dh + 4 * k);
@@ -140,7 +153,7 @@ __global__ __launch_bounds__(64 * kCa64Waves) void cache_attn_d64_kernel(CacheAt
 #pragma unroll
     for (int k = 0; k < kCa64Chunk; ++k) {
       const int64_t jv = j0 + k < T ? j0 + k : T - 1;
-      vv[k] = vbase[jv * D + lane];
+      vv[k] = vnb && jv >= P ? vnb[(jv - P) * p.ldn + lane] : vbase[jv * D + lane];
     }
     const bool masked = mrow != nullptr && mrow[jc * p.ms[3]] != 0;
     float dot = 0.0f;
@@ -205,7 +218,9 @@ __global__ __launch_bounds__(256) void cache_write_tokens_kernel(int64_t B, int6
                                                                  int64_t t0,
                                                                  const float* __restrict__ src,
                                                                  int64_t ld,
-                                                                 float* __restrict__ cache) {
+                                                                 float* __restrict__ cache,
+                                                                 const int64_t* pos) {
+  if (pos) t0 += *pos;
   const int64_t total = B * S * nH * dh;
   for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < total;
        e += int64_t(gridDim.x) * 256) {
@@ -214,12 +229,49 @@ __global__ __launch_bounds__(256) void cache_write_tokens_kernel(int64_t B, int6
   }
 }
 
+// out[i, :] = table[min(*pos + i, rows - 1), :]
+__global__ __launch_bounds__(256) void gather_rows_at_kernel(int64_t rows, int64_t row_len,
+                                                             const float* __restrict__ table,
+                                                             const int64_t* __restrict__ pos,
+                                                             int64_t n, float* __restrict__ out) {
+  const int64_t p0 = *pos;
+  for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < n * row_len;
+       e += int64_t(gridDim.x) * 256) {
+    const int64_t i = e / row_len, c = e % row_len;
+    int64_t rw = p0 + i;
+    rw = rw < 0 ? 0 : rw < rows ? rw : rows - 1;
+    out[e] = table[rw * row_len + c];
+  }
+}
+
+__global__ void advance_position_kernel(int64_t* pos, int64_t step) {
+  if (threadIdx.x == 0) *pos += step;
+}
+
 }  // namespace
+
+void gather_rows_at(inferc_hip_ctx* ctx, int64_t rows, int64_t row_len, const float* table,
+                    const int64_t* pos, int64_t n, float* out) {
+  IH_REQUIRE(rows > 0 && row_len >= 0 && n >= 0, INFERC_ERR_SHAPE, "gather: bad shape");
+  if (n == 0 || row_len == 0) return;
+  IH_REQUIRE(table && pos && out, INFERC_ERR_ARG, "gather: null pointer");
+  const int64_t blocks = ceil_div(n * row_len, 256);
+  hipLaunchKernelGGL(gather_rows_at_kernel, dim3(unsigned(blocks > 1024 ? 1024 : blocks)),
+                     dim3(256), 0, ctx->stream, rows, row_len, table, pos, n, out);
+  check_launch("gather at position");
+}
+
+void advance_position(inferc_hip_ctx* ctx, int64_t* pos, int64_t step) {
+  IH_REQUIRE(pos != nullptr, INFERC_ERR_ARG, "advance: null position");
+  hipLaunchKernelGGL(advance_position_kernel, dim3(1), dim3(64), 0, ctx->stream, pos, step);
+  check_launch("advance position");
+}
 
 void cache_attention(inferc_hip_ctx* ctx, const CacheAttnArgs& a) {
   IH_REQUIRE(a.dh > 0 && a.dh <= kCaMaxDh, INFERC_ERR_UNSUPPORTED,
              "attention over a cache: head_dim must be in [1, 256]");
-  IH_REQUIRE(a.T >= 1 && a.T <= a.max_t && a.S >= 1 && a.S <= a.T, INFERC_ERR_SHAPE,
+  // (with the past length on the device, the caller checks T against max_t)
+  IH_REQUIRE(a.S >= 1 && (a.pos != nullptr || (a.T >= a.S && a.T <= a.max_t)), INFERC_ERR_SHAPE,
              "attention over a cache: bad lengths");
   IH_REQUIRE(a.ldq >= a.nH * a.dh && a.ldo >= a.nH * a.dh, INFERC_ERR_SHAPE,
              "attention over a cache: row stride smaller than the hidden size");
@@ -228,25 +280,39 @@ void cache_attention(inferc_hip_ctx* ctx, const CacheAttnArgs& a) {
   const float scale = 1.0f / sqrtf(float(a.dh));
   auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
   if (a.dh == 64 && a.ldq % 4 == 0 && al16(a.q) && al16(a.kc) && al16(a.vc) &&
+      (a.kn == nullptr || (a.ldn % 4 == 0 && al16(a.kn) && al16(a.vn))) &&
       rows < (int64_t(1) << 31)) {
     hipLaunchKernelGGL(cache_attn_d64_kernel, dim3(unsigned(rows)), dim3(64 * kCa64Waves), 0,
                        ctx->stream, a, scale);
     check_launch("cache attention");
     return;
   }
+  CacheAttnArgs g = a;
+  if (a.kn) {
+    // the general kernel reads every key from the cache: append first
+    const int64_t t0 = a.pos ? 0 : a.T - a.S;
+    cache_write_tokens(ctx, a.B, a.S, a.nH, a.dh, a.max_t, t0, a.kn, a.ldn,
+                       const_cast<float*>(a.kc), a.pos);
+    cache_write_tokens(ctx, a.B, a.S, a.nH, a.dh, a.max_t, t0, a.vn, a.ldn,
+                       const_cast<float*>(a.vc), a.pos);
+    g.kn = g.vn = nullptr;
+  }
   hipLaunchKernelGGL(cache_attn_kernel, dim3(unsigned(ceil_div(rows, kCaWaves))),
-                     dim3(64 * kCaWaves), 0, ctx->stream, a, scale);
+                     dim3(64 * kCaWaves), 0, ctx->stream, g, scale);
   check_launch("cache attention");
 }
 
 void cache_write_tokens(inferc_hip_ctx* ctx, int64_t B, int64_t S, int64_t nH, int64_t dh,
-                        int64_t max_t, int64_t t0, const float* src, int64_t ld, float* cache) {
-  IH_REQUIRE(t0 >= 0 && t0 + S <= max_t, INFERC_ERR_SHAPE, "KV cache: append past max_t");
+                        int64_t max_t, int64_t t0, const float* src, int64_t ld, float* cache,
+                        const int64_t* pos) {
+  // (with an offset on the device, the caller checks it against max_t)
+  IH_REQUIRE(t0 >= 0 && (pos != nullptr || t0 + S <= max_t), INFERC_ERR_SHAPE,
+             "KV cache: append past max_t");
   const int64_t total = B * S * nH * dh;
   if (total == 0) return;
   const int64_t blocks = ceil_div(total, 256);
   hipLaunchKernelGGL(cache_write_tokens_kernel, dim3(unsigned(blocks > 8192 ? 8192 : blocks)),
-                     dim3(256), 0, ctx->stream, B, S, nH, dh, max_t, t0, src, ld, cache);
+                     dim3(256), 0, ctx->stream, B, S, nH, dh, max_t, t0, src, ld, cache, pos);
   check_launch("cache write");
 }
 

@@ -58,6 +58,14 @@ std::string shape_str(const std::vector<int64_t>& s);
 struct CacheAttnArgs {
   int64_t B = 0, S = 0, nH = 0, dh = 0;
   int64_t T = 0, max_t = 0;
+  // Past length on the device (decode mode; null: T - S): the S new rows sit
+  // at *pos .. *pos + S - 1 and T is taken as *pos + S in the kernel.
+  const int64_t* pos = nullptr;
+  // New K/V rows [B, S, nH*dh] (row stride ldn), appended to the cache by
+  // the attention kernel itself (null: already in the cache).
+  const float* kn = nullptr;
+  const float* vn = nullptr;
+  int64_t ldn = 0;
   const float* q = nullptr;
   int64_t ldq = 0;
   const float* kc = nullptr;
@@ -69,8 +77,16 @@ struct CacheAttnArgs {
   int64_t ldo = 0;
 };
 void cache_attention(inferc_hip_ctx* ctx, const CacheAttnArgs& a);
-// cache[b, h, t0 + s, :] = src[b, s, h*dh : (h+1)*dh] for s < S.
+// cache[b, h, t0 + s, :] = src[b, s, h*dh : (h+1)*dh] for s < S, with t0
+// offset by *pos when pos (device) is given.
 void cache_write_tokens(inferc_hip_ctx* ctx, int64_t B, int64_t S, int64_t nH, int64_t dh,
-                        int64_t max_t, int64_t t0, const float* src, int64_t ld, float* cache);
+                        int64_t max_t, int64_t t0, const float* src, int64_t ld, float* cache,
+                        const int64_t* pos = nullptr);
+// out[i, :] = table[*pos + i, :] for i < n (rows clamped to the table): the
+// position-embedding rows of a decode step whose past length is on the device.
+void gather_rows_at(inferc_hip_ctx* ctx, int64_t rows, int64_t row_len, const float* table,
+                    const int64_t* pos, int64_t n, float* out);
+// *pos += step (one thread): a decode step's advance, recorded with the step.
+void advance_position(inferc_hip_ctx* ctx, int64_t* pos, int64_t step);
 
 }  // namespace ih

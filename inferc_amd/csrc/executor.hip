@@ -200,6 +200,20 @@ struct inferc_executor {
     int64_t rows = 0, T = 0, dh = 0, max_t = 0;
   };
   std::map<std::string, CacheView> cache_views;
+  // Decode mode (inferc_executor_set_decode_position): the KV caches hold
+  // decode_len positions, a count also kept on the device (decode_pos). A
+  // run walks the graph as if the past were empty, with an attention mask of
+  // the new positions alone: the attention nodes take the past length from
+  // the device (and ignore the mask: all ones), the position-embedding
+  // gathers (pos_gathers) add it to their rows, and the walk ends by
+  // advancing it. Every step then walks the same graph, and the second one
+  // on records the HIP graph that the rest replay.
+  bool decode = false;
+  int64_t decode_len = 0;
+  int64_t decode_step = 0;  // new positions per run (from the last walk)
+  int64_t* decode_pos = nullptr;
+  std::set<std::string> pos_gathers;
+  void plan_decode(const std::string& mask_input);
 
   void free_kv() {
     for (auto& c : kv) {
@@ -219,6 +233,7 @@ struct inferc_executor {
       if (kv.second.from_host && kv.second.v.dev) (void)hipFree(kv.second.v.dev);
     for (void* p : init_allocs) (void)hipFree(p);
     if (gather_err) (void)hipFree(gather_err);
+    if (decode_pos) (void)hipFree(decode_pos);
   }
 
   void drop_graph() {
@@ -1281,6 +1296,27 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     std::vector<int64_t> os(data.shape.begin(), data.shape.begin() + axis);
     for (int64_t d : idx.shape) os.push_back(d);
     for (int64_t i = axis + 1; i < r; ++i) os.push_back(data.shape[size_t(i)]);
+    if (decode && pos_gathers.count(n.name)) {
+      // decode mode: the indices, walked for an empty past, are the new
+      // positions 0 .. n-1; the rows are those past the device's past length
+      IH_REQUIRE(idx.host && idx.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED,
+                 "Gather: decode mode needs host-known position indices");
+      const std::vector<int64_t> ix = host_i64(idx, "Gather");
+      for (size_t i = 0; i < ix.size(); ++i)
+        IH_REQUIRE(ix[i] == int64_t(i), INFERC_ERR_UNSUPPORTED,
+                   "Gather: decode mode needs the positions of the new tokens in order");
+      require_f32(data, "data");
+      int64_t inner = 1;
+      for (int64_t i = axis + 1; i < r; ++i) inner *= data.shape[size_t(i)];
+      const int64_t ad = data.shape[size_t(axis)];
+      IH_REQUIRE(axis == 0, INFERC_ERR_UNSUPPORTED, "Gather: decode mode gathers rows (axis 0)");
+      IH_REQUIRE(decode_len + int64_t(ix.size()) <= ad, INFERC_ERR_SHAPE,
+                 "Gather: position past the end of the embedding table");
+      const float* dp = static_cast<const float*>(dev_of(n.in[0]));
+      float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, os).dev);
+      if (!dry) gather_rows_at(ctx, ad, inner, dp, decode_pos, idx.numel(), y);
+      return;
+    }
     if (data.host && idx.host && (data.dtype == INFERC_DT_I64 || data.dtype == INFERC_DT_I32) &&
         axis == 0 && r == 1) {
       // host shape plumbing (e.g. Gather(Shape(x), 1))
@@ -1641,6 +1677,10 @@ void inferc_executor::exec_attention_past(const inferc_graph::Node& n) {
   }
   const float* kn = static_cast<const float*>(dev_of(n.in[1]));
   const float* vn = static_cast<const float*>(dev_of(n.in[2]));
+  // the attention kernel appends the new rows itself
+  a.kn = kn;
+  a.vn = vn;
+  a.ldn = H;
   a.out = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, q.shape).dev);
   const std::vector<int64_t> present = {B, nH, T, dh};
   auto has_data = [&](const Value& v) { return v.dev != nullptr || v.host != nullptr; };
@@ -1659,14 +1699,21 @@ void inferc_executor::exec_attention_past(const inferc_graph::Node& n) {
         copy2d(ctx, ko, T * dh, pkp, P * dh, P * dh, B * nH);
         copy2d(ctx, vo, T * dh, pvp, P * dh, P * dh, B * nH);
       }
-      cache_write_tokens(ctx, B, S, nH, dh, T, P, kn, H, ko);
-      cache_write_tokens(ctx, B, S, nH, dh, T, P, vn, H, vo);
       cache_attention(ctx, a);
     }
     return;
   }
-  IH_REQUIRE(T <= kv_max_t, INFERC_ERR_SHAPE,
-             "FusedAttentionPast: " + std::to_string(T) + " positions exceed the KV cache (" +
+  if (decode) {
+    IH_REQUIRE(P == 0, INFERC_ERR_STATE,
+               "FusedAttentionPast: in decode mode the past inputs carry no positions (length 0)");
+    a.mask = nullptr;  // all ones: every cached key and the new ones (one row a step)
+    a.pos = decode_pos;
+    a.T = decode_len + S;
+    decode_step = S;
+  }
+  const int64_t Tc = decode ? decode_len + S : T;  // positions held after this run
+  IH_REQUIRE(Tc <= kv_max_t, INFERC_ERR_SHAPE,
+             "FusedAttentionPast: " + std::to_string(Tc) + " positions exceed the KV cache (" +
                  std::to_string(kv_max_t) + ")");
   KvCache& c = kv[n.name];
   if (c.k == nullptr || c.B != B || c.nH != nH || c.dh != dh) {
@@ -1683,8 +1730,8 @@ void inferc_executor::exec_attention_past(const inferc_graph::Node& n) {
     IH_HIP(hipMalloc(&c.v, bytes));
     c.B = B; c.nH = nH; c.dh = dh;
   }
-  const bool seed = P > 0 && has_data(pk) && has_data(pv);
-  IH_REQUIRE(seed || P <= c.len, INFERC_ERR_STATE,
+  const bool seed = !decode && P > 0 && has_data(pk) && has_data(pv);
+  IH_REQUIRE(decode || seed || P <= c.len, INFERC_ERR_STATE,
              "FusedAttentionPast: the KV cache holds " + std::to_string(c.len) +
                  " positions, the past says " + std::to_string(P));
   a.kc = c.k;
@@ -1696,16 +1743,14 @@ void inferc_executor::exec_attention_past(const inferc_graph::Node& n) {
     copy2d(ctx, c.k, kv_max_t * dh, pkp, P * dh, P * dh, B * nH);
     copy2d(ctx, c.v, kv_max_t * dh, pvp, P * dh, P * dh, B * nH);
   }
-  cache_write_tokens(ctx, B, S, nH, dh, kv_max_t, P, kn, H, c.k);
-  cache_write_tokens(ctx, B, S, nH, dh, kv_max_t, P, vn, H, c.v);
-  cache_attention(ctx, a);
-  c.len = T;
+  if (!dry) cache_attention(ctx, a);
+  c.len = Tc;
   for (int o = 1; o <= 2; ++o) {
     Value v;
     v.dtype = INFERC_DT_F32;
-    v.shape = present;
+    v.shape = {B, nH, Tc, dh};
     vals[n.out[size_t(o)]] = v;  // no contiguous data: read through the view
-    cache_views[n.out[size_t(o)]] = CacheView{o == 1 ? c.k : c.v, B * nH, T, dh, kv_max_t};
+    cache_views[n.out[size_t(o)]] = CacheView{o == 1 ? c.k : c.v, B * nH, Tc, dh, kv_max_t};
   }
 }
 
@@ -1970,6 +2015,7 @@ void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
     }
     if (act) act->push_back(track ? live_activation_bytes() : 0);
   }
+  if (decode && !dry) ih::advance_position(ctx, decode_pos, decode_step);
   if (events) IH_HIP(hipEventRecord(prof_ev[nodes.size()], ctx->stream));
   for (const auto& o : outputs) get(o);  // every graph output must exist
 }
@@ -2000,11 +2046,15 @@ void inferc_executor::run() {
     return;
   }
   ctx->make_current();
+  if (decode)
+    IH_REQUIRE(decode_len + std::max<int64_t>(decode_step, 1) <= kv_max_t, INFERC_ERR_SHAPE,
+               "decode: the KV cache (" + std::to_string(kv_max_t) + " positions) is full");
   stage_inputs();
   const std::string sig = signature();
   if (graph_mode && exec && graph_sig == sig && graph_ws_gen == ctx->ws_generation &&
       graph_route_gen == ctx->route_generation) {
     IH_HIP(hipGraphLaunch(exec, ctx->stream));
+    if (decode) decode_len += decode_step;
     return;
   }
   // a changed GEMV route is planned by an eager pass, as a new signature is
@@ -2015,6 +2065,7 @@ void inferc_executor::run() {
     walk();
     last_sig = sig;
     graph_route_gen = ctx->route_generation;
+    if (decode) decode_len += decode_step;
     return;
   }
   // second run with the same signature: record it, then replay
@@ -2038,6 +2089,62 @@ void inferc_executor::run() {
   graph_ws_gen = gen;
   graph_route_gen = route_gen;
   IH_HIP(hipGraphLaunch(exec, ctx->stream));
+  if (decode) decode_len += decode_step;
+}
+
+// Decode mode's plan: the values computed from the attention nodes' past
+// inputs and from the attention-mask input carry the past length. They may
+// reach the attention nodes only as their past or mask inputs, which decode
+// mode replaces by the cache and the device length, and the indices of
+// Gathers from an initializer (the position embeddings), which decode mode
+// offsets by the device length; no graph output may depend on them.
+void inferc_executor::plan_decode(const std::string& mask_input) {
+  // the graph inputs the attention nodes' past inputs are computed from
+  std::map<std::string, const inferc_graph::Node*> producer;
+  for (const auto& n : nodes)
+    for (const auto& o : n.out) producer[o] = &n;
+  std::set<std::string> mark, seen;
+  std::vector<std::string> todo;
+  for (const auto& n : nodes)
+    if (n.op == "FusedAttentionPast" && n.in.size() >= 5)
+      for (size_t k = 3; k <= 4; ++k)
+        if (!n.in[k].empty()) todo.push_back(n.in[k]);
+  IH_REQUIRE(!todo.empty(), INFERC_ERR_UNSUPPORTED,
+             "decode mode: the graph has no attention over a past");
+  while (!todo.empty()) {
+    const std::string v = todo.back();
+    todo.pop_back();
+    if (!seen.insert(v).second) continue;
+    auto pr = producer.find(v);
+    if (pr == producer.end()) {
+      if (!inits.count(v)) mark.insert(v);  // a graph input
+      continue;
+    }
+    for (const auto& i : pr->second->in)
+      if (!i.empty()) todo.push_back(i);
+  }
+  if (!mask_input.empty()) mark.insert(mask_input);
+  pos_gathers.clear();
+  for (const auto& n : nodes) {  // (in order: producers come first)
+    if (n.op == "FusedAttentionPast") {
+      for (size_t k = 0; k < 3 && k < n.in.size(); ++k)
+        IH_REQUIRE(!mark.count(n.in[k]), INFERC_ERR_UNSUPPORTED,
+                   "decode mode: attention input '" + n.in[k] + "' depends on the past length");
+      continue;
+    }
+    bool any = false;
+    for (const auto& i : n.in) any = any || mark.count(i) != 0;
+    if (!any) continue;
+    if (n.op == "Gather" && n.in.size() >= 2 && mark.count(n.in[1]) && !mark.count(n.in[0]) &&
+        inits.count(n.in[0])) {
+      pos_gathers.insert(n.name);
+      continue;
+    }
+    for (const auto& o : n.out) mark.insert(o);
+  }
+  for (const auto& o : outputs)
+    IH_REQUIRE(!mark.count(o), INFERC_ERR_UNSUPPORTED,
+               "decode mode: graph output '" + o + "' depends on the past length");
 }
 
 // Waits for the stream, then fails if a device-index gather of the passes
@@ -2099,10 +2206,17 @@ void inferc_executor::run_profiled(inferc_profiler* p) {
     drop_graph();  // buffers may be reallocated for the new shapes
     walk();
     last_sig = sig;
+    if (decode) {
+      // that pass advanced the device position: rewind it; the recorded pass
+      // then writes the same cache rows again
+      IH_HIP(hipStreamSynchronize(ctx->stream));
+      IH_HIP(hipMemcpy(decode_pos, &decode_len, sizeof(int64_t), hipMemcpyHostToDevice));
+    }
   }
   IH_HIP(hipStreamSynchronize(ctx->stream));
   p->begin_iteration();
   walk(&act, p->track_activation_bytes);
+  if (decode) decode_len += decode_step;
   IH_HIP(hipEventSynchronize(prof_ev[nodes.size()]));
   check_gather_err();
   for (size_t i = 0; i < nodes.size(); ++i) {
@@ -2463,6 +2577,9 @@ int inferc_executor_output_info(inferc_executor* ex, const char* name, int* dtyp
     *dtype = v.dtype;
     *rank = int(v.shape.size());
     for (size_t i = 0; i < v.shape.size(); ++i) shape[i] = v.shape[i];
+    // a present view in decode mode holds the positions of the last run
+    if (ex->decode && ex->cache_views.count(name) && v.shape.size() == 4)
+      shape[2] = ex->decode_len;
   });
 }
 
@@ -2484,7 +2601,10 @@ int inferc_executor_get_output(inferc_executor* ex, const char* name, void* host
     auto cv = ex->cache_views.find(name);
     if (!v.dev && !v.host && cv != ex->cache_views.end()) {
       const auto& w = cv->second;
-      const size_t row = size_t(w.T * w.dh) * sizeof(float);
+      const int64_t T = ex->decode ? ex->decode_len : w.T;
+      IH_REQUIRE(capacity_bytes >= size_t(w.rows * T * w.dh) * sizeof(float), INFERC_ERR_ARG,
+                 "output buffer too small");
+      const size_t row = size_t(T * w.dh) * sizeof(float);
       IH_HIP(hipMemcpy2D(host_dst, row, w.base, size_t(w.max_t * w.dh) * sizeof(float), row,
                          size_t(w.rows), hipMemcpyDeviceToHost));
       return;
@@ -2516,6 +2636,48 @@ int inferc_executor_bind_kv_cache(inferc_executor* ex, int64_t max_t) {
     ex->free_kv();
     ex->kv_max_t = max_t;
     ex->last_sig.clear();
+    ex->decode = false;
+  });
+}
+
+int inferc_executor_set_decode_position(inferc_executor* ex, int64_t len,
+                                        const char* mask_input) {
+  return ih::guard([&] {
+    check_ex(ex);
+    if (ex->dry) {
+      // planning only (no cache, no device): the plan's checks
+      ex->decode = len >= 0;
+      ex->decode_len = len;
+      if (ex->decode) ex->plan_decode(mask_input ? mask_input : "");
+      return;
+    }
+    IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+    ex->drop_graph();
+    ex->last_sig.clear();
+    if (len < 0) {
+      if (ex->decode)
+        for (auto& kv : ex->kv) kv.second.len = ex->decode_len;
+      ex->decode = false;
+      return;
+    }
+    IH_REQUIRE(ex->kv_max_t > 0, INFERC_ERR_STATE, "decode mode needs a bound KV cache");
+    IH_REQUIRE(len <= ex->kv_max_t, INFERC_ERR_SHAPE, "decode: position past the KV cache");
+    for (const auto& kv : ex->kv)
+      IH_REQUIRE(kv.second.len >= len, INFERC_ERR_STATE,
+                 "decode: the KV cache holds fewer positions than the decode position");
+    ex->plan_decode(mask_input ? mask_input : "");
+    if (!ex->decode_pos) IH_HIP(hipMalloc(&ex->decode_pos, sizeof(int64_t)));
+    IH_HIP(hipMemcpy(ex->decode_pos, &len, sizeof(int64_t), hipMemcpyHostToDevice));
+    ex->decode = true;
+    ex->decode_len = len;
+  });
+}
+
+int inferc_executor_decode_position(inferc_executor* ex, int64_t* len) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(len != nullptr, INFERC_ERR_ARG, "null argument");
+    *len = ex->decode ? ex->decode_len : -1;
   });
 }
 

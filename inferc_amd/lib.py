@@ -120,6 +120,8 @@ _SIGS = {
     "inferc_executor_set_input_shape": [vp, C.c_char_p, i32, i32, P(i64)],
     "inferc_executor_output_argmax": [vp, C.c_char_p, P(i64)],
     "inferc_executor_device_bytes": [vp, P(i64), P(i64), P(i64)],
+    "inferc_executor_set_decode_position": [vp, i64, C.c_char_p],
+    "inferc_executor_decode_position": [vp, P(i64)],
     "inferc_executor_output_device": [vp, C.c_char_p, P(vp)],
     "inferc_profiler_create": [P(vp)],
     "inferc_profiler_destroy": [vp],

@@ -795,6 +795,19 @@ class Executor:
         max_t positions (0 unbinds); see inferc_executor_bind_kv_cache."""
         check(self.ctx._lib.inferc_executor_bind_kv_cache(self.handle, max_t))
 
+    def set_decode_position(self, length: int, mask_input: str | None = None) -> None:
+        """Decode mode (inferc_executor_set_decode_position): the KV caches
+        hold `length` positions, counted on the device; every run is one step
+        with the past given by shape with length 0 and an all-ones mask of
+        the new positions. A negative length leaves decode mode."""
+        check(self.ctx._lib.inferc_executor_set_decode_position(
+            self.handle, int(length), mask_input.encode() if mask_input else None))
+
+    def decode_position(self) -> int:
+        v = C.c_int64()
+        check(self.ctx._lib.inferc_executor_decode_position(self.handle, C.byref(v)))
+        return v.value
+
     def set_input_shape(self, name: str, dtype, shape: Sequence[int]) -> None:
         """An input that carries only its shape (a past the KV cache holds)."""
         check(self.ctx._lib.inferc_executor_set_input_shape(
@@ -926,12 +939,24 @@ class OnnxDecoder:
             self.ex.run_async()
         return self.ex.output_argmax("logits")
 
+    def _decode_step(self, tok: int, profiler=None) -> int:
+        """One step in the executor's decode mode: only the token changes."""
+        self.ex.set_input("input_ids", np.array([[tok]], np.int64))
+        if profiler is not None:
+            self.ex.run_profiled(profiler)
+        else:
+            self.ex.run_async()
+        return self.ex.output_argmax("logits")
+
     def generate(self, prompt: np.ndarray, max_tokens: int, profiler=None,
-                 step_ms: list | None = None) -> np.ndarray:
+                 step_ms: list | None = None, decode_mode: bool = True) -> np.ndarray:
         """Greedy tokens. With a prefill graph the prompt runs there
         (main.cpp:786-828) and its present.* seed the cache on the first
         step, device to device; without one the prompt is the with-past
-        graph's first step. `profiler` records each post-prompt step as one
+        graph's first step. The steps after the first run in the executor's
+        decode mode (inferc_executor_set_decode_position), where they replay
+        one recorded step; decode_mode=False walks every step with its grown
+        shapes instead. `profiler` records each post-prompt step as one
         iteration (main.cpp:846-872). `step_ms`, when given, receives each
         post-prompt step's host wall time in ms, from setting its inputs to
         its token (the step timer of main.cpp:863-872 around Run)."""
@@ -950,13 +975,26 @@ class OnnxDecoder:
                     for i in self.past}
         else:
             toks = [self._step(p, n)]
+        self.ex.set_decode_position(-1)
         for k in range(1, max_tokens):
             t0 = time.perf_counter()
-            toks.append(self._step(np.array([[toks[-1]]], np.int64), n + k, seed=seed,
-                                   profiler=profiler))
+            if decode_mode and k >= 2:
+                toks.append(self._decode_step(toks[-1], profiler))
+            else:
+                toks.append(self._step(np.array([[toks[-1]]], np.int64), n + k, seed=seed,
+                                       profiler=profiler))
+                if decode_mode and k + 1 < max_tokens:
+                    # the caches now hold n + k positions: switch to decode mode
+                    # (past by shape with length 0, the new position's mask)
+                    self.ex.set_decode_position(n + k, "attention_mask")
+                    for i in self.past:
+                        self.ex.set_input_shape(i["name"], np.float32,
+                                                [1, i["shape"][1], 0, i["shape"][3]])
+                    self.ex.set_input("attention_mask", np.ones((1, 1), np.int64))
             if step_ms is not None:
                 step_ms.append((time.perf_counter() - t0) * 1e3)
             seed = None
+        self.ex.set_decode_position(-1)
         return np.array(toks, np.int64)
 
     def logits(self) -> np.ndarray:

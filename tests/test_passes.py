@@ -524,3 +524,37 @@ def test_gpt2_weights_read_back_from_the_exported_graph():
     assert len(got) == len(w)
     for a, b in zip(got, w):
         np.testing.assert_array_equal(a, b)
+
+
+def test_decode_plan_on_exported_gpt2():
+    """inferc_executor_set_decode_position's plan on the GPT-2-small with-past
+    export: the values computed from the past inputs and the attention mask
+    reach only the attention nodes' past/mask inputs and the position
+    embedding's Gather, so decode mode is accepted; a graph output computed
+    from the mask's length is refused."""
+    from inferc_amd import graphs
+    from inferc_amd.rt import Executor
+
+    cfg = graphs.GPT2_SMALL
+    path = Path(__file__).resolve().parent / "golden" / "gpt2_small_past_noparams.onnx"
+    g = Graph.from_onnx(path)
+    graphs.gpt2_bind_weights(g, cfg, graphs.gpt2_weights(cfg, 2))
+    g.optimize()
+    ex = Executor.dry(g)
+    ex.set_decode_position(33, "attention_mask")
+    ex.set_input("input_ids", np.array([[5]], np.int64))
+    ex.set_input("attention_mask", np.ones((1, 1), np.int64))
+    for l in range(12):
+        for kv in ("key", "value"):
+            ex.set_input(f"past_key_values.{l}.{kv}", np.zeros((1, 12, 0, 64), np.float32))
+    ex.run_async()
+    assert ex.output_shape("logits") == ((1, 1, 50257), np.dtype(np.float32))
+    # an output that depends on the past length: refused
+    g2 = Graph.from_onnx(path)
+    graphs.gpt2_bind_weights(g2, cfg, graphs.gpt2_weights(cfg, 2))
+    g2.optimize()
+    g2.add_node("Shape", ["attention_mask"], ["mask_shape"])
+    g2.add_output("mask_shape")
+    ex2 = Executor.dry(g2)
+    with pytest.raises(RuntimeError, match="depends on the past length"):
+        ex2.set_decode_position(33, "attention_mask")
