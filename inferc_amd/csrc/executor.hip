@@ -76,6 +76,13 @@ int64_t attr_int(const inferc_graph::Node& n, const char* key, int64_t def) {
   return std::stoll(it->second);
 }
 
+// A float as attribute text that reads back to the same float.
+std::string float_text(float f) {
+  char b[32];
+  std::snprintf(b, sizeof b, "%.9g", double(f));
+  return b;
+}
+
 float attr_float(const inferc_graph::Node& n, const char* key, float def) {
   auto it = n.attrs.find(key);
   if (it == n.attrs.end()) return def;
@@ -572,6 +579,111 @@ void inferc_executor::peephole() {
       }
     }
   }
+  // Gemm chains of exported transformer layers, where views (Reshape) sit
+  // between the ops:
+  //  - Gemm -> [Reshape] -> Relu / Gelu / GeluTanh  ==>  Gemm with that
+  //    activation as its epilogue (the activation acts elementwise, so it
+  //    commutes with the view);
+  //  - Gemm -> [Reshape] -> Add(., r)  ==>  Gemm with r as its residual,
+  //    when r is no initializer and exists before the Gemm runs (the
+  //    residual stream of a pre-LN layer);
+  //  - FusedLayerNorm(x) -> [Reshape] -> Gemm (as A)  ==>  Gemm normalizing
+  //    its A rows, the view taking x (LayerNorm acts on rows over the last
+  //    axis, which the view must keep: checked when the Gemm runs).
+  // Each intermediate must have the one reader. On the one-row GEMV route
+  // all three become the GEMV's prologue and epilogue.
+  auto sole_reader = [&](const std::string& t, size_t from) -> int {
+    if (uses[t] != 1) return -1;
+    for (size_t j = from; j < nodes.size(); ++j) {
+      if (dead[j]) continue;
+      if (std::find(nodes[j].in.begin(), nodes[j].in.end(), t) != nodes[j].in.end())
+        return int(j);
+    }
+    return -1;
+  };
+  static const std::map<std::string, int> gemm_acts = {
+      {"Relu", INFERC_ACT_RELU}, {"Gelu", INFERC_ACT_GELU_ERF},
+      {"GeluTanh", INFERC_ACT_GELU_TANH}};
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    inferc_graph::Node& n = nodes[i];
+    if (dead[i] || n.op != "Gemm" || n.out.size() != 1 || n.attrs.count("__act") ||
+        ih::attr_int(n, "transA", 0) != 0)
+      continue;
+    int c = sole_reader(n.out[0], i + 1);
+    if (c < 0) continue;
+    int view = -1;  // a Reshape between the Gemm and its reader
+    if (nodes[size_t(c)].op == "Reshape" && nodes[size_t(c)].in[0] == n.out[0] &&
+        nodes[size_t(c)].out.size() == 1) {
+      view = c;
+      c = sole_reader(nodes[size_t(c)].out[0], size_t(c) + 1);
+      if (c < 0) continue;
+    }
+    inferc_graph::Node& d = nodes[size_t(c)];
+    const std::string t = view >= 0 ? nodes[size_t(view)].out[0] : n.out[0];
+    auto act = gemm_acts.find(d.op);
+    if (act != gemm_acts.end() && d.in.size() == 1 && d.in[0] == t && d.out.size() == 1) {
+      n.attrs["__act"] = std::to_string(act->second);
+    } else if (d.op == "Add" && d.in.size() == 2 && d.out.size() == 1 &&
+               (d.in[0] == t) != (d.in[1] == t)) {
+      const std::string res = d.in[0] == t ? d.in[1] : d.in[0];
+      const int pr = producer(res);
+      if (inits.count(res) || pr >= int(i) || n.in.size() < 2) continue;
+      n.attrs["__res"] = res;
+    } else {
+      continue;
+    }
+    // the reader's output is now the Gemm's (through the view, if any)
+    if (view >= 0)
+      nodes[size_t(view)].out = d.out;
+    else
+      n.out = d.out;
+    dead[size_t(c)] = true;
+  }
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    inferc_graph::Node& ln = nodes[i];
+    if (dead[i] || ln.op != "FusedLayerNorm" || ln.in.size() != 3 || ln.out.size() != 1 ||
+        !inits.count(ln.in[1]) || !inits.count(ln.in[2]) ||
+        std::find(outputs.begin(), outputs.end(), ln.out[0]) != outputs.end())
+      continue;
+    // readers of the LayerNorm's output; Shape nodes only need its shape,
+    // which is its input's
+    std::vector<size_t> shapes;
+    int c = -1, others = 0;
+    for (size_t j = i + 1; j < nodes.size(); ++j) {
+      if (dead[j]) continue;
+      const auto& in = nodes[j].in;
+      if (std::find(in.begin(), in.end(), ln.out[0]) == in.end()) continue;
+      if (nodes[j].op == "Shape") {
+        shapes.push_back(j);
+      } else {
+        c = int(j);
+        ++others;
+      }
+    }
+    if (others != 1 || c < 0) continue;
+    int view = -1;
+    if (nodes[size_t(c)].op == "Reshape" && nodes[size_t(c)].in[0] == ln.out[0] &&
+        nodes[size_t(c)].out.size() == 1) {
+      view = c;
+      c = sole_reader(nodes[size_t(c)].out[0], size_t(c) + 1);
+      if (c < 0) continue;
+    }
+    inferc_graph::Node& g = nodes[size_t(c)];
+    const std::string t = view >= 0 ? nodes[size_t(view)].out[0] : ln.out[0];
+    if (g.op != "Gemm" || g.in.empty() || g.in[0] != t || ih::attr_int(g, "transA", 0) != 0 ||
+        g.attrs.count("__ln_g"))
+      continue;
+    g.attrs["__ln_g"] = ln.in[1];
+    g.attrs["__ln_b"] = ln.in[2];
+    g.attrs["__ln_eps"] = ih::float_text(ih::attr_float(ln, "epsilon", 1e-5f));
+    g.attrs["__ln_x"] = ln.in[0];  // the rows normalized, for the last-axis check
+    if (view >= 0)
+      nodes[size_t(view)].in[0] = ln.in[0];
+    else
+      g.in[0] = ln.in[0];
+    for (size_t j : shapes) nodes[j].in[0] = ln.in[0];
+    dead[i] = true;
+  }
   // Add(a, b) -> FusedLayerNorm (its only reader)  ==>  LayerNorm with a
   // residual input: the embedding sum word + position goes straight into
   // the LayerNorm kernel (activation.cc:103-150 on the summed rows).
@@ -617,7 +729,7 @@ void inferc_executor::peephole() {
         for (inferc_graph::Node* t : {&c, &gt}) {
           t->attrs["__ln_g"] = ln.in[1];
           t->attrs["__ln_b"] = ln.in[2];
-          t->attrs["__ln_eps"] = std::to_string(ih::attr_float(ln, "epsilon", 1e-5f));
+          t->attrs["__ln_eps"] = ih::float_text(ih::attr_float(ln, "epsilon", 1e-5f));
         }
         gt.in[0] = ln.in[0];
         dead[size_t(li)] = true;
@@ -1070,17 +1182,31 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
       g.C = static_cast<const float*>(dev_of(n.in[2]));
     }
     g.act = int(attr_int(n, "__act", INFERC_ACT_NONE));
+    auto rs = n.attrs.find("__res");
+    if (rs != n.attrs.end()) {
+      // the residual Add folded in by the peephole (through a view)
+      const Value& rv = get(rs->second);
+      IH_REQUIRE(rv.dtype == INFERC_DT_F32 && rv.numel() == g.M * g.N, INFERC_ERR_UNSUPPORTED,
+                 "Gemm: the residual added to its result must match it element for element");
+      g.R = static_cast<const float*>(dev_of(rs->second));
+      g.ldr = g.N;
+    }
     g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, {g.M, g.N}).dev);
     g.ldy = g.N;
     batch1_route(g, n.in[1]);
     auto ln = n.attrs.find("__ln_g");
     if (ln != n.attrs.end() && !ln_gemm_off.count(n.in[0])) {
-      // A's rows through the LayerNorm that preceded the Gather (peephole)
+      // A's rows through a LayerNorm that the peephole moved here (it
+      // preceded a Gather or a view of A)
       const float* lg = static_cast<const float*>(dev_of(ln->second));
       const float* lb = static_cast<const float*>(dev_of(n.attrs.at("__ln_b")));
       const float eps = std::stof(n.attrs.at("__ln_eps"));
       IH_REQUIRE(!g.trans_a && inits.at(ln->second).numel() == g.K, INFERC_ERR_SHAPE,
                  "Gemm: LayerNorm of A: scale size must equal K");
+      auto lx = n.attrs.find("__ln_x");
+      IH_REQUIRE(lx == n.attrs.end() || get(lx->second).shape.back() == g.K,
+                 INFERC_ERR_UNSUPPORTED,
+                 "Gemm: the view between a LayerNorm and A must keep the feature axis");
       if (gemm_gemv_route(ctx, g)) {
         g.gemv_ln_g = lg;
         g.gemv_ln_b = lb;
@@ -1498,6 +1624,27 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     int64_t outer = 1, inner = 1;
     for (int64_t i = 0; i < axis; ++i) outer *= x.shape[size_t(i)];
     for (int64_t i = axis + 1; i < r; ++i) inner *= x.shape[size_t(i)];
+    IH_REQUIRE(int64_t(sizes.size()) <= int64_t(n.out.size()), INFERC_ERR_ARG,
+               "Split: more parts than outputs");
+    if (outer == 1) {
+      // nothing before the axis: each part is a contiguous range of X, read
+      // in place (one decode row split into q, k, v)
+      int64_t off = 0;
+      for (int64_t sz : sizes) off += sz;
+      IH_REQUIRE(off == x.shape[size_t(axis)], INFERC_ERR_SHAPE, "Split: sizes do not add up");
+      const float* xp = static_cast<const float*>(dev_of(n.in[0]));
+      off = 0;
+      for (size_t i = 0; i < sizes.size(); ++i) {
+        Value v;
+        v.dtype = INFERC_DT_F32;
+        v.shape = x.shape;
+        v.shape[size_t(axis)] = sizes[i];
+        v.dev = const_cast<float*>(xp) + off * inner;
+        vals[n.out[i]] = v;
+        off += sizes[i];
+      }
+      return;
+    }
     std::vector<float*> outs;
     for (size_t i = 0; i < sizes.size() && i < n.out.size(); ++i) {
       std::vector<int64_t> s = x.shape;
