@@ -244,8 +244,9 @@ void orc_softmax(int64_t outer, int64_t axis_dim, int64_t inner,
 }
 
 /* src/kernels/elementwise.cc:69-189,225 (broadcast Add), restricted to the
- * trailing-repeat broadcasts the hot path uses. Pinned: kernels_test.cc
- * Elementwise.* known answers. */
+ * trailing-repeat broadcasts the hot path uses (b repeats over a's leading
+ * axes). Pinned: kernels_test.cc:165-171, 267-291 known answers and the
+ * :196-216 input, as add_* cases of the golden KAT file. */
 void orc_add_bcast(int64_t n, const float* a, const float* b, int64_t b_n,
                    float* y) {
   for (int64_t i = 0; i < n; ++i) y[i] = a[i] + b[i % b_n];

@@ -124,6 +124,27 @@ def test_kat_concat():
     np.testing.assert_array_equal(O.concat([f32(p) for p in c["parts"]], c["axis"]), c["expect"])
 
 
+@pytest.mark.parametrize("name", ["add_row_broadcast", "add_no_broadcast", "add_scalar"])
+def test_kat_add_broadcast(name):
+    c = KAT[name]
+    y = O.add_bcast(f32(c["a"]), f32(c["b"])).ravel()
+    for i, v in c["expect_at"]:
+        assert abs(y[i] - v) <= c["tol"], (name, i, y[i], v)
+
+
+def test_kat_add_parallel_rows():
+    # kernels_test.cc:196-216 input: a[i] = i - 192 over [4, 96], a row of 2.0.
+    c = KAT["add_parallel_rows"]
+    n = int(np.prod(c["a_shape"]))
+    a = (np.arange(n, dtype=np.float32) - 192.0).reshape(c["a_shape"])
+    b = np.full((1, c["a_shape"][1]), c["b_value"], np.float32)
+    np.testing.assert_array_equal(O.add_bcast(a, b), a + np.float32(c["b_value"]))
+    # A per-row bias (not a repeat of one row) must not pass for the row broadcast.
+    col = np.arange(c["a_shape"][1], dtype=np.float32)
+    y = O.add_bcast(a, col[None, :])
+    np.testing.assert_array_equal(y[3], a[3] + col)
+
+
 # --------------------------------------------------- closed-form fixtures
 
 def test_gemm_fixture_sin_cos():
