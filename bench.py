@@ -491,10 +491,12 @@ def cpu_info() -> dict:
 
 
 def _time_cpu(fn, budget_s: float, max_n: int = 1000,
-              min_n: int = 1) -> tuple[float, float, int]:
+              min_n: int = 1, warm: bool = True) -> tuple[float, float, int]:
     """(min, mean) seconds of fn over as many calls as fit in budget_s (at
-    least min_n, at most max_n, after one untimed call)."""
-    fn()
+    least min_n, at most max_n, after one untimed call unless warm is
+    False)."""
+    if warm:
+        fn()
     ts = []
     t_end = time.perf_counter() + budget_s
     while len(ts) < min_n or (time.perf_counter() < t_end and len(ts) < max_n):
@@ -517,10 +519,11 @@ def cpu_baseline(enc_w, gpt2_w, full: bool) -> dict:
     """The C oracle (this repo's restatement of inferc's CPU kernels) timed on
     the host's cores, all cores (OpenMP default) and 1 thread, on bounded
     samples of every config: encoder b1 (the `value` workload) and b32,
-    FFN+LN M=128, QKV+MHA S=128, GPT-2 decode steps at cache lengths 32-47
-    and 144-159 (config 4 spans 32-159), and the 49-matrix int4 GEMV at B=1
-    and B=8 with GB/s as streamed int4 bytes / best time
-    (bench/amx/int4_gemv_amx.cc:556-567)."""
+    FFN+LN M=128/1024/4096, QKV+MHA S=128/512, GPT-2 decode steps at cache
+    lengths 32-47 and 144-159 (config 4 spans 32-159), and the 49-matrix
+    int4 GEMV at B=1 and B=8 with GB/s as streamed int4 bytes / best time
+    (bench/amx/int4_gemv_amx.cc:556-567). The 1-thread encoder b32 row is
+    one cold forward (about 9 s of work)."""
     import oracle as O
     from inferc_amd import graphs
 
@@ -531,14 +534,14 @@ def cpu_baseline(enc_w, gpt2_w, full: bool) -> dict:
     res = {"threads_all": all_t, "cpu": info, "configs": {}}
     c = res["configs"]
 
-    def timed(name, fn, budget_all, budget_1, unit_ms=True):
+    def timed(name, fn, budget_all, budget_1, warm_1=True):
         row = {}
         for th, budget in ((all_t, budget_all), (1, budget_1)):
             if budget is None:
                 continue
             O.set_num_threads(th)
             try:
-                best, mean, n = _time_cpu(fn, budget)
+                best, mean, n = _time_cpu(fn, budget, warm=th == all_t or warm_1)
             finally:
                 O.set_num_threads(all_t)
             key = "all" if th == all_t else "1t"
@@ -551,28 +554,31 @@ def cpu_baseline(enc_w, gpt2_w, full: bool) -> dict:
     if full:
         ids32, mask32 = graphs.encoder_inputs(cfg, 32, 128)
         log("  cpu: encoder b32 s128")
-        timed("encoder_b32_s128", lambda: O.encoder_forward(cfg, enc_w, ids32, mask32), 2.0, None)
-        g, x = ffn_ln_graph(128)
-        w1, b1, w2, b2 = (g.initializer(n) for n in ("w1", "b1", "w2", "b2"))
+        timed("encoder_b32_s128", lambda: O.encoder_forward(cfg, enc_w, ids32, mask32), 2.0,
+              0.0, warm_1=False)
         ones, zeros = np.ones(768, np.float32), np.zeros(768, np.float32)
+        for M in (128, 1024, 4096):
+            g, x = ffn_ln_graph(M)
+            w1, b1, w2, b2 = (g.initializer(n) for n in ("w1", "b1", "w2", "b2"))
 
-        def ffn():
-            f = O.fused_matmul_add_gelu(x, w1, b1)
-            return O.layernorm(O.add_bcast(O.matmul(f, w2), b2), ones, zeros, 1e-12)
+            def ffn(x=x, w1=w1, b1=b1, w2=w2, b2=b2):
+                f = O.fused_matmul_add_gelu(x, w1, b1)
+                return O.layernorm(O.add_bcast(O.matmul(f, w2), b2), ones, zeros, 1e-12)
 
-        log("  cpu: ffn+ln M=128")
-        timed("ffn_ln_m128", ffn, 2.0, 1.0)
-        g, xq, mask, _ = qkv_mha_graph(128)
-        qw = [g.initializer(n) for n in ("wq", "bq", "wk", "bk", "wv", "bv")]
-        x2 = xq.reshape(-1, 768)
+            log(f"  cpu: ffn+ln M={M}")
+            timed(f"ffn_ln_m{M}", ffn, 2.0, 1.0)
+        for S in (128, 512):
+            g, xq, mask, _ = qkv_mha_graph(S)
+            qw = [g.initializer(n) for n in ("wq", "bq", "wk", "bk", "wv", "bv")]
+            x2 = xq.reshape(-1, 768)
 
-        def qkv_mha():
-            q, k, v = O.fused_qkv(x2, *qw)
-            return O.fused_attention(q.reshape(32, 128, 768), k.reshape(32, 128, 768),
-                                     v.reshape(32, 128, 768), mask, 64, graphs.FILL_MIN)
+            def qkv_mha(x2=x2, qw=qw, mask=mask, S=S):
+                q, k, v = O.fused_qkv(x2, *qw)
+                return O.fused_attention(q.reshape(32, S, 768), k.reshape(32, S, 768),
+                                         v.reshape(32, S, 768), mask, 64, graphs.FILL_MIN)
 
-        log("  cpu: qkv+mha S=128")
-        timed("qkv_mha_b32_s128", qkv_mha, 2.0, None)
+            log(f"  cpu: qkv+mha S={S}")
+            timed(f"qkv_mha_b32_s{S}", qkv_mha, 2.0, 1.0, warm_1=False)
         gcfg = graphs.GPT2_SMALL
         dec = {}
         for lo, steps_all, steps_1 in ((32, 15, 6), (144, 15, 6)):
@@ -798,7 +804,7 @@ def main(argv=None) -> int:
     dec = None
     if not args.quick:
         log("encoder b32 s128")
-        ms_b32, _, _ = bench_encoder(ctx, 32, max(5, args.steps // 5), 2, enc_w)
+        ms_b32, _, _ = bench_encoder(ctx, 32, max(20, args.steps // 5), 3, enc_w)
         fl_b32 = encoder_flops(graphs.DISTILBERT, 32, 128)
         extra["encoder_b32_s128"] = {"ms": round(ms_b32, 4), "gflop": round(fl_b32 / 1e9, 2),
                                      "tflops": round(fl_b32 / (ms_b32 * 1e-3) / 1e12, 2),
