@@ -91,6 +91,11 @@ struct inferc_hip_ctx {
   // reference's g_gemv_decode_enabled, src/kernels/matmul.cc:56-61,207-216).
   bool gemv_decode = true;
   uint64_t route_generation = 0;  // bumped when gemv_decode changes
+  // Arrival counters of the small-M GEMM's tiles when K is split over blocks
+  // (zeroed once here; each launch leaves them zero). Launches on the
+  // context's one stream run in order, so they never share a counter.
+  static constexpr int64_t kKsCounters = 8192;
+  unsigned* ks_count = nullptr;
 
   // Device copies of small launch descriptor tables, keyed by their bytes,
   // so repeated launches over the same operands skip the upload.

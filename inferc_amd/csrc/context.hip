@@ -108,8 +108,12 @@ int inferc_hip_create(int device, inferc_hip_ctx** out) {
       IH_HIP(hipEventCreate(&c->ev_start));
       IH_HIP(hipEventCreate(&c->ev_stop));
       c->ws(size_t(16) << 20);
+      IH_HIP(hipMalloc(&c->ks_count, sizeof(unsigned) * inferc_hip_ctx::kKsCounters));
+      IH_HIP(hipMemset(c->ks_count, 0, sizeof(unsigned) * inferc_hip_ctx::kKsCounters));
       ih::init_gemm_scratch(device);
     } catch (...) {
+      if (c->ks_count) (void)hipFree(c->ks_count);
+      if (c->workspace) (void)hipFree(c->workspace);
       if (c->stream) (void)hipStreamDestroy(c->stream);
       delete c;
       throw;
@@ -126,6 +130,7 @@ int inferc_hip_destroy(inferc_hip_ctx* ctx) {
     for (auto& t : ctx->tables) (void)hipFree(t.dev);
     ctx->tables.clear();
     if (ctx->workspace) (void)hipFree(ctx->workspace);
+    if (ctx->ks_count) (void)hipFree(ctx->ks_count);
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

@@ -19,7 +19,9 @@
 // Shapes with too few 128x128 tiles to fill the 256 CUs go to one of two
 // other paths. Small M with float4-aligned row-major A (the b=1 encoder, GPT-2
 // prefill) goes to gemm_f32_ksplit: K is split between the waves of a block,
-// and the partial tiles are summed through LDS in the same launch. Other
+// and the partial tiles are summed through LDS in the same launch (for a long
+// K also over two blocks per tile, the later of which sums both partials in a
+// fixed order). Other
 // shapes run the 64x64 kernel with K split over blocks; partial sums land in
 // the context workspace, and a second kernel reduces them in fixed order
 // (deterministic) and applies the epilogue.
@@ -60,14 +62,24 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(GemmParams p) {
 // operand reuse for blocks to spread over the CUs, or 16x16 tiles when even
 // those give at most a quarter as many blocks as CUs (M=32, N=768 prefill:
 // 13.7 us vs 19.2 us).
-KsCfg pick_ksplit(int64_t M, int64_t N, int64_t slices, int64_t cus) {
+//
+// With K >= 2048, where 16x32 tiles leave CUs idle, K is also split over two
+// blocks of 16x48 tiles when that gives between one and two blocks per CU:
+// the b=1 FFN-down (M=128, N=768, K=3072) takes 11.8 us on 256 blocks
+// against 13.3 us on 192 (16x32, K whole); splitting out-proj, FFN-up or
+// QKV (K=768) the same way was slower in every form measured.
+KsCfg pick_ksplit(int64_t M, int64_t N, int64_t K, int64_t slices, int64_t cus, bool split_k) {
   const int64_t b48 = ceil_div(M, 32) * ceil_div(N, 48) * slices;
-  if (N % 48 == 0 && 4 * b48 >= 3 * cus) return KsCfg{32, 48, 8, 2};
+  if (N % 48 == 0 && 4 * b48 >= 3 * cus) return KsCfg{32, 48, 8, 2, 1};
   const int64_t big_blocks = ceil_div(M, 32) * ceil_div(N, 64) * slices;
-  if (2 * big_blocks >= cus) return KsCfg{32, 64, 8, 3};
+  if (2 * big_blocks >= cus) return KsCfg{32, 64, 8, 3, 1};
   const int64_t b16 = ceil_div(M, 16) * ceil_div(N, 32) * slices;
-  if (4 * b16 <= cus) return KsCfg{16, 16, 8, 2};
-  return KsCfg{16, 32, 8, 2};
+  if (4 * b16 <= cus) return KsCfg{16, 16, 8, 2, 1};
+  const int64_t z48 = 2 * ceil_div(M, 16) * (N / 48) * slices;
+  if (split_k && K >= 2048 && N % 48 == 0 && z48 >= cus && z48 <= 2 * cus &&
+      z48 / 2 <= inferc_hip_ctx::kKsCounters)
+    return KsCfg{16, 48, 8, 2, 2};
+  return KsCfg{16, 32, 8, 2, 1};
 }
 
 bool ksplit_supported(const GemmParams& p, int64_t slices, bool ta, bool vec, int64_t cus,
@@ -78,12 +90,21 @@ bool ksplit_supported(const GemmParams& p, int64_t slices, bool ta, bool vec, in
          ks_fits_i32(p);
 }
 
-void run_ksplit(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool tb) {
-  const KsCfg c = pick_ksplit(p.M, p.N, slices, ctx->num_cus);
-  if (c.wn == 48) launch_ksplit<32, 48, 8, 2>(p, slices, tb, ctx->stream);
-  else if (c.wm == 32) launch_ksplit<32, 64, 8, 3>(p, slices, tb, ctx->stream);
-  else if (c.wn == 16) launch_ksplit<16, 16, 8, 2>(p, slices, tb, ctx->stream);
-  else launch_ksplit<16, 32, 8, 2>(p, slices, tb, ctx->stream);
+// split_k: K may also be split over blocks (not for the allocation-free
+// entry point, whose scratch holds no counters).
+void run_ksplit(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool tb, bool split_k) {
+  const KsCfg c = pick_ksplit(p.M, p.N, p.K, slices, ctx->num_cus, split_k);
+  if (c.z > 1) {
+    const int64_t tiles = ceil_div(p.M, c.wm) * ceil_div(p.N, c.wn) * slices;
+    p.partial = static_cast<float*>(
+        ctx->ws(size_t(tiles) * size_t(c.z) * size_t(c.wm) * size_t(c.wn) * sizeof(float)));
+    p.ks_count = ctx->ks_count;
+  }
+  if (c.wm == 16 && c.wn == 48) launch_ksplit<16, 48, 8, 2>(p, slices, tb, c.z, ctx->stream);
+  else if (c.wn == 48) launch_ksplit<32, 48, 8, 2>(p, slices, tb, c.z, ctx->stream);
+  else if (c.wm == 32) launch_ksplit<32, 64, 8, 3>(p, slices, tb, c.z, ctx->stream);
+  else if (c.wn == 16) launch_ksplit<16, 16, 8, 2>(p, slices, tb, c.z, ctx->stream);
+  else launch_ksplit<16, 32, 8, 2>(p, slices, tb, c.z, ctx->stream);
   check_launch("gemm_f32_ksplit");
 }
 
@@ -97,7 +118,8 @@ void run(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool ta, bool tb, bo
   const int64_t cus = ctx->num_cus;
   const Cfg big{128, 128, 16}, mid{128, 96, 32}, wide{128, 64, 16}, small{64, 64, 32};
   auto tiles = [&](const Cfg& c) { return ceil_div(p.M, c.bm) * ceil_div(p.N, c.bn) * slices; };
-  if (ksplit_supported(p, slices, ta, vec, cus, tiles(big))) return run_ksplit(ctx, p, slices, tb);
+  if (ksplit_supported(p, slices, ta, vec, cus, tiles(big)))
+    return run_ksplit(ctx, p, slices, tb, partial_buf == nullptr);
   IH_REQUIRE(p.na_stats == nullptr && p.nr_stats == nullptr && p.st_out == nullptr,
              INFERC_ERR_UNSUPPORTED,
              "gemm: LayerNorm-on-read operands and row statistics need the small-M path");

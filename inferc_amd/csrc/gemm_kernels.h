@@ -41,6 +41,10 @@ struct GemmParams {
   int splits;
   int64_t k_per_split;
   float* partial;  // [slices][splits][M][N] when splits > 1
+  // small-M path with K also split over blocks (gridDim.z > 1): each tile's
+  // per-block partial sums ([slices][tiles][z][WM*WN] in partial) and its
+  // arrival counter (zero between launches)
+  unsigned* ks_count;
   // small-M path: LayerNorm of A's rows (over K) and R's rows (over N) as
   // read, from producer partials; Y's per-16-column (mean, M2) out
   const float* na_stats;
@@ -609,12 +613,17 @@ struct KsFrag {
 };
 
 // P is the register ring depth: k-groups in flight per wave.
+// With gridDim.z = Z > 1 the K range is also split over Z blocks per tile
+// (kpb_ each). Every block stores its partial tile, and the last of the Z to
+// arrive (an atomic counter per tile) sums the Z partials in z order, so the
+// result does not depend on arrival order, and runs the epilogue; it also
+// sets the counter back to zero for the next launch.
 template <int WM, int WN, int W, int P, bool TB, bool LNA, bool LNR>
 __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(const float* __restrict__ A0,
                                                           const float* __restrict__ B0,
                                                           int lda_, int ldb_, int M_, int N_, int K_,
                                                           int kps_, int tiles_m_, int tiles_n_,
-                                                          GemmParams p) {
+                                                          int kpb_, GemmParams p) {
   // The first ring needs only the leading scalar arguments, which the
   // hardware preloads into SGPRs at wave launch; the rest of p (epilogue,
   // LayerNorm terms, other slices) is read while those loads are in flight.
@@ -645,11 +654,13 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(const float* __restric
     B = p.use_table ? p.Bt[slice] : p.B + slice * p.sb;
   }
 
-  // Wave w owns K range [kb, ke); it runs `rings` rounds of P 16-deep
-  // k-groups (the host sizes k_per_split so that rounds are mostly full;
-  // groups past ke load zeros).
-  const int64_t kb = int64_t(wave) * kps;
-  const int64_t ke = kb + kps < K ? kb + kps : K;
+  // Wave w owns K range [kb, ke) of the block's [kbb, keb); it runs `rings`
+  // rounds of P 16-deep k-groups (the host sizes k_per_split so that rounds
+  // are mostly full; groups past ke load zeros).
+  const int64_t kbb = int64_t(blockIdx.z) * kpb_;
+  const int64_t keb = kbb + kpb_ < K ? kbb + kpb_ : K;
+  const int64_t kb = kbb + int64_t(wave) * kps;
+  const int64_t ke = kb + kps < keb ? kb + kps : keb;
   const int64_t rings = (kps + 16 * P - 1) / (16 * P);
 
   floatx4 acc[RA][CB];
@@ -743,14 +754,61 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(const float* __restric
     }
   __syncthreads();
 
+  float sum[EPT];
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int e = tid + 64 * W * k;
+    float s = 0.0f;
+    if (e < WM * WN) {
+      s = red[e];
+#pragma unroll
+      for (int w = 1; w < W; ++w) s += red[w * (WM * WN) + e];
+    }
+    sum[k] = s;
+  }
+  if (gridDim.z > 1) {
+    const int Z = gridDim.z;
+    __shared__ int last;
+    unsigned* cnt = p.ks_count + int64_t(slice) * T + t;
+    float* part = p.partial + (int64_t(slice) * T + t) * Z * (WM * WN);
+    // The partials are agent-scope atomic stores and loads, which write
+    // through to and read from the device-coherent level, so no fence has
+    // to write back or invalidate a whole L2 (a device-scope fence per block
+    // made these launches 10x slower). Each thread waits for its stores to
+    // complete before the barrier that precedes the count.
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = tid + 64 * W * k;
+      if (e < WM * WN)
+        __hip_atomic_store(part + int64_t(blockIdx.z) * (WM * WN) + e, sum[k], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+      last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             unsigned(Z - 1);
+    __syncthreads();
+    if (!last) return;
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = tid + 64 * W * k;
+      if (e >= WM * WN) continue;
+      float s = __hip_atomic_load(part + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int z = 1; z < Z; ++z)
+        s += __hip_atomic_load(part + int64_t(z) * (WM * WN) + e, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      sum[k] = s;
+    }
+    if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
   float* Y = p.use_table ? p.Yt[slice] : p.Y + slice * p.sy;
 #pragma unroll
   for (int k = 0; k < EPT; ++k) {
     const int e = tid + 64 * W * k;
     if (e >= WM * WN) break;
-    float s = red[e];
-#pragma unroll
-    for (int w = 1; w < W; ++w) s += red[w * (WM * WN) + e];
+    float s = sum[k];
     const int64_t row = m0 + e / WN, col = n0 + e % WN;
     if (row < M && col < N) {
       if constexpr (LNA) {
@@ -803,7 +861,7 @@ __global__ __launch_bounds__(64 * W) void gemm_f32_ksplit(const float* __restric
   }
 }
 
-struct KsCfg { int wm, wn, w, p; };
+struct KsCfg { int wm, wn, w, p, z; };  // z: blocks sharing one tile's K
 
 // The small-M kernel takes its extents and leading dimensions as 32-bit
 // kernel arguments.
@@ -817,13 +875,25 @@ inline int64_t ks_k_per_wave(int64_t K, int w, int depth) {
   return ceil_div(ceil_div(K, w), 16 * depth) * 16 * depth;
 }
 
+// K per block when K is split over z blocks per tile: a multiple of 16.
+inline int64_t ks_k_per_block(int64_t K, int z) { return ceil_div(ceil_div(K, z), 16) * 16; }
+
+// Launches the small-M kernel; z > 1 also splits K over z blocks per tile,
+// which needs p.partial (z * tiles * slices * WM * WN floats) and p.ks_count
+// (tiles * slices counters, zero).
 template <int WM, int WN, int W, int P>
-void launch_ksplit(GemmParams p, int64_t slices, bool tb, hipStream_t s) {
+void launch_ksplit(GemmParams p, int64_t slices, bool tb, int z, hipStream_t s) {
   p.splits = 1;
-  p.partial = nullptr;
-  p.k_per_split = ks_k_per_wave(p.K, W, P);
+  if (z <= 1) {
+    z = 1;
+    p.partial = nullptr;
+    p.ks_count = nullptr;
+  }
+  const int64_t kpb = z > 1 ? ks_k_per_block(p.K, z) : p.K;
+  p.k_per_split = ks_k_per_wave(kpb, W, P);
   const int64_t tm = ceil_div(p.M, WM), tn = ceil_div(p.N, WN);
-  const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(slices));
+  const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(slices),
+                  static_cast<unsigned>(z));
   const dim3 block(64 * W);
   const bool lna = p.na_stats != nullptr, lnr = p.nr_stats != nullptr;
   const float* B0 = p.use_table ? p.Bt[0] : p.B;  // slice 0's B
@@ -832,7 +902,7 @@ void launch_ksplit(GemmParams p, int64_t slices, bool tb, hipStream_t s) {
   if (tb == TB_ && lna == LNA_ && lnr == LNR_) {                                         \
     hipLaunchKernelGGL((gemm_f32_ksplit<WM, WN, W, P, TB_, LNA_, LNR_>), grid, block, 0, s, \
                        p.A, B0, int(p.lda), int(p.ldb), int(p.M), int(p.N), int(p.K),   \
-                       int(p.k_per_split), int(tm), int(tn), p);                        \
+                       int(p.k_per_split), int(tm), int(tn), int(kpb), p);              \
     return;                                                                               \
   }
   IH_KS(false, false, false)

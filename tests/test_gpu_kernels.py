@@ -206,6 +206,26 @@ def test_gemm_deterministic(ctx):
         np.testing.assert_array_equal(rt.Gemm(a, b).numpy(), first)
 
 
+def test_gemm_k_split_over_blocks_interleaved(ctx):
+    """Long-K small-M products whose K is also split over two blocks per
+    tile (the b=1 FFN-down shape and a ragged neighbour), launched
+    interleaved many times: each tile's arrival counter must be back at zero
+    after every launch, so every repeat gives the first result's bits, and
+    that result matches float64."""
+    cases = []
+    for M, seed in ((128, 31), (160, 32), (256, 33)):
+        A, B = rnd((M, 3072), seed), rnd((3072, 768), seed + 10, 0.03)
+        bias, res = rnd(768, seed + 20), rnd((M, 768), seed + 30)
+        args = (T(ctx, A), T(ctx, B), T(ctx, bias))
+        r = T(ctx, res)
+        got = rt.Gemm(*args, 1.0, 1.0, residual=r).numpy()
+        close(got, (A.astype(np.float64) @ B + bias) + res)
+        cases.append((args, r, got))
+    for _ in range(8):
+        for args, r, first in cases:
+            np.testing.assert_array_equal(rt.Gemm(*args, 1.0, 1.0, residual=r).numpy(), first)
+
+
 @pytest.mark.parametrize("M", [128, 1024, 4096])
 def test_config2_ffn_gelu_then_layernorm(ctx, M):
     """GELU_erf(X W1 + b1) -> W2 + b2 -> LayerNorm(eps 1e-12)."""
