@@ -64,10 +64,11 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(GemmParams p) {
 // 13.7 us vs 19.2 us).
 //
 // With K >= 2048, where 16x32 tiles leave CUs idle, K is also split over two
-// blocks of 16x48 tiles when that gives between one and two blocks per CU:
-// the b=1 FFN-down (M=128, N=768, K=3072) takes 11.8 us on 256 blocks
-// against 13.3 us on 192 (16x32, K whole); splitting out-proj, FFN-up or
-// QKV (K=768) the same way was slower in every form measured.
+// blocks of 16x48 tiles (16 waves each) when that gives between one and two
+// blocks per CU: the b=1 FFN-down (M=128, N=768, K=3072) takes 11.3 us on
+// 256 blocks against 13.3 us on 192 (16x32, K whole; 8 waves per 16x48
+// block: 11.7 us); splitting out-proj, FFN-up or QKV (K=768) the same way
+// was slower in every form measured.
 KsCfg pick_ksplit(int64_t M, int64_t N, int64_t K, int64_t slices, int64_t cus, bool split_k) {
   const int64_t b48 = ceil_div(M, 32) * ceil_div(N, 48) * slices;
   if (N % 48 == 0 && 4 * b48 >= 3 * cus) return KsCfg{32, 48, 8, 2, 1};
@@ -78,7 +79,7 @@ KsCfg pick_ksplit(int64_t M, int64_t N, int64_t K, int64_t slices, int64_t cus, 
   const int64_t z48 = 2 * ceil_div(M, 16) * (N / 48) * slices;
   if (split_k && K >= 2048 && N % 48 == 0 && z48 >= cus && z48 <= 2 * cus &&
       z48 / 2 <= inferc_hip_ctx::kKsCounters)
-    return KsCfg{16, 48, 8, 2, 2};
+    return KsCfg{16, 48, 16, 2, 2};
   return KsCfg{16, 32, 8, 2, 1};
 }
 
@@ -100,7 +101,7 @@ void run_ksplit(inferc_hip_ctx* ctx, GemmParams p, int64_t slices, bool tb, bool
         ctx->ws(size_t(tiles) * size_t(c.z) * size_t(c.wm) * size_t(c.wn) * sizeof(float)));
     p.ks_count = ctx->ks_count;
   }
-  if (c.wm == 16 && c.wn == 48) launch_ksplit<16, 48, 8, 2>(p, slices, tb, c.z, ctx->stream);
+  if (c.wm == 16 && c.wn == 48) launch_ksplit<16, 48, 16, 2>(p, slices, tb, c.z, ctx->stream);
   else if (c.wn == 48) launch_ksplit<32, 48, 8, 2>(p, slices, tb, c.z, ctx->stream);
   else if (c.wm == 32) launch_ksplit<32, 64, 8, 3>(p, slices, tb, c.z, ctx->stream);
   else if (c.wn == 16) launch_ksplit<16, 16, 8, 2>(p, slices, tb, c.z, ctx->stream);
