@@ -421,6 +421,25 @@ int inferc_executor_set_decode_position(inferc_executor* ex, int64_t len,
                                         const char* mask_input);
 /* Positions the caches hold in decode mode (-1 outside it). */
 int inferc_executor_decode_position(inferc_executor* ex, int64_t* len);
+/* Decode feedback, in decode mode: each run ends with the greedy token of
+ * `inferc decode` (first maximum of the last row of output `logits`,
+ * main.cpp:875-879), which becomes the value of input `ids` (bound by this
+ * call to a device [1,1] int64 holding first_token) for the next run and is
+ * recorded on the device at its sequence position; so steps run back to back
+ * with no host copy between them (the reference copies the token through
+ * host tensors each step, main.cpp:880-889). logits = NULL turns it off;
+ * leaving decode mode turns it off too. */
+int inferc_executor_set_decode_feedback(inferc_executor* ex, const char* logits,
+                                        const char* ids, int64_t first_token);
+/* `steps` runs of the executor back to back; with step_ms (steps floats) it
+ * waits for them and returns each run's device time from HIP events between
+ * the runs, as main.cpp:863-872 times each step; without, it returns once
+ * they are enqueued. */
+int inferc_executor_run_steps(inferc_executor* ex, int64_t steps, float* step_ms);
+/* The fed-back tokens at sequence positions first_pos .. first_pos + n - 1
+ * (the first is first_token's position). Synchronises the stream. */
+int inferc_executor_decode_tokens(inferc_executor* ex, int64_t first_pos, int64_t n,
+                                  int64_t* tokens);
 /* An input that carries only a shape (no data): a past the KV cache holds.
  * A node that needs its data fails with INFERC_ERR_STATE. */
 int inferc_executor_set_input_shape(inferc_executor* ex, const char* name,

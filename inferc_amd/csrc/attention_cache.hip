@@ -248,6 +248,19 @@ __global__ void advance_position_kernel(int64_t* pos, int64_t step) {
   if (threadIdx.x == 0) *pos += step;
 }
 
+// Decode feedback: the step's arg-max token becomes the next step's input
+// (ids[0]) and is recorded at its position in the history (hist[pos + step]);
+// then the position advances.
+__global__ void decode_feedback_kernel(int64_t* pos, int64_t step, const int64_t* tok,
+                                       int64_t* ids, int64_t* hist) {
+  if (threadIdx.x == 0) {
+    const int64_t p = *pos + step, t = *tok;
+    ids[0] = t;
+    hist[p] = t;
+    *pos = p;
+  }
+}
+
 }  // namespace
 
 void gather_rows_at(inferc_hip_ctx* ctx, int64_t rows, int64_t row_len, const float* table,
@@ -265,6 +278,14 @@ void advance_position(inferc_hip_ctx* ctx, int64_t* pos, int64_t step) {
   IH_REQUIRE(pos != nullptr, INFERC_ERR_ARG, "advance: null position");
   hipLaunchKernelGGL(advance_position_kernel, dim3(1), dim3(64), 0, ctx->stream, pos, step);
   check_launch("advance position");
+}
+
+void decode_feedback(inferc_hip_ctx* ctx, int64_t* pos, int64_t step, const int64_t* tok,
+                     int64_t* ids, int64_t* hist) {
+  IH_REQUIRE(pos && tok && ids && hist, INFERC_ERR_ARG, "decode feedback: null pointer");
+  hipLaunchKernelGGL(decode_feedback_kernel, dim3(1), dim3(64), 0, ctx->stream, pos, step, tok,
+                     ids, hist);
+  check_launch("decode feedback");
 }
 
 void cache_attention(inferc_hip_ctx* ctx, const CacheAttnArgs& a) {

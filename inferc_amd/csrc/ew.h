@@ -88,5 +88,10 @@ void gather_rows_at(inferc_hip_ctx* ctx, int64_t rows, int64_t row_len, const fl
                     const int64_t* pos, int64_t n, float* out);
 // *pos += step (one thread): a decode step's advance, recorded with the step.
 void advance_position(inferc_hip_ctx* ctx, int64_t* pos, int64_t step);
+// *pos advances by step after hist[*pos + step] = ids[0] = *tok (the decode
+// step's arg-max fed back as the next step's token; hist holds a position's
+// token at its index, so it needs the cache's max_t + 1 entries).
+void decode_feedback(inferc_hip_ctx* ctx, int64_t* pos, int64_t step, const int64_t* tok,
+                     int64_t* ids, int64_t* hist);
 
 }  // namespace ih

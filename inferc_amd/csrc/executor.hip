@@ -124,7 +124,8 @@ struct inferc_executor {
   struct Input {
     ih::Value v;
     bool from_host = false;
-    std::vector<uint8_t> staged;  // host bytes awaiting upload
+    std::vector<uint8_t> staged;  // host bytes, uploaded when set (dirty)
+    bool dirty = false;
     size_t cap = 0;               // bytes of the device buffer of a host input
   };
   std::unordered_map<std::string, Input> inputs;
@@ -219,8 +220,20 @@ struct inferc_executor {
   int64_t decode_len = 0;
   int64_t decode_step = 0;  // new positions per run (from the last walk)
   int64_t* decode_pos = nullptr;
-  std::set<std::string> pos_gathers;
+  // Per node (by index; node names may be empty or repeated): a position
+  // gather, and a node whose results decode mode never reads (the attention
+  // mask's own arithmetic: the attention nodes ignore the mask there).
+  std::vector<char> pos_gather_at, decode_skip_at;
+  size_t node_index(const inferc_graph::Node& n) const { return size_t(&n - nodes.data()); }
   void plan_decode(const std::string& mask_input);
+  // Decode feedback (inferc_executor_set_decode_feedback): every decode-mode
+  // run ends with the arg-max of fb_logits' last row, which becomes input
+  // fb_ids' value for the next run (fb_buf[0]) and is recorded at its
+  // position (fb_buf[1 + position]), so the steps replay back to back with
+  // no host copy between them.
+  std::string fb_logits, fb_ids;
+  int64_t* fb_buf = nullptr;
+  std::vector<hipEvent_t> step_ev;  // inferc_executor_run_steps' step timing
 
   void free_kv() {
     for (auto& c : kv) {
@@ -241,6 +254,8 @@ struct inferc_executor {
     for (void* p : init_allocs) (void)hipFree(p);
     if (gather_err) (void)hipFree(gather_err);
     if (decode_pos) (void)hipFree(decode_pos);
+    if (fb_buf) (void)hipFree(fb_buf);
+    for (hipEvent_t e : step_ev) (void)hipEventDestroy(e);
   }
 
   void drop_graph() {
@@ -1422,7 +1437,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     std::vector<int64_t> os(data.shape.begin(), data.shape.begin() + axis);
     for (int64_t d : idx.shape) os.push_back(d);
     for (int64_t i = axis + 1; i < r; ++i) os.push_back(data.shape[size_t(i)]);
-    if (decode && pos_gathers.count(n.name)) {
+    if (decode && pos_gather_at[node_index(n)]) {
       // decode mode: the indices, walked for an empty past, are the new
       // positions 0 .. n-1; the rows are those past the device's past length
       IH_REQUIRE(idx.host && idx.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED,
@@ -1807,7 +1822,8 @@ void inferc_executor::exec_attention_past(const inferc_graph::Node& n) {
   a.fill = attr_float(n, "fill", -3.0e38f);
   a.q = static_cast<const float*>(dev_of(n.in[0]));
   a.ldq = a.ldo = H;
-  if (n.in.size() >= 6 && !n.in[5].empty()) {
+  // (decode mode ignores the mask: it holds only the new positions, all kept)
+  if (!decode && n.in.size() >= 6 && !n.in[5].empty()) {
     const Value& m = get(n.in[5]);
     IH_REQUIRE(m.dtype == INFERC_DT_BOOL || m.dtype == INFERC_DT_U8, INFERC_ERR_UNSUPPORTED,
                "FusedAttentionPast: mask must be bool");
@@ -2146,6 +2162,10 @@ void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
     const inferc_graph::Node& n = nodes[i];
     if (fold && const_done[i]) continue;
     if (events) IH_HIP(hipEventRecord(prof_ev[i], ctx->stream));
+    if (decode && decode_skip_at[i]) {
+      if (act) act->push_back(track ? live_activation_bytes() : 0);
+      continue;
+    }
     try {
       exec_node(n);
       if (fold && n.op == "Constant" && n.out.size() == 1) {
@@ -2162,7 +2182,19 @@ void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
     }
     if (act) act->push_back(track ? live_activation_bytes() : 0);
   }
-  if (decode && !dry) ih::advance_position(ctx, decode_pos, decode_step);
+  if (decode && !dry) {
+    if (!fb_logits.empty()) {
+      const ih::Value& v = get(fb_logits);
+      IH_REQUIRE(v.dtype == INFERC_DT_F32 && v.dev && !v.shape.empty() && v.shape.back() > 0,
+                 INFERC_ERR_ARG, "decode feedback: '" + fb_logits + "' is not a float32 device output");
+      const int64_t n = v.shape.back();
+      int64_t* d = static_cast<int64_t*>(buf("__argmax__", sizeof(int64_t)));
+      ih::argmax(ctx, n, static_cast<const float*>(v.dev) + (v.numel() - n), d, nullptr);
+      ih::decode_feedback(ctx, decode_pos, decode_step, d, fb_buf, fb_buf + 1);
+    } else {
+      ih::advance_position(ctx, decode_pos, decode_step);
+    }
+  }
   if (events) IH_HIP(hipEventRecord(prof_ev[nodes.size()], ctx->stream));
   for (const auto& o : outputs) get(o);  // every graph output must exist
 }
@@ -2181,9 +2213,10 @@ std::string inferc_executor::signature() const {
 void inferc_executor::stage_inputs() {
   for (auto& kv : inputs) {
     Input& in = kv.second;
-    if (!in.from_host) continue;
+    if (!in.from_host || !in.dirty) continue;  // (the graph reads inputs, never writes them)
     const size_t bytes = in.v.bytes();
     IH_HIP(hipMemcpyAsync(in.v.dev, in.staged.data(), bytes, hipMemcpyHostToDevice, ctx->stream));
+    in.dirty = false;
   }
 }
 
@@ -2271,7 +2304,7 @@ void inferc_executor::plan_decode(const std::string& mask_input) {
       if (!i.empty()) todo.push_back(i);
   }
   if (!mask_input.empty()) mark.insert(mask_input);
-  pos_gathers.clear();
+  pos_gather_at.assign(nodes.size(), 0);
   for (const auto& n : nodes) {  // (in order: producers come first)
     if (n.op == "FusedAttentionPast") {
       for (size_t k = 0; k < 3 && k < n.in.size(); ++k)
@@ -2284,7 +2317,7 @@ void inferc_executor::plan_decode(const std::string& mask_input) {
     if (!any) continue;
     if (n.op == "Gather" && n.in.size() >= 2 && mark.count(n.in[1]) && !mark.count(n.in[0]) &&
         inits.count(n.in[0])) {
-      pos_gathers.insert(n.name);
+      pos_gather_at[node_index(n)] = 1;
       continue;
     }
     for (const auto& o : n.out) mark.insert(o);
@@ -2292,6 +2325,36 @@ void inferc_executor::plan_decode(const std::string& mask_input) {
   for (const auto& o : outputs)
     IH_REQUIRE(!mark.count(o), INFERC_ERR_UNSUPPORTED,
                "decode mode: graph output '" + o + "' depends on the past length");
+  // Nodes decode mode need not run: every output depends on the past or the
+  // mask and is read only as an attention node's mask or by other such nodes
+  // (readers come later in the order, so one backward pass decides).
+  std::map<std::string, std::vector<std::pair<size_t, size_t>>> readers;  // (node, slot)
+  for (size_t i = 0; i < nodes.size(); ++i)
+    for (size_t k = 0; k < nodes[i].in.size(); ++k)
+      if (!nodes[i].in[k].empty()) readers[nodes[i].in[k]].push_back({i, k});
+  const std::set<std::string> outs(outputs.begin(), outputs.end());
+  decode_skip_at.assign(nodes.size(), 0);
+  for (size_t i = nodes.size(); i-- > 0;) {
+    const inferc_graph::Node& n = nodes[i];
+    if (n.op == "FusedAttentionPast" || pos_gather_at[i] || n.out.empty()) continue;
+    bool dead = true;
+    for (const auto& o : n.out) {
+      if (o.empty()) continue;
+      if (!mark.count(o) || outs.count(o)) {
+        dead = false;
+        break;
+      }
+      for (const auto& r : readers[o]) {
+        const bool mask_slot = nodes[r.first].op == "FusedAttentionPast" && r.second == 5;
+        if (!mask_slot && !decode_skip_at[r.first]) {
+          dead = false;
+          break;
+        }
+      }
+      if (!dead) break;
+    }
+    decode_skip_at[i] = dead ? 1 : 0;
+  }
 }
 
 // Waits for the stream, then fails if a device-index gather of the passes
@@ -2679,6 +2742,7 @@ int inferc_executor_set_input(inferc_executor* ex, const char* name, int dtype, 
     in.v.host.reset();
     in.staged.assign(static_cast<const uint8_t*>(host_data),
                      static_cast<const uint8_t*>(host_data) + bytes);
+    in.dirty = true;
   });
 }
 
@@ -2805,6 +2869,7 @@ int inferc_executor_set_decode_position(inferc_executor* ex, int64_t len,
       if (ex->decode)
         for (auto& kv : ex->kv) kv.second.len = ex->decode_len;
       ex->decode = false;
+      ex->fb_logits.clear();  // (the fed-back input stays bound, holding the last token)
       return;
     }
     IH_REQUIRE(ex->kv_max_t > 0, INFERC_ERR_STATE, "decode mode needs a bound KV cache");
@@ -2825,6 +2890,80 @@ int inferc_executor_decode_position(inferc_executor* ex, int64_t* len) {
     check_ex(ex);
     IH_REQUIRE(len != nullptr, INFERC_ERR_ARG, "null argument");
     *len = ex->decode ? ex->decode_len : -1;
+  });
+}
+
+int inferc_executor_set_decode_feedback(inferc_executor* ex, const char* logits,
+                                        const char* ids, int64_t first_token) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(!ex->dry, INFERC_ERR_STATE, "decode feedback needs a device");
+    IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+    ex->drop_graph();
+    ex->last_sig.clear();
+    if (logits == nullptr) {
+      ex->fb_logits.clear();
+      ex->fb_ids.clear();
+      return;
+    }
+    IH_REQUIRE(ids != nullptr, INFERC_ERR_ARG, "null input name");
+    IH_REQUIRE(ex->decode, INFERC_ERR_STATE, "decode feedback needs decode mode");
+    IH_REQUIRE(first_token >= 0, INFERC_ERR_ARG, "decode feedback: negative token");
+    if (!ex->fb_buf) {
+      IH_HIP(hipMalloc(&ex->fb_buf, sizeof(int64_t) * size_t(ex->kv_max_t + 2)));
+      IH_HIP(hipMemset(ex->fb_buf, 0, sizeof(int64_t) * size_t(ex->kv_max_t + 2)));
+    }
+    IH_HIP(hipMemcpy(ex->fb_buf, &first_token, sizeof(int64_t), hipMemcpyHostToDevice));
+    IH_HIP(hipMemcpy(ex->fb_buf + 1 + ex->decode_len, &first_token, sizeof(int64_t),
+                     hipMemcpyHostToDevice));
+    inferc_executor::Input& in = ex->inputs[ids];
+    if (in.from_host && in.v.dev) IH_HIP(hipFree(in.v.dev));
+    in = inferc_executor::Input{};
+    in.v.dtype = INFERC_DT_I64;
+    in.v.shape = {1, 1};
+    in.v.dev = ex->fb_buf;
+    ex->fb_logits = logits;
+    ex->fb_ids = ids;
+  });
+}
+
+int inferc_executor_run_steps(inferc_executor* ex, int64_t steps, float* step_ms) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(steps >= 0, INFERC_ERR_ARG, "run_steps: negative count");
+    if (ex->dry || step_ms == nullptr) {
+      for (int64_t i = 0; i < steps; ++i) ex->run();
+      return;
+    }
+    ex->ctx->make_current();
+    while (int64_t(ex->step_ev.size()) < steps + 1) {
+      hipEvent_t e;
+      IH_HIP(hipEventCreate(&e));
+      ex->step_ev.push_back(e);
+    }
+    IH_HIP(hipEventRecord(ex->step_ev[0], ex->ctx->stream));
+    for (int64_t i = 0; i < steps; ++i) {
+      ex->run();
+      IH_HIP(hipEventRecord(ex->step_ev[size_t(i + 1)], ex->ctx->stream));
+    }
+    IH_HIP(hipEventSynchronize(ex->step_ev[size_t(steps)]));
+    for (int64_t i = 0; i < steps; ++i)
+      IH_HIP(hipEventElapsedTime(&step_ms[i], ex->step_ev[size_t(i)], ex->step_ev[size_t(i + 1)]));
+  });
+}
+
+int inferc_executor_decode_tokens(inferc_executor* ex, int64_t first_pos, int64_t n,
+                                  int64_t* tokens) {
+  return ih::guard([&] {
+    check_ex(ex);
+    IH_REQUIRE(tokens != nullptr || n == 0, INFERC_ERR_ARG, "null argument");
+    IH_REQUIRE(ex->fb_buf != nullptr, INFERC_ERR_STATE, "no decode feedback has run");
+    IH_REQUIRE(first_pos >= 0 && n >= 0 && first_pos + n <= ex->kv_max_t + 1, INFERC_ERR_SHAPE,
+               "decode tokens: positions past the KV cache");
+    IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+    if (n) IH_HIP(hipMemcpy(tokens, ex->fb_buf + 1 + first_pos, sizeof(int64_t) * size_t(n),
+                            hipMemcpyDeviceToHost));
+    ex->check_gather_err();
   });
 }
 

@@ -122,6 +122,9 @@ _SIGS = {
     "inferc_executor_device_bytes": [vp, P(i64), P(i64), P(i64)],
     "inferc_executor_set_decode_position": [vp, i64, C.c_char_p],
     "inferc_executor_decode_position": [vp, P(i64)],
+    "inferc_executor_set_decode_feedback": [vp, C.c_char_p, C.c_char_p, i64],
+    "inferc_executor_run_steps": [vp, i64, P(C.c_float)],
+    "inferc_executor_decode_tokens": [vp, i64, i64, P(i64)],
     "inferc_executor_output_device": [vp, C.c_char_p, P(vp)],
     "inferc_profiler_create": [P(vp)],
     "inferc_profiler_destroy": [vp],

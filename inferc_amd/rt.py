@@ -808,6 +808,32 @@ class Executor:
         check(self.ctx._lib.inferc_executor_decode_position(self.handle, C.byref(v)))
         return v.value
 
+    def set_decode_feedback(self, logits: str | None, ids: str = "input_ids",
+                            first_token: int = 0) -> None:
+        """In decode mode, every run feeds the greedy token of `logits` back
+        as input `ids` on the device and records it by position
+        (inferc_executor_set_decode_feedback); None turns it off."""
+        check(self.ctx._lib.inferc_executor_set_decode_feedback(
+            self.handle, logits.encode() if logits else None, ids.encode(), int(first_token)))
+
+    def run_steps(self, steps: int, timed: bool = True) -> list[float] | None:
+        """`steps` runs back to back (inferc_executor_run_steps); with timed,
+        waits and returns each run's device ms from HIP events."""
+        if not timed:
+            check(self.ctx._lib.inferc_executor_run_steps(self.handle, int(steps), None))
+            return None
+        ms = (C.c_float * max(1, int(steps)))()
+        check(self.ctx._lib.inferc_executor_run_steps(self.handle, int(steps), ms))
+        return [float(ms[i]) for i in range(int(steps))]
+
+    def decode_tokens(self, first_pos: int, n: int) -> np.ndarray:
+        """The fed-back tokens at positions first_pos .. first_pos + n - 1."""
+        out = np.zeros(max(0, int(n)), np.int64)
+        check(self.ctx._lib.inferc_executor_decode_tokens(
+            self.handle, int(first_pos), int(n),
+            out.ctypes.data_as(C.POINTER(C.c_int64))))
+        return out
+
     def set_input_shape(self, name: str, dtype, shape: Sequence[int]) -> None:
         """An input that carries only its shape (a past the KV cache holds)."""
         check(self.ctx._lib.inferc_executor_set_input_shape(
@@ -955,11 +981,15 @@ class OnnxDecoder:
         step, device to device; without one the prompt is the with-past
         graph's first step. The steps after the first run in the executor's
         decode mode (inferc_executor_set_decode_position), where they replay
-        one recorded step; decode_mode=False walks every step with its grown
-        shapes instead. `profiler` records each post-prompt step as one
-        iteration (main.cpp:846-872). `step_ms`, when given, receives each
-        post-prompt step's host wall time in ms, from setting its inputs to
-        its token (the step timer of main.cpp:863-872 around Run)."""
+        one recorded step back to back, each step's greedy token fed back on
+        the device as the next one's input (set_decode_feedback; with a
+        profiler, one step at a time through the host instead);
+        decode_mode=False walks every step with its grown shapes instead.
+        `profiler` records each post-prompt step as one iteration
+        (main.cpp:846-872). `step_ms`, when given, receives each post-prompt
+        step's time in ms (the step timer of main.cpp:863-872 around Run):
+        host wall time for the steps run one at a time, device time between
+        HIP events for the fed-back ones."""
         p = np.asarray(prompt, np.int64).reshape(1, -1)
         n = p.shape[1]
         if n + max_tokens - 1 > self.max_t:
@@ -978,6 +1008,15 @@ class OnnxDecoder:
         self.ex.set_decode_position(-1)
         for k in range(1, max_tokens):
             t0 = time.perf_counter()
+            if decode_mode and k >= 2 and profiler is None:
+                # the remaining steps on the device, each one's token fed back
+                # as the next one's input; per-step device times by events
+                self.ex.set_decode_feedback("logits", "input_ids", toks[-1])
+                ms = self.ex.run_steps(max_tokens - k, timed=True)
+                toks.extend(int(t) for t in self.ex.decode_tokens(n + k, max_tokens - k))
+                if step_ms is not None:
+                    step_ms.extend(ms)
+                break
             if decode_mode and k >= 2:
                 toks.append(self._decode_step(toks[-1], profiler))
             else:

@@ -80,6 +80,33 @@ def test_exported_gpt2_with_past_step(ctx, optimize, bound):
         np.testing.assert_allclose(got[outs[1 + k]], ref, atol=1e-4)
 
 
+def test_decode_feedback_matches_host_steps(ctx):
+    """Decode mode with the token fed back on the device (steps replayed back
+    to back, tokens read once at the end) against the same decode mode one
+    step at a time through the host (a profiler forces that path) and
+    against walking every step with grown shapes: the same tokens, and the
+    same last logits bit for bit; run_steps reports one device time per
+    step; decode_tokens refuses positions past the cache."""
+    from inferc_amd.profiler import Profiler
+
+    io = np.load(GOLDEN / "gpt2_tiny_past_io.npz")
+    dec = rt.OnnxDecoder(ctx, GOLDEN / "gpt2_tiny_past.onnx", max_t=32)
+    ms: list = []
+    fed = dec.generate(io["prompt"], 12, step_ms=ms)
+    fed_logits = dec.logits()
+    host = dec.generate(io["prompt"], 12, profiler=Profiler())
+    host_logits = dec.logits()
+    walked = dec.generate(io["prompt"], 12, decode_mode=False)
+    np.testing.assert_array_equal(fed, io["gen_tokens"])
+    np.testing.assert_array_equal(host, fed)
+    np.testing.assert_array_equal(walked, fed)
+    np.testing.assert_array_equal(fed_logits, host_logits)
+    assert len(ms) == 11 and all(m > 0 for m in ms)
+    with pytest.raises(RuntimeError, match="past the KV cache"):
+        dec.ex.decode_tokens(30, 4)
+    dec.close()
+
+
 def test_onnx_decoder_greedy_tokens_match_torch(ctx):
     """`inferc decode` over the exported with-past graph with the device KV
     cache: the 12 greedy tokens equal torch's generation with its own cache
