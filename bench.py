@@ -179,10 +179,12 @@ GPT2_SMALL_PAST_ONNX = ROOT / "tests" / "golden" / "gpt2_small_past_noparams.onn
 def bench_onnx_decode(ctx, weights, prompt, max_tokens: int = 128):
     """`inferc decode` over the exported with-past graph of GPT-2-small (the
     reference's own caller, main.cpp:700-936): the structure-only export with
-    the config-4 weights bound, the pass pipeline, the device KV cache, and
-    each step run eagerly through the executor (its input shapes grow by one
-    position per step). ms/token is the host wall time of each post-prompt
-    step, as main.cpp:863-872 times Run."""
+    the config-4 weights bound, the pass pipeline, the device KV cache. The
+    first post-prompt step runs with its grown shapes; the rest run in the
+    executor's decode mode (past length on the device, one recorded step
+    replayed, each greedy token fed back on the device). ms/token is each
+    post-prompt step's time as main.cpp:863-872 times Run: host wall time for
+    the first, device time between HIP events for the replayed ones."""
     from inferc_amd import graphs, rt
 
     g = rt.Graph.from_onnx(str(GPT2_SMALL_PAST_ONNX))
