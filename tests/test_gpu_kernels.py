@@ -78,6 +78,45 @@ def test_kat_pointwise(ctx):
     np.testing.assert_allclose(y.var(-1), 1, atol=c["var_tol"])
 
 
+@pytest.mark.parametrize("shape,axis", [((3, 1), -1), ((5, 7), -1), ((4, 1000), -1),
+                                        ((2, 50257), -1), ((2, 12, 128, 128), -1),
+                                        ((3, 5, 6), 1), ((7, 4, 3), 0), ((2, 3, 4, 5), -2)])
+def test_softmax_vs_float64_and_oracle(ctx, shape, axis):
+    """Softmax (activation.cc:52-101) over every axis position of rank 2-4
+    shapes, rows of 1 to 50257 entries (the LM head's), scores offset by up
+    to 1e3 (the max subtraction keeps them finite): within 1e-6 of float64
+    and within 1e-4 of the oracle (whose serial float32 sum over a 50257-entry
+    row is itself off by up to ~1e-4 relative), rows summing to 1."""
+    rng = np.random.default_rng(sum(shape) + axis)
+    x = (rng.standard_normal(shape) * 4 + rng.uniform(-1e3, 1e3)).astype(np.float32)
+    got = rt.Softmax(T(ctx, x), axis).numpy()
+    close(got, ref64.softmax(x, axis), 1e-6)
+    close(got, O.softmax(x, axis))
+    np.testing.assert_allclose(got.astype(np.float64).sum(axis), 1.0, atol=1e-5)
+
+
+def test_softmax_masked_and_degenerate_rows(ctx):
+    """Rows as attention masks leave them: -inf scores get exactly 0 and a
+    single finite score exactly 1; equal scores give the uniform row; scores
+    near the float32 maximum stay finite; a row of -inf only is NaN
+    throughout, as the reference's exp(-inf - (-inf)) makes it."""
+    ninf = -np.inf
+    x = np.array([[0.5, ninf, ninf, ninf],
+                  [ninf, 2.0, ninf, 1.0],
+                  [3.0, 3.0, 3.0, 3.0],
+                  [3.0e38, 3.0e38, -3.0e38, 0.0],
+                  [ninf, ninf, ninf, ninf]], np.float32)
+    got = rt.Softmax(T(ctx, x)).numpy()
+    ref = O.softmax(x)
+    np.testing.assert_array_equal(got[0], [1.0, 0.0, 0.0, 0.0])
+    assert got[1, 0] == 0.0 and got[1, 2] == 0.0
+    close(got[1], ref64.softmax(np.array([-np.inf, 2.0, -np.inf, 1.0])), 1e-6)
+    np.testing.assert_allclose(got[2], 0.25, rtol=0, atol=1e-7)
+    np.testing.assert_allclose(got[3], [0.5, 0.5, 0.0, 0.0], rtol=0, atol=1e-7)
+    assert np.all(np.isnan(got[4])) and np.all(np.isnan(ref[4]))
+    np.testing.assert_allclose(got[:4], ref[:4], rtol=0, atol=1e-7)
+
+
 def test_kat_gather_split_concat_exact(ctx):
     for name in ("gather_rows", "gather_matrix_indices"):
         c = KAT[name]
