@@ -1158,7 +1158,10 @@ constexpr int kI4SlabSteps = kI4SlabK / 128;  // 128 k (64 bytes of a row) per M
 //   acc - 8 fold (below 2^24, exact in fp32) are scaled by 2^(8 limb - F);
 //   with S > 1 the group's S waves meet in LDS and add their terms in slab
 //   order, then a batch's 4 limbs (a lane quad) add and the row's scale
-//   applies.
+//   applies. The outputs collect in LDS ([batch][row of the block]).
+// - At its end the block stores its rows of every batch, 256 consecutive
+//   bytes per store instruction (measured: 16.3 -> 15.8 us on the 49-matrix
+//   GPT-2 set at batch 8, against 16-row pieces stored after each tile).
 // Each block reads its own descriptor (one scalar load): at a launch's start
 // every dependent load is a full memory round trip.
 struct I4B8Block {
@@ -1191,14 +1194,15 @@ __device__ __forceinline__ int wave_sum_int(int v) {
          (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 
-template <int G, int NW>
+template <int G, int NW, int ROWS>
 struct I4B8Smem {
   // B operands: [slab][step][parity][group][lane][16 bytes]
   __attribute__((aligned(16))) uint32_t bop[4 * kI4SlabSteps * 2 * G * 64 * 4];
   int sfold[4][G][16];  // per slab and column: the sum of its limbs
   int sF[4][4 * G];     // per slab and batch: x scaled by 2^F before rounding
   int sfin[4][4 * G];   // per slab and batch: 0 if x holds a NaN or inf
-  __attribute__((aligned(16))) float ystage[NW][4 * G][16];  // a tile's outputs, per wave
+  // the block's outputs, [batch][row of the block], stored at its end
+  __attribute__((aligned(16))) float yblk[4 * G][ROWS];
 };
 
 // One block of int4_gemv_b8_kernel for rows of S slabs: each wave runs U
@@ -1210,10 +1214,11 @@ struct I4B8Smem {
 // compiler cannot count an instruction behind a branch: the wait for the next
 // unit would then also wait for as many later loads as such stores issued,
 // draining the ring. So S is a template parameter (no branch around a tile's
-// epilogue), and the outputs go out as buffer stores whose lanes that must
-// not write get an offset past the buffer's end, which the hardware drops.
-template <int G, int S, int U, int R, int RE, int NW>
-__device__ __forceinline__ void int4_b8_block(I4B8Smem<G, NW>& sm, const I4B8Block& d, int batch) {
+// epilogue), and the outputs collect in LDS and leave at the block's end, as
+// whole rows of each batch.
+template <int G, int S, int U, int R, int RE, int NW, int ROWS>
+__device__ __forceinline__ void int4_b8_block(I4B8Smem<G, NW, ROWS>& sm, const I4B8Block& d,
+                                              int batch) {
   constexpr int ST = kI4SlabSteps;  // 6 MFMA steps of 128 k per slab
   constexpr int NB = 4 * G;         // batch columns
   constexpr int SMAX = 4;
@@ -1232,6 +1237,10 @@ __device__ __forceinline__ void int4_b8_block(I4B8Smem<G, NW>& sm, const I4B8Blo
   const int r = lane & 15, g = lane >> 4, col = lane & 15, cl = col & 3;
   // unit u: tile (tile0 + u / S) * NW + wave, slab u % S
   auto tile_of = [&](int u) { return (tile0 + (u >> ls)) * NW + wave; };
+  // the block's rows: [row0, row0 + BROWS), tiles tile0 * NW .. (tile0 + U/S) * NW - 1
+  constexpr int BROWS = (U / S) * NW * 16;
+  static_assert(BROWS <= ROWS, "the block's outputs must fit its LDS stage");
+  const int64_t row0 = tile0 * NW * 16;
 
   // 1. x loads of this wave's (batch, slab) tasks: lane l of piece j holds
   //    positions 256 j + 4 l + e (e < 4) of the slab. Idle tasks load the
@@ -1396,9 +1405,8 @@ __device__ __forceinline__ void int4_b8_block(I4B8Smem<G, NW>& sm, const I4B8Blo
     if (q == S - 1) {
       // a batch's 4 limb terms (a lane quad) add in fp32, times the rows'
       // scales (from lanes 4 g + v); lane (4 bb, g) then holds rows 4 g ..
-      // 4 g + 3 of batch 4 gr + bb, staged in LDS so that each store writes
-      // 16 consecutive rows of a batch per 16 lanes
-      const int64_t row_base = tile_of(u) * 16;
+      // 4 g + 3 of batch 4 gr + bb, kept in LDS until the block's end
+      const int lrow = int(tile_of(u) * 16 - row0);
       float sc[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) sc[v] = __shfl(scale, 4 * g + v, 64);
@@ -1413,36 +1421,39 @@ __device__ __forceinline__ void int4_b8_block(I4B8Smem<G, NW>& sm, const I4B8Blo
           t2 += quad_xor_f<2>(t2);
           o[v] = sc[v] * t2;
         }
-        if (cl == 0) *reinterpret_cast<f32x4_t*>(&sm.ystage[wave][b][4 * g]) = o;
-      }
-#pragma unroll
-      for (int k = 0; k < G; ++k) {
-        const int b = 4 * k + lane / 16, rr = lane % 16;
-        const int64_t row = row_base + rr;
-        const float v = sm.ystage[wave][b][rr];
-        const int off = b < batch && row < N ? int((int64_t(b) * N + row) * int64_t(sizeof(float)))
-                                             : int(0x80000000u);
-        // nontemporal (streaming) stores: measured 0.8 us faster per launch
-        // on the GPT-2 set than write-back stores (16.8 -> 15.9 us)
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ybuf, off, 0, 2 /* nt */);
+        if (cl == 0) *reinterpret_cast<f32x4_t*>(&sm.yblk[b][lrow + 4 * g]) = o;
       }
     }
   }
+  // The block's rows of every batch, 256 consecutive bytes per store
+  // instruction; nontemporal (streaming) stores, and offsets past the buffer
+  // for rows past N and batches past the call's, which the hardware drops.
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < (4 * G * BROWS + 64 * NW - 1) / (64 * NW); ++k) {
+    const int e = tid + 64 * NW * k;
+    const int b = e / BROWS, r = e % BROWS;
+    const int64_t row = row0 + r;
+    const bool on = e < 4 * G * BROWS && b < batch && row < N;
+    const float v = sm.yblk[on ? b : 0][on ? r : 0];
+    const int off = on ? int((int64_t(b) * N + row) * int64_t(sizeof(float))) : int(0x80000000u);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ybuf, off, 0, 2 /* nt */);
+  }
 }
-
 // U1 units per wave for K = 768 and 1536, U4 for K = 3072 (whose blocks
 // prepare four slabs of x and so stream fewer units).
 template <int G, int U1, int U4, int R, int RE, int NW>
 __global__ __launch_bounds__(64 * NW) void int4_gemv_b8_kernel(const I4B8Block* __restrict__ tab,
                                                                int batch) {
-  __shared__ I4B8Smem<G, NW> sm;
+  constexpr int ROWS = U1 * NW * 16;  // the most rows a block covers (K = 768)
+  __shared__ I4B8Smem<G, NW, ROWS> sm;
   const I4B8Block d = tab[blockIdx.x];
   if (d.S == 4)
-    int4_b8_block<G, 4, U4, R, RE, NW>(sm, d, batch);
+    int4_b8_block<G, 4, U4, R, RE, NW, ROWS>(sm, d, batch);
   else if (d.S == 2)
-    int4_b8_block<G, 2, U1, R, RE, NW>(sm, d, batch);
+    int4_b8_block<G, 2, U1, R, RE, NW, ROWS>(sm, d, batch);
   else
-    int4_b8_block<G, 1, U1, R, RE, NW>(sm, d, batch);
+    int4_b8_block<G, 1, U1, R, RE, NW, ROWS>(sm, d, batch);
 }
 
 // Fallback for K not a multiple of 32: one thread per (b, row), exact formula.
