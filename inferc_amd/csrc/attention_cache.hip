@@ -280,6 +280,58 @@ void advance_position(inferc_hip_ctx* ctx, int64_t* pos, int64_t step) {
   check_launch("advance position");
 }
 
+// The same after reducing the LM head's per-block (max, first index) partials
+// to the greedy token (first maximum wins; with no finite maximum, token 0).
+__global__ __launch_bounds__(256) void decode_feedback_parts_kernel(
+    const ValIdxPart* __restrict__ parts, int64_t n, int64_t* pos, int64_t step,
+    int64_t* ids, int64_t* hist) {
+  __shared__ float sv[4];
+  __shared__ int64_t si[4];
+  float v = -INFINITY;
+  int64_t i = INT64_MAX;
+  for (int64_t e = threadIdx.x; e < n; e += 256) {
+    const ValIdxPart q = parts[e];
+    if (q.v > v || (q.v == v && q.i < i)) {
+      v = q.v;
+      i = q.i;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float w = __shfl_xor(v, o, 64);
+    const int64_t j = __shfl_xor(i, o, 64);
+    if (w > v || (w == v && j < i)) {
+      v = w;
+      i = j;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = v;
+    si[threadIdx.x >> 6] = i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w)
+      if (sv[w] > v || (sv[w] == v && si[w] < i)) {
+        v = sv[w];
+        i = si[w];
+      }
+    const int64_t t = i == INT64_MAX ? 0 : i, p = *pos + step;
+    ids[0] = t;
+    hist[p] = t;
+    *pos = p;
+  }
+}
+
+void decode_feedback_parts(inferc_hip_ctx* ctx, const ValIdxPart* parts, int64_t n, int64_t* pos,
+                           int64_t step, int64_t* ids, int64_t* hist) {
+  IH_REQUIRE(parts && n > 0 && pos && ids && hist, INFERC_ERR_ARG,
+             "decode feedback: bad partials");
+  hipLaunchKernelGGL(decode_feedback_parts_kernel, dim3(1), dim3(256), 0, ctx->stream, parts, n,
+                     pos, step, ids, hist);
+  check_launch("decode feedback");
+}
+
 void decode_feedback(inferc_hip_ctx* ctx, int64_t* pos, int64_t step, const int64_t* tok,
                      int64_t* ids, int64_t* hist) {
   IH_REQUIRE(pos && tok && ids && hist, INFERC_ERR_ARG, "decode feedback: null pointer");

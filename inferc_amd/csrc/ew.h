@@ -93,5 +93,9 @@ void advance_position(inferc_hip_ctx* ctx, int64_t* pos, int64_t step);
 // token at its index, so it needs the cache's max_t + 1 entries).
 void decode_feedback(inferc_hip_ctx* ctx, int64_t* pos, int64_t step, const int64_t* tok,
                      int64_t* ids, int64_t* hist);
+// The same with the token reduced from n (max, first index) partials of an
+// arg-max GEMV (first maximum wins).
+void decode_feedback_parts(inferc_hip_ctx* ctx, const ValIdxPart* parts, int64_t n, int64_t* pos,
+                           int64_t step, int64_t* ids, int64_t* hist);
 
 }  // namespace ih

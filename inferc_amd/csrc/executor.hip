@@ -233,6 +233,9 @@ struct inferc_executor {
   // no host copy between them.
   std::string fb_logits, fb_ids;
   int64_t* fb_buf = nullptr;
+  // This walk's LM-head arg-max partials, when its GEMV wrote them.
+  const ih::ValIdxPart* fb_parts = nullptr;
+  int64_t fb_parts_n = 0;
   std::vector<hipEvent_t> step_ev;  // inferc_executor_run_steps' step timing
 
   void free_kv() {
@@ -469,6 +472,7 @@ struct inferc_executor {
   }
   void generic_binary(const inferc_graph::Node& n, int ewop);
   void exec_attention_past(const inferc_graph::Node& n);
+  void ln_prologue(const inferc_graph::Node& n, ih::GemmArgs& g);
   bool exec_generic(const inferc_graph::Node& n);
   // With `act`, records an event before each node and after the last on the
   // stream, and appends each node's activation bytes (0 unless `track`).
@@ -602,9 +606,10 @@ void inferc_executor::peephole() {
   //  - Gemm -> [Reshape] -> Add(., r)  ==>  Gemm with r as its residual,
   //    when r is no initializer and exists before the Gemm runs (the
   //    residual stream of a pre-LN layer);
-  //  - FusedLayerNorm(x) -> [Reshape] -> Gemm (as A)  ==>  Gemm normalizing
-  //    its A rows, the view taking x (LayerNorm acts on rows over the last
-  //    axis, which the view must keep: checked when the Gemm runs).
+  //  - FusedLayerNorm(x) -> [Reshape] -> Gemm or MatMul (as A, a 2-D
+  //    initializer as B: the LM head)  ==>  the product normalizing its A
+  //    rows, the view taking x (LayerNorm acts on rows over the last axis,
+  //    which the view must keep: checked when the product runs).
   // Each intermediate must have the one reader. On the one-row GEMV route
   // all three become the GEMV's prologue and epilogue.
   auto sole_reader = [&](const std::string& t, size_t from) -> int {
@@ -685,8 +690,10 @@ void inferc_executor::peephole() {
     }
     inferc_graph::Node& g = nodes[size_t(c)];
     const std::string t = view >= 0 ? nodes[size_t(view)].out[0] : ln.out[0];
-    if (g.op != "Gemm" || g.in.empty() || g.in[0] != t || ih::attr_int(g, "transA", 0) != 0 ||
-        g.attrs.count("__ln_g"))
+    const bool mm = g.op == "MatMul" && g.in.size() == 2 && inits.count(g.in[1]) &&
+                    inits.at(g.in[1]).shape.size() == 2;
+    if ((g.op != "Gemm" && !mm) || g.in.empty() || g.in[0] != t ||
+        ih::attr_int(g, "transA", 0) != 0 || g.attrs.count("__ln_g"))
       continue;
     g.attrs["__ln_g"] = ln.in[1];
     g.attrs["__ln_b"] = ln.in[2];
@@ -1156,6 +1163,24 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     // (after the row statistics are decided: a product that writes them
     // stays off the GEMV route)
     if (!lna) batch1_route(g, n.in[1]);
+    if (op == "MatMul") ln_prologue(n, g);
+    if (!dry && decode && !fb_logits.empty() && n.out[0] == fb_logits &&
+        gemm_gemv_route(ctx, g) && gemv2_supported(g.K) && aligned16(g.B) && aligned16(g.A) &&
+        (!g.gemv_ln_g || (aligned16(g.gemv_ln_g) && aligned16(g.gemv_ln_b))) &&
+        g.c_kind == INFERC_C_NONE && g.R == nullptr) {
+      // the fed-back logits' GEMV also leaves its blocks' (max, first index)
+      // for the step's feedback to reduce
+      Gemv2Args a;
+      a.N = g.N; a.K = g.K; a.W = g.B; a.x = g.A;
+      a.ln_g = g.gemv_ln_g; a.ln_b = g.gemv_ln_b; a.ln_eps = g.gemv_ln_eps;
+      a.act = g.act; a.y = g.Y;
+      fb_parts_n = gemv2_blocks(ctx, g.N, g.K, true);
+      a.amax = static_cast<ValIdxPart*>(
+          buf("__fbparts__", size_t(fb_parts_n) * sizeof(ValIdxPart)));
+      fb_parts = a.amax;
+      gemv2(ctx, a);
+      return;
+    }
     if (!dry) {
       gemm(ctx, g);
     }
@@ -1209,30 +1234,7 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     g.Y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, {g.M, g.N}).dev);
     g.ldy = g.N;
     batch1_route(g, n.in[1]);
-    auto ln = n.attrs.find("__ln_g");
-    if (ln != n.attrs.end() && !ln_gemm_off.count(n.in[0])) {
-      // A's rows through a LayerNorm that the peephole moved here (it
-      // preceded a Gather or a view of A)
-      const float* lg = static_cast<const float*>(dev_of(ln->second));
-      const float* lb = static_cast<const float*>(dev_of(n.attrs.at("__ln_b")));
-      const float eps = std::stof(n.attrs.at("__ln_eps"));
-      IH_REQUIRE(!g.trans_a && inits.at(ln->second).numel() == g.K, INFERC_ERR_SHAPE,
-                 "Gemm: LayerNorm of A: scale size must equal K");
-      auto lx = n.attrs.find("__ln_x");
-      IH_REQUIRE(lx == n.attrs.end() || get(lx->second).shape.back() == g.K,
-                 INFERC_ERR_UNSUPPORTED,
-                 "Gemm: the view between a LayerNorm and A must keep the feature axis");
-      if (gemm_gemv_route(ctx, g)) {
-        g.gemv_ln_g = lg;
-        g.gemv_ln_b = lb;
-        g.gemv_ln_eps = eps;
-      } else {
-        float* t = static_cast<float*>(buf("__lnrows:" + n.out[0], size_t(g.M * g.K) * 4));
-        IH_REQUIRE(g.lda == g.K, INFERC_ERR_SHAPE, "Gemm: LayerNorm of A needs dense rows");
-        if (!dry) layernorm_res_period(ctx, g.M, g.K, g.A, nullptr, 1, lg, lb, eps, t);
-        g.A = t;
-      }
-    }
+    if (!ln_gemm_off.count(n.in[0])) ln_prologue(n, g);
     if (!dry) {
       gemm(ctx, g);
     }
@@ -1791,6 +1793,35 @@ void inferc_executor::generic_binary(const inferc_graph::Node& n, int ewop) {
 //    [0, P); a shape-only past input says the cache already holds them. The
 //    new rows are appended at P, attention reads the cache, and present_*
 //    are views of its first T rows, copied out only when asked for.
+// A's rows through a LayerNorm that the peephole moved onto a Gemm or
+// MatMul (it preceded A directly, through a view, or through a Gather): on
+// the one-row GEMV route the GEMV's LayerNorm prologue applies it, else a
+// LayerNorm of A's rows into a buffer that becomes A.
+void inferc_executor::ln_prologue(const inferc_graph::Node& n, ih::GemmArgs& g) {
+  using namespace ih;
+  auto ln = n.attrs.find("__ln_g");
+  if (ln == n.attrs.end()) return;
+  const float* lg = static_cast<const float*>(dev_of(ln->second));
+  const float* lb = static_cast<const float*>(dev_of(n.attrs.at("__ln_b")));
+  const float eps = std::stof(n.attrs.at("__ln_eps"));
+  IH_REQUIRE(!g.trans_a && inits.at(ln->second).numel() == g.K, INFERC_ERR_SHAPE,
+             n.op + ": LayerNorm of A: scale size must equal K");
+  auto lx = n.attrs.find("__ln_x");
+  IH_REQUIRE(lx == n.attrs.end() || get(lx->second).shape.back() == g.K, INFERC_ERR_UNSUPPORTED,
+             n.op + ": the view between a LayerNorm and A must keep the feature axis");
+  if (gemm_gemv_route(ctx, g)) {
+    g.gemv_ln_g = lg;
+    g.gemv_ln_b = lb;
+    g.gemv_ln_eps = eps;
+  } else {
+    float* t = static_cast<float*>(buf("__lnrows:" + n.out[0], size_t(g.M * g.K) * 4));
+    IH_REQUIRE(g.lda == g.K && g.batch == 1, INFERC_ERR_SHAPE,
+               n.op + ": LayerNorm of A needs dense rows");
+    if (!dry) layernorm_res_period(ctx, g.M, g.K, g.A, nullptr, 1, lg, lb, eps, t);
+    g.A = t;
+  }
+}
+
 void inferc_executor::exec_attention_past(const inferc_graph::Node& n) {
   using namespace ih;
   IH_REQUIRE(n.in.size() >= 5 && n.out.size() == 3, INFERC_ERR_ARG,
@@ -2148,6 +2179,8 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
 void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
   vals.clear();
   dev_gather = false;
+  fb_parts = nullptr;
+  fb_parts_n = 0;
   ln_gemm_off.clear();
   pending_gather.clear();
   eq_done.clear();
@@ -2183,7 +2216,10 @@ void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
     if (act) act->push_back(track ? live_activation_bytes() : 0);
   }
   if (decode && !dry) {
-    if (!fb_logits.empty()) {
+    if (fb_parts) {
+      ih::decode_feedback_parts(ctx, fb_parts, fb_parts_n, decode_pos, decode_step, fb_buf,
+                                fb_buf + 1);
+    } else if (!fb_logits.empty()) {
       const ih::Value& v = get(fb_logits);
       IH_REQUIRE(v.dtype == INFERC_DT_F32 && v.dev && !v.shape.empty() && v.shape.back() > 0,
                  INFERC_ERR_ARG, "decode feedback: '" + fb_logits + "' is not a float32 device output");
