@@ -282,19 +282,33 @@ void advance_position(inferc_hip_ctx* ctx, int64_t* pos, int64_t step) {
 
 // The same after reducing the LM head's per-block (max, first index) partials
 // to the greedy token (first maximum wins; with no finite maximum, token 0).
-__global__ __launch_bounds__(256) void decode_feedback_parts_kernel(
+// Each thread loads kFbPer partials, and the position, before it compares any
+// of them: one memory round trip per 8192 partials instead of one per partial.
+constexpr int kFbThreads = 1024;
+constexpr int kFbPer = 8;
+
+__global__ __launch_bounds__(kFbThreads) void decode_feedback_parts_kernel(
     const ValIdxPart* __restrict__ parts, int64_t n, int64_t* pos, int64_t step,
     int64_t* ids, int64_t* hist) {
-  __shared__ float sv[4];
-  __shared__ int64_t si[4];
+  __shared__ float sv[kFbThreads / 64];
+  __shared__ int64_t si[kFbThreads / 64];
+  // read by every thread before thread 0 rewrites it behind the barrier
+  const int64_t p0 = *pos;
   float v = -INFINITY;
   int64_t i = INT64_MAX;
-  for (int64_t e = threadIdx.x; e < n; e += 256) {
-    const ValIdxPart q = parts[e];
-    if (q.v > v || (q.v == v && q.i < i)) {
-      v = q.v;
-      i = q.i;
+  for (int64_t base = 0; base < n; base += int64_t(kFbThreads) * kFbPer) {
+    ValIdxPart q[kFbPer];
+#pragma unroll
+    for (int k = 0; k < kFbPer; ++k) {
+      const int64_t e = base + threadIdx.x + int64_t(k) * kFbThreads;
+      q[k] = e < n ? parts[e] : ValIdxPart{-INFINITY, INT64_MAX};
     }
+#pragma unroll
+    for (int k = 0; k < kFbPer; ++k)
+      if (q[k].v > v || (q[k].v == v && q[k].i < i)) {
+        v = q[k].v;
+        i = q[k].i;
+      }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -311,12 +325,12 @@ __global__ __launch_bounds__(256) void decode_feedback_parts_kernel(
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; ++w)
+    for (int w = 1; w < kFbThreads / 64; ++w)
       if (sv[w] > v || (sv[w] == v && si[w] < i)) {
         v = sv[w];
         i = si[w];
       }
-    const int64_t t = i == INT64_MAX ? 0 : i, p = *pos + step;
+    const int64_t t = i == INT64_MAX ? 0 : i, p = p0 + step;
     ids[0] = t;
     hist[p] = t;
     *pos = p;
@@ -327,8 +341,8 @@ void decode_feedback_parts(inferc_hip_ctx* ctx, const ValIdxPart* parts, int64_t
                            int64_t step, int64_t* ids, int64_t* hist) {
   IH_REQUIRE(parts && n > 0 && pos && ids && hist, INFERC_ERR_ARG,
              "decode feedback: bad partials");
-  hipLaunchKernelGGL(decode_feedback_parts_kernel, dim3(1), dim3(256), 0, ctx->stream, parts, n,
-                     pos, step, ids, hist);
+  hipLaunchKernelGGL(decode_feedback_parts_kernel, dim3(1), dim3(kFbThreads), 0, ctx->stream,
+                     parts, n, pos, step, ids, hist);
   check_launch("decode feedback");
 }
 

@@ -144,10 +144,30 @@ struct inferc_executor {
   // Dry run: shape inference and peephole only, no device (host-logic tests).
   bool dry = false;
   uintptr_t dry_next = 0x10000;
-  std::string last_sig;
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
-  std::string graph_sig;
+  std::string last_key;  // run_key() of the last unrecorded (planning) pass
+  // Recorded runs by run_key(), the most recently used last. A recording is
+  // replayed only while the workspace, the GEMV route and every executor
+  // buffer it names are still the ones it was recorded with: input buffers
+  // through the key (their addresses are part of it), the arena and the KV
+  // caches through buf_gen.
+  // With each recording, the value table its pass left (shapes and buffers of
+  // every tensor), which outputs are read through after a replay.
+  struct CacheView {
+    const float* base = nullptr;
+    int64_t rows = 0, T = 0, dh = 0, max_t = 0;
+  };
+  struct Recorded {
+    std::string key;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    uint64_t ws_gen = 0, route_gen = 0, buf_gen = 0;
+    std::unordered_map<std::string, ih::Value> vals;
+    std::map<std::string, CacheView> views;
+  };
+  static constexpr size_t kMaxRecorded = 4;
+  std::vector<Recorded> recorded;
+  uint64_t buf_gen = 0;         // bumped before an arena or KV-cache buffer is freed
+  uint64_t plan_route_gen = 0;  // the GEMV route the last planning pass saw
   // A LayerNorm whose input h comes from a FusedGemmEpilogue and whose
   // readers are all GEMM operands (A of FusedQKV / FusedMatMulAddGELU /
   // FusedGemmEpilogue, the residual of a FusedGemmEpilogue): peephole lists
@@ -163,8 +183,6 @@ struct inferc_executor {
   };
   std::unordered_map<std::string, LnRead> ln_reads;  // by h
   std::unordered_map<std::string, bool> ln_on;       // this run, by h
-  uint64_t graph_ws_gen = 0;
-  uint64_t graph_route_gen = 0;
   // Sticky device flag of the gathers whose indices live on the device: set
   // by the kernel on an out-of-range index, read (and cleared) by the calls
   // that wait for the stream, which then fail as Gather does on the host
@@ -203,11 +221,8 @@ struct inferc_executor {
   };
   std::map<std::string, KvCache> kv;  // keyed by the node's name
   // present.* outputs that live in a KV cache: name -> (cache, rows held)
-  struct CacheView {
-    const float* base = nullptr;
-    int64_t rows = 0, T = 0, dh = 0, max_t = 0;
-  };
   std::map<std::string, CacheView> cache_views;
+  std::string vals_key;  // the run_key() of the pass that left vals
   // Decode mode (inferc_executor_set_decode_position): the KV caches hold
   // decode_len positions, a count also kept on the device (decode_pos). A
   // run walks the graph as if the past were empty, with an attention mask of
@@ -232,6 +247,7 @@ struct inferc_executor {
   // position (fb_buf[1 + position]), so the steps replay back to back with
   // no host copy between them.
   std::string fb_logits, fb_ids;
+  std::string decode_mask;  // decode mode's attention-mask input
   int64_t* fb_buf = nullptr;
   // This walk's LM-head arg-max partials, when its GEMV wrote them.
   const ih::ValIdxPart* fb_parts = nullptr;
@@ -261,12 +277,17 @@ struct inferc_executor {
     for (hipEvent_t e : step_ev) (void)hipEventDestroy(e);
   }
 
+  static void destroy(Recorded& r) {
+    if (r.exec) (void)hipGraphExecDestroy(r.exec);
+    if (r.graph) (void)hipGraphDestroy(r.graph);
+    r.exec = nullptr;
+    r.graph = nullptr;
+  }
+  // Drops every recording (the caller has drained the stream where a
+  // recording may still run).
   void drop_graph() {
-    if (exec) (void)hipGraphExecDestroy(exec);
-    if (graph) (void)hipGraphDestroy(graph);
-    exec = nullptr;
-    graph = nullptr;
-    graph_sig.clear();
+    for (Recorded& r : recorded) destroy(r);
+    recorded.clear();
   }
 
   // Device buffer for tensor `name` of at least `bytes`, reused across runs.
@@ -292,6 +313,7 @@ struct inferc_executor {
     size_t want = bytes;
     if (b.p) {
       IH_HIP(hipStreamSynchronize(ctx->stream));
+      ++buf_gen;  // recordings naming this buffer are stale
       IH_HIP(hipFree(b.p));
       b.p = nullptr;
       const size_t grown = b.bytes + b.bytes / 2;
@@ -323,7 +345,8 @@ struct inferc_executor {
 
   // Device pointer of a value. Host-only values (shape math consumed by a
   // kernel) are uploaded into the arena once and reused while their bytes
-  // stay the same, so a captured run needs no copy.
+  // stay the same, so a captured run needs no copy. New bytes make the
+  // recordings stale (one may read the old ones).
   struct Upload {
     std::vector<uint8_t> bytes;
     void* p = nullptr;
@@ -341,6 +364,7 @@ struct inferc_executor {
       return up.p;
     }
     IH_REQUIRE(dry || !ctx->capturing, INFERC_ERR_STATE, "host constant changed inside capture");
+    if (up.p) ++buf_gen;
     up.bytes = *v.host;
     up.p = buf("__h2d__" + name, v.bytes());
     if (dry) {
@@ -478,6 +502,7 @@ struct inferc_executor {
   // stream, and appends each node's activation bytes (0 unless `track`).
   void walk(std::vector<int64_t>* act = nullptr, bool track = false);
   std::string signature() const;
+  std::string run_key() const;
   void stage_inputs();
   void run();
   void run_profiled(inferc_profiler* p);
@@ -1915,6 +1940,7 @@ void inferc_executor::exec_attention_past(const inferc_graph::Node& n) {
     IH_REQUIRE(!ctx->capturing, INFERC_ERR_STATE, "KV cache allocation during graph capture");
     if (c.k) {
       IH_HIP(hipStreamSynchronize(ctx->stream));
+      ++buf_gen;
       (void)hipFree(c.k);
       (void)hipFree(c.v);
     }
@@ -2245,6 +2271,15 @@ std::string inferc_executor::signature() const {
   return o.str();
 }
 
+// The key of a run's recording: the input signature and, in decode mode, the
+// mode's mask input and the decode feedback's logits and ids names, which
+// change what a step launches.
+std::string inferc_executor::run_key() const {
+  std::string k = signature();
+  if (decode) k += "|decode:" + decode_mask + "|feedback:" + fb_logits + "," + fb_ids;
+  return k;
+}
+
 // Host inputs are copied into their device buffers outside any graph.
 void inferc_executor::stage_inputs() {
   for (auto& kv : inputs) {
@@ -2266,27 +2301,51 @@ void inferc_executor::run() {
     IH_REQUIRE(decode_len + std::max<int64_t>(decode_step, 1) <= kv_max_t, INFERC_ERR_SHAPE,
                "decode: the KV cache (" + std::to_string(kv_max_t) + " positions) is full");
   stage_inputs();
-  const std::string sig = signature();
-  if (graph_mode && exec && graph_sig == sig && graph_ws_gen == ctx->ws_generation &&
-      graph_route_gen == ctx->route_generation) {
-    IH_HIP(hipGraphLaunch(exec, ctx->stream));
-    if (decode) decode_len += decode_step;
-    return;
+  const std::string key = run_key();
+  if (graph_mode) {
+    for (size_t i = 0; i < recorded.size(); ++i) {
+      if (recorded[i].key != key) continue;
+      const Recorded& r = recorded[i];
+      if (r.ws_gen == ctx->ws_generation && r.route_gen == ctx->route_generation &&
+          r.buf_gen == buf_gen) {
+        IH_HIP(hipGraphLaunch(r.exec, ctx->stream));
+        if (vals_key != key) {  // another key's pass ran since: its tape is not this one's
+          vals = r.vals;
+          cache_views = r.views;
+          vals_key = key;
+        }
+        std::rotate(recorded.begin() + long(i), recorded.begin() + long(i) + 1, recorded.end());
+        if (decode) decode_len += decode_step;
+        return;
+      }
+      IH_HIP(hipStreamSynchronize(ctx->stream));  // stale: drop it
+      destroy(recorded[i]);
+      recorded.erase(recorded.begin() + long(i));
+      break;
+    }
   }
   // a changed GEMV route is planned by an eager pass, as a new signature is
-  if (graph_route_gen != ctx->route_generation) last_sig.clear();
-  if (!graph_mode || sig != last_sig) {
-    // first run for this input signature: eager (allocates the arena)
-    drop_graph();
+  if (plan_route_gen != ctx->route_generation) last_key.clear();
+  if (!graph_mode || key != last_key) {
+    // first run for this key: eager, unrecorded (allocates the arena)
     walk();
-    last_sig = sig;
-    graph_route_gen = ctx->route_generation;
+    vals_key = key;
+    last_key = key;
+    plan_route_gen = ctx->route_generation;
     if (decode) decode_len += decode_step;
     return;
   }
-  // second run with the same signature: record it, then replay
-  drop_graph();
-  const uint64_t gen = ctx->ws_generation, route_gen = ctx->route_generation;
+  // second run with the same key: record it, then replay
+  if (recorded.size() >= kMaxRecorded) {
+    IH_HIP(hipStreamSynchronize(ctx->stream));
+    destroy(recorded.front());
+    recorded.erase(recorded.begin());
+  }
+  Recorded r;
+  r.key = key;
+  r.ws_gen = ctx->ws_generation;
+  r.route_gen = ctx->route_generation;
+  r.buf_gen = buf_gen;
   IH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
   ctx->capturing = true;
   try {
@@ -2299,12 +2358,16 @@ void inferc_executor::run() {
     throw;
   }
   ctx->capturing = false;
-  IH_HIP(hipStreamEndCapture(ctx->stream, &graph));
-  IH_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
-  graph_sig = sig;
-  graph_ws_gen = gen;
-  graph_route_gen = route_gen;
-  IH_HIP(hipGraphLaunch(exec, ctx->stream));
+  IH_HIP(hipStreamEndCapture(ctx->stream, &r.graph));
+  if (hipGraphInstantiate(&r.exec, r.graph, nullptr, nullptr, 0) != hipSuccess) {
+    destroy(r);
+    ih::fail(INFERC_ERR_HIP, "executor: graph instantiation failed");
+  }
+  vals_key = key;
+  r.vals = vals;
+  r.views = cache_views;
+  recorded.push_back(std::move(r));
+  IH_HIP(hipGraphLaunch(recorded.back().exec, ctx->stream));
   if (decode) decode_len += decode_step;
 }
 
@@ -2424,8 +2487,9 @@ void inferc_executor::check_gather_err() {
 // recorded on the stream before and after it (host-only shape nodes read
 // about 0 ms); the iteration total is the host wall clock from the first
 // node's enqueue until the stream has drained, so it includes launch and
-// host work. A dry executor records 0 ms per node. The captured graph of
-// this input signature, if any, stays valid: the pass reuses its buffers.
+// host work. A dry executor records 0 ms per node. The recordings stay
+// valid: the pass reuses their buffers (a buffer it has to grow makes those
+// naming it stale).
 void inferc_executor::run_profiled(inferc_profiler* p) {
   std::vector<int64_t> act;
   act.reserve(nodes.size());
@@ -2444,14 +2508,13 @@ void inferc_executor::run_profiled(inferc_profiler* p) {
     prof_ev.push_back(e);
   }
   stage_inputs();
-  const std::string sig = signature();
-  if (sig != last_sig) {
-    // a new input signature: one unrecorded eager pass first, so that the
-    // arena allocations and the one-row products' transposed weight copies
-    // (blocking allocations and uploads) fall outside the recorded pass
-    drop_graph();  // buffers may be reallocated for the new shapes
+  const std::string key = run_key();
+  if (key != last_key) {
+    // a new key: one unrecorded eager pass first, so that the arena
+    // allocations and the one-row products' transposed weight copies
+    // (blocking allocations and uploads) fall outside the timed pass
     walk();
-    last_sig = sig;
+    last_key = key;
     if (decode) {
       // that pass advanced the device position: rewind it; the recorded pass
       // then writes the same cache rows again
@@ -2462,6 +2525,7 @@ void inferc_executor::run_profiled(inferc_profiler* p) {
   IH_HIP(hipStreamSynchronize(ctx->stream));
   p->begin_iteration();
   walk(&act, p->track_activation_bytes);
+  vals_key = key;
   if (decode) decode_len += decode_step;
   IH_HIP(hipEventSynchronize(prof_ev[nodes.size()]));
   check_gather_err();
@@ -2869,7 +2933,10 @@ int inferc_executor_set_graph_mode(inferc_executor* ex, int enabled) {
   return ih::guard([&] {
     check_ex(ex);
     ex->graph_mode = enabled != 0;
-    if (!ex->graph_mode) ex->drop_graph();
+    if (!ex->graph_mode && !ex->dry) {
+      IH_HIP(hipStreamSynchronize(ex->ctx->stream));
+      ex->drop_graph();
+    }
   });
 }
 
@@ -2882,7 +2949,7 @@ int inferc_executor_bind_kv_cache(inferc_executor* ex, int64_t max_t) {
     ex->drop_graph();
     ex->free_kv();
     ex->kv_max_t = max_t;
-    ex->last_sig.clear();
+    ex->last_key.clear();
     ex->decode = false;
   });
 }
@@ -2895,16 +2962,17 @@ int inferc_executor_set_decode_position(inferc_executor* ex, int64_t len,
       // planning only (no cache, no device): the plan's checks
       ex->decode = len >= 0;
       ex->decode_len = len;
+      ex->decode_mask = ex->decode && mask_input ? mask_input : "";
       if (ex->decode) ex->plan_decode(mask_input ? mask_input : "");
       return;
     }
     IH_HIP(hipStreamSynchronize(ex->ctx->stream));
-    ex->drop_graph();
-    ex->last_sig.clear();
+    ex->last_key.clear();  // (recordings stay: the mode is part of their key)
     if (len < 0) {
       if (ex->decode)
         for (auto& kv : ex->kv) kv.second.len = ex->decode_len;
       ex->decode = false;
+      ex->decode_mask.clear();
       ex->fb_logits.clear();  // (the fed-back input stays bound, holding the last token)
       return;
     }
@@ -2918,6 +2986,7 @@ int inferc_executor_set_decode_position(inferc_executor* ex, int64_t len,
     IH_HIP(hipMemcpy(ex->decode_pos, &len, sizeof(int64_t), hipMemcpyHostToDevice));
     ex->decode = true;
     ex->decode_len = len;
+    ex->decode_mask = mask_input ? mask_input : "";
   });
 }
 
@@ -2935,8 +3004,7 @@ int inferc_executor_set_decode_feedback(inferc_executor* ex, const char* logits,
     check_ex(ex);
     IH_REQUIRE(!ex->dry, INFERC_ERR_STATE, "decode feedback needs a device");
     IH_HIP(hipStreamSynchronize(ex->ctx->stream));
-    ex->drop_graph();
-    ex->last_sig.clear();
+    ex->last_key.clear();  // (recordings stay: the feedback is part of their key)
     if (logits == nullptr) {
       ex->fb_logits.clear();
       ex->fb_ids.clear();

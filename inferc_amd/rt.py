@@ -974,16 +974,25 @@ class OnnxDecoder:
             self.ex.run_async()
         return self.ex.output_argmax("logits")
 
+    def _enter_decode(self, length: int) -> None:
+        """Decode mode with the caches holding `length` positions: the past
+        inputs by shape with length 0, the new position's mask."""
+        self.ex.set_decode_position(length, "attention_mask")
+        for i in self.past:
+            self.ex.set_input_shape(i["name"], np.float32, [1, i["shape"][1], 0, i["shape"][3]])
+        self.ex.set_input("attention_mask", np.ones((1, 1), np.int64))
+
     def generate(self, prompt: np.ndarray, max_tokens: int, profiler=None,
                  step_ms: list | None = None, decode_mode: bool = True) -> np.ndarray:
         """Greedy tokens. With a prefill graph the prompt runs there
         (main.cpp:786-828) and its present.* seed the cache on the first
         step, device to device; without one the prompt is the with-past
-        graph's first step. The steps after the first run in the executor's
-        decode mode (inferc_executor_set_decode_position), where they replay
-        one recorded step back to back, each step's greedy token fed back on
-        the device as the next one's input (set_decode_feedback; with a
-        profiler, one step at a time through the host instead);
+        graph's first step. The steps after the prompt (after the first step
+        past it with a prefill graph, which seeds the cache) run in the
+        executor's decode mode (inferc_executor_set_decode_position), where
+        they replay one recorded step back to back, each step's greedy token
+        fed back on the device as the next one's input (set_decode_feedback;
+        with a profiler, one step at a time through the host instead);
         decode_mode=False walks every step with its grown shapes instead.
         `profiler` records each post-prompt step as one iteration
         (main.cpp:846-872). `step_ms`, when given, receives each post-prompt
@@ -1006,9 +1015,14 @@ class OnnxDecoder:
         else:
             toks = [self._step(p, n)]
         self.ex.set_decode_position(-1)
+        # the first step in decode mode: the one after the prompt, or with a
+        # prefill graph the one after the step that seeds the cache
+        first = 1 if seed is None else 2
+        if decode_mode and first == 1 and max_tokens > 1:
+            self._enter_decode(n)
         for k in range(1, max_tokens):
             t0 = time.perf_counter()
-            if decode_mode and k >= 2 and profiler is None:
+            if decode_mode and k >= first and profiler is None:
                 # the remaining steps on the device, each one's token fed back
                 # as the next one's input; per-step device times by events
                 self.ex.set_decode_feedback("logits", "input_ids", toks[-1])
@@ -1017,19 +1031,13 @@ class OnnxDecoder:
                 if step_ms is not None:
                     step_ms.extend(ms)
                 break
-            if decode_mode and k >= 2:
+            if decode_mode and k >= first:
                 toks.append(self._decode_step(toks[-1], profiler))
             else:
                 toks.append(self._step(np.array([[toks[-1]]], np.int64), n + k, seed=seed,
                                        profiler=profiler))
                 if decode_mode and k + 1 < max_tokens:
-                    # the caches now hold n + k positions: switch to decode mode
-                    # (past by shape with length 0, the new position's mask)
-                    self.ex.set_decode_position(n + k, "attention_mask")
-                    for i in self.past:
-                        self.ex.set_input_shape(i["name"], np.float32,
-                                                [1, i["shape"][1], 0, i["shape"][3]])
-                    self.ex.set_input("attention_mask", np.ones((1, 1), np.int64))
+                    self._enter_decode(n + k)  # the caches now hold n + k positions
             if step_ms is not None:
                 step_ms.append((time.perf_counter() - t0) * 1e3)
             seed = None

@@ -2,7 +2,7 @@
 src/kernels/matmul.cc:207-216 behind rt::SetGemvDecodeEnabled, :56-61):
 the transposed weight copies it reads, the context switch that turns it off
 (`inferc decode --no-gemv`), and a fed input that shadows an initializer of
-the same name."""
+the same name; and when a recorded run may be replayed."""
 from __future__ import annotations
 
 import numpy as np
@@ -80,4 +80,26 @@ def test_fed_input_shadowing_an_initializer(ctx):
         y = ex.run({"x": x, "W": w_fed}, ["y"])["y"]
         np.testing.assert_allclose(y, _ref(x, w_fed), rtol=1e-4, atol=1e-4)
     assert ex.device_bytes()["transposed_copies"] == 0
+    ex.close()
+
+
+def test_recording_not_replayed_after_its_uploaded_constant_changed(ctx):
+    """y = x * float(S) for x [1, S]: the scalar is host shape math that the
+    Mul kernel reads from an uploaded device copy. The longer length runs
+    first, so both lengths share the input and output buffers and their
+    recordings differ only in that constant's bytes: after the other length
+    uploads its value, a recording must be planned again, not replayed."""
+    g = rt.Graph()
+    g.add_initializer("one", np.array(1, np.int64))
+    g.add_node("Shape", ["x"], ["s"])
+    g.add_node("Gather", ["s", "one"], ["n"], axis=0)
+    g.add_node("Cast", ["n"], ["nf"], to=1)
+    g.add_node("Mul", ["x", "nf"], ["y"])
+    g.add_output("y")
+    ex = rt.Executor(ctx, g)
+    rng = np.random.default_rng(11)
+    xs = {S: rng.standard_normal((1, S)).astype(np.float32) for S in (8, 6)}
+    for S in (8, 8, 8, 6, 6, 6, 8, 8, 8, 6, 8, 6, 6):
+        y = ex.run({"x": xs[S]}, ["y"])["y"]
+        np.testing.assert_array_equal(y, xs[S] * np.float32(S), err_msg=f"S={S}")
     ex.close()

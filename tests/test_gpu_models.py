@@ -41,6 +41,27 @@ def test_encoder_small_ragged_and_graph_replay(ctx):
         O.encoder_forward(cfg, w, ids2, mask2), atol=1e-4)
 
 
+def test_encoder_recordings_of_several_signatures(ctx):
+    """The executor keeps a recording per input signature (up to four): runs
+    that alternate between batch shapes replay each shape's recording, with
+    that shape's outputs, after runs of the others; a larger shape, whose
+    pass grows the buffers, makes the recordings naming the old ones stale
+    instead of replaying them; a fifth signature evicts the least recently
+    used. Every run against the oracle."""
+    cfg = graphs.small_encoder_cfg()
+    w, ex = _encoder(ctx, cfg, 22)
+    shapes = {"a": (2, 24), "b": (3, 40), "c": (1, 16), "d": (2, 8), "e": (1, 40)}
+    inputs = {k: graphs.encoder_inputs(cfg, B, S, ragged=True, seed=30 + i)
+              for i, (k, (B, S)) in enumerate(shapes.items())}
+    refs = {k: O.encoder_forward(cfg, w, *inputs[k]) for k in shapes}
+    for k in "aaa" "bbb" "aaa" "bab" "ccc" "abc" "ddd" "eee" "abcde" "edcba":
+        ids, mask = inputs[k]
+        out = ex.run({"input_ids": ids, "attention_mask": mask}, ["logits"])["logits"]
+        assert out.shape == (shapes[k][0], 2), k
+        np.testing.assert_allclose(out, refs[k], atol=1e-4, err_msg=k)
+    ex.close()
+
+
 def test_encoder_unsupported_op_raises(ctx):
     g = rt.Graph()
     g.add_node("NonZero", ["x"], ["y"])
