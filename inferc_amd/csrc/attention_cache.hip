@@ -244,6 +244,28 @@ __global__ __launch_bounds__(256) void gather_rows_at_kernel(int64_t rows, int64
   }
 }
 
+// out[i, :] = a[ids[i], :] + b[min(*pos + i, b_rows - 1), :]: a token
+// embedding row (negative ids wrap; an id out of range reads zeros and sets
+// *err, as gather_kernel does) plus the position embedding row at the device
+// position.
+__global__ __launch_bounds__(256) void embed_add_at_kernel(
+    const float* __restrict__ a, int64_t a_rows, const int64_t* __restrict__ ids,
+    const float* __restrict__ b, int64_t b_rows, const int64_t* __restrict__ pos, int64_t n,
+    int64_t row_len, float* __restrict__ out, int32_t* err) {
+  const int64_t p0 = *pos;
+  for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < n * row_len;
+       e += int64_t(gridDim.x) * 256) {
+    const int64_t i = e / row_len, c = e % row_len;
+    int64_t t = ids[i];
+    if (t < 0) t += a_rows;
+    const bool ok = t >= 0 && t < a_rows;
+    if (!ok && err) *err = 1;
+    int64_t rw = p0 + i;
+    rw = rw < 0 ? 0 : rw < b_rows ? rw : b_rows - 1;
+    out[e] = (ok ? a[t * row_len + c] : 0.0f) + b[rw * row_len + c];
+  }
+}
+
 __global__ void advance_position_kernel(int64_t* pos, int64_t step) {
   if (threadIdx.x == 0) *pos += step;
 }
@@ -272,6 +294,20 @@ void gather_rows_at(inferc_hip_ctx* ctx, int64_t rows, int64_t row_len, const fl
   hipLaunchKernelGGL(gather_rows_at_kernel, dim3(unsigned(blocks > 1024 ? 1024 : blocks)),
                      dim3(256), 0, ctx->stream, rows, row_len, table, pos, n, out);
   check_launch("gather at position");
+}
+
+void embed_add_at(inferc_hip_ctx* ctx, const float* a, int64_t a_rows, const int64_t* ids,
+                  const float* b, int64_t b_rows, const int64_t* pos, int64_t n, int64_t row_len,
+                  float* out, int32_t* err) {
+  IH_REQUIRE(a_rows > 0 && b_rows > 0 && row_len >= 0 && n >= 0, INFERC_ERR_SHAPE,
+             "embedding add: bad shape");
+  if (n == 0 || row_len == 0) return;
+  IH_REQUIRE(a && ids && b && pos && out, INFERC_ERR_ARG, "embedding add: null pointer");
+  const int64_t blocks = ceil_div(n * row_len, 256);
+  hipLaunchKernelGGL(embed_add_at_kernel, dim3(unsigned(blocks > 1024 ? 1024 : blocks)),
+                     dim3(256), 0, ctx->stream, a, a_rows, ids, b, b_rows, pos, n, row_len, out,
+                     err);
+  check_launch("embedding add");
 }
 
 void advance_position(inferc_hip_ctx* ctx, int64_t* pos, int64_t step) {

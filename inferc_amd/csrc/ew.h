@@ -82,6 +82,11 @@ void cache_attention(inferc_hip_ctx* ctx, const CacheAttnArgs& a);
 void cache_write_tokens(inferc_hip_ctx* ctx, int64_t B, int64_t S, int64_t nH, int64_t dh,
                         int64_t max_t, int64_t t0, const float* src, int64_t ld, float* cache,
                         const int64_t* pos = nullptr);
+// out[i, :] = a[ids[i], :] + b[*pos + i, :] for i < n (ids on the device; one
+// out of range sets *err when err is given and reads zeros).
+void embed_add_at(inferc_hip_ctx* ctx, const float* a, int64_t a_rows, const int64_t* ids,
+                  const float* b, int64_t b_rows, const int64_t* pos, int64_t n, int64_t row_len,
+                  float* out, int32_t* err);
 // out[i, :] = table[*pos + i, :] for i < n (rows clamped to the table): the
 // position-embedding rows of a decode step whose past length is on the device.
 void gather_rows_at(inferc_hip_ctx* ctx, int64_t rows, int64_t row_len, const float* table,

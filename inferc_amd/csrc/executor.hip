@@ -200,7 +200,18 @@ struct inferc_executor {
     int64_t vocab, feat, n;
   };
   std::unordered_map<std::string, PendingGather> pending_gather;  // this walk
+  // Decode mode: the Add of a token-embedding Gather (device ids) and the
+  // position-embedding Gather runs as one kernel; the two gathers leave
+  // their rows pending for it (embed_gather_at / embed_add_at, by node).
+  struct PendingEmbed {
+    const float* table;
+    int64_t rows, feat, n;
+    const int64_t* ids;  // token rows by these device ids; null: rows at the device position
+  };
+  std::unordered_map<std::string, PendingEmbed> pending_embed;  // this walk
+  std::vector<char> embed_gather_at, embed_add_at;
   void materialize_gather(const std::string& name);
+  void materialize_embed(const std::string& name);
   // Equals on graph inputs and initializers, each computed by the launch of
   // a LayerNorm before it (by that LayerNorm's output; decided when
   // planning), and the ones done so in this walk.
@@ -353,6 +364,7 @@ struct inferc_executor {
   };
   std::unordered_map<std::string, Upload> uploads;
   void* dev_of(const std::string& name) {
+    if (!pending_embed.empty()) materialize_embed(name);  // (a reader the plan did not expect)
     ih::Value* vp = find_val(name);
     if (!vp) ih::fail(INFERC_ERR_STATE, "Executor: missing tensor '" + name + "'");
     ih::Value& v = *vp;
@@ -1374,6 +1386,26 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     return;
   }
   if (op == "Add") {
+    if (decode && embed_add_at[node_index(n)] && n.in.size() == 2) {
+      auto e0 = pending_embed.find(n.in[0]), e1 = pending_embed.find(n.in[1]);
+      if (e0 != pending_embed.end() && e1 != pending_embed.end() &&
+          (e0->second.ids == nullptr) != (e1->second.ids == nullptr) &&
+          get(n.in[0]).shape == get(n.in[1]).shape && e0->second.feat == e1->second.feat &&
+          e0->second.n == e1->second.n) {
+        const PendingEmbed& tok = e0->second.ids ? e0->second : e1->second;
+        const PendingEmbed& pos = e0->second.ids ? e1->second : e0->second;
+        float* y = static_cast<float*>(make_dev(n.out[0], INFERC_DT_F32, get(n.in[0]).shape).dev);
+        if (!dry) {
+          ih::embed_add_at(ctx, tok.table, tok.rows, tok.ids, pos.table, pos.rows, decode_pos,
+                           tok.n, tok.feat, y, gather_err);
+          dev_gather = true;
+        }
+        pending_embed.erase(n.in[0]);
+        pending_embed.erase(n.in[1]);
+        return;
+      }
+      for (int k = 0; k < 2; ++k) materialize_embed(n.in[size_t(k)]);
+    }
     const Value& a0 = in(0);
     const Value& b0 = in(1);
     if (a0.host && b0.host && a0.dtype == INFERC_DT_I64 && b0.dtype == INFERC_DT_I64 &&
@@ -1464,7 +1496,30 @@ void inferc_executor::exec_node(const inferc_graph::Node& n) {
     std::vector<int64_t> os(data.shape.begin(), data.shape.begin() + axis);
     for (int64_t d : idx.shape) os.push_back(d);
     for (int64_t i = axis + 1; i < r; ++i) os.push_back(data.shape[size_t(i)]);
-    if (decode && pos_gather_at[node_index(n)]) {
+    const size_t ni = node_index(n);
+    if (decode && embed_gather_at[ni] && axis == 0 && r == 2 && data.dtype == INFERC_DT_F32 &&
+        idx.dtype == INFERC_DT_I64 && (pos_gather_at[ni] || !idx.host)) {
+      // rows for the embedding Add that reads this output (one kernel there)
+      PendingEmbed pe{static_cast<const float*>(dev_of(n.in[0])), data.shape[0], data.shape[1],
+                      idx.numel(), nullptr};
+      if (pos_gather_at[ni]) {
+        const std::vector<int64_t> ix = host_i64(idx, "Gather");
+        for (size_t i = 0; i < ix.size(); ++i)
+          IH_REQUIRE(ix[i] == int64_t(i), INFERC_ERR_UNSUPPORTED,
+                     "Gather: decode mode needs the positions of the new tokens in order");
+        IH_REQUIRE(decode_len + int64_t(ix.size()) <= data.shape[0], INFERC_ERR_SHAPE,
+                   "Gather: position past the end of the embedding table");
+      } else {
+        pe.ids = static_cast<const int64_t*>(dev_of(n.in[1]));
+      }
+      ih::Value v;
+      v.dtype = INFERC_DT_F32;
+      v.shape = os;
+      vals[n.out[0]] = v;
+      pending_embed[n.out[0]] = pe;
+      return;
+    }
+    if (decode && pos_gather_at[ni]) {
       // decode mode: the indices, walked for an empty past, are the new
       // positions 0 .. n-1; the rows are those past the device's past length
       IH_REQUIRE(idx.host && idx.dtype == INFERC_DT_I64, INFERC_ERR_UNSUPPORTED,
@@ -2065,6 +2120,12 @@ bool inferc_executor::exec_generic(const inferc_graph::Node& n) {
     (void)dtype_size(to);
     if (to == x.dtype) {
       alias(n.out[0], x, x.shape);
+      auto pe = pending_embed.find(n.in[0]);  // rows pending for an embedding Add
+      if (pe != pending_embed.end()) {
+        const PendingEmbed e = pe->second;
+        pending_embed.erase(pe);
+        pending_embed[n.out[0]] = e;
+      }
       return true;
     }
     if (host_foldable(n, x.numel())) {
@@ -2221,6 +2282,7 @@ void inferc_executor::walk(std::vector<int64_t>* act, bool track) {
   fb_parts_n = 0;
   ln_gemm_off.clear();
   pending_gather.clear();
+  pending_embed.clear();
   eq_done.clear();
   cache_views.clear();
   for (auto& kv : inputs) vals[kv.first] = kv.second.v;
@@ -2466,6 +2528,49 @@ void inferc_executor::plan_decode(const std::string& mask_input) {
     }
     decode_skip_at[i] = dead ? 1 : 0;
   }
+  // Add(token rows, position rows): the Add of a row Gather from an
+  // initializer table (the token embedding) and the position gather, each
+  // read by the Add alone (through at most one same-type Cast; Shape nodes
+  // read only the shape, which a pending value has), runs as one
+  // kernel. Whether the token ids are on the device is decided at run time
+  // (host-known ids leave the gathers as they are).
+  embed_gather_at.assign(nodes.size(), 0);
+  embed_add_at.assign(nodes.size(), 0);
+  auto sole = [&](const std::string& v) {  // one reader of the data (Shape reads no data)
+    auto it = readers.find(v);
+    if (outs.count(v) || it == readers.end()) return false;
+    size_t data_readers = 0;
+    for (const auto& r : it->second) data_readers += nodes[r.first].op != "Shape";
+    return data_readers == 1;
+  };
+  for (size_t i = 0; i < nodes.size(); ++i) {
+    const inferc_graph::Node& n = nodes[i];
+    if (n.op != "Add" || n.in.size() != 2 || n.out.size() != 1 || decode_skip_at[i]) continue;
+    size_t g[2] = {0, 0};
+    int n_pos = 0;
+    bool ok = true;
+    for (size_t k = 0; k < 2 && ok; ++k) {
+      std::string v = n.in[k];
+      auto pr = producer.find(v);
+      ok = pr != producer.end() && sole(v);
+      if (ok && pr->second->op == "Cast" && !pr->second->in.empty()) {
+        v = pr->second->in[0];
+        pr = producer.find(v);
+        ok = pr != producer.end() && sole(v);
+      }
+      if (!ok) break;
+      g[k] = node_index(*pr->second);
+      const inferc_graph::Node& gn = nodes[g[k]];
+      auto t = inits.find(gn.in.empty() ? std::string() : gn.in[0]);
+      ok = gn.op == "Gather" && gn.in.size() == 2 && gn.out.size() == 1 && t != inits.end() &&
+           t->second.shape.size() == 2 && ih::attr_int(gn, "axis", 0) == 0 &&
+           !gn.attrs.count("__ln_g");
+      if (ok && pos_gather_at[g[k]]) ++n_pos;
+    }
+    if (!ok || n_pos != 1) continue;
+    embed_add_at[i] = 1;
+    embed_gather_at[g[0]] = embed_gather_at[g[1]] = 1;
+  }
 }
 
 // Waits for the stream, then fails if a device-index gather of the passes
@@ -2481,6 +2586,24 @@ void inferc_executor::materialize_gather(const std::string& name) {
   if (!dry) {
     ih::gather_axis(ctx, 1, g.vocab, g.feat, g.table, g.ids, g.n, y, gather_err);
     dev_gather = true;
+  }
+}
+
+// Rows left pending for an embedding Add that cannot take them as one kernel
+// after all: written out on their own.
+void inferc_executor::materialize_embed(const std::string& name) {
+  auto it = pending_embed.find(name);
+  if (it == pending_embed.end()) return;
+  const PendingEmbed e = it->second;
+  pending_embed.erase(it);
+  const std::vector<int64_t> shape = get(name).shape;
+  float* y = static_cast<float*>(make_dev(name, INFERC_DT_F32, shape).dev);
+  if (dry) return;
+  if (e.ids) {
+    ih::gather_axis(ctx, 1, e.rows, e.feat, e.table, e.ids, e.n, y, gather_err);
+    dev_gather = true;
+  } else {
+    ih::gather_rows_at(ctx, e.rows, e.feat, e.table, decode_pos, e.n, y);
   }
 }
 

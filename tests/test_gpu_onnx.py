@@ -107,6 +107,28 @@ def test_decode_feedback_matches_host_steps(ctx):
     dec.close()
 
 
+def test_decode_mode_token_out_of_range(ctx):
+    """In decode mode the token and position embedding rows are one kernel:
+    a token id out of the vocabulary still fails the step as Gather does on
+    the host (embedding.cc:63), in the planning pass and in a replay, and the
+    steps after it run clean."""
+    io = np.load(GOLDEN / "gpt2_tiny_past_io.npz")
+    dec = rt.OnnxDecoder(ctx, GOLDEN / "gpt2_tiny_past.onnx", max_t=32)
+    prompt = np.asarray(io["prompt"], np.int64).reshape(1, -1)
+    n = prompt.shape[1]
+    tok = dec._step(prompt, n)
+    dec._enter_decode(n)
+    for bad in (True, False, False, True, False):  # planning pass, recording, replays
+        if bad:
+            with pytest.raises(RuntimeError, match="index out of range"):
+                dec._decode_step(2 ** 40)
+        else:
+            tok = dec._decode_step(tok)
+            assert 0 <= tok < dec.logits().shape[-1]
+    dec.ex.set_decode_position(-1)
+    dec.close()
+
+
 def test_onnx_decoder_greedy_tokens_match_torch(ctx):
     """`inferc decode` over the exported with-past graph with the device KV
     cache: the 12 greedy tokens equal torch's generation with its own cache
