@@ -137,20 +137,26 @@ struct AttnDecP {
 
 constexpr int kDecWaves = 8;
 
-__global__ __launch_bounds__(64 * kDecWaves) void attn_decode_d64(AttnDecP p) {
+// The operands are scalar arguments (not an AttnDecP by value): the leading
+// ones arrive preloaded in SGPRs, so the position and row loads wait on no
+// load of the argument block.
+__global__ __launch_bounds__(64 * kDecWaves) void attn_decode_d64(
+    const int64_t* __restrict__ pos_p, const float* __restrict__ q_all,
+    const float* __restrict__ k_new, const float* __restrict__ v_new, float* kc_all,
+    float* vc_all, float* out, int64_t T) {
   constexpr int D = 64;
   __shared__ float sm[kDecWaves], sl[kDecWaves];
   __shared__ float so[kDecWaves][D];
   __shared__ __align__(16) float se[kDecWaves][kDecChunk];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t h = blockIdx.x;
-  const int64_t pos = *p.pos;
-  if (pos < 0 || pos >= p.T) return;  // uniform: the host keeps pos < T
+  const int64_t pos = *pos_p;
+  if (pos < 0 || pos >= T) return;  // uniform: the host keeps pos < T
   const int64_t t = pos + 1;
-  float* kc = p.kc + h * p.T * D;
-  float* vc = p.vc + h * p.T * D;
-  const float* kn = p.k_new + h * D;
-  const float* vn = p.v_new + h * D;
+  float* kc = kc_all + h * T * D;
+  float* vc = vc_all + h * T * D;
+  const float* kn = k_new + h * D;
+  const float* vn = v_new + h * D;
   if (wave == 0) {
     // Rows of position pos are read from kn/vn below, never from the cache,
     // so this append needs no barrier.
@@ -160,7 +166,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode_d64(AttnDecP p) {
   const int dh = (lane & 1) * 32;
   float4 qv[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) qv[i] = *reinterpret_cast<const float4*>(p.q + h * D + dh + 4 * i);
+  for (int i = 0; i < 8; ++i) qv[i] = *reinterpret_cast<const float4*>(q_all + h * D + dh + 4 * i);
   const float rs = sqrtf(float(D));
   float M = -INFINITY, L = 0.0f, O = 0.0f;
   for (int64_t j0 = int64_t(wave) * kDecChunk; j0 < t; j0 += kDecWaves * kDecChunk) {
@@ -228,8 +234,13 @@ __global__ __launch_bounds__(64 * kDecWaves) void attn_decode_d64(AttnDecP p) {
       Lt += c * sl[w];
       Ot += c * so[w][lane];
     }
-    p.out[h * D + lane] = Ot / Lt;
+    out[h * D + lane] = Ot / Lt;
   }
+}
+
+void launch_attn_decode(const AttnDecP& p, int64_t heads, hipStream_t s) {
+  hipLaunchKernelGGL(attn_decode_d64, dim3(unsigned(heads)), dim3(64 * kDecWaves), 0, s, p.pos,
+                     p.q, p.k_new, p.v_new, p.kc, p.vc, p.out, p.T);
 }
 
 // The decode step's tail, one block of 1024 threads: merges the LM-head
@@ -370,9 +381,7 @@ void kv_append_attend(inferc_hip_ctx* ctx, int64_t nH, int64_t D, int64_t T,
   IH_REQUIRE(aligned16(q) && aligned16(k_new) && aligned16(kc) && aligned16(vc),
              INFERC_ERR_ARG, "kv_append_attend: pointers must be 16-byte aligned");
   if (D == 64) {
-    AttnDecP ap{T, pos, q, k_new, v_new, kc, vc, out};
-    hipLaunchKernelGGL(attn_decode_d64, dim3(unsigned(nH)), dim3(64 * kDecWaves), 0, ctx->stream,
-                       ap);
+    launch_attn_decode(AttnDecP{T, pos, q, k_new, v_new, kc, vc, out}, nH, ctx->stream);
     check_launch("attn_decode");
     return;
   }
@@ -521,9 +530,9 @@ struct inferc_gpt2 {
         ih::int4_gemv_dec(ctx, 3 * Hh, Hh, L.attn_q, L.attn_s, h, L.ln1_g, L.ln1_b, cfg.eps,
                           L.attn_b, nullptr, INFERC_ACT_NONE, qkv, nullptr);
         mark(kOpAttn, l, ".attn");
-        ih::AttnDecP ap{max_t, state, qkv, qkv + Hh, qkv + 2 * Hh, kc_l(l), vc_l(l), att};
-        hipLaunchKernelGGL(ih::attn_decode_d64, dim3(unsigned(cfg.heads)),
-                           dim3(64 * ih::kDecWaves), 0, s, ap);
+        ih::launch_attn_decode(
+            ih::AttnDecP{max_t, state, qkv, qkv + Hh, qkv + 2 * Hh, kc_l(l), vc_l(l), att},
+            cfg.heads, s);
         ih::check_launch("attn_decode");
         mark(kOpProjRes, l, ".attn.proj");
         ih::int4_gemv_dec(ctx, Hh, Hh, L.proj_q, L.proj_s, att, nullptr, nullptr, 0.0f, L.proj_b,
@@ -545,9 +554,9 @@ struct inferc_gpt2 {
                INFERC_ACT_NONE, qkv);
       mark(kOpAttn, l, ".attn");
       if (fast()) {
-        ih::AttnDecP ap{max_t, state, qkv, qkv + Hh, qkv + 2 * Hh, kc_l(l), vc_l(l), att};
-        hipLaunchKernelGGL(ih::attn_decode_d64, dim3(unsigned(cfg.heads)),
-                           dim3(64 * ih::kDecWaves), 0, s, ap);
+        ih::launch_attn_decode(
+            ih::AttnDecP{max_t, state, qkv, qkv + Hh, qkv + 2 * Hh, kc_l(l), vc_l(l), att},
+            cfg.heads, s);
         ih::check_launch("attn_decode");
       } else {
         ih::kv_append_attend(ctx, cfg.heads, D(), max_t, state, qkv, qkv + Hh, qkv + 2 * Hh,
