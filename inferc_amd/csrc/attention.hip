@@ -641,25 +641,31 @@ __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_ks(AttnP p) {
 // block w for all 16 queries.
 
 template <int KW, bool MROW>
-__global__ __launch_bounds__(64 * KW) void attn_fwd_d64_q16(AttnP p) {
+// The operands of the first loads lead the arguments as scalars (preloaded
+// in SGPRs); the rest of the launch's parameters come in p.
+__global__ __launch_bounds__(64 * KW) void attn_fwd_d64_q16(const float* __restrict__ q_,
+                                                            const float* __restrict__ k_,
+                                                            const float* __restrict__ v_,
+                                                            int64_t S_, int64_t ldq, int64_t ldk,
+                                                            int64_t ldv, AttnP p) {
   __shared__ __attribute__((aligned(16))) float obuf[KW][16][kD + 4];
   __shared__ float sm[KW][16], sl[KW][16];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t b = blockIdx.z, h = blockIdx.y, S = p.S;
+  const int64_t b = blockIdx.z, h = blockIdx.y, S = S_;
   const int64_t q0 = int64_t(blockIdx.x) * 16;
   const int64_t qi = q0 + r;
   const int64_t qc = qi < S ? qi : S - 1;
-  const float* qbase = p.q + b * S * p.ldq + h * kD;
-  const float* kbase = p.k + b * S * p.ldk + h * kD;
-  const float* vbase = p.v + b * S * p.ldv + h * kD;
+  const float* qbase = q_ + b * S * ldq + h * kD;
+  const float* kbase = k_ + b * S * ldk + h * kD;
+  const float* vbase = v_ + b * S * ldv + h * kD;
   const uint8_t* mbase = p.mask ? p.mask + b * p.ms0 + h * p.ms1 : nullptr;
 
   float4 qv[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
-    qv[c] = *reinterpret_cast<const float4*>(qbase + qc * p.ldq + 16 * g + 4 * c);
+    qv[c] = *reinterpret_cast<const float4*>(qbase + qc * ldq + 16 * g + 4 * c);
 
   floatx4 oacc[4];
 #pragma unroll
@@ -677,14 +683,14 @@ __global__ __launch_bounds__(64 * KW) void attn_fwd_d64_q16(AttnP p) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int64_t kr = k0 + 16 * kb + r;
-      const float* kp = kbase + (kr < S ? kr : S - 1) * p.ldk + 16 * g;
+      const float* kp = kbase + (kr < S ? kr : S - 1) * ldk + 16 * g;
 #pragma unroll
       for (int c = 0; c < 4; ++c) kv[kb][c] = *reinterpret_cast<const float4*>(kp + 4 * c);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int64_t key = k0 + 16 * kb + 4 * g + v;
         const int64_t kc = key < S ? key : S - 1;
-        vv[kb][v] = *reinterpret_cast<const floatx4*>(vbase + kc * p.ldv + 4 * r);
+        vv[kb][v] = *reinterpret_cast<const floatx4*>(vbase + kc * ldv + 4 * r);
         if (!MROW)
           mk[kb][v] = (mbase && !p.causal && qi < S) ? mbase[qi * p.ms2 + kc * p.ms3] : uint8_t(0);
       }
@@ -851,9 +857,11 @@ void attention(inferc_hip_ctx* ctx, const AttnArgs& a) {
       // few blocks: 16 queries per block, four waves splitting the key tiles
       dim3 grid(unsigned(ceil_div(a.S, 16)), unsigned(p.nH), unsigned(a.B));
       if (p.mask != nullptr && !p.causal && p.ms2 == 0)
-        hipLaunchKernelGGL((attn_fwd_d64_q16<4, true>), grid, dim3(256), 0, ctx->stream, p);
+        hipLaunchKernelGGL((attn_fwd_d64_q16<4, true>), grid, dim3(256), 0, ctx->stream, p.q, p.k,
+                           p.v, p.S, p.ldq, p.ldk, p.ldv, p);
       else
-        hipLaunchKernelGGL((attn_fwd_d64_q16<4, false>), grid, dim3(256), 0, ctx->stream, p);
+        hipLaunchKernelGGL((attn_fwd_d64_q16<4, false>), grid, dim3(256), 0, ctx->stream, p.q,
+                           p.k, p.v, p.S, p.ldq, p.ldk, p.ldv, p);
     } else if (blocks4 >= ctx->num_cus && a.S <= 4 * kKT &&
                (p.mask == nullptr || p.causal || p.ms2 == 0)) {
       // short sequences: the whole K/V of a (batch, head) staged at once
