@@ -146,15 +146,16 @@ struct Gemv2P {
 // x (and LayerNorm's gamma and beta) for the lane's columns; the loads go
 // out before any of them is used.
 template <int KV, int XSRC>
-__device__ __forceinline__ void gemv2_x_load(const Gemv2P& p, const float* x, int lane,
-                                             float4 (&xv)[KV], float4 (&lg)[KV], float4 (&lb)[KV]) {
+__device__ __forceinline__ void gemv2_x_load(const float* ln_g, const float* ln_b, const float* x,
+                                             int lane, float4 (&xv)[KV], float4 (&lg)[KV],
+                                             float4 (&lb)[KV]) {
 #pragma unroll
   for (int j = 0; j < KV; ++j) xv[j] = *reinterpret_cast<const float4*>(x + 4 * lane + 256 * j);
   if (XSRC == XSRC_LN) {
 #pragma unroll
     for (int j = 0; j < KV; ++j) {
-      lg[j] = *reinterpret_cast<const float4*>(p.ln_g + 4 * lane + 256 * j);
-      lb[j] = *reinterpret_cast<const float4*>(p.ln_b + 4 * lane + 256 * j);
+      lg[j] = *reinterpret_cast<const float4*>(ln_g + 4 * lane + 256 * j);
+      lb[j] = *reinterpret_cast<const float4*>(ln_b + 4 * lane + 256 * j);
     }
   }
 }
@@ -198,11 +199,16 @@ __device__ __forceinline__ float4 w_load_nt(const float* p) {
 }
 
 template <int R, int KV, int XSRC, bool ARGMAX>
-// W, x and N lead the arguments, so the first loads wait on no scalar load of
-// the argument block (leading arguments arrive in SGPRs); every other operand
-// (LayerNorm terms, bias, residual) is fetched right behind them.
+// W, x and N lead the arguments, then the LayerNorm terms, bias, residual
+// and output: none of the kernel's loads waits on a scalar load of the
+// argument block (leading arguments arrive in SGPRs). Only the epsilon, the
+// activation and the arg-max partials come in p.
 __global__ __launch_bounds__(kBlock) void gemv2_kernel(const float* __restrict__ W,
                                                       const float* __restrict__ x, int64_t N,
+                                                      const float* __restrict__ ln_g,
+                                                      const float* __restrict__ ln_b,
+                                                      const float* __restrict__ bias,
+                                                      const float* __restrict__ res, float* y,
                                                       Gemv2P p) {
   constexpr int K = 256 * KV;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -216,15 +222,15 @@ __global__ __launch_bounds__(kBlock) void gemv2_kernel(const float* __restrict__
       w[i][j] = w_load_nt(W + rc * K + 4 * lane + 256 * j);
   }
   float4 xv[KV], lg[KV], lb[KV];
-  gemv2_x_load<KV, XSRC>(p, x, lane, xv, lg, lb);
+  gemv2_x_load<KV, XSRC>(ln_g, ln_b, x, lane, xv, lg, lb);
   // the epilogue's bias and residual of the wave's rows (an absent operand
   // reads W instead)
   float bb[R], rr[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int64_t rc = r0 + i < N ? r0 + i : N - 1;
-    bb[i] = (p.bias ? p.bias : W)[p.bias ? rc : 0];
-    rr[i] = (p.res ? p.res : W)[p.res ? rc : 0];
+    bb[i] = (bias ? bias : W)[bias ? rc : 0];
+    rr[i] = (res ? res : W)[res ? rc : 0];
   }
   gemv2_x<KV, XSRC>(p, lane, xv, lg, lb);
   float acc[R];
@@ -243,10 +249,10 @@ __global__ __launch_bounds__(kBlock) void gemv2_kernel(const float* __restrict__
     const int64_t r = r0 + i;
     if (r < N) {
       float v = acc[i];
-      if (p.bias) v = v + bb[i];
-      if (p.res) v = v + rr[i];
+      if (bias) v = v + bb[i];
+      if (res) v = v + rr[i];
       v = apply_act(v, p.act);
-      if (lane == i) p.y[r] = v;
+      if (lane == i) y[r] = v;
       if (ARGMAX && v > bv) {  // rows ascend: strict '>' keeps the first max
         bv = v;
         bi = r;
@@ -1507,17 +1513,16 @@ int gemv2_rows(inferc_hip_ctx* ctx, int64_t N, int64_t K) {
 template <int R, int KV>
 void gemv2_launch_r(const Gemv2P& p, unsigned blocks, int xsrc, bool argmax, hipStream_t s) {
   const dim3 g(blocks), b(kBlock);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, g, b, 0, s, p.W, p.x, p.N, p.ln_g, p.ln_b, p.bias, p.res, p.y, p);
+  };
   if (argmax) {
-    if (xsrc == XSRC_LN)
-      hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_LN, true>), g, b, 0, s, p.W, p.x, p.N, p);
-    else
-      hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_PLAIN, true>), g, b, 0, s, p.W, p.x, p.N, p);
+    if (xsrc == XSRC_LN) go(gemv2_kernel<R, KV, XSRC_LN, true>);
+    else go(gemv2_kernel<R, KV, XSRC_PLAIN, true>);
     return;
   }
-  if (xsrc == XSRC_LN)
-    hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_LN, false>), g, b, 0, s, p.W, p.x, p.N, p);
-  else
-    hipLaunchKernelGGL((gemv2_kernel<R, KV, XSRC_PLAIN, false>), g, b, 0, s, p.W, p.x, p.N, p);
+  if (xsrc == XSRC_LN) go(gemv2_kernel<R, KV, XSRC_LN, false>);
+  else go(gemv2_kernel<R, KV, XSRC_PLAIN, false>);
 }
 
 }  // namespace
