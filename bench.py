@@ -196,9 +196,12 @@ def bench_graph(ctx, g, inputs: dict, steps: int, warmup: int) -> float:
     return ms
 
 
-def bench_decode(ctx, max_tokens: int = 128, prompt_len: int = 32, int4: bool = False):
+def bench_decode(ctx, max_tokens: int = 128, prompt_len: int = 32, int4: bool = False,
+                 warm: bool = True):
     """Config 4 (int4=False), or the same model switched to int4 weight-only
-    decode (inferc_gpt2_use_int4)."""
+    decode (inferc_gpt2_use_int4). warm=False times the first generate (the
+    --decode-only mode for kernel traces: under the tracer, a run that
+    replayed one step graph over two generates died in the tracer)."""
     from inferc_amd import graphs, rt
 
     cfg = graphs.GPT2_SMALL
@@ -211,7 +214,8 @@ def bench_decode(ctx, max_tokens: int = 128, prompt_len: int = 32, int4: bool = 
     # it, and the GPU returns to its sustained clocks after the weight upload),
     # then one generate whose every post-prefill step is timed
     # (main.cpp:863-872).
-    dec.generate(prompt, max_tokens)
+    if warm:
+        dec.generate(prompt, max_tokens)
     toks, steps, _ = dec.generate(prompt, max_tokens, want_step_ms=True)
     dec.close()
     return float(np.mean(steps)), float(np.median(steps)), float(np.min(steps)), toks, w, prompt
@@ -834,7 +838,7 @@ def main(argv=None) -> int:
         return 0
     if args.decode_only:
         for int4 in {"fp32": (False,), "int4": (True,), "both": (False, True)}[args.decode_only]:
-            mean, p50, _, _, _, _ = bench_decode(ctx, int4=int4)
+            mean, p50, _, _, _, _ = bench_decode(ctx, int4=int4, warm=False)
             print(f"gpt2 decode {'int4' if int4 else 'fp32'}: {mean:.4f} ms/token "
                   f"(p50 {p50:.4f})", flush=True)
         ctx.close()
