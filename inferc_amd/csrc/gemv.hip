@@ -1263,6 +1263,12 @@ __device__ __forceinline__ void int4_b8_block(I4B8Smem<G, NW, ROWS>& sm, const I
     for (int j = 0; j < 3; ++j) xv[k][j] = gload_f4(xs + 64 * j + lane);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // Every wave's x requests go out before any weight request of the block:
+  // a CU serves its waves' loads in issue order, and x queued behind the
+  // other waves' first units held up the preparation. A bare s_barrier
+  // leaves the loads in flight.
+  asm volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
   // the ring: slot j holds a unit's 6 steps (lane (r, g): row 16 i + r,
   // bytes [384 q + 64 t + 16 g, +16)) and, with the slab-0 unit of a tile,
   // the scale of row 16 i + r; rows past N are clamped and never stored

@@ -109,6 +109,29 @@ def test_int4_grouped_mixed_row_lengths_and_odd_rows(ctx, B):
         _check_rows(y.numpy(), W, s, x, K)
 
 
+@pytest.mark.parametrize("B,seed", [(3, 0), (8, 1), (8, 2)])
+def test_int4_grouped_many_ragged_matrices(ctx, B, seed):
+    """Many K = 768 matrices of ragged row counts (1, 16, 17 and random up to
+    700 rows) in one grouped call of the batched kernel, shuffled with one
+    K = 3072 matrix: every row of every matrix against the oracle, outputs
+    pre-filled with NaN so a row left unwritten fails."""
+    rng = np.random.default_rng(900 + seed)
+    shapes = [(int(n), 768) for n in rng.integers(1, 700, 23)] + [(1, 768), (16, 768), (17, 768),
+                                                                   (300, 3072)]
+    rng.shuffle(shapes)
+    mats, host = [], []
+    for i, (N, K) in enumerate(shapes):
+        W, s = graphs.int4_weights(N, K, 1000 + 40 * seed + i, f"span{i}")
+        x = rnd((B, K), 8000 + 50 * seed + i)
+        y = Tensor.empty(ctx, (B, N))
+        _fill(y, np.nan)
+        mats.append((T(ctx, W, np.uint8), T(ctx, s), T(ctx, x), y, K))
+        host.append((W, s, x, K))
+    rt.int4_gemv_grouped(ctx, mats, B)
+    for (_, _, _, y, _), (W, s, x, K) in zip(mats, host):
+        _check_rows(y.numpy(), W, s, x, K)
+
+
 def test_int4_grouped_table_cache_eviction(ctx):
     """A fresh context fills its descriptor-table cache to one slot short of
     full with single-table batch-1 launches; a batch-8 grouped launch then
