@@ -278,6 +278,43 @@ def test_gpt2_generate_profiled_config4(ctx, gpt2_full):
     assert rep["op_counts"] == _decode_counts(cfg["layers"], embed=False)
 
 
+@pytest.mark.parametrize("int4", [False, True])
+def test_gpt2_decode_fills_the_cache_exactly(ctx, gpt2_full, int4):
+    """GPT-2 small (the step's fast kernels): prompt 32 and 9 tokens on a
+    40-position cache, so the last step attends over every slot; tokens equal
+    the oracle's (on the dequantised weights for int4), and one token more is
+    refused before anything runs."""
+    cfg, w = gpt2_full
+    prompt = graphs.gpt2_prompt(cfg, 32)
+    dec = rt.Gpt2Decoder(ctx, cfg, w, max_t=40)
+    ref_w = w
+    if int4:
+        dec.use_int4()
+        ref_w = graphs.gpt2_int4_dequantized(cfg, w)
+    toks, _, logits = dec.generate(prompt, 9, want_logits=True)
+    ref_toks, ref_logits, _ = O.gpt2_generate(cfg, ref_w, prompt, 9)
+    np.testing.assert_array_equal(toks, ref_toks)
+    assert np.max(np.abs(logits - ref_logits)) <= 1e-4
+    with pytest.raises(RuntimeError, match="exceed the KV cache"):
+        dec.generate(prompt, 10)
+    np.testing.assert_array_equal(dec.generate(prompt, 9)[0], toks)
+
+
+def test_gpt2_small_cfg_decode_fills_the_cache_exactly(ctx):
+    """The general step kernels (a model off the GPT-2-small shape): prompt 5
+    and 12 tokens on a 16-position cache."""
+    cfg = graphs.small_gpt2_cfg()
+    w = graphs.gpt2_weights(cfg, 25)
+    prompt = graphs.gpt2_prompt(cfg, 5)
+    dec = rt.Gpt2Decoder(ctx, cfg, w, max_t=16)
+    toks, _, logits = dec.generate(prompt, 12, want_logits=True)
+    ref_toks, ref_logits, _ = O.gpt2_generate(cfg, w, prompt, 12)
+    np.testing.assert_array_equal(toks, ref_toks)
+    np.testing.assert_allclose(logits, ref_logits, atol=1e-4)
+    with pytest.raises(RuntimeError, match="exceed the KV cache"):
+        dec.generate(prompt, 13)
+
+
 def test_gpt2_greedy_decode_config4_bit_exact(ctx, gpt2_full):
     """prompt 32, 128 generated tokens, sequence bit-exact."""
     cfg, w = gpt2_full
