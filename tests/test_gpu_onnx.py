@@ -179,6 +179,30 @@ def test_gpt2_small_with_past_graph_decode_config4(ctx):
     dec.close()
 
 
+def test_gpt2_small_with_past_graph_fills_the_cache_exactly(ctx):
+    """The with-past graph at GPT-2-small shape in decode mode (the native
+    attention kernel on the graph's cache) with prompt 32 and 9 tokens on a
+    40-position cache: the last step attends over every slot. Tokens equal
+    the oracle's; one token more is refused, and the decoder still generates
+    the same tokens after the refusal."""
+    import oracle as O
+    from inferc_amd import graphs
+
+    cfg = graphs.GPT2_SMALL
+    w = graphs.gpt2_weights(cfg, 2)
+    g = rt.Graph.from_onnx(GOLDEN / "gpt2_small_past_noparams.onnx")
+    graphs.gpt2_bind_weights(g, cfg, w)
+    prompt = graphs.gpt2_prompt(cfg, 32)
+    dec = rt.OnnxDecoder(ctx, g, max_t=40)
+    toks = dec.generate(prompt, 9)
+    ref, _, _ = O.gpt2_generate(cfg, w, prompt, 9)
+    np.testing.assert_array_equal(toks, ref)
+    with pytest.raises(RuntimeError, match="exceed the KV cache"):
+        dec.generate(prompt, 10)
+    np.testing.assert_array_equal(dec.generate(prompt, 9), toks)
+    dec.close()
+
+
 def test_gpt2_small_graph_on_the_native_decoder_int4(ctx):
     """`inferc decode --int4`'s route at GPT-2-small shape: the exported
     with-past graph with config 4's weights bound, read back by parameter
