@@ -300,6 +300,21 @@ def test_gpt2_decode_fills_the_cache_exactly(ctx, gpt2_full, int4):
     np.testing.assert_array_equal(dec.generate(prompt, 9)[0], toks)
 
 
+@pytest.mark.parametrize("n_prompt,n_tok", [(1, 6), (1, 1), (4, 1)])
+def test_gpt2_decode_one_token_prompt_and_no_decode_step(ctx, gpt2_full, n_prompt, n_tok):
+    """A one-token prompt (the prefill is a single row), and a generate of one
+    token (the prefill's arg-max alone, no decode step replayed): tokens and
+    the last logits against the oracle."""
+    cfg, w = gpt2_full
+    prompt = graphs.gpt2_prompt(cfg, n_prompt)
+    dec = rt.Gpt2Decoder(ctx, cfg, w, max_t=16)
+    toks, steps, logits = dec.generate(prompt, n_tok, want_step_ms=True, want_logits=True)
+    ref_toks, ref_logits, _ = O.gpt2_generate(cfg, w, prompt, n_tok)
+    np.testing.assert_array_equal(toks, ref_toks)
+    assert np.max(np.abs(logits - ref_logits)) <= 1e-4
+    assert steps.shape == (n_tok - 1,)
+
+
 def test_gpt2_small_cfg_decode_fills_the_cache_exactly(ctx):
     """The general step kernels (a model off the GPT-2-small shape): prompt 5
     and 12 tokens on a 16-position cache."""

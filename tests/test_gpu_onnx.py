@@ -203,6 +203,26 @@ def test_gpt2_small_with_past_graph_fills_the_cache_exactly(ctx):
     dec.close()
 
 
+@pytest.mark.parametrize("n_prompt,n_tok", [(1, 6), (1, 1)])
+def test_gpt2_small_with_past_graph_one_token_prompt(ctx, n_prompt, n_tok):
+    """The with-past graph at GPT-2-small shape with a one-token prompt (an
+    empty past on the first step), and a generate of one token (the prompt
+    step alone): tokens against the oracle."""
+    import oracle as O
+    from inferc_amd import graphs
+
+    cfg = graphs.GPT2_SMALL
+    w = graphs.gpt2_weights(cfg, 2)
+    g = rt.Graph.from_onnx(GOLDEN / "gpt2_small_past_noparams.onnx")
+    graphs.gpt2_bind_weights(g, cfg, w)
+    prompt = graphs.gpt2_prompt(cfg, n_prompt)
+    dec = rt.OnnxDecoder(ctx, g, max_t=16)
+    toks = dec.generate(prompt, n_tok)
+    ref, _, _ = O.gpt2_generate(cfg, w, prompt, n_tok)
+    np.testing.assert_array_equal(toks, ref)
+    dec.close()
+
+
 def test_gpt2_small_graph_on_the_native_decoder_int4(ctx):
     """`inferc decode --int4`'s route at GPT-2-small shape: the exported
     with-past graph with config 4's weights bound, read back by parameter
