@@ -191,6 +191,23 @@ def test_distilbert_encoder_config1(ctx, B, ragged):
     np.testing.assert_array_equal(again, got)
 
 
+@pytest.mark.parametrize("B,S,ragged", [(1, 1, False), (1, 77, True), (3, 200, True)])
+def test_distilbert_encoder_odd_sequence_lengths(ctx, B, S, ragged):
+    """The config-1 encoder off its S = 128: one token (every product a
+    single row), 77 tokens (row counts off the tile grid) and 3 x 200 ragged
+    rows (the large-M GEMM forms, attention over 200 keys); logits within
+    1e-4 of the oracle, and a second run bit-identical."""
+    cfg = graphs.DISTILBERT
+    w, ex = _encoder(ctx, cfg, 1)
+    ids, mask = graphs.encoder_inputs(cfg, B, S, seed=11, ragged=ragged)
+    got = ex.run({"input_ids": ids, "attention_mask": mask}, ["logits"])["logits"]
+    ref = O.encoder_forward(cfg, w, ids, mask)
+    assert got.shape == (B, 2)
+    assert np.max(np.abs(got - ref)) <= 1e-4, np.max(np.abs(got - ref))
+    again = ex.run({"input_ids": ids, "attention_mask": mask}, ["logits"])["logits"]
+    np.testing.assert_array_equal(again, got)
+
+
 def test_gpt2_small_generate_and_forward(ctx):
     cfg = graphs.small_gpt2_cfg()
     w = graphs.gpt2_weights(cfg, 22)
